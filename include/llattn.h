@@ -1,0 +1,154 @@
+/*
+ * llattn.h -- C ABI of the MI355X (gfx950) local+latent attention kernels.
+ *
+ * Plain C: device pointers, element strides, sizes and an opaque stream
+ * (a hipStream_t passed as void*).  No torch or HIP types appear here, so the
+ * library binds from ctypes, cffi or any other FFI.  Every entry point is
+ * asynchronous on the given stream, allocates nothing, keeps no global
+ * mutable state apart from the calling thread's last error message, and
+ * returns LLATTN_OK (0) or one of the status codes below; the message is
+ * then available from llattn_last_error().
+ *
+ * Semantics are those of the reference PyTorch path LocalLatentAttention
+ * (reference models.py:61-462); the entry points replace the launches of the
+ * reference's fused op (reference kernels/llattn_op.py:34-181) and its
+ * pooling helpers (reference llattn_triton.py:97-115, models.py:159-230).
+ *
+ * Tensor views (llattn_tensor) describe rows of head vectors
+ * x[b][n][h][d] at ptr + b*sb + n*sn + h*sh + d (element strides; the head
+ * dimension d is contiguous).  Rows and bases must be 16-byte aligned.
+ */
+#ifndef LLATTN_H
+#define LLATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LLATTN_ABI_VERSION 1
+
+/* status codes */
+#define LLATTN_OK 0
+#define LLATTN_ERR_SHAPE 1        /* inconsistent or non-positive sizes */
+#define LLATTN_ERR_DTYPE 2        /* unknown dtype code */
+#define LLATTN_ERR_LAYOUT 3       /* stride / alignment the kernels cannot read */
+#define LLATTN_ERR_UNSUPPORTED 4  /* head dim or latent head dim outside the compiled set */
+#define LLATTN_ERR_WORKSPACE 5    /* workspace missing or too small */
+#define LLATTN_ERR_LAUNCH 6       /* the HIP runtime refused a launch */
+
+/* dtype codes: storage type of every activation; accumulation is fp32 */
+#define LLATTN_F32 0
+#define LLATTN_BF16 1
+
+/* pooling divisors */
+#define LLATTN_DIV_COUNT 0  /* mean over the real tokens of a segment (reference models.py:182-200) */
+#define LLATTN_DIV_SEG 1    /* sum / segment length, zero-padded mean (reference models.py:218-225) */
+#define LLATTN_DIV_ONE 2    /* plain sum */
+
+/* workspace kinds for llattn_workspace_size */
+#define LLATTN_WS_LOCAL_BWD 0
+#define LLATTN_WS_LATENT_BWD 1
+
+typedef struct llattn_tensor {
+  void* ptr;
+  int64_t sb; /* batch stride */
+  int64_t sn; /* row (token / latent / latent-query) stride */
+  int64_t sh; /* head stride */
+} llattn_tensor;
+
+typedef struct llattn_shape {
+  int32_t B, T;          /* batch, sequence length */
+  int32_t H, Dh;         /* local heads, head dim (reference models.py:66-68) */
+  int32_t Lh, Ldh;       /* latent heads, latent head dim (reference models.py:72-74) */
+  int32_t window;        /* local window W (reference models.py:69) */
+  int32_t block;         /* resolved local block size min(T, max(W, local_block_size)) (reference models.py:249) */
+  int32_t chunk;         /* latent chunk ceil(T / min(latent_tokens, T)) (reference models.py:175-180) */
+  int32_t n_chunks;      /* latent count (reference models.py:206-208) */
+  int32_t q_block;       /* tokens per latent query: 1 token-wise, else min(T, qbs) (reference models.py:218) */
+  int32_t n_q;           /* number of latent queries: T or ceil(T / q_block) */
+  int32_t dtype;         /* LLATTN_F32 or LLATTN_BF16 */
+  int32_t gate_per_head; /* 0: one gate vector shared by all heads (reference models.py:89-90); 1: [H][Dh] */
+} llattn_shape;
+
+/* ABI version of the loaded library (LLATTN_ABI_VERSION). */
+int32_t llattn_abi_version(void);
+
+/* Message of the calling thread's last failed call ("" when none). */
+const char* llattn_last_error(void);
+
+/* Bytes of workspace that llattn_local_gate_bwd (kind LLATTN_WS_LOCAL_BWD) or
+ * llattn_latent_bwd (kind LLATTN_WS_LATENT_BWD) needs for this shape;
+ * 0 on a bad shape (see llattn_last_error). */
+size_t llattn_workspace_size(const llattn_shape* s, int32_t kind);
+
+/* Segment pooling out[b][n][:] = sum_{t in segment n} x[b][t][:] / divisor.
+ * Segments are [n*seg, min((n+1)*seg, T)).  Replaces _pool_to_latents
+ * (reference models.py:159-214; LLATTN_DIV_COUNT) and _pool_query_blocks
+ * (reference models.py:216-230; LLATTN_DIV_SEG); LLATTN_DIV_ONE folds
+ * per-token gradients onto latent queries (backward of repeat_interleave,
+ * reference models.py:398-412). */
+int32_t llattn_pool_fwd(const void* x, int64_t x_sb, int64_t x_st, void* out, int64_t out_sb, int64_t out_sn,
+                        int32_t B, int32_t T, int32_t D, int32_t seg, int32_t n_seg, int32_t divisor,
+                        int32_t dtype, void* stream);
+
+/* Backward of llattn_pool_fwd: dx[b][t][:] (+)= dpooled[b][t/seg][:] / divisor.
+ * accumulate = 0 overwrites dx, 1 adds into it. */
+int32_t llattn_pool_bwd(const void* dpooled, int64_t dp_sb, int64_t dp_sn, void* dx, int64_t dx_sb, int64_t dx_st,
+                        int32_t B, int32_t T, int32_t D, int32_t seg, int32_t n_seg, int32_t divisor,
+                        int32_t accumulate, int32_t dtype, void* stream);
+
+/* Chunk-causal latent attention (reference models.py:361-375): query s of
+ * latent head lh attends latents n < chunk_of(s) with scale 1/sqrt(Ldh);
+ * queries with no latent output 0.  rq: [B][n_q][Lh][Ldh], gk/gv:
+ * [B][n_chunks][Lh][Ldh], out: [B][n_q][Lh][Ldh]; lse: fp32 [B][Lh][n_q]
+ * contiguous (-inf for empty rows).  Replaces the latent half of the
+ * reference fused forward launch (reference kernels/llattn_op.py:34-84). */
+int32_t llattn_latent_fwd(const llattn_shape* s, const llattn_tensor* rq, const llattn_tensor* gk,
+                          const llattn_tensor* gv, const llattn_tensor* out, float* lse, void* stream);
+
+/* Backward of llattn_latent_fwd given dL = d(out) and the forward's lse:
+ * writes drq, dgk, dgv (same layouts as rq, gk, gv).  The attention weights
+ * are recomputed from lse in fp32.  Deterministic: per-tile partial sums in
+ * the workspace, then an ordered reduction (no atomics).  Replaces the latent
+ * part of the reference backward launches (reference kernels/llattn_op.py:87-181). */
+int32_t llattn_latent_bwd(const llattn_shape* s, const llattn_tensor* rq, const llattn_tensor* gk,
+                          const llattn_tensor* gv, const float* lse, const llattn_tensor* dout,
+                          const llattn_tensor* drq, const llattn_tensor* dgk, const llattn_tensor* dgv,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* Windowed local attention with the gate epilogue (reference models.py:232-305
+ * and 416-438).  Query i attends keys max(0, i-W, floor(i/block)*block-W+1)
+ * <= j <= i-1 with scale 1/sqrt(Dh); empty key sets give 0.  remote holds the
+ * r_out output per latent query ([B][n_q][H][Dh]); token i reads row
+ * i / q_block.  gate_l / gate_r: fp32 [Dh] (shared) or [H][Dh].  Writes
+ * y = w*O + (1-w)*remote with w = sigmoid(gate_l.O - gate_r.remote),
+ * o_local = O (pre-gate), lse [B][H][T] and w [B][H][T] (fp32, contiguous).
+ * q/k/v/y/o_local: [B][T][H][Dh].  Replaces the local + gate half of the
+ * reference fused forward launch (reference kernels/llattn_op.py:34-84). */
+int32_t llattn_local_gate_fwd(const llattn_shape* s, const llattn_tensor* q, const llattn_tensor* k,
+                              const llattn_tensor* v, const llattn_tensor* remote, const float* gate_l,
+                              const float* gate_r, const llattn_tensor* y, const llattn_tensor* o_local,
+                              float* lse, float* w, void* stream);
+
+/* Backward of llattn_local_gate_fwd given dy: writes dq, dk, dv
+ * ([B][T][H][Dh]), dremote per token ([B][T][H][Dh]; fold it onto latent
+ * queries with llattn_pool_fwd(LLATTN_DIV_ONE) in macro-block mode) and the
+ * fp32 gate gradients dgate_l / dgate_r ([H][Dh], per head; sum over heads for
+ * a shared gate).  No atomics.  Replaces the local + gate part of the
+ * reference backward launches (reference kernels/llattn_op.py:87-181). */
+int32_t llattn_local_gate_bwd(const llattn_shape* s, const llattn_tensor* q, const llattn_tensor* k,
+                              const llattn_tensor* v, const llattn_tensor* remote, const float* gate_l,
+                              const float* gate_r, const llattn_tensor* o_local, const float* lse,
+                              const float* w, const llattn_tensor* dy, const llattn_tensor* dq,
+                              const llattn_tensor* dk, const llattn_tensor* dv, const llattn_tensor* dremote,
+                              float* dgate_l, float* dgate_r, void* workspace, size_t workspace_bytes,
+                              void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LLATTN_H */

@@ -1,0 +1,43 @@
+// Host-side helpers shared by the entry points: error state and argument checks.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+
+#include "llattn.h"
+
+namespace llattn {
+
+// Records a formatted message as the calling thread's last error and returns `code`.
+int32_t fail(int32_t code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Clears the calling thread's last error.
+void clear_error();
+// Converts a pending launch error into LLATTN_ERR_LAUNCH.
+int32_t check_launch(const char* what);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline int64_t elem_size(int32_t dtype) { return dtype == LLATTN_F32 ? 4 : 2; }
+// smallest padded head dim (multiple of 32) supported by the compiled kernels, or 0
+inline int padded_head_dim(int d) {
+  if (d <= 0) return 0;
+  if (d <= 32) return 32;
+  if (d <= 64) return 64;
+  if (d <= 96) return 96;
+  if (d <= 128) return 128;
+  return 0;
+}
+inline int padded_latent_dim(int d) {
+  if (d <= 0) return 0;
+  if (d <= 8) return 8;
+  if (d <= 16) return 16;
+  if (d <= 32) return 32;
+  if (d <= 64) return 64;
+  return 0;
+}
+// Validates a view whose innermost (head-dim) rows are read with 16-byte accesses.
+int32_t check_view(const char* name, const llattn_tensor* t, int32_t dtype, bool heads);
+int32_t check_shape(const llattn_shape* s);
+
+}  // namespace llattn

@@ -1,0 +1,198 @@
+// Device helpers shared by the gfx950 local+latent attention kernels.
+//
+// Storage types: float (fp32) or uint16_t holding bfloat16 bits.  All
+// arithmetic accumulates in fp32.
+//
+// MFMA conventions (lane layouts checked on MI355X): a 64-lane wave is split
+// into four lane groups g = lane/16 of 16 lanes, r = lane%16.
+//   * 16x16 accumulator tile C[m][n]: lane (r, g) holds C[4g+i][r], i = 0..3.
+//   * "row" products contract over a head dimension held row-major by both
+//     operands (S = K Q^T, dP = V dO^T, ...).  Lane (r, g) supplies row r's
+//     dims [g*DQ, (g+1)*DQ) where DQ = DHP/4 (DHP = head dim padded to a
+//     multiple of 32); any consistent assignment of dims to MFMA k-slots
+//     yields the same dot products.
+//       bf16: v_mfma_f32_16x16x32_bf16, 8 dims per lane per step;
+//       fp32: v_mfma_f32_16x16x4_f32,   1 dim per lane per step.
+//   * "col" products contract over the 16 rows of a previous accumulator tile
+//     (O^T = V^T P^T, dQ^T = K^T dS^T, ...).  The B operand is the lane's own
+//     four accumulator values (k = 4g+i); the A operand is read from LDS as
+//     four consecutive k of row m = r.
+//       bf16: v_mfma_f32_16x16x16_bf16 (4 k per lane);
+//       fp32: four v_mfma_f32_16x16x4_f32, step i uses k = 4g+i.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+namespace llattn {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_inff();
+
+__device__ __forceinline__ float bf2f(uint16_t u) { return __uint_as_float(static_cast<uint32_t>(u) << 16); }
+__device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f)); }
+
+template <typename T>
+__device__ __forceinline__ float to_f(T v) {
+  if constexpr (std::is_same_v<T, float>) return v; else return bf2f(v);
+}
+template <typename T>
+__device__ __forceinline__ T from_f(float v) {
+  if constexpr (std::is_same_v<T, float>) return v; else return f2bf(v);
+}
+// value as it is stored (rounded to T) and read back
+template <typename T>
+__device__ __forceinline__ float round_t(float v) { return to_f<T>(from_f<T>(v)); }
+
+// 16-byte vector of T
+template <typename T> struct Vec16;
+template <> struct Vec16<float> { static constexpr int N = 4; };
+template <> struct Vec16<uint16_t> { static constexpr int N = 8; };
+
+// ---- 4 consecutive elements <-> float[4] ------------------------------------
+template <typename T>
+__device__ __forceinline__ void load4(const T* p, float v[4]) {
+  if constexpr (std::is_same_v<T, float>) {
+    const float4 x = *reinterpret_cast<const float4*>(p);
+    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+  } else {
+    const uint2 x = *reinterpret_cast<const uint2*>(p);
+    v[0] = __uint_as_float(x.x << 16); v[1] = __uint_as_float(x.x & 0xffff0000u);
+    v[2] = __uint_as_float(x.y << 16); v[3] = __uint_as_float(x.y & 0xffff0000u);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void store4(T* p, const float v[4]) {
+  if constexpr (std::is_same_v<T, float>) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    uint2 x;
+    x.x = static_cast<uint32_t>(f2bf(v[0])) | (static_cast<uint32_t>(f2bf(v[1])) << 16);
+    x.y = static_cast<uint32_t>(f2bf(v[2])) | (static_cast<uint32_t>(f2bf(v[3])) << 16);
+    *reinterpret_cast<uint2*>(p) = x;
+  }
+}
+// ---- 16-byte copies (global <-> LDS) -----------------------------------------
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ void st16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
+
+// ---- row fragments ------------------------------------------------------------
+template <typename T, int DQ> struct RowFrag;
+
+template <int DQ> struct RowFrag<uint16_t, DQ> {
+  static constexpr int N = DQ / 8;
+  bf16x8 v[N];
+  // row points at dim 0; dims >= Dh read as zero (Dh is a multiple of 8)
+  __device__ __forceinline__ void load(const uint16_t* row, int g, int Dh, bool valid) {
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      const int d = g * DQ + 8 * e;
+      uint4 x = make_uint4(0, 0, 0, 0);
+      if (valid && d < Dh) x = ld16(row + d);
+      v[e] = __builtin_bit_cast(bf16x8, x);
+    }
+  }
+  // LDS row already zero-padded to the full padded width
+  __device__ __forceinline__ void load_lds(const uint16_t* row, int g) {
+#pragma unroll
+    for (int e = 0; e < N; ++e) v[e] = __builtin_bit_cast(bf16x8, ld16(row + g * DQ + 8 * e));
+  }
+};
+
+template <int DQ> struct RowFrag<float, DQ> {
+  static constexpr int N = DQ / 4;
+  f32x4 v[N];
+  __device__ __forceinline__ void load(const float* row, int g, int Dh, bool valid) {
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      const int d = g * DQ + 4 * e;
+      uint4 x = make_uint4(0, 0, 0, 0);
+      if (valid && d < Dh) x = ld16(row + d);
+      v[e] = __builtin_bit_cast(f32x4, x);
+    }
+  }
+  __device__ __forceinline__ void load_lds(const float* row, int g) {
+#pragma unroll
+    for (int e = 0; e < N; ++e) v[e] = __builtin_bit_cast(f32x4, ld16(row + g * DQ + 4 * e));
+  }
+};
+
+template <int DQ>
+__device__ __forceinline__ f32x4 row_mma(const RowFrag<uint16_t, DQ>& a, const RowFrag<uint16_t, DQ>& b, f32x4 acc) {
+#pragma unroll
+  for (int e = 0; e < RowFrag<uint16_t, DQ>::N; ++e)
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v[e], b.v[e], acc, 0, 0, 0);
+  return acc;
+}
+template <int DQ>
+__device__ __forceinline__ f32x4 row_mma(const RowFrag<float, DQ>& a, const RowFrag<float, DQ>& b, f32x4 acc) {
+#pragma unroll
+  for (int e = 0; e < RowFrag<float, DQ>::N; ++e)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[e][c], b.v[e][c], acc, 0, 0, 0);
+  return acc;
+}
+
+// ---- col products: A = 4 consecutive k of row m (LDS), B = lane's 4 values ----
+__device__ __forceinline__ f32x4 col_mma(const uint16_t* a, const float b[4], f32x4 acc) {
+  const i16x4 av = *reinterpret_cast<const i16x4*>(a);
+  i16x4 bv;
+  bv[0] = static_cast<short>(f2bf(b[0]));
+  bv[1] = static_cast<short>(f2bf(b[1]));
+  bv[2] = static_cast<short>(f2bf(b[2]));
+  bv[3] = static_cast<short>(f2bf(b[3]));
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bv, acc, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 col_mma(const float* a, const float b[4], f32x4 acc) {
+  const f32x4 av = *reinterpret_cast<const f32x4*>(a);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], b[i], acc, 0, 0, 0);
+  return acc;
+}
+
+// ---- wave reductions over the four lane groups (same r) ------------------------
+__device__ __forceinline__ float sum_groups(float x) {
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+__device__ __forceinline__ float max_groups(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16));
+  x = fmaxf(x, __shfl_xor(x, 32));
+  return x;
+}
+// sum over the 16 lanes of a group (same g)
+__device__ __forceinline__ float sum_rows16(float x) {
+  x += __shfl_xor(x, 1);
+  x += __shfl_xor(x, 2);
+  x += __shfl_xor(x, 4);
+  x += __shfl_xor(x, 8);
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Workgroups are dispatched round-robin over the 8 XCDs; remap so that each
+// XCD receives a contiguous range of logical tiles (neighbouring query tiles
+// of one head share K/V rows, which then stay in that XCD's L2).
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+  if (nblocks % 8 != 0) return bid;
+  return (bid % 8) * (nblocks / 8) + bid / 8;
+}
+
+// First key of query i (inclusive); the last is i-1.  The reference runs SDPA
+// per block of `bs` queries over keys [max(0, q0-W+1), q_end) with the mask
+// 0 < i-j <= W (reference models.py:249-292).
+__device__ __forceinline__ int key_lo(int i, int W, int bs) {
+  const int q0 = (i / bs) * bs;
+  return max(max(0, i - W), q0 - W + 1);
+}
+
+}  // namespace llattn

@@ -1,0 +1,589 @@
+// Windowed local attention with the fused gate epilogue, forward and backward,
+// for gfx950 (64-wide waves, bf16/fp32 MFMA, LDS-staged key/value tiles).
+//
+// Semantics (reference models.py:232-305, 416-438): query i attends keys
+// max(0, i-W, floor(i/bs)*bs - W + 1) <= j <= i-1 with scale 1/sqrt(Dh);
+// a query without keys outputs 0.  The gate mixes the local output O with the
+// remote row R of the token: w = sigmoid(g_l.O - g_r.R), y = w O + (1-w) R.
+//
+// Work decomposition: one 256-thread workgroup per (batch, head, tile of 64
+// queries) [forward, dQ pass] or (batch, head, tile of 64 keys) [dK/dV pass];
+// each of the four waves owns 16 rows of the tile.  Keys (resp. queries) are
+// streamed through LDS in tiles of 64 and consumed in 16-row sub-tiles.
+#include "llattn_abi.h"
+#include "llattn_device.h"
+
+#include <climits>
+
+namespace llattn {
+
+struct LocalArgs {
+  int B, T, H, Dh, W, bs, q_block, n_qt, gate_hs;
+  float scale, scale_log2;
+  const void* q; int64_t q_sb, q_st, q_sh;
+  const void* k; int64_t k_sb, k_st, k_sh;
+  const void* v; int64_t v_sb, v_st, v_sh;
+  const void* rem; int64_t r_sb, r_sn, r_sh;
+  const float* gl;
+  const float* gr;
+  void* y; int64_t y_sb, y_st, y_sh;
+  void* ol; int64_t o_sb, o_st, o_sh;
+  float* lse;  // [B][H][T]
+  float* w;    // [B][H][T]
+  const void* dy; int64_t dy_sb, dy_st, dy_sh;
+  void* dq; int64_t dq_sb, dq_st, dq_sh;
+  void* dk; int64_t dk_sb, dk_st, dk_sh;
+  void* dv; int64_t dv_sb, dv_st, dv_sh;
+  void* dr; int64_t dr_sb, dr_st, dr_sh;
+  void* dO;      // workspace [B][T][H][Dh], storage type
+  float* Dsum;   // workspace [B][H][T]
+  float* gpart;  // workspace [B*H*n_qt][2][Dh]
+};
+
+template <typename T> constexpr int kRowPad = std::is_same_v<T, float> ? 4 : 8;
+constexpr int kTP = 68;  // pitch of transposed LDS tiles [dim][64 rows + 4]
+
+// Rows [r0, r0+64) of a head-row view (base at (b, h), row stride st) into LDS
+// row-major [64][P]; rows >= r_end and dims >= Dh are zero.
+template <typename T, int DHP, int P>
+__device__ __forceinline__ void stage_rows(T* lds, const T* base, int64_t st, int r0, int r_end, int Dh) {
+  constexpr int V = Vec16<T>::N, CPR = DHP / V;
+  for (int c = threadIdx.x; c < 64 * CPR; c += 256) {
+    const int row = c / CPR, col = (c % CPR) * V, rr = r0 + row;
+    uint4 x = make_uint4(0, 0, 0, 0);
+    if (rr < r_end && col < Dh) x = ld16(base + (int64_t)rr * st + col);
+    st16(lds + row * P + col, x);
+  }
+}
+// Same rows, stored transposed into LDS [DHP][kTP]; optionally also row-major.
+template <typename T, int DHP, int P, bool kRows>
+__device__ __forceinline__ void stage_rows_t(T* lds_rows, T* lds_t, const T* base, int64_t st, int r0, int r_end,
+                                             int Dh) {
+  constexpr int V = Vec16<T>::N, CPR = DHP / V;
+  for (int c = threadIdx.x; c < 64 * CPR; c += 256) {
+    const int row = c / CPR, col = (c % CPR) * V, rr = r0 + row;
+    uint4 x = make_uint4(0, 0, 0, 0);
+    if (rr < r_end && col < Dh) x = ld16(base + (int64_t)rr * st + col);
+    if constexpr (kRows) st16(lds_rows + row * P + col, x);
+    const T* e = reinterpret_cast<const T*>(&x);
+#pragma unroll
+    for (int j = 0; j < V; ++j) lds_t[(col + j) * kTP + row] = e[j];
+  }
+}
+
+// ----------------------------------------------------------------------------
+// forward: local attention + gate mix
+// ----------------------------------------------------------------------------
+template <typename T, int DHP>
+__global__ __launch_bounds__(256) void local_fwd_kernel(const LocalArgs a) {
+  constexpr int DQ = DHP / 4, NT = DHP / 16, KP = DHP + kRowPad<T>;
+  __shared__ __align__(16) T Ks[64 * KP];
+  __shared__ __align__(16) T Vt[DHP * kTP];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, g = lane >> 4;
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int qt = bid % a.n_qt, bh = bid / a.n_qt, h = bh % a.H, b = bh / a.H;
+  const int T_ = a.T;
+  const int q0 = qt * 64, qw = q0 + wave * 16, qi = qw + r;
+  const bool qv = qi < T_;
+
+  const T* qbase = static_cast<const T*>(a.q) + b * a.q_sb + h * a.q_sh;
+  const T* kbase = static_cast<const T*>(a.k) + b * a.k_sb + h * a.k_sh;
+  const T* vbase = static_cast<const T*>(a.v) + b * a.v_sb + h * a.v_sh;
+
+  RowFrag<T, DQ> qf;
+  qf.load(qbase + (int64_t)qi * a.q_st, g, a.Dh, qv);
+  const int lo = qv ? key_lo(qi, a.W, a.bs) : INT_MAX;
+  const int hi = qi - 1;
+
+  float m_run = kNegInf, l_run = 0.f;
+  f32x4 acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int kbeg = max(0, q0 - a.W);
+  const int kend = min(T_, q0 + 64) - 1;                     // exclusive
+  const int wlo = max(0, qw - a.W), whi = min(qw + 15, T_ - 1) - 1;  // keys any query of this wave may use
+  for (int k0 = kbeg; k0 < kend; k0 += 64) {
+    __syncthreads();
+    stage_rows<T, DHP, KP>(Ks, kbase, a.k_st, k0, kend, a.Dh);
+    stage_rows_t<T, DHP, KP, false>(nullptr, Vt, vbase, a.v_st, k0, kend, a.Dh);
+    __syncthreads();
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int s0 = k0 + 16 * st;
+      if (s0 >= kend || s0 + 15 < wlo || s0 > whi) continue;  // uniform over the wave
+      RowFrag<T, DQ> kf;
+      kf.load_lds(Ks + (16 * st + r) * KP, g);
+      const f32x4 s = row_mma(kf, qf, f32x4{0.f, 0.f, 0.f, 0.f});  // S^T[key 4g+i][query r]
+      float sv[4], mloc = kNegInf;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = s0 + 4 * g + i;
+        sv[i] = (j >= lo && j <= hi) ? s[i] * a.scale_log2 : kNegInf;
+        mloc = fmaxf(mloc, sv[i]);
+      }
+      mloc = max_groups(mloc);
+      const float m_new = fmaxf(m_run, mloc);
+      const float mu = (m_new == kNegInf) ? 0.f : m_new;
+      const float alpha = fast_exp2(m_run - mu);
+      float pv[4], ps = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pv[i] = fast_exp2(sv[i] - mu);
+        ps += pv[i];
+      }
+      l_run = l_run * alpha + ps;
+      m_run = m_new;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        acc[t] *= alpha;
+        acc[t] = col_mma(Vt + (16 * t + r) * kTP + 16 * st + 4 * g, pv, acc[t]);  // O^T[dim][query]
+      }
+    }
+  }
+
+  // ---- epilogue: normalise, gate, store ----
+  const float l = sum_groups(l_run);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const float* glp = a.gl + h * a.gate_hs;
+  const float* grp = a.gr + h * a.gate_hs;
+  const int rrow = qv ? qi / a.q_block : 0;
+  const T* rp = static_cast<const T*>(a.rem) + b * a.r_sb + h * a.r_sh + (int64_t)rrow * a.r_sn;
+  float o[NT][4], rv[NT][4];
+  float sl = 0.f, sr = 0.f;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int d = 16 * t + 4 * g;
+    const bool dok = qv && d < a.Dh;
+    float gl4[4] = {0.f, 0.f, 0.f, 0.f}, gr4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { o[t][i] = round_t<T>(acc[t][i] * inv); rv[t][i] = 0.f; }
+    if (dok) {
+      load4<T>(rp + d, rv[t]);
+      load4<float>(glp + d, gl4);
+      load4<float>(grp + d, gr4);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sl += o[t][i] * gl4[i];
+      sr += rv[t][i] * gr4[i];
+    }
+  }
+  sl = sum_groups(sl);
+  sr = sum_groups(sr);
+  const float mm = fmaxf(sl, sr);
+  const float el = __expf(sl - mm), er = __expf(sr - mm);
+  const float wl = el / (el + er), wr = er / (el + er);
+  if (qv) {
+    T* yp = static_cast<T*>(a.y) + b * a.y_sb + h * a.y_sh + (int64_t)qi * a.y_st;
+    T* op = static_cast<T*>(a.ol) + b * a.o_sb + h * a.o_sh + (int64_t)qi * a.o_st;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int d = 16 * t + 4 * g;
+      if (d < a.Dh) {
+        float yv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) yv[i] = wl * o[t][i] + wr * rv[t][i];
+        store4<T>(yp + d, yv);
+        store4<T>(op + d, o[t]);
+      }
+    }
+    if (g == 0) {
+      const int64_t idx = ((int64_t)b * a.H + h) * T_ + qi;
+      a.lse[idx] = l > 0.f ? (m_run + __log2f(l)) * kLn2 : kNegInf;
+      a.w[idx] = wl;
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// backward pass 1 (query tiles): gate backward, dremote, dO_local, D = dO.O,
+// gate partial sums, dQ
+// ----------------------------------------------------------------------------
+template <typename T, int DHP>
+__global__ __launch_bounds__(256) void local_bwd_q_kernel(const LocalArgs a) {
+  constexpr int DQ = DHP / 4, NT = DHP / 16, KP = DHP + kRowPad<T>;
+  __shared__ __align__(16) T Ks[64 * KP];
+  __shared__ __align__(16) T Kt[DHP * kTP];
+  __shared__ __align__(16) T Vs[64 * KP];
+  __shared__ __align__(16) T Ds[64 * KP];
+  __shared__ float gsum[4][2][DHP];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane & 15, g = lane >> 4;
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int qt = bid % a.n_qt, bh = bid / a.n_qt, h = bh % a.H, b = bh / a.H;
+  const int T_ = a.T, Dh = a.Dh;
+  const int q0 = qt * 64, qw = q0 + wave * 16, qi = qw + r;
+  const bool qv = qi < T_;
+  const int64_t hrow = ((int64_t)b * a.H + h) * T_;
+
+  // ---- phase 1: gate backward in the accumulator layout (dims 16t+4g+i) ----
+  const float wq = qv ? a.w[hrow + qi] : 0.f;
+  const T* dyp = static_cast<const T*>(a.dy) + b * a.dy_sb + h * a.dy_sh + (int64_t)qi * a.dy_st;
+  const T* olp = static_cast<const T*>(a.ol) + b * a.o_sb + h * a.o_sh + (int64_t)qi * a.o_st;
+  const int rrow = qv ? qi / a.q_block : 0;
+  const T* rp = static_cast<const T*>(a.rem) + b * a.r_sb + h * a.r_sh + (int64_t)rrow * a.r_sn;
+  const float* glp = a.gl + h * a.gate_hs;
+  const float* grp = a.gr + h * a.gate_hs;
+  float dyv[NT][4], olv[NT][4], rv[NT][4], gl4[NT][4], gr4[NT][4];
+  float dot1 = 0.f;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int d = 16 * t + 4 * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dyv[t][i] = olv[t][i] = rv[t][i] = gl4[t][i] = gr4[t][i] = 0.f;
+    if (qv && d < Dh) {
+      load4<T>(dyp + d, dyv[t]);
+      load4<T>(olp + d, olv[t]);
+      load4<T>(rp + d, rv[t]);
+      load4<float>(glp + d, gl4[t]);
+      load4<float>(grp + d, gr4[t]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dot1 += dyv[t][i] * (olv[t][i] - rv[t][i]);
+  }
+  dot1 = sum_groups(dot1);
+  const float delta = wq * (1.f - wq) * dot1;
+  float Dq = 0.f;
+  T* drp = static_cast<T*>(a.dr) + b * a.dr_sb + h * a.dr_sh + (int64_t)qi * a.dr_st;
+  T* dop = static_cast<T*>(a.dO) + (((int64_t)b * T_ + qi) * a.H + h) * Dh;
+  T* dsrow = Ds + (wave * 16 + r) * KP;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int d = 16 * t + 4 * g;
+    float dov[4], drv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      dov[i] = round_t<T>(wq * dyv[t][i] + delta * gl4[t][i]);
+      drv[i] = (1.f - wq) * dyv[t][i] - delta * gr4[t][i];
+      Dq += dov[i] * olv[t][i];
+    }
+    store4<T>(dsrow + d, dov);  // zero beyond Dh (all inputs were zero there)
+    if (qv && d < Dh) {
+      store4<T>(drp + d, drv);
+      store4<T>(dop + d, dov);
+    }
+    // gate partial sums over the 16 queries of this wave
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float pl = sum_rows16(delta * olv[t][i]);
+      const float pr = sum_rows16(-delta * rv[t][i]);
+      if (r == 0) {
+        gsum[wave][0][d + i] = pl;
+        gsum[wave][1][d + i] = pr;
+      }
+    }
+  }
+  Dq = sum_groups(Dq);
+  if (qv && g == 0) a.Dsum[hrow + qi] = Dq;
+  __syncthreads();
+  for (int idx = tid; idx < 2 * DHP; idx += 256) {
+    const int which = idx / DHP, d = idx % DHP;
+    if (d < Dh) {
+      const float s = gsum[0][which][d] + gsum[1][which][d] + gsum[2][which][d] + gsum[3][which][d];
+      a.gpart[((((int64_t)b * a.H + h) * a.n_qt + qt) * 2 + which) * Dh + d] = s;
+    }
+  }
+
+  // ---- phase 2: dQ = scale * sum_j dS_ij k_j ----
+  const T* qbase = static_cast<const T*>(a.q) + b * a.q_sb + h * a.q_sh;
+  const T* kbase = static_cast<const T*>(a.k) + b * a.k_sb + h * a.k_sh;
+  const T* vbase = static_cast<const T*>(a.v) + b * a.v_sb + h * a.v_sh;
+  RowFrag<T, DQ> qf, dof;
+  qf.load(qbase + (int64_t)qi * a.q_st, g, Dh, qv);
+  dof.load_lds(dsrow, g);  // same wave wrote it; the barrier above orders it
+  const float lse_nat = qv ? a.lse[hrow + qi] : kNegInf;
+  const float lse2 = (lse_nat == kNegInf) ? 0.f : lse_nat * kLog2e;
+  const int lo = qv ? key_lo(qi, a.W, a.bs) : INT_MAX;
+  const int hi = qi - 1;
+  f32x4 acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int kbeg = max(0, q0 - a.W);
+  const int kend = min(T_, q0 + 64) - 1;
+  const int wlo = max(0, qw - a.W), whi = min(qw + 15, T_ - 1) - 1;
+  for (int k0 = kbeg; k0 < kend; k0 += 64) {
+    __syncthreads();
+    stage_rows_t<T, DHP, KP, true>(Ks, Kt, kbase, a.k_st, k0, kend, Dh);
+    stage_rows<T, DHP, KP>(Vs, vbase, a.v_st, k0, kend, Dh);
+    __syncthreads();
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int s0 = k0 + 16 * st;
+      if (s0 >= kend || s0 + 15 < wlo || s0 > whi) continue;
+      RowFrag<T, DQ> kf, vf;
+      kf.load_lds(Ks + (16 * st + r) * KP, g);
+      vf.load_lds(Vs + (16 * st + r) * KP, g);
+      const f32x4 s = row_mma(kf, qf, f32x4{0.f, 0.f, 0.f, 0.f});    // S^T[key][query]
+      const f32x4 dp = row_mma(vf, dof, f32x4{0.f, 0.f, 0.f, 0.f});  // dP^T[key][query]
+      float ds[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = s0 + 4 * g + i;
+        const float p = (j >= lo && j <= hi) ? fast_exp2(s[i] * a.scale_log2 - lse2) : 0.f;
+        ds[i] = p * (dp[i] - Dq);
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[t] = col_mma(Kt + (16 * t + r) * kTP + 16 * st + 4 * g, ds, acc[t]);
+    }
+  }
+  if (qv) {
+    T* dqp = static_cast<T*>(a.dq) + b * a.dq_sb + h * a.dq_sh + (int64_t)qi * a.dq_st;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int d = 16 * t + 4 * g;
+      if (d < Dh) {
+        float v4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v4[i] = acc[t][i] * a.scale;
+        store4<T>(dqp + d, v4);
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// backward pass 2 (key tiles): dK, dV.  Every key's contributions come from the
+// queries j+1 .. j+W, all visited by the one workgroup that owns the key.
+// ----------------------------------------------------------------------------
+template <typename T, int DHP>
+__global__ __launch_bounds__(256) void local_bwd_kv_kernel(const LocalArgs a) {
+  constexpr int DQ = DHP / 4, NT = DHP / 16, KP = DHP + kRowPad<T>;
+  __shared__ __align__(16) T Qs[64 * KP];
+  __shared__ __align__(16) T Qt[DHP * kTP];
+  __shared__ __align__(16) T Os[64 * KP];
+  __shared__ __align__(16) T Ot[DHP * kTP];
+  __shared__ float lse2s[64], Dss[64];
+  __shared__ int los[64];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane & 15, g = lane >> 4;
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int kt = bid % a.n_qt, bh = bid / a.n_qt, h = bh % a.H, b = bh / a.H;
+  const int T_ = a.T, Dh = a.Dh;
+  const int j0 = kt * 64, kw = j0 + wave * 16, kj = kw + r;
+  const bool kv = kj < T_;
+  const int64_t hrow = ((int64_t)b * a.H + h) * T_;
+
+  const T* qbase = static_cast<const T*>(a.q) + b * a.q_sb + h * a.q_sh;
+  const T* kbase = static_cast<const T*>(a.k) + b * a.k_sb + h * a.k_sh;
+  const T* vbase = static_cast<const T*>(a.v) + b * a.v_sb + h * a.v_sh;
+  const T* obase = static_cast<const T*>(a.dO) + (int64_t)b * T_ * a.H * Dh + (int64_t)h * Dh;
+  const int64_t o_st = (int64_t)a.H * Dh;
+
+  RowFrag<T, DQ> kf, vf;
+  kf.load(kbase + (int64_t)kj * a.k_st, g, Dh, kv);
+  vf.load(vbase + (int64_t)kj * a.v_st, g, Dh, kv);
+  f32x4 dk[NT], dv[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) dk[t] = dv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int qbeg = j0 + 1;
+  const int qend = (int)min((int64_t)T_, (int64_t)j0 + 64 + a.W);  // exclusive
+  const int wqlo = kw + 1, wqhi = (int)min((int64_t)T_ - 1, (int64_t)kw + 15 + a.W);
+  for (int q0 = qbeg; q0 < qend; q0 += 64) {
+    __syncthreads();
+    stage_rows_t<T, DHP, KP, true>(Qs, Qt, qbase, a.q_st, q0, qend, Dh);
+    stage_rows_t<T, DHP, KP, true>(Os, Ot, obase, o_st, q0, qend, Dh);
+    if (tid < 64) {
+      const int qq = q0 + tid;
+      if (qq < qend) {
+        const float ls = a.lse[hrow + qq];
+        lse2s[tid] = (ls == kNegInf) ? 0.f : ls * kLog2e;
+        Dss[tid] = a.Dsum[hrow + qq];
+        los[tid] = key_lo(qq, a.W, a.bs);
+      } else {
+        lse2s[tid] = 0.f;
+        Dss[tid] = 0.f;
+        los[tid] = INT_MAX;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int s0 = q0 + 16 * st;
+      if (s0 >= qend || s0 + 15 < wqlo || s0 > wqhi) continue;
+      RowFrag<T, DQ> qf, of;
+      qf.load_lds(Qs + (16 * st + r) * KP, g);
+      of.load_lds(Os + (16 * st + r) * KP, g);
+      const f32x4 s = row_mma(qf, kf, f32x4{0.f, 0.f, 0.f, 0.f});   // S[query 4g+i][key r]
+      const f32x4 dp = row_mma(of, vf, f32x4{0.f, 0.f, 0.f, 0.f});  // dP[query][key]
+      float p[4], ds[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ql = 16 * st + 4 * g + i, qq = q0 + ql;
+        const bool ok = kv && kj >= los[ql] && kj <= qq - 1;
+        p[i] = ok ? fast_exp2(s[i] * a.scale_log2 - lse2s[ql]) : 0.f;
+        ds[i] = p[i] * (dp[i] - Dss[ql]);
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        dv[t] = col_mma(Ot + (16 * t + r) * kTP + 16 * st + 4 * g, p, dv[t]);   // dV^T[dim][key]
+        dk[t] = col_mma(Qt + (16 * t + r) * kTP + 16 * st + 4 * g, ds, dk[t]);  // dK^T[dim][key]
+      }
+    }
+  }
+  if (kv) {
+    T* dkp = static_cast<T*>(a.dk) + b * a.dk_sb + h * a.dk_sh + (int64_t)kj * a.dk_st;
+    T* dvp = static_cast<T*>(a.dv) + b * a.dv_sb + h * a.dv_sh + (int64_t)kj * a.dv_st;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int d = 16 * t + 4 * g;
+      if (d < Dh) {
+        float kv4[4], vv4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          kv4[i] = dk[t][i] * a.scale;
+          vv4[i] = dv[t][i];
+        }
+        store4<T>(dkp + d, kv4);
+        store4<T>(dvp + d, vv4);
+      }
+    }
+  }
+}
+
+// Ordered sum of the per-tile gate partials: dgate[h][d] = sum_{b, tile} part.
+__global__ __launch_bounds__(256) void gate_reduce_kernel(const float* __restrict__ part, float* dgl, float* dgr,
+                                                          int B, int H, int n_qt, int Dh) {
+  const int h = blockIdx.x;
+  for (int idx = threadIdx.x; idx < 2 * Dh; idx += 256) {
+    const int which = idx / Dh, d = idx % Dh;
+    float s = 0.f;
+    for (int b = 0; b < B; ++b) {
+      const float* p = part + (((int64_t)b * H + h) * n_qt * 2 + which) * Dh + d;
+      for (int t = 0; t < n_qt; ++t) s += p[(int64_t)t * 2 * Dh];
+    }
+    (which == 0 ? dgl : dgr)[h * Dh + d] = s;
+  }
+}
+
+// ----------------------------------------------------------------------------
+// host launchers
+// ----------------------------------------------------------------------------
+namespace {
+
+template <typename T, int DHP>
+void launch_fwd(const LocalArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((local_fwd_kernel<T, DHP>), dim3(a.B * a.H * a.n_qt), dim3(256), 0, stream, a);
+}
+template <typename T, int DHP>
+void launch_bwd(const LocalArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((local_bwd_q_kernel<T, DHP>), dim3(a.B * a.H * a.n_qt), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((local_bwd_kv_kernel<T, DHP>), dim3(a.B * a.H * a.n_qt), dim3(256), 0, stream, a);
+}
+
+template <typename T>
+bool dispatch(int dhp, bool fwd, const LocalArgs& a, hipStream_t s) {
+  switch (dhp) {
+    case 32: fwd ? launch_fwd<T, 32>(a, s) : launch_bwd<T, 32>(a, s); return true;
+    case 64: fwd ? launch_fwd<T, 64>(a, s) : launch_bwd<T, 64>(a, s); return true;
+    case 96: fwd ? launch_fwd<T, 96>(a, s) : launch_bwd<T, 96>(a, s); return true;
+    case 128: fwd ? launch_fwd<T, 128>(a, s) : launch_bwd<T, 128>(a, s); return true;
+    default: return false;
+  }
+}
+
+void set_view(const llattn_tensor* t, const void** p, int64_t* sb, int64_t* sn, int64_t* sh) {
+  *p = t->ptr;
+  *sb = t->sb;
+  *sn = t->sn;
+  *sh = t->sh;
+}
+void set_view(const llattn_tensor* t, void** p, int64_t* sb, int64_t* sn, int64_t* sh) {
+  *p = t->ptr;
+  *sb = t->sb;
+  *sn = t->sn;
+  *sh = t->sh;
+}
+
+int32_t common_args(const llattn_shape* s, const llattn_tensor* q, const llattn_tensor* k, const llattn_tensor* v,
+                    const llattn_tensor* remote, const float* gate_l, const float* gate_r, LocalArgs* a) {
+  int32_t rc = check_shape(s);
+  if (rc) return rc;
+  if ((rc = check_view("q", q, s->dtype, true)) || (rc = check_view("k", k, s->dtype, true)) ||
+      (rc = check_view("v", v, s->dtype, true)) || (rc = check_view("remote", remote, s->dtype, true)))
+    return rc;
+  if (!gate_l || !gate_r || !aligned16(gate_l) || !aligned16(gate_r))
+    return fail(LLATTN_ERR_LAYOUT, "gate vectors must be non-null 16-byte aligned fp32 arrays");
+  *a = LocalArgs{};
+  a->B = s->B; a->T = s->T; a->H = s->H; a->Dh = s->Dh; a->W = s->window; a->bs = s->block;
+  a->q_block = s->q_block; a->n_qt = (s->T + 63) / 64; a->gate_hs = s->gate_per_head ? s->Dh : 0;
+  a->scale = 1.0f / sqrtf((float)s->Dh);
+  a->scale_log2 = a->scale * kLog2e;
+  set_view(q, &a->q, &a->q_sb, &a->q_st, &a->q_sh);
+  set_view(k, &a->k, &a->k_sb, &a->k_st, &a->k_sh);
+  set_view(v, &a->v, &a->v_sb, &a->v_st, &a->v_sh);
+  set_view(remote, &a->rem, &a->r_sb, &a->r_sn, &a->r_sh);
+  a->gl = gate_l;
+  a->gr = gate_r;
+  return LLATTN_OK;
+}
+
+}  // namespace
+}  // namespace llattn
+
+using namespace llattn;
+
+extern "C" int32_t llattn_local_gate_fwd(const llattn_shape* s, const llattn_tensor* q, const llattn_tensor* k,
+                                         const llattn_tensor* v, const llattn_tensor* remote, const float* gate_l,
+                                         const float* gate_r, const llattn_tensor* y, const llattn_tensor* o_local,
+                                         float* lse, float* w, void* stream) {
+  LocalArgs a;
+  int32_t rc = common_args(s, q, k, v, remote, gate_l, gate_r, &a);
+  if (rc) return rc;
+  if ((rc = check_view("y", y, s->dtype, true)) || (rc = check_view("o_local", o_local, s->dtype, true))) return rc;
+  if (!lse || !w) return fail(LLATTN_ERR_LAYOUT, "lse / w outputs must be non-null");
+  set_view(y, &a.y, &a.y_sb, &a.y_st, &a.y_sh);
+  set_view(o_local, &a.ol, &a.o_sb, &a.o_st, &a.o_sh);
+  a.lse = lse;
+  a.w = w;
+  const int dhp = padded_head_dim(s->Dh);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool ok = s->dtype == LLATTN_F32 ? dispatch<float>(dhp, true, a, st) : dispatch<uint16_t>(dhp, true, a, st);
+  if (!ok) return fail(LLATTN_ERR_UNSUPPORTED, "head_dim %d unsupported", s->Dh);
+  return check_launch("llattn_local_gate_fwd");
+}
+
+extern "C" int32_t llattn_local_gate_bwd(const llattn_shape* s, const llattn_tensor* q, const llattn_tensor* k,
+                                         const llattn_tensor* v, const llattn_tensor* remote, const float* gate_l,
+                                         const float* gate_r, const llattn_tensor* o_local, const float* lse,
+                                         const float* w, const llattn_tensor* dy, const llattn_tensor* dq,
+                                         const llattn_tensor* dk, const llattn_tensor* dv,
+                                         const llattn_tensor* dremote, float* dgate_l, float* dgate_r,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+  LocalArgs a;
+  int32_t rc = common_args(s, q, k, v, remote, gate_l, gate_r, &a);
+  if (rc) return rc;
+  if ((rc = check_view("o_local", o_local, s->dtype, true)) || (rc = check_view("dy", dy, s->dtype, true)) ||
+      (rc = check_view("dq", dq, s->dtype, true)) || (rc = check_view("dk", dk, s->dtype, true)) ||
+      (rc = check_view("dv", dv, s->dtype, true)) || (rc = check_view("dremote", dremote, s->dtype, true)))
+    return rc;
+  if (!lse || !w || !dgate_l || !dgate_r) return fail(LLATTN_ERR_LAYOUT, "lse / w / dgate pointers must be non-null");
+  const size_t need = llattn_workspace_size(s, LLATTN_WS_LOCAL_BWD);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace))
+    return fail(LLATTN_ERR_WORKSPACE, "local backward needs %zu workspace bytes (got %zu)", need, workspace_bytes);
+  set_view(o_local, &a.ol, &a.o_sb, &a.o_st, &a.o_sh);
+  set_view(dy, &a.dy, &a.dy_sb, &a.dy_st, &a.dy_sh);
+  set_view(dq, &a.dq, &a.dq_sb, &a.dq_st, &a.dq_sh);
+  set_view(dk, &a.dk, &a.dk_sb, &a.dk_st, &a.dk_sh);
+  set_view(dv, &a.dv, &a.dv_sb, &a.dv_st, &a.dv_sh);
+  set_view(dremote, &a.dr, &a.dr_sb, &a.dr_st, &a.dr_sh);
+  a.lse = const_cast<float*>(lse);
+  a.w = const_cast<float*>(w);
+  auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
+  char* ws = static_cast<char*>(workspace);
+  const size_t n_do = up((size_t)s->B * s->T * s->H * s->Dh * elem_size(s->dtype));
+  const size_t n_d = up((size_t)s->B * s->H * s->T * 4);
+  a.dO = ws;
+  a.Dsum = reinterpret_cast<float*>(ws + n_do);
+  a.gpart = reinterpret_cast<float*>(ws + n_do + n_d);
+  const int dhp = padded_head_dim(s->Dh);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool ok =
+      s->dtype == LLATTN_F32 ? dispatch<float>(dhp, false, a, st) : dispatch<uint16_t>(dhp, false, a, st);
+  if (!ok) return fail(LLATTN_ERR_UNSUPPORTED, "head_dim %d unsupported", s->Dh);
+  hipLaunchKernelGGL(gate_reduce_kernel, dim3(s->H), dim3(256), 0, st, a.gpart, dgate_l, dgate_r, s->B, s->H, a.n_qt,
+                     s->Dh);
+  return check_launch("llattn_local_gate_bwd");
+}

@@ -1,0 +1,151 @@
+"""Drop-in attention block backed by the gfx950 HIP kernels.
+
+``LocalLatentAttentionTriton`` keeps the constructor, ``forward`` and profiling
+surface of the reference's fused module (reference llattn_triton.py:33-176) and
+the parameter names, shapes, initialisation order and math of the reference
+PyTorch block ``LocalLatentAttention`` (reference models.py:61-462), so
+checkpoints interchange with the PyTorch path and outputs match it.
+
+Data flow of one forward (B, T, D = batch, tokens, d_model):
+
+1. ``qkvr = x @ [W_qkv; W_rq]^T + b`` -- one GEMM for q|k|v and the token-wise
+   latent queries (macro-block mode: ``qkv`` GEMM, HIP query-block pooling,
+   ``rq_proj`` GEMM);
+2. ``pooled = chunk means of x`` (HIP) and ``gkgv = rkv_proj(pooled)`` (GEMM);
+3. :class:`~llattn_amd.ops.LLAttnCore` -- HIP latent attention, ``r_out``
+   GEMM, HIP windowed attention with the gate mix fused in its epilogue;
+4. ``out`` GEMM.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib as L
+from .ops import LLAttnCore, _Prof, pool
+
+
+class LocalLatentAttentionTriton(nn.Module):
+    """``LocalLatentAttentionTriton(d_model, n_heads, latent_heads, latent_dim, n_latents, window,
+    bias=True, local_block_size=256, latent_query_block_size=0)``.
+
+    The first six arguments are those the reference dispatcher passes
+    (reference models.py:480-487).  ``local_block_size`` and
+    ``latent_query_block_size`` default to the reference ``ModelConfig`` values
+    (reference models.py:31, 35).  ``bias`` defaults to True so the parameter set
+    equals ``LocalLatentAttention``'s (reference models.py:80-84).
+    """
+
+    def __init__(self, d_model: int, n_heads: int, latent_heads: int, latent_dim: int, n_latents: int,
+                 window: int, bias: bool = True, local_block_size: int = 256,
+                 latent_query_block_size: int = 0) -> None:
+        super().__init__()
+        # reference llattn_triton.py:45-47 and models.py:64-65
+        assert d_model % n_heads == 0, "d_model must be divisible by n_heads"
+        assert latent_dim % latent_heads == 0, "latent_dim must be divisible by latent_heads"
+        self.d_model = d_model
+        self.n_heads = n_heads
+        self.head_dim = d_model // n_heads
+        self.latent_heads = latent_heads
+        self.latent_dim = latent_dim
+        self.latent_d_model = latent_dim
+        self.latent_head_dim = latent_dim // latent_heads
+        self.n_latents = n_latents
+        self.latent_tokens = n_latents
+        self.window = window
+        self.local_block_size = local_block_size
+        self.latent_query_block_size = max(0, latent_query_block_size)
+        # same names, shapes and creation order as reference models.py:80-90
+        self.qkv_proj = nn.Linear(d_model, 3 * d_model, bias=bias)
+        self.rq_proj = nn.Linear(d_model, latent_dim, bias=bias)
+        self.rkv_proj = nn.Linear(d_model, 2 * latent_dim, bias=bias)
+        self.r_out = nn.Linear(latent_dim, d_model, bias=bias)
+        self.out = nn.Linear(d_model, d_model, bias=bias)
+        self.gate_local = nn.Linear(self.head_dim, 1, bias=False)
+        self.gate_remote = nn.Linear(self.head_dim, 1, bias=False)
+        self.profile_enabled = False
+        self.profile_totals: dict[str, float] = {}
+        self.profile_steps = 0
+
+    # ---- checkpoint compatibility: split legacy projections (reference models.py:98-129)
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
+                              error_msgs):
+        for fused, parts in (("qkv_proj", ("q_proj", "k_proj", "v_proj")), ("rkv_proj", ("rk_proj", "rv_proj"))):
+            for kind in ("weight", "bias"):
+                key = f"{prefix}{fused}.{kind}"
+                old = [f"{prefix}{p}.{kind}" for p in parts]
+                if key not in state_dict and all(o in state_dict for o in old):
+                    state_dict[key] = torch.cat([state_dict.pop(o) for o in old], dim=0)
+        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
+                                      error_msgs)
+
+    # ---- profiling API (reference models.py:131-152; llattn_triton.py:83-90)
+    def set_profile(self, enabled: bool) -> None:
+        self.profile_enabled = enabled
+        self.profile_totals = {}
+        self.profile_steps = 0
+
+    def get_profile_stats(self) -> dict[str, float]:
+        if not self.profile_enabled or self.profile_steps == 0:
+            return {}
+        n = self.profile_steps
+        return {f"profile_{k}": v / n for k, v in self.profile_totals.items()}
+
+    def layout(self, B: int, T: int) -> L.Layout:
+        return L.resolve_layout(B, T, self.d_model, self.n_heads, self.latent_dim, self.latent_heads, self.window,
+                                self.local_block_size, self.n_latents, self.latent_query_block_size)
+
+    def forward(self, x: torch.Tensor, _positions: Optional[torch.Tensor] = None) -> torch.Tensor:
+        B, T, D = x.shape
+        if D != self.d_model:
+            raise ValueError(f"expected d_model={self.d_model}, got input of width {D}")
+        L.require_gpu(x)
+        lay = self.layout(B, T)
+        prof = _Prof(self.profile_enabled, x.device) if self.profile_enabled else None
+        if prof is not None:
+            prof.start()
+        macro = self.latent_query_block_size > 1
+        if macro:
+            qkvr = self.qkv_proj(x)
+            rq = self.rq_proj(pool(x, lay.q_block, lay.n_q, L.DIV_SEG))
+        else:
+            w = torch.cat([self.qkv_proj.weight, self.rq_proj.weight], dim=0)
+            b = None if self.qkv_proj.bias is None else torch.cat([self.qkv_proj.bias, self.rq_proj.bias], dim=0)
+            qkvr = F.linear(x, w, b)
+            rq = None
+        if prof is not None:
+            prof.lap("qkv_ms")
+        gkgv = self.rkv_proj(pool(x, lay.chunk, lay.n_chunks, L.DIV_COUNT))
+        if prof is not None:
+            prof.lap("pool_ms")
+        rqc = None if rq is None else rq.to(qkvr.dtype)
+        y = LLAttnCore.apply(qkvr, rqc, gkgv.to(qkvr.dtype), self.gate_local.weight, self.gate_remote.weight,
+                             self.r_out.weight, self.r_out.bias, lay, prof)
+        if prof is not None:
+            # the gate mix runs in the local kernel's epilogue: its time is in local_attention_ms
+            prof.t["gate_mix_ms"] = 0.0
+            self._record_profile(prof, lay)
+        return self.out(y)
+
+    def _record_profile(self, prof, lay: L.Layout) -> None:
+        t = prof.t
+        tot = self.profile_totals
+        total = sum(t.values())
+        for key in ("qkv_ms", "pool_ms", "local_attention_ms", "latent_attention_ms", "gate_mix_ms"):
+            tot[key] = tot.get(key, 0.0) + t.get(key, 0.0)
+        tot["local_latent_total_ms"] = tot.get("local_latent_total_ms", 0.0) + total
+        tot["gate_mean"] = tot.get("gate_mean", 0.0) + float(prof.gate_mean.mean().item())
+        tot["seq_len"] = tot.get("seq_len", 0.0) + lay.T
+        tot["local_block_size"] = tot.get("local_block_size", 0.0) + lay.block
+        tot["latent_count"] = tot.get("latent_count", 0.0) + lay.n_chunks
+        tot["latent_chunk_size"] = tot.get("latent_chunk_size", 0.0) + math.ceil(lay.T / lay.n_chunks)
+        tot["latent_query_block_size"] = tot.get("latent_query_block_size", 0.0) + lay.q_block
+        self.profile_steps += 1
+
+
+# name used by this package; the class above keeps the reference module's name
+LocalLatentAttentionHIP = LocalLatentAttentionTriton

@@ -1,0 +1,79 @@
+"""Helpers shared by the GPU parity tests."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle.llattn_oracle import BlockShape
+
+FP32_TOL = 1e-4            # max-abs, fp32 kernels vs the float64 / fp32 reference
+BF16_MAX_TOL = 2e-2        # max-abs, bf16 kernels vs the fp32 reference
+BF16_MEANREL_TOL = 1e-2    # mean(|a-b|) / mean(|b|)
+
+
+def require_cuda():
+    assert torch.cuda.is_available(), "GPU test run without a visible GPU"
+    return torch.device("cuda:0")
+
+
+def build_module(shape: BlockShape, params: dict | None = None, device="cuda:0", dtype=torch.float32):
+    from llattn_amd import LocalLatentAttentionTriton
+    m = LocalLatentAttentionTriton(shape.d_model, shape.n_heads, shape.latent_heads, shape.latent_d_model,
+                                   shape.latent_tokens, shape.window, local_block_size=shape.local_block_size,
+                                   latent_query_block_size=shape.latent_query_block_size)
+    if params is not None:
+        sd = {k: torch.as_tensor(np.asarray(v)).to(torch.float32) for k, v in params.items()}
+        m.load_state_dict(sd)
+    return m.to(device=device, dtype=dtype)
+
+
+def run_module(m, x: torch.Tensor, dout: torch.Tensor, autocast_bf16: bool = False):
+    x = x.detach().clone().requires_grad_(True)
+    for p in m.parameters():
+        p.grad = None
+    with torch.autocast(device_type="cuda", dtype=torch.bfloat16, enabled=autocast_bf16):
+        out = m(x)
+    out.backward(dout.to(out.dtype))
+    grads = {n: p.grad.detach().float().cpu().double().numpy() for n, p in m.named_parameters()}
+    return out.detach().float().cpu().double().numpy(), x.grad.detach().float().cpu().double().numpy(), grads
+
+
+def err_stats(a, ref):
+    """(max|a-ref| / max(1, max|ref|), mean|a-ref| / mean|ref|).  The mean-relative term is 0 when the
+    reference is zero to rounding (e.g. dQ with a single key per query, where the softmax is saturated):
+    a relative error of an exact zero carries no information, and the max-abs term still bounds it."""
+    a = np.asarray(a, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    d = np.abs(a - ref)
+    scale = max(1.0, float(np.abs(ref).max()))
+    mref = float(np.abs(ref).mean())
+    mean_rel = float(d.mean() / mref) if mref > 1e-9 * scale else 0.0
+    return float(d.max()) / scale, mean_rel
+
+
+def assert_fp32_close(a, ref, what=""):
+    mx, _ = err_stats(a, ref)
+    assert mx <= FP32_TOL, f"{what}: scaled max-abs {mx:.3e} > {FP32_TOL}"
+
+
+def assert_bf16_close(a, ref, what="", floor=None):
+    """bf16 bar: scaled max-abs <= 2e-2 and mean-rel <= 1e-2.  With ``floor`` = the (max, mean-rel) error
+    that the reference math itself reaches when run under bf16 autocast on the same inputs, the bar is
+    raised to twice that floor where the floor alone already exceeds it."""
+    mx, mr = err_stats(a, ref)
+    tmx, tmr = BF16_MAX_TOL, BF16_MEANREL_TOL
+    if floor is not None:
+        tmx, tmr = max(tmx, 2.0 * floor[0]), max(tmr, 2.0 * floor[1])
+    assert mx <= tmx, f"{what}: scaled max-abs {mx:.3e} > {tmx:.3e}"
+    assert mr <= tmr, f"{what}: mean-rel {mr:.3e} > {tmr:.3e}"
+
+
+def bf16_floor(params: dict, x_bf16: np.ndarray, dout: np.ndarray, shape, grads_ref: dict) -> dict:
+    """Per-parameter (max, mean-rel) error of the reference math (torch CPU restatement) under
+    bf16 autocast against the float64 golden gradients: the precision a bf16 run can be expected to reach."""
+    from oracle import torch_ref
+    p = {k: torch.tensor(np.asarray(v), dtype=torch.float32) for k, v in params.items()}
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        _, _, g = torch_ref.block_forward_backward(p, torch.tensor(x_bf16, dtype=torch.float32),
+                                                   torch.tensor(dout, dtype=torch.float32), shape)
+    return {n: err_stats(g[n].float().numpy(), grads_ref[n]) for n in grads_ref}

@@ -1,0 +1,206 @@
+"""CPU tests of the C ABI and the host logic (no kernel launches: every call here
+fails validation before it reaches the HIP runtime)."""
+from __future__ import annotations
+
+import ctypes
+import re
+
+import pytest
+import torch
+
+from conftest import REPO
+
+
+def _lib():
+    from llattn_amd import _lib as L
+    return L, L.load()
+
+
+def _declared_functions():
+    text = (REPO / "include" / "llattn.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:int32_t|size_t|const char\*)\s+(llattn_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    L, lib = _lib()
+    names = _declared_functions()
+    assert len(names) == 9, names
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in L.SIGNATURES, f"{n} has no ctypes signature"
+    assert set(L.SIGNATURES) == set(names)
+
+
+def test_abi_version_and_empty_error():
+    L, lib = _lib()
+    assert lib.llattn_abi_version() == L.ABI_VERSION == 1
+
+
+def _shape(L, **kw):
+    base = dict(B=2, T=97, H=2, Dh=32, Lh=2, Ldh=8, window=16, block=32, chunk=17, n_chunks=6, q_block=1, n_q=97,
+                dtype=L.BF16, gate_per_head=0)
+    base.update(kw)
+    return L.LlattnShape(**base)
+
+
+def test_workspace_sizes():
+    L, lib = _lib()
+    s = _shape(L)
+    n_local = lib.llattn_workspace_size(ctypes.byref(s), L.WS_LOCAL_BWD)
+    # dO (bf16) + row sums + gate partials, each rounded up to 256 bytes
+    up = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    assert n_local == up(2 * 97 * 2 * 32 * 2) + up(2 * 2 * 97 * 4) + up(2 * 2 * 2 * 2 * 32 * 4)
+    assert lib.llattn_workspace_size(ctypes.byref(s), L.WS_LATENT_BWD) == up(2 * 2 * 1 * 6 * 2 * 8 * 4)
+    assert lib.llattn_workspace_size(ctypes.byref(s), 7) == 0
+    assert b"unknown workspace kind" in lib.llattn_last_error()
+
+
+@pytest.mark.parametrize("field,value,code,msg", [
+    ("window", 0, 1, b"local_window must be positive"),
+    ("T", 0, 1, b"sizes must be positive"),
+    ("dtype", 5, 2, b"unknown dtype"),
+    ("Dh", 20, 4, b"head_dim 20 unsupported"),
+    ("Dh", 160, 4, b"head_dim 160 unsupported"),
+    ("Ldh", 128, 4, b"latent head_dim 128 unsupported"),
+    ("chunk", 5, 1, b"does not tile"),
+    ("n_q", 50, 1, b"does not tile"),
+    ("block", 98, 1, b"local block size"),
+])
+def test_shape_validation_codes(field, value, code, msg):
+    L, lib = _lib()
+    s = _shape(L, **{field: value})
+    t = L.LlattnTensor(None, 0, 0, 0)
+    rc = lib.llattn_local_gate_fwd(ctypes.byref(s), *(ctypes.byref(t),) * 4, None, None, ctypes.byref(t),
+                                   ctypes.byref(t), None, None, None)
+    assert rc == code
+    assert msg in lib.llattn_last_error()
+    with pytest.raises(ValueError):
+        L.check(rc, "llattn_local_gate_fwd")
+
+
+def test_null_and_misaligned_views_are_layout_errors():
+    L, lib = _lib()
+    s = _shape(L)
+    null = L.LlattnTensor(None, 0, 0, 0)
+    rc = lib.llattn_latent_fwd(ctypes.byref(s), *(ctypes.byref(null),) * 4, None, None)
+    assert rc == L.ERR_LAYOUT and b"null tensor" in lib.llattn_last_error()
+    odd = L.LlattnTensor(ctypes.c_void_p(0x1008), 8, 8, 8)  # never dereferenced: validation rejects it first
+    rc = lib.llattn_latent_fwd(ctypes.byref(s), *(ctypes.byref(odd),) * 4, None, None)
+    assert rc == L.ERR_LAYOUT and b"16-byte aligned" in lib.llattn_last_error()
+    bad_stride = L.LlattnTensor(ctypes.c_void_p(0x1000), 8, 12, 8)
+    rc = lib.llattn_latent_fwd(ctypes.byref(s), *(ctypes.byref(bad_stride),) * 4, None, None)
+    assert rc == L.ERR_LAYOUT and b"multiples of 8" in lib.llattn_last_error()
+
+
+def test_pool_validation():
+    L, lib = _lib()
+    rc = lib.llattn_pool_fwd(None, 0, 0, None, 0, 0, 2, 97, 8, 17, 5, 0, L.F32, None)
+    assert rc == L.ERR_SHAPE and b"do not tile" in lib.llattn_last_error()
+    rc = lib.llattn_pool_fwd(None, 0, 0, None, 0, 0, 2, 97, 8, 17, 6, 0, L.F32, None)
+    assert rc == L.ERR_LAYOUT
+    rc = lib.llattn_pool_bwd(None, 0, 0, None, 0, 0, 2, 97, 8, 17, 6, 9, 0, L.F32, None)
+    assert rc == L.ERR_SHAPE and b"bad divisor" in lib.llattn_last_error()
+
+
+def test_workspace_too_small_is_runtime_error():
+    L, lib = _lib()
+    s = _shape(L)
+    t = L.LlattnTensor(ctypes.c_void_p(0x1000), 64, 64, 32)
+    g = ctypes.c_void_p(0x2000)
+    rc = lib.llattn_local_gate_bwd(ctypes.byref(s), *(ctypes.byref(t),) * 4, g, g, ctypes.byref(t), g, g,
+                                   *(ctypes.byref(t),) * 5, g, g, g, 16, None)
+    assert rc == L.ERR_WORKSPACE
+    with pytest.raises(RuntimeError, match="workspace"):
+        L.check(rc, "llattn_local_gate_bwd")
+
+
+# ---------------------------------------------------------------- host logic
+
+def test_resolve_layout_matches_reference_rules():
+    from llattn_amd import resolve_layout
+    from oracle.llattn_oracle import BlockShape, seq_layout
+    for T, W, lbs, ntok, qbs in [(2048, 64, 256, 16, 0), (97, 16, 32, 6, 24), (40, 1, 8, 64, 0), (16384, 512, 256, 256, 0),
+                                 (8192, 256, 256, 128, 64), (33, 8, 4, 5, 1), (5, 3, 2, 3, 2)]:
+        lay = resolve_layout(2, T, 64, 2, 16, 2, W, lbs, ntok, qbs)
+        ref = seq_layout(BlockShape(d_model=64, n_heads=2, window=W, local_block_size=lbs, latent_tokens=ntok,
+                                    latent_d_model=16, latent_heads=2, latent_query_block_size=qbs), T)
+        assert (lay.block, lay.chunk, lay.n_chunks, lay.q_block, lay.n_q) == (ref.bs, ref.chunk, ref.n_chunks,
+                                                                             ref.qb, ref.n_q)
+
+
+@pytest.mark.parametrize("kw,msg", [(dict(T=0), "seq_len must be positive"),
+                                    (dict(latent_tokens=0), "latent_tokens must be positive"),
+                                    (dict(window=0), "local_window must be positive")])
+def test_resolve_layout_errors_match_reference(kw, msg):
+    from llattn_amd import resolve_layout
+    args = dict(B=1, T=16, d_model=8, n_heads=2, latent_d_model=4, latent_heads=2, window=4, local_block_size=8,
+                latent_tokens=4, latent_query_block_size=0)
+    args.update(kw)
+    with pytest.raises(ValueError, match=msg):
+        resolve_layout(**args)
+
+
+def test_module_surface_and_cpu_refusal():
+    import llattn_triton  # the drop-in module name
+    from kernels.llattn_op import LLAttnFunction  # the drop-in op path
+    from llattn_amd import LLAttnFunction as F2, LocalLatentAttentionTriton
+    assert LLAttnFunction is F2
+    assert llattn_triton.LocalLatentAttentionTriton is LocalLatentAttentionTriton
+    m = LocalLatentAttentionTriton(64, 2, 2, 16, 6, 16)  # positional args of the reference dispatcher
+    names = [n for n, _ in m.named_parameters()]
+    assert names == ["qkv_proj.weight", "qkv_proj.bias", "rq_proj.weight", "rq_proj.bias", "rkv_proj.weight",
+                     "rkv_proj.bias", "r_out.weight", "r_out.bias", "out.weight", "out.bias", "gate_local.weight",
+                     "gate_remote.weight"]
+    assert m.get_profile_stats() == {}
+    m.set_profile(True)
+    assert m.get_profile_stats() == {}
+    with pytest.raises(RuntimeError, match="GPUs only"):
+        m(torch.randn(1, 8, 64))
+    with pytest.raises(AssertionError):
+        LocalLatentAttentionTriton(65, 2, 2, 16, 6, 16)
+
+
+def test_same_init_as_reference_block_under_seed(c1_golden):
+    """Parameters are created in the reference order, so torch.manual_seed(0) reproduces config 1's weights."""
+    from llattn_amd import LocalLatentAttentionTriton
+    _, params, *_ = c1_golden
+    torch.manual_seed(0)
+    m = LocalLatentAttentionTriton(256, 4, 2, 32, 8, 128)
+    for n, p in m.named_parameters():
+        assert torch.equal(p.detach(), params[n]), n
+
+
+def test_legacy_split_projection_keys_load():
+    from llattn_amd import LocalLatentAttentionTriton
+    m = LocalLatentAttentionTriton(32, 2, 2, 8, 4, 4)
+    sd = m.state_dict()
+    legacy = {k: v for k, v in sd.items() if not k.startswith(("qkv_proj", "rkv_proj"))}
+    for i, n in enumerate(("q_proj", "k_proj", "v_proj")):
+        legacy[f"{n}.weight"] = sd["qkv_proj.weight"][i * 32:(i + 1) * 32]
+        legacy[f"{n}.bias"] = sd["qkv_proj.bias"][i * 32:(i + 1) * 32]
+    for i, n in enumerate(("rk_proj", "rv_proj")):
+        legacy[f"{n}.weight"] = sd["rkv_proj.weight"][i * 8:(i + 1) * 8]
+        legacy[f"{n}.bias"] = sd["rkv_proj.bias"][i * 8:(i + 1) * 8]
+    m2 = LocalLatentAttentionTriton(32, 2, 2, 8, 4, 4)
+    m2.load_state_dict(legacy)
+    for k, v in sd.items():
+        assert torch.equal(m2.state_dict()[k], v), k
+
+
+def test_build_attention_dispatch():
+    from llattn_amd import LocalLatentAttentionTriton, ModelConfig, build_attention
+    m = build_attention(ModelConfig(d_model=64, n_heads=2, local_block_size=32, latent_query_block_size=8))
+    assert isinstance(m, LocalLatentAttentionTriton)
+    assert (m.local_block_size, m.latent_query_block_size) == (32, 8)
+    with pytest.raises(RuntimeError):
+        build_attention(ModelConfig(use_triton_kernel=False))
+    with pytest.raises(ValueError):
+        build_attention(ModelConfig(dropout=0.1))
+
+
+def test_oracle_is_not_imported_by_the_product():
+    import pathlib
+    pkg = REPO / "local-latent-attention_amd"
+    for f in pkg.rglob("*.py"):
+        text = f.read_text()
+        assert "oracle" not in text.replace("oracle/", ""), f"{f} mentions the oracle"
