@@ -55,8 +55,8 @@ int32_t check_shape(const llattn_shape* s) {
   const int vec = s->dtype == LLATTN_F32 ? 4 : 8;
   if (s->Dh % vec || padded_head_dim(s->Dh) == 0)
     return fail(LLATTN_ERR_UNSUPPORTED, "head_dim %d unsupported (needs a multiple of %d, at most 128)", s->Dh, vec);
-  if (s->Ldh % vec || padded_latent_dim(s->Ldh) == 0)
-    return fail(LLATTN_ERR_UNSUPPORTED, "latent head_dim %d unsupported (needs a multiple of %d, at most 64)", s->Ldh,
+  if (s->Ldh % vec || padded_head_dim(s->Ldh) == 0)
+    return fail(LLATTN_ERR_UNSUPPORTED, "latent head_dim %d unsupported (needs a multiple of %d, at most 128)", s->Ldh,
                 vec);
   return LLATTN_OK;
 }
@@ -72,8 +72,9 @@ int32_t llattn_abi_version(void) { return LLATTN_ABI_VERSION; }
 const char* llattn_last_error(void) { return g_last_error; }
 
 // Local backward workspace: dO_local [B][T][H][Dh] (storage type), row sums
-// D [B][H][T] fp32 and gate partials [B*H*n_qtiles][2][Dh] fp32.
-// Latent backward workspace: partial dgk/dgv [B*Lh*n_tiles][n_chunks][2][Ldh] fp32.
+// D [B][H][T] fp32 and gate partials [H][2][Dh][B*n_qtiles] fp32.
+// Latent backward workspace: D [B][Lh][n_q] fp32 and per-segment dgk/dgv partials
+// [B][Lh][n_segments][16*ceil(n_chunks/16)][2][Ldh] fp32 (see llattn_latent.hip).
 size_t llattn_workspace_size(const llattn_shape* s, int32_t kind) {
   if (check_shape(s) != LLATTN_OK) return 0;
   const size_t B = s->B, T = s->T, H = s->H, Dh = s->Dh;
@@ -82,10 +83,7 @@ size_t llattn_workspace_size(const llattn_shape* s, int32_t kind) {
     const size_t nqt = (T + 63) / 64;
     return up(B * T * H * Dh * elem_size(s->dtype)) + up(B * H * T * 4) + up(B * H * nqt * 2 * Dh * 4);
   }
-  if (kind == LLATTN_WS_LATENT_BWD) {
-    const size_t ntile = (size_t(s->n_q) + 255) / 256;
-    return up(size_t(s->B) * s->Lh * ntile * s->n_chunks * 2 * s->Ldh * 4);
-  }
+  if (kind == LLATTN_WS_LATENT_BWD) return latent_workspace_bytes(s);
   fail(LLATTN_ERR_SHAPE, "unknown workspace kind %d", kind);
   return 0;
 }

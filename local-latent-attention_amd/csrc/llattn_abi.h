@@ -28,16 +28,10 @@ inline int padded_head_dim(int d) {
   if (d <= 128) return 128;
   return 0;
 }
-inline int padded_latent_dim(int d) {
-  if (d <= 0) return 0;
-  if (d <= 8) return 8;
-  if (d <= 16) return 16;
-  if (d <= 32) return 32;
-  if (d <= 64) return 64;
-  return 0;
-}
 // Validates a view whose innermost (head-dim) rows are read with 16-byte accesses.
 int32_t check_view(const char* name, const llattn_tensor* t, int32_t dtype, bool heads);
 int32_t check_shape(const llattn_shape* s);
+// workspace bytes of llattn_latent_bwd for a checked shape
+size_t latent_workspace_bytes(const llattn_shape* s);
 
 }  // namespace llattn

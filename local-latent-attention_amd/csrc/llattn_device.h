@@ -179,6 +179,98 @@ __device__ __forceinline__ float sum_rows16(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ---- LDS staging of 64-row tiles (256 threads) --------------------------------
+constexpr int kTP = 68;  // pitch (elements) of transposed tiles [dim][64 rows + 4]
+template <typename T> constexpr int kRowPad = std::is_same_v<T, float> ? 4 : 8;
+
+// Rows [r0, r0+64) of a row view (row stride st) into LDS row-major [64][P];
+// rows >= r_end and dims >= Dh are zero.  Consecutive threads take consecutive
+// 16-byte chunks of a row (coalesced reads).
+template <typename T, int DHP, int P>
+__device__ __forceinline__ void stage_rows(T* lds, const T* base, int64_t st, int r0, int r_end, int Dh) {
+  constexpr int V = Vec16<T>::N, CPR = DHP / V;
+  for (int c = threadIdx.x; c < 64 * CPR; c += 256) {
+    const int row = c / CPR, col = (c % CPR) * V, rr = r0 + row;
+    uint4 x = make_uint4(0, 0, 0, 0);
+    if (rr < r_end && col < Dh) x = ld16(base + (int64_t)rr * st + col);
+    st16(lds + row * P + col, x);
+  }
+}
+
+// The same rows stored transposed into LDS [DHP][kTP] (row index contiguous),
+// and row-major into lds_rows as well when kRows.  Writes are whole dwords
+// with the row index varying fastest across lanes (bank-conflict free): bf16
+// threads handle a pair of rows and pack the two rows' elements of one dim.
+template <typename T, int DHP, int P, bool kRows>
+__device__ __forceinline__ void stage_rows_t(T* lds_rows, T* lds_t, const T* base, int64_t st, int r0, int r_end,
+                                             int Dh) {
+  constexpr int V = Vec16<T>::N, CPR = DHP / V;
+  if constexpr (std::is_same_v<T, float>) {
+    for (int task = threadIdx.x; task < 64 * CPR; task += 256) {
+      const int row = task % 64, col = (task / 64) * V, rr = r0 + row;
+      uint4 x = make_uint4(0, 0, 0, 0);
+      if (rr < r_end && col < Dh) x = ld16(base + (int64_t)rr * st + col);
+      if constexpr (kRows) st16(lds_rows + row * P + col, x);
+      lds_t[(col + 0) * kTP + row] = __uint_as_float(x.x);
+      lds_t[(col + 1) * kTP + row] = __uint_as_float(x.y);
+      lds_t[(col + 2) * kTP + row] = __uint_as_float(x.z);
+      lds_t[(col + 3) * kTP + row] = __uint_as_float(x.w);
+    }
+  } else {
+    for (int task = threadIdx.x; task < 32 * CPR; task += 256) {
+      const int row = 2 * (task % 32), col = (task / 32) * V, rr = r0 + row;
+      uint4 x0 = make_uint4(0, 0, 0, 0), x1 = make_uint4(0, 0, 0, 0);
+      if (col < Dh) {
+        if (rr < r_end) x0 = ld16(base + (int64_t)rr * st + col);
+        if (rr + 1 < r_end) x1 = ld16(base + (int64_t)(rr + 1) * st + col);
+      }
+      if constexpr (kRows) {
+        st16(lds_rows + row * P + col, x0);
+        st16(lds_rows + (row + 1) * P + col, x1);
+      }
+      const uint32_t a[4] = {x0.x, x0.y, x0.z, x0.w}, b[4] = {x1.x, x1.y, x1.z, x1.w};
+      uint32_t* dst = reinterpret_cast<uint32_t*>(lds_t + col * kTP + row);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        dst[(2 * j) * (kTP / 2)] = (a[j] & 0xffffu) | (b[j] << 16);
+        dst[(2 * j + 1) * (kTP / 2)] = (a[j] >> 16) | (b[j] & 0xffff0000u);
+      }
+    }
+  }
+}
+
+// ---- online softmax + PV for one 16-key sub-tile -----------------------------
+// s: S^T[key 4g+i][query r] (raw scores); ok[i]: key 4g+i visible to query r.
+// Updates the running max / partial sum of query r (max shared by the four
+// lane groups) and O^T += V^T P^T with vt = &Vt[r][16*sub + 4g] (LDS, pitch kTP).
+template <int NT, typename T>
+__device__ __forceinline__ void online_softmax_pv(const f32x4& s, const bool ok[4], float scale_log2, float& m_run,
+                                                  float& l_run, f32x4 (&acc)[NT], const T* vt) {
+  float sv[4], mloc = kNegInf;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    sv[i] = ok[i] ? s[i] * scale_log2 : kNegInf;
+    mloc = fmaxf(mloc, sv[i]);
+  }
+  mloc = max_groups(mloc);
+  const float m_new = fmaxf(m_run, mloc);
+  const float mu = (m_new == kNegInf) ? 0.f : m_new;
+  const float alpha = fast_exp2(m_run - mu);
+  float pv[4], ps = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    pv[i] = fast_exp2(sv[i] - mu);
+    ps += pv[i];
+  }
+  l_run = l_run * alpha + ps;
+  m_run = m_new;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    acc[t] *= alpha;
+    acc[t] = col_mma(vt + 16 * t * kTP, pv, acc[t]);
+  }
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs; remap so that each
 // XCD receives a contiguous range of logical tiles (neighbouring query tiles
 // of one head share K/V rows, which then stay in that XCD's L2).

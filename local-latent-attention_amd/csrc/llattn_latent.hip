@@ -1,242 +1,314 @@
-// Chunk-causal latent attention, forward and backward, for gfx950.
+// Chunk-causal latent attention, forward and backward, for gfx950 (bf16/fp32 MFMA).
 //
-// Semantics (reference models.py:361-375): latent query s of head lh attends
-// latents n < c(s), where c(s) = (s * q_block) / chunk is the chunk id of the
-// query's first token (token-wise queries: q_block = 1); scale 1/sqrt(Ldh);
-// queries with c(s) = 0 output 0.
+// Semantics (reference models.py:361-375): latent query s of latent head lh
+// attends latents n < c(s), where c(s) = (s * q_block) / chunk is the chunk id
+// of the query's first token (token-wise queries: q_block = 1), with scale
+// 1/sqrt(Ldh); queries with c(s) = 0 output 0.
 //
-// One thread owns one latent query (its Ldh-vector lives in registers); a
-// 256-thread workgroup covers 256 queries of one (batch, latent head) and
-// streams the latent keys/values it can see through LDS.  The latent count is
-// small (16 at the 0.55b shape, 256 at the long-context shape), so the work is
-// a bandwidth-bound pass over the queries.  The backward reduces the dgk / dgv
-// contributions of a wave with a halving butterfly (each step exchanges half of
-// the remaining vector), combines the four waves in LDS, writes one partial per
-// workgroup and sums the partials in tile order in a second kernel: no atomics,
-// bitwise deterministic.
+// The latents play the role of keys/values of a small attention, so the
+// kernels reuse the tile machinery of the local kernels: one 256-thread
+// workgroup per (batch, latent head, 64 queries), waves of 16 queries, latent
+// tiles of 64 staged in LDS, S^T = GK RQ^T and O^T = GV^T P^T on MFMA.
+//
+// Backward, without atomics:
+//   pass Q  (per query tile): D_s = sum_n P_sn (dL_s . gv_n) in fp32 from the
+//           recomputed weights, then drq = scale * sum_n dS_sn gk_n;
+//   pass KV (per 16-latent tile and query segment): dgk, dgv partial sums over
+//           the segment's queries (the four waves split the query sub-tiles and
+//           are summed in LDS in wave order); a last kernel adds the segment
+//           partials in segment order.
 #include "llattn_abi.h"
 #include "llattn_device.h"
 
 namespace llattn {
 
 struct LatentArgs {
-  int B, Lh, Ldh, n_q, q_block, chunk, n_chunks, n_tiles;
+  int B, Lh, Ldh, n_q, q_block, chunk, n_chunks, n_qt, n_lt, n_seg;
   float scale, scale_log2;
   const void* rq; int64_t rq_sb, rq_sn, rq_sh;
   const void* gk; int64_t gk_sb, gk_sn, gk_sh;
   const void* gv; int64_t gv_sb, gv_sn, gv_sh;
-  const void* out; int64_t o_sb, o_sn, o_sh;
+  void* out; int64_t o_sb, o_sn, o_sh;
   float* lse;  // [B][Lh][n_q]
   const void* dout; int64_t do_sb, do_sn, do_sh;
   void* drq; int64_t drq_sb, drq_sn, drq_sh;
   void* dgk; int64_t dgk_sb, dgk_sn, dgk_sh;
   void* dgv; int64_t dgv_sb, dgv_sn, dgv_sh;
-  float* part;  // [B*Lh*n_tiles][n_chunks][2][Ldh]
+  float* Dsum;  // workspace [B][Lh][n_q]
+  float* part;  // workspace [B][Lh][n_seg][n_lt*16][2][Ldh]
 };
 
-constexpr int kQTile = 256;
+constexpr int kSeg = 512;  // queries per segment of the latent-stationary pass
 
 // number of latents visible to latent query s
 __device__ __forceinline__ int visible(int s, const LatentArgs& a) {
   return min((int)(((int64_t)s * a.q_block) / a.chunk), a.n_chunks);
 }
 
-template <typename T, int LDP>
-__device__ __forceinline__ void load_vec(float (&v)[LDP], const T* p, int Ldh, bool valid) {
-#pragma unroll
-  for (int d = 0; d < LDP; d += 4) {
-    if (valid && d < Ldh) {
-      load4<T>(p + d, &v[d]);
-    } else {
-      v[d] = v[d + 1] = v[d + 2] = v[d + 3] = 0.f;
-    }
-  }
-}
-
-// latents [n0, n0+NL) of one (b, lh) into LDS as fp32 rows (zero past n_end / Ldh)
-template <typename T, int LDP, int NL>
-__device__ __forceinline__ void stage_latents(float (*gks)[LDP], float (*gvs)[LDP], const T* gk, int64_t gk_sn,
-                                              const T* gv, int64_t gv_sn, int n0, int n_end, int Ldh) {
-  for (int idx = threadIdx.x; idx < NL * (LDP / 4); idx += 256) {
-    const int n = idx / (LDP / 4), d = (idx % (LDP / 4)) * 4, nn = n0 + n;
-    float kv[4] = {0.f, 0.f, 0.f, 0.f}, vv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (nn < n_end && d < Ldh) {
-      load4<T>(gk + (int64_t)nn * gk_sn + d, kv);
-      load4<T>(gv + (int64_t)nn * gv_sn + d, vv);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      gks[n][d + j] = kv[j];
-      gvs[n][d + j] = vv[j];
-    }
-  }
-}
-
-template <typename T, int LDP>
+// ----------------------------------------------------------------------------
+// forward
+// ----------------------------------------------------------------------------
+template <typename T, int DHP>
 __global__ __launch_bounds__(256) void latent_fwd_kernel(const LatentArgs a) {
-  constexpr int NL = 64;
-  __shared__ __align__(16) float gks[NL][LDP];
-  __shared__ __align__(16) float gvs[NL][LDP];
-  const int tile = blockIdx.x % a.n_tiles, bh = blockIdx.x / a.n_tiles, lh = bh % a.Lh, b = bh / a.Lh;
-  const int s = tile * kQTile + threadIdx.x;
-  const bool sv = s < a.n_q;
-  const int ncq = sv ? visible(s, a) : 0;
-  const int nmax = visible(min(tile * kQTile + kQTile - 1, a.n_q - 1), a);
-
+  constexpr int DQ = DHP / 4, NT = DHP / 16, KP = DHP + kRowPad<T>;
+  __shared__ __align__(16) T Ks[64 * KP];
+  __shared__ __align__(16) T Vt[DHP * kTP];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, g = lane >> 4;
+  const int qt = blockIdx.x % a.n_qt, bh = blockIdx.x / a.n_qt, lh = bh % a.Lh, b = bh / a.Lh;
+  const int q0 = qt * 64, qw = q0 + 16 * wave, qi = qw + r;
+  const bool qv = qi < a.n_q;
+  const int ncq = qv ? visible(qi, a) : 0;
+  const int nmax = visible(min(q0 + 63, a.n_q - 1), a);
+  const int wmax = qw < a.n_q ? visible(min(qw + 15, a.n_q - 1), a) : 0;
   const T* gkb = static_cast<const T*>(a.gk) + b * a.gk_sb + lh * a.gk_sh;
   const T* gvb = static_cast<const T*>(a.gv) + b * a.gv_sb + lh * a.gv_sh;
-  float q[LDP], acc[LDP];
-  load_vec<T, LDP>(q, static_cast<const T*>(a.rq) + b * a.rq_sb + lh * a.rq_sh + (int64_t)s * a.rq_sn, a.Ldh, sv);
+
+  RowFrag<T, DQ> qf;
+  qf.load(static_cast<const T*>(a.rq) + b * a.rq_sb + lh * a.rq_sh + (int64_t)qi * a.rq_sn, g, a.Ldh, qv);
+  float m_run = kNegInf, l_run = 0.f;
+  f32x4 acc[NT];
 #pragma unroll
-  for (int d = 0; d < LDP; ++d) acc[d] = 0.f;
-  float m = kNegInf, l = 0.f;
-  for (int n0 = 0; n0 < nmax; n0 += NL) {
+  for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int n0 = 0; n0 < nmax; n0 += 64) {
     __syncthreads();
-    stage_latents<T, LDP, NL>(gks, gvs, gkb, a.gk_sn, gvb, a.gv_sn, n0, nmax, a.Ldh);
+    stage_rows<T, DHP, KP>(Ks, gkb, a.gk_sn, n0, nmax, a.Ldh);
+    stage_rows_t<T, DHP, KP, false>(nullptr, Vt, gvb, a.gv_sn, n0, nmax, a.Ldh);
     __syncthreads();
-    const int nend = min(NL, ncq - n0);
-    for (int n = 0; n < nend; ++n) {
-      float sc = 0.f;
 #pragma unroll
-      for (int d = 0; d < LDP; ++d) sc += q[d] * gks[n][d];
-      sc *= a.scale_log2;
-      const float m_new = fmaxf(m, sc);
-      const float alpha = fast_exp2(m - m_new);
-      const float p = fast_exp2(sc - m_new);
-      l = l * alpha + p;
+    for (int st = 0; st < 4; ++st) {
+      const int s0 = n0 + 16 * st;
+      if (s0 >= wmax) continue;  // uniform over the wave
+      RowFrag<T, DQ> kf;
+      kf.load_lds(Ks + (16 * st + r) * KP, g);
+      const f32x4 s = row_mma(kf, qf, f32x4{0.f, 0.f, 0.f, 0.f});
+      bool ok[4];
 #pragma unroll
-      for (int d = 0; d < LDP; ++d) acc[d] = acc[d] * alpha + p * gvs[n][d];
-      m = m_new;
+      for (int i = 0; i < 4; ++i) ok[i] = s0 + 4 * g + i < ncq;
+      online_softmax_pv<NT>(s, ok, a.scale_log2, m_run, l_run, acc, Vt + r * kTP + 16 * st + 4 * g);
     }
   }
-  if (sv) {
+  const float l = sum_groups(l_run);
+  if (qv) {
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    T* op = static_cast<T*>(const_cast<void*>(a.out)) + b * a.o_sb + lh * a.o_sh + (int64_t)s * a.o_sn;
+    T* op = static_cast<T*>(a.out) + b * a.o_sb + lh * a.o_sh + (int64_t)qi * a.o_sn;
 #pragma unroll
-    for (int d = 0; d < LDP; d += 4) {
+    for (int t = 0; t < NT; ++t) {
+      const int d = 16 * t + 4 * g;
       if (d < a.Ldh) {
-        float v4[4] = {acc[d] * inv, acc[d + 1] * inv, acc[d + 2] * inv, acc[d + 3] * inv};
+        float v4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v4[i] = acc[t][i] * inv;
         store4<T>(op + d, v4);
       }
     }
-    a.lse[((int64_t)b * a.Lh + lh) * a.n_q + s] = l > 0.f ? (m + __log2f(l)) * kLn2 : kNegInf;
+    if (g == 0) a.lse[((int64_t)b * a.Lh + lh) * a.n_q + qi] = l > 0.f ? (m_run + __log2f(l)) * kLn2 : kNegInf;
   }
 }
 
-// Halving butterfly: on entry every lane holds a length-M vector; on exit lane
-// `lane` holds element (lane >> (6 - log2 M)) of the wave-wide sum (M <= 64).
-template <int M, int O>
-__device__ __forceinline__ void butterfly(float* v, int lane) {
-  if constexpr (O > 0) {
-    if constexpr (M > 1) {
-      constexpr int H = M / 2;
-      const bool up = (lane & O) != 0;
-#pragma unroll
-      for (int j = 0; j < H; ++j) {
-        const float keep = up ? v[j + H] : v[j];
-        const float send = up ? v[j] : v[j + H];
-        v[j] = keep + __shfl_xor(send, O);
-      }
-      butterfly<H, O / 2>(v, lane);
-    } else {
-      v[0] += __shfl_xor(v[0], O);
-      butterfly<1, O / 2>(v, lane);
-    }
-  }
-}
-template <int M>
-constexpr int log2i() { return M <= 1 ? 0 : 1 + log2i<M / 2>(); }
-
-template <typename T, int LDP>
-__global__ __launch_bounds__(256) void latent_bwd_kernel(const LatentArgs a) {
-  constexpr int NL = 16, SHIFT = 6 - log2i<LDP>();
-  __shared__ __align__(16) float gks[NL][LDP];
-  __shared__ __align__(16) float gvs[NL][LDP];
-  __shared__ float red[4][NL][2][LDP];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int tile = blockIdx.x % a.n_tiles, bh = blockIdx.x / a.n_tiles, lh = bh % a.Lh, b = bh / a.Lh;
-  const int s = tile * kQTile + threadIdx.x;
-  const bool sv = s < a.n_q;
-  const int ncq = sv ? visible(s, a) : 0;
-  const int nmax = visible(min(tile * kQTile + kQTile - 1, a.n_q - 1), a);
-
+// ----------------------------------------------------------------------------
+// backward pass Q: D and drq
+// ----------------------------------------------------------------------------
+template <typename T, int DHP>
+__global__ __launch_bounds__(256) void latent_bwd_q_kernel(const LatentArgs a) {
+  constexpr int DQ = DHP / 4, NT = DHP / 16, KP = DHP + kRowPad<T>;
+  __shared__ __align__(16) T Ks[64 * KP];
+  __shared__ __align__(16) T Kt[DHP * kTP];
+  __shared__ __align__(16) T Vs[64 * KP];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, g = lane >> 4;
+  const int qt = blockIdx.x % a.n_qt, bh = blockIdx.x / a.n_qt, lh = bh % a.Lh, b = bh / a.Lh;
+  const int q0 = qt * 64, qw = q0 + 16 * wave, qi = qw + r;
+  const bool qv = qi < a.n_q;
+  const int ncq = qv ? visible(qi, a) : 0;
+  const int nmax = visible(min(q0 + 63, a.n_q - 1), a);
+  const int wmax = qw < a.n_q ? visible(min(qw + 15, a.n_q - 1), a) : 0;
   const T* gkb = static_cast<const T*>(a.gk) + b * a.gk_sb + lh * a.gk_sh;
   const T* gvb = static_cast<const T*>(a.gv) + b * a.gv_sb + lh * a.gv_sh;
-  float q[LDP], dl[LDP], drq[LDP], c[LDP];
-  load_vec<T, LDP>(q, static_cast<const T*>(a.rq) + b * a.rq_sb + lh * a.rq_sh + (int64_t)s * a.rq_sn, a.Ldh, sv);
-  load_vec<T, LDP>(dl, static_cast<const T*>(a.dout) + b * a.do_sb + lh * a.do_sh + (int64_t)s * a.do_sn, a.Ldh, sv);
-#pragma unroll
-  for (int d = 0; d < LDP; ++d) drq[d] = 0.f;
-  const float lse_nat = sv ? a.lse[((int64_t)b * a.Lh + lh) * a.n_q + s] : kNegInf;
+  const int64_t row = ((int64_t)b * a.Lh + lh) * a.n_q + qi;
+
+  RowFrag<T, DQ> qf, dof;
+  qf.load(static_cast<const T*>(a.rq) + b * a.rq_sb + lh * a.rq_sh + (int64_t)qi * a.rq_sn, g, a.Ldh, qv);
+  dof.load(static_cast<const T*>(a.dout) + b * a.do_sb + lh * a.do_sh + (int64_t)qi * a.do_sn, g, a.Ldh, qv);
+  const float lse_nat = qv ? a.lse[row] : kNegInf;
   const float lse2 = lse_nat == kNegInf ? 0.f : lse_nat * kLog2e;
+  const bool single = nmax <= 64;  // one latent tile: stage it once for both passes
 
-  // pass 1: D = sum_n P_n (dL . gv_n) in fp32 from the recomputed weights.  (dL . L with L read back
-  // at storage precision would cancel badly when the latent softmax is peaked.)
-  float Dsum = 0.f;
-  for (int n0 = 0; n0 < nmax; n0 += NL) {
+  // pass 1: D = sum_n P_n dP_n
+  float D = 0.f;
+  for (int n0 = 0; n0 < nmax; n0 += 64) {
     __syncthreads();
-    stage_latents<T, LDP, NL>(gks, gvs, gkb, a.gk_sn, gvb, a.gv_sn, n0, nmax, a.Ldh);
+    if (single) {
+      stage_rows_t<T, DHP, KP, true>(Ks, Kt, gkb, a.gk_sn, n0, nmax, a.Ldh);
+    } else {
+      stage_rows<T, DHP, KP>(Ks, gkb, a.gk_sn, n0, nmax, a.Ldh);
+    }
+    stage_rows<T, DHP, KP>(Vs, gvb, a.gv_sn, n0, nmax, a.Ldh);
     __syncthreads();
-    const int nend = min(NL, ncq - n0);
-    for (int n = 0; n < nend; ++n) {
-      float sc = 0.f, dp = 0.f;
 #pragma unroll
-      for (int d = 0; d < LDP; ++d) {
-        sc += q[d] * gks[n][d];
-        dp += dl[d] * gvs[n][d];
-      }
-      Dsum += fast_exp2(sc * a.scale_log2 - lse2) * dp;
+    for (int st = 0; st < 4; ++st) {
+      const int s0 = n0 + 16 * st;
+      if (s0 >= wmax) continue;
+      RowFrag<T, DQ> kf, vf;
+      kf.load_lds(Ks + (16 * st + r) * KP, g);
+      vf.load_lds(Vs + (16 * st + r) * KP, g);
+      const f32x4 s = row_mma(kf, qf, f32x4{0.f, 0.f, 0.f, 0.f});
+      const f32x4 dp = row_mma(vf, dof, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (s0 + 4 * g + i < ncq) D += fast_exp2(s[i] * a.scale_log2 - lse2) * dp[i];
     }
   }
-  float* part = a.part + (((int64_t)b * a.Lh + lh) * a.n_tiles + tile) * a.n_chunks * 2 * a.Ldh;
+  D = sum_groups(D);
+  if (qv && g == 0) a.Dsum[row] = D;
 
-  // pass 2: dS, drq and the per-workgroup dgk / dgv partials
-  for (int n0 = 0; n0 < nmax; n0 += NL) {
-    __syncthreads();
-    stage_latents<T, LDP, NL>(gks, gvs, gkb, a.gk_sn, gvb, a.gv_sn, n0, nmax, a.Ldh);
-    __syncthreads();
-    const int cnt = min(NL, nmax - n0);  // uniform over the workgroup
-    for (int n = 0; n < cnt; ++n) {
-      float sc = 0.f, dp = 0.f;
+  // pass 2: drq^T += GK^T dS^T
+  f32x4 acc[NT];
 #pragma unroll
-      for (int d = 0; d < LDP; ++d) {
-        sc += q[d] * gks[n][d];
-        dp += dl[d] * gvs[n][d];
-      }
-      const float p = (n0 + n < ncq) ? fast_exp2(sc * a.scale_log2 - lse2) : 0.f;
-      const float ds = p * (dp - Dsum) * a.scale;
-#pragma unroll
-      for (int d = 0; d < LDP; ++d) {
-        drq[d] += ds * gks[n][d];
-        c[d] = ds * q[d];
-      }
-      butterfly<LDP, 32>(c, lane);
-      if ((lane & ((1 << SHIFT) - 1)) == 0) red[wave][n][0][lane >> SHIFT] = c[0];
-#pragma unroll
-      for (int d = 0; d < LDP; ++d) c[d] = p * dl[d];
-      butterfly<LDP, 32>(c, lane);
-      if ((lane & ((1 << SHIFT) - 1)) == 0) red[wave][n][1][lane >> SHIFT] = c[0];
+  for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int n0 = 0; n0 < nmax; n0 += 64) {
+    if (!single) {
+      __syncthreads();
+      stage_rows_t<T, DHP, KP, true>(Ks, Kt, gkb, a.gk_sn, n0, nmax, a.Ldh);
+      stage_rows<T, DHP, KP>(Vs, gvb, a.gv_sn, n0, nmax, a.Ldh);
+      __syncthreads();
     }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < cnt * 2 * a.Ldh; idx += 256) {
-      const int n = idx / (2 * a.Ldh), rem = idx % (2 * a.Ldh), which = rem / a.Ldh, d = rem % a.Ldh;
-      part[(int64_t)(n0 + n) * 2 * a.Ldh + which * a.Ldh + d] =
-          red[0][n][which][d] + red[1][n][which][d] + red[2][n][which][d] + red[3][n][which][d];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int s0 = n0 + 16 * st;
+      if (s0 >= wmax) continue;
+      RowFrag<T, DQ> kf, vf;
+      kf.load_lds(Ks + (16 * st + r) * KP, g);
+      vf.load_lds(Vs + (16 * st + r) * KP, g);
+      const f32x4 s = row_mma(kf, qf, f32x4{0.f, 0.f, 0.f, 0.f});
+      const f32x4 dp = row_mma(vf, dof, f32x4{0.f, 0.f, 0.f, 0.f});
+      float ds[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = (s0 + 4 * g + i < ncq) ? fast_exp2(s[i] * a.scale_log2 - lse2) : 0.f;
+        ds[i] = p * (dp[i] - D);
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[t] = col_mma(Kt + (16 * t + r) * kTP + 16 * st + 4 * g, ds, acc[t]);
     }
   }
-  if (sv) {
-    T* p = static_cast<T*>(a.drq) + b * a.drq_sb + lh * a.drq_sh + (int64_t)s * a.drq_sn;
+  if (qv) {
+    T* p = static_cast<T*>(a.drq) + b * a.drq_sb + lh * a.drq_sh + (int64_t)qi * a.drq_sn;
 #pragma unroll
-    for (int d = 0; d < LDP; d += 4)
-      if (d < a.Ldh) store4<T>(p + d, &drq[d]);
+    for (int t = 0; t < NT; ++t) {
+      const int d = 16 * t + 4 * g;
+      if (d < a.Ldh) {
+        float v4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v4[i] = acc[t][i] * a.scale;
+        store4<T>(p + d, v4);
+      }
+    }
   }
 }
 
-// dgk / dgv [b][n][lh][d] = sum over query tiles (in tile order) of the partials;
-// tiles whose queries see fewer than n+1 latents wrote nothing for n.
+// ----------------------------------------------------------------------------
+// backward pass KV: dgk / dgv partial sums of one 16-latent tile over one segment of queries
+// ----------------------------------------------------------------------------
+template <typename T, int DHP>
+__global__ __launch_bounds__(256) void latent_bwd_kv_kernel(const LatentArgs a) {
+  constexpr int DQ = DHP / 4, NT = DHP / 16, KP = DHP + kRowPad<T>;
+  __shared__ __align__(16) T Qs[64 * KP];
+  __shared__ __align__(16) T Qt[DHP * kTP];
+  __shared__ __align__(16) T Os[64 * KP];
+  __shared__ __align__(16) T Ot[DHP * kTP];
+  __shared__ float lse2s[64], Dss[64];
+  __shared__ int vis[64];
+  static_assert(sizeof(T) * 64 * KP >= 2 * DHP * 16 * sizeof(float), "reduction buffer does not fit in Qs");
+  float* red = reinterpret_cast<float*>(Qs);  // [2][DHP][16] after the query loop
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane & 15, g = lane >> 4;
+  const int seg = blockIdx.x % a.n_seg, rest = blockIdx.x / a.n_seg;
+  const int lt = rest % a.n_lt, bh = rest / a.n_lt, lh = bh % a.Lh, b = bh / a.Lh;
+  const int n0 = lt * 16, kj = n0 + r;
+  const bool kv = kj < a.n_chunks;
+  const T* rqb = static_cast<const T*>(a.rq) + b * a.rq_sb + lh * a.rq_sh;
+  const T* dlb = static_cast<const T*>(a.dout) + b * a.do_sb + lh * a.do_sh;
+  const int64_t hrow = ((int64_t)b * a.Lh + lh) * a.n_q;
+
+  RowFrag<T, DQ> kf, vf;
+  kf.load(static_cast<const T*>(a.gk) + b * a.gk_sb + lh * a.gk_sh + (int64_t)kj * a.gk_sn, g, a.Ldh, kv);
+  vf.load(static_cast<const T*>(a.gv) + b * a.gv_sb + lh * a.gv_sh + (int64_t)kj * a.gv_sn, g, a.Ldh, kv);
+  f32x4 dk[NT], dv[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) dk[t] = dv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // first query that sees latent n0: s * q_block >= (n0 + 1) * chunk
+  const int64_t need = (int64_t)(n0 + 1) * a.chunk;
+  const int s_first = (int)((need + a.q_block - 1) / a.q_block);
+  const int qbeg = max(seg * kSeg, s_first);
+  const int qend = min((seg + 1) * kSeg, a.n_q);
+  for (int q0 = qbeg; q0 < qend; q0 += 64) {
+    __syncthreads();
+    stage_rows_t<T, DHP, KP, true>(Qs, Qt, rqb, a.rq_sn, q0, qend, a.Ldh);
+    stage_rows_t<T, DHP, KP, true>(Os, Ot, dlb, a.do_sn, q0, qend, a.Ldh);
+    if (tid < 64) {
+      const int qq = q0 + tid;
+      if (qq < qend) {
+        const float ls = a.lse[hrow + qq];
+        lse2s[tid] = ls == kNegInf ? 0.f : ls * kLog2e;
+        Dss[tid] = a.Dsum[hrow + qq];
+        vis[tid] = visible(qq, a);
+      } else {
+        lse2s[tid] = 0.f;
+        Dss[tid] = 0.f;
+        vis[tid] = 0;
+      }
+    }
+    __syncthreads();
+    const int s0 = q0 + 16 * wave;  // each wave takes one 16-query sub-tile
+    if (s0 < qend) {
+      RowFrag<T, DQ> qf, of;
+      qf.load_lds(Qs + (16 * wave + r) * KP, g);
+      of.load_lds(Os + (16 * wave + r) * KP, g);
+      const f32x4 s = row_mma(qf, kf, f32x4{0.f, 0.f, 0.f, 0.f});   // S[query 4g+i][latent r]
+      const f32x4 dp = row_mma(of, vf, f32x4{0.f, 0.f, 0.f, 0.f});  // dP[query][latent]
+      float p[4], ds[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ql = 16 * wave + 4 * g + i;
+        p[i] = (kv && kj < vis[ql]) ? fast_exp2(s[i] * a.scale_log2 - lse2s[ql]) : 0.f;
+        ds[i] = p[i] * (dp[i] - Dss[ql]);
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        dv[t] = col_mma(Ot + (16 * t + r) * kTP + 16 * wave + 4 * g, p, dv[t]);
+        dk[t] = col_mma(Qt + (16 * t + r) * kTP + 16 * wave + 4 * g, ds, dk[t]);
+      }
+    }
+  }
+  // sum the four waves in order: red[which][dim][latent]
+  for (int w = 0; w < 4; ++w) {
+    __syncthreads();
+    if (wave == w) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d = 16 * t + 4 * g + i;
+          float* rk = red + (0 * DHP + d) * 16 + r;
+          float* rv = red + (1 * DHP + d) * 16 + r;
+          *rk = (w == 0 ? 0.f : *rk) + dk[t][i] * a.scale;
+          *rv = (w == 0 ? 0.f : *rv) + dv[t][i];
+        }
+    }
+  }
+  __syncthreads();
+  float* part = a.part + ((((int64_t)b * a.Lh + lh) * a.n_seg + seg) * a.n_lt * 16) * 2 * a.Ldh;
+  for (int idx = tid; idx < 16 * 2 * a.Ldh; idx += 256) {
+    const int n = idx / (2 * a.Ldh), which = (idx / a.Ldh) % 2, d = idx % a.Ldh;
+    part[(int64_t)(n0 + n) * 2 * a.Ldh + which * a.Ldh + d] = red[(which * DHP + d) * 16 + n];
+  }
+}
+
+// dgk / dgv [b][n][lh][d] = sum over segments (in order) of the partials.
 template <typename T>
 __global__ __launch_bounds__(256) void latent_reduce_kernel(const LatentArgs a) {
   const int64_t total = (int64_t)a.B * a.Lh * a.n_chunks * 2 * a.Ldh;
+  const int64_t seg_stride = (int64_t)a.n_lt * 16 * 2 * a.Ldh;
   for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
     int64_t rest = idx;
     const int d = rest % a.Ldh; rest /= a.Ldh;
@@ -244,12 +316,10 @@ __global__ __launch_bounds__(256) void latent_reduce_kernel(const LatentArgs a) 
     const int n = rest % a.n_chunks; rest /= a.n_chunks;
     const int lh = rest % a.Lh;
     const int b = rest / a.Lh;
-    const float* p = a.part + ((int64_t)b * a.Lh + lh) * a.n_tiles * a.n_chunks * 2 * a.Ldh +
-                     (int64_t)n * 2 * a.Ldh + which * a.Ldh + d;
+    const float* p = a.part + ((int64_t)b * a.Lh + lh) * a.n_seg * seg_stride + (int64_t)n * 2 * a.Ldh +
+                     which * a.Ldh + d;
     float s = 0.f;
-    for (int t = 0; t < a.n_tiles; ++t) {
-      if (visible(min(t * kQTile + kQTile - 1, a.n_q - 1), a) > n) s += p[(int64_t)t * a.n_chunks * 2 * a.Ldh];
-    }
+    for (int k = 0; k < a.n_seg; ++k) s += p[k * seg_stride];
     T* out = which == 0 ? static_cast<T*>(a.dgk) + b * a.dgk_sb + lh * a.dgk_sh + (int64_t)n * a.dgk_sn + d
                         : static_cast<T*>(a.dgv) + b * a.dgv_sb + lh * a.dgv_sh + (int64_t)n * a.dgv_sn + d;
     *out = from_f<T>(s);
@@ -258,25 +328,25 @@ __global__ __launch_bounds__(256) void latent_reduce_kernel(const LatentArgs a) 
 
 namespace {
 
-template <typename T, int LDP>
+template <typename T, int DHP>
 void launch(bool fwd, const LatentArgs& a, hipStream_t st) {
-  const dim3 grid(a.B * a.Lh * a.n_tiles);
   if (fwd) {
-    hipLaunchKernelGGL((latent_fwd_kernel<T, LDP>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((latent_fwd_kernel<T, DHP>), dim3(a.B * a.Lh * a.n_qt), dim3(256), 0, st, a);
   } else {
-    hipLaunchKernelGGL((latent_bwd_kernel<T, LDP>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((latent_bwd_q_kernel<T, DHP>), dim3(a.B * a.Lh * a.n_qt), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((latent_bwd_kv_kernel<T, DHP>), dim3(a.B * a.Lh * a.n_lt * a.n_seg), dim3(256), 0, st, a);
     const int64_t total = (int64_t)a.B * a.Lh * a.n_chunks * 2 * a.Ldh;
     const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
     hipLaunchKernelGGL((latent_reduce_kernel<T>), dim3(blocks), dim3(256), 0, st, a);
   }
 }
 template <typename T>
-bool dispatch(int ldp, bool fwd, const LatentArgs& a, hipStream_t st) {
-  switch (ldp) {
-    case 8: launch<T, 8>(fwd, a, st); return true;
-    case 16: launch<T, 16>(fwd, a, st); return true;
+bool dispatch(int dhp, bool fwd, const LatentArgs& a, hipStream_t st) {
+  switch (dhp) {
     case 32: launch<T, 32>(fwd, a, st); return true;
     case 64: launch<T, 64>(fwd, a, st); return true;
+    case 96: launch<T, 96>(fwd, a, st); return true;
+    case 128: launch<T, 128>(fwd, a, st); return true;
     default: return false;
   }
 }
@@ -290,7 +360,10 @@ int32_t common(const llattn_shape* s, const llattn_tensor* rq, const llattn_tens
     return rc;
   *a = LatentArgs{};
   a->B = s->B; a->Lh = s->Lh; a->Ldh = s->Ldh; a->n_q = s->n_q; a->q_block = s->q_block;
-  a->chunk = s->chunk; a->n_chunks = s->n_chunks; a->n_tiles = (s->n_q + kQTile - 1) / kQTile;
+  a->chunk = s->chunk; a->n_chunks = s->n_chunks;
+  a->n_qt = (s->n_q + 63) / 64;
+  a->n_lt = (s->n_chunks + 15) / 16;
+  a->n_seg = (s->n_q + kSeg - 1) / kSeg;
   a->scale = 1.0f / sqrtf((float)s->Ldh);
   a->scale_log2 = a->scale * kLog2e;
   a->rq = rq->ptr; a->rq_sb = rq->sb; a->rq_sn = rq->sn; a->rq_sh = rq->sh;
@@ -300,6 +373,13 @@ int32_t common(const llattn_shape* s, const llattn_tensor* rq, const llattn_tens
 }
 
 }  // namespace
+
+size_t latent_workspace_bytes(const llattn_shape* s) {
+  auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
+  const size_t n_lt = (s->n_chunks + 15) / 16, n_seg = (s->n_q + kSeg - 1) / kSeg;
+  return up((size_t)s->B * s->Lh * s->n_q * 4) + up((size_t)s->B * s->Lh * n_seg * n_lt * 16 * 2 * s->Ldh * 4);
+}
+
 }  // namespace llattn
 
 using namespace llattn;
@@ -313,9 +393,9 @@ extern "C" int32_t llattn_latent_fwd(const llattn_shape* s, const llattn_tensor*
   if (!lse) return fail(LLATTN_ERR_LAYOUT, "lse output must be non-null");
   a.out = out->ptr; a.o_sb = out->sb; a.o_sn = out->sn; a.o_sh = out->sh;
   a.lse = lse;
-  const int ldp = padded_latent_dim(s->Ldh);
+  const int dhp = padded_head_dim(s->Ldh);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool ok = s->dtype == LLATTN_F32 ? dispatch<float>(ldp, true, a, st) : dispatch<uint16_t>(ldp, true, a, st);
+  const bool ok = s->dtype == LLATTN_F32 ? dispatch<float>(dhp, true, a, st) : dispatch<uint16_t>(dhp, true, a, st);
   if (!ok) return fail(LLATTN_ERR_UNSUPPORTED, "latent head_dim %d unsupported", s->Ldh);
   return check_launch("llattn_latent_fwd");
 }
@@ -339,10 +419,12 @@ extern "C" int32_t llattn_latent_bwd(const llattn_shape* s, const llattn_tensor*
   a.drq = drq->ptr; a.drq_sb = drq->sb; a.drq_sn = drq->sn; a.drq_sh = drq->sh;
   a.dgk = dgk->ptr; a.dgk_sb = dgk->sb; a.dgk_sn = dgk->sn; a.dgk_sh = dgk->sh;
   a.dgv = dgv->ptr; a.dgv_sb = dgv->sb; a.dgv_sn = dgv->sn; a.dgv_sh = dgv->sh;
-  a.part = static_cast<float*>(workspace);
-  const int ldp = padded_latent_dim(s->Ldh);
+  auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
+  a.Dsum = static_cast<float*>(workspace);
+  a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + up((size_t)s->B * s->Lh * s->n_q * 4));
+  const int dhp = padded_head_dim(s->Ldh);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool ok = s->dtype == LLATTN_F32 ? dispatch<float>(ldp, false, a, st) : dispatch<uint16_t>(ldp, false, a, st);
+  const bool ok = s->dtype == LLATTN_F32 ? dispatch<float>(dhp, false, a, st) : dispatch<uint16_t>(dhp, false, a, st);
   if (!ok) return fail(LLATTN_ERR_UNSUPPORTED, "latent head_dim %d unsupported", s->Ldh);
   return check_launch("llattn_latent_bwd");
 }

@@ -37,39 +37,8 @@ struct LocalArgs {
   void* dr; int64_t dr_sb, dr_st, dr_sh;
   void* dO;      // workspace [B][T][H][Dh], storage type
   float* Dsum;   // workspace [B][H][T]
-  float* gpart;  // workspace [B*H*n_qt][2][Dh]
+  float* gpart;  // workspace [H][2][Dh][B*n_qt]
 };
-
-template <typename T> constexpr int kRowPad = std::is_same_v<T, float> ? 4 : 8;
-constexpr int kTP = 68;  // pitch of transposed LDS tiles [dim][64 rows + 4]
-
-// Rows [r0, r0+64) of a head-row view (base at (b, h), row stride st) into LDS
-// row-major [64][P]; rows >= r_end and dims >= Dh are zero.
-template <typename T, int DHP, int P>
-__device__ __forceinline__ void stage_rows(T* lds, const T* base, int64_t st, int r0, int r_end, int Dh) {
-  constexpr int V = Vec16<T>::N, CPR = DHP / V;
-  for (int c = threadIdx.x; c < 64 * CPR; c += 256) {
-    const int row = c / CPR, col = (c % CPR) * V, rr = r0 + row;
-    uint4 x = make_uint4(0, 0, 0, 0);
-    if (rr < r_end && col < Dh) x = ld16(base + (int64_t)rr * st + col);
-    st16(lds + row * P + col, x);
-  }
-}
-// Same rows, stored transposed into LDS [DHP][kTP]; optionally also row-major.
-template <typename T, int DHP, int P, bool kRows>
-__device__ __forceinline__ void stage_rows_t(T* lds_rows, T* lds_t, const T* base, int64_t st, int r0, int r_end,
-                                             int Dh) {
-  constexpr int V = Vec16<T>::N, CPR = DHP / V;
-  for (int c = threadIdx.x; c < 64 * CPR; c += 256) {
-    const int row = c / CPR, col = (c % CPR) * V, rr = r0 + row;
-    uint4 x = make_uint4(0, 0, 0, 0);
-    if (rr < r_end && col < Dh) x = ld16(base + (int64_t)rr * st + col);
-    if constexpr (kRows) st16(lds_rows + row * P + col, x);
-    const T* e = reinterpret_cast<const T*>(&x);
-#pragma unroll
-    for (int j = 0; j < V; ++j) lds_t[(col + j) * kTP + row] = e[j];
-  }
-}
 
 // ----------------------------------------------------------------------------
 // forward: local attention + gate mix
@@ -116,30 +85,13 @@ __global__ __launch_bounds__(256) void local_fwd_kernel(const LocalArgs a) {
       RowFrag<T, DQ> kf;
       kf.load_lds(Ks + (16 * st + r) * KP, g);
       const f32x4 s = row_mma(kf, qf, f32x4{0.f, 0.f, 0.f, 0.f});  // S^T[key 4g+i][query r]
-      float sv[4], mloc = kNegInf;
+      bool ok[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = s0 + 4 * g + i;
-        sv[i] = (j >= lo && j <= hi) ? s[i] * a.scale_log2 : kNegInf;
-        mloc = fmaxf(mloc, sv[i]);
+        ok[i] = j >= lo && j <= hi;
       }
-      mloc = max_groups(mloc);
-      const float m_new = fmaxf(m_run, mloc);
-      const float mu = (m_new == kNegInf) ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run - mu);
-      float pv[4], ps = 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        pv[i] = fast_exp2(sv[i] - mu);
-        ps += pv[i];
-      }
-      l_run = l_run * alpha + ps;
-      m_run = m_new;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        acc[t] *= alpha;
-        acc[t] = col_mma(Vt + (16 * t + r) * kTP + 16 * st + 4 * g, pv, acc[t]);  // O^T[dim][query]
-      }
+      online_softmax_pv<NT>(s, ok, a.scale_log2, m_run, l_run, acc, Vt + r * kTP + 16 * st + 4 * g);
     }
   }
 
@@ -278,11 +230,14 @@ __global__ __launch_bounds__(256) void local_bwd_q_kernel(const LocalArgs a) {
   Dq = sum_groups(Dq);
   if (qv && g == 0) a.Dsum[hrow + qi] = Dq;
   __syncthreads();
-  for (int idx = tid; idx < 2 * DHP; idx += 256) {
-    const int which = idx / DHP, d = idx % DHP;
-    if (d < Dh) {
-      const float s = gsum[0][which][d] + gsum[1][which][d] + gsum[2][which][d] + gsum[3][which][d];
-      a.gpart[((((int64_t)b * a.H + h) * a.n_qt + qt) * 2 + which) * Dh + d] = s;
+  {
+    const int nrow = a.B * a.n_qt, row = b * a.n_qt + qt;
+    for (int idx = tid; idx < 2 * DHP; idx += 256) {
+      const int which = idx / DHP, d = idx % DHP;
+      if (d < Dh) {
+        const float s = gsum[0][which][d] + gsum[1][which][d] + gsum[2][which][d] + gsum[3][which][d];
+        a.gpart[(((int64_t)h * 2 + which) * Dh + d) * nrow + row] = s;
+      }
     }
   }
 
@@ -443,17 +398,20 @@ __global__ __launch_bounds__(256) void local_bwd_kv_kernel(const LocalArgs a) {
   }
 }
 
-// Ordered sum of the per-tile gate partials: dgate[h][d] = sum_{b, tile} part.
+// Ordered sum of the per-tile gate partials: dgate[h][d] = sum over (b, tile) of part[h][which][d][b*n_qt + tile].
+// One wave per output: lanes stride over the contiguous partials, then a fixed butterfly.
 __global__ __launch_bounds__(256) void gate_reduce_kernel(const float* __restrict__ part, float* dgl, float* dgr,
-                                                          int B, int H, int n_qt, int Dh) {
-  const int h = blockIdx.x;
-  for (int idx = threadIdx.x; idx < 2 * Dh; idx += 256) {
-    const int which = idx / Dh, d = idx % Dh;
-    float s = 0.f;
-    for (int b = 0; b < B; ++b) {
-      const float* p = part + (((int64_t)b * H + h) * n_qt * 2 + which) * Dh + d;
-      for (int t = 0; t < n_qt; ++t) s += p[(int64_t)t * 2 * Dh];
-    }
+                                                          int H, int Dh, int nrow) {
+  const int lane = threadIdx.x & 63;
+  const int o = blockIdx.x * 4 + (threadIdx.x >> 6);  // over H * 2 * Dh
+  if (o >= H * 2 * Dh) return;                         // whole waves exit; no barrier follows
+  const float* p = part + (int64_t)o * nrow;
+  float s = 0.f;
+  for (int i = lane; i < nrow; i += 64) s += p[i];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+  if (lane == 0) {
+    const int h = o / (2 * Dh), which = (o / Dh) % 2, d = o % Dh;
     (which == 0 ? dgl : dgr)[h * Dh + d] = s;
   }
 }
@@ -583,7 +541,7 @@ extern "C" int32_t llattn_local_gate_bwd(const llattn_shape* s, const llattn_ten
   const bool ok =
       s->dtype == LLATTN_F32 ? dispatch<float>(dhp, false, a, st) : dispatch<uint16_t>(dhp, false, a, st);
   if (!ok) return fail(LLATTN_ERR_UNSUPPORTED, "head_dim %d unsupported", s->Dh);
-  hipLaunchKernelGGL(gate_reduce_kernel, dim3(s->H), dim3(256), 0, st, a.gpart, dgate_l, dgate_r, s->B, s->H, a.n_qt,
-                     s->Dh);
+  hipLaunchKernelGGL(gate_reduce_kernel, dim3((s->H * 2 * s->Dh + 3) / 4), dim3(256), 0, st, a.gpart, dgate_l, dgate_r,
+                     s->H, s->Dh, s->B * a.n_qt);
   return check_launch("llattn_local_gate_bwd");
 }

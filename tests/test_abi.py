@@ -50,7 +50,8 @@ def test_workspace_sizes():
     # dO (bf16) + row sums + gate partials, each rounded up to 256 bytes
     up = lambda x: (x + 255) // 256 * 256  # noqa: E731
     assert n_local == up(2 * 97 * 2 * 32 * 2) + up(2 * 2 * 97 * 4) + up(2 * 2 * 2 * 2 * 32 * 4)
-    assert lib.llattn_workspace_size(ctypes.byref(s), L.WS_LATENT_BWD) == up(2 * 2 * 1 * 6 * 2 * 8 * 4)
+    # D per latent query + per-segment partials of 16-latent tiles (one segment of 512 queries here)
+    assert lib.llattn_workspace_size(ctypes.byref(s), L.WS_LATENT_BWD) == up(2 * 2 * 97 * 4) + up(2 * 2 * 1 * 16 * 2 * 8 * 4)
     assert lib.llattn_workspace_size(ctypes.byref(s), 7) == 0
     assert b"unknown workspace kind" in lib.llattn_last_error()
 
@@ -61,7 +62,7 @@ def test_workspace_sizes():
     ("dtype", 5, 2, b"unknown dtype"),
     ("Dh", 20, 4, b"head_dim 20 unsupported"),
     ("Dh", 160, 4, b"head_dim 160 unsupported"),
-    ("Ldh", 128, 4, b"latent head_dim 128 unsupported"),
+    ("Ldh", 136, 4, b"latent head_dim 136 unsupported"),
     ("chunk", 5, 1, b"does not tile"),
     ("n_q", 50, 1, b"does not tile"),
     ("block", 98, 1, b"local block size"),

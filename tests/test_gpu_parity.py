@@ -152,6 +152,9 @@ OP_CASES = [
     (2, 150, 2, 32, 2, 32, 40, 64, 10, 16),
     (1, 61, 4, 16, 2, 8, 20, 16, 9, 10),
     (1, 300, 1, 96, 2, 32, 300, 300, 1, 0),
+    (1, 140, 2, 32, 1, 128, 20, 32, 2, 0),      # latent head dim 128, 70 latents (two latent tiles)
+    (1, 1100, 1, 32, 1, 16, 16, 64, 8, 0),      # 3 query segments x 9 latent tiles in the latent backward
+    (2, 700, 2, 64, 2, 32, 48, 128, 7, 9),      # macro-block queries over several query tiles
 ]
 
 
@@ -272,3 +275,39 @@ def test_c2_deterministic_and_finite():
     for n in a[2]:
         assert np.isfinite(a[2][n]).all(), n
         np.testing.assert_array_equal(a[2][n], b[2][n], err_msg=n)
+
+
+def _config_row_check(cfg_name, rows):
+    """Full-size BASELINE config on the GPU (bf16 autocast); rows of the batch vs the fp32 CPU reference."""
+    from oracle import torch_ref
+    dev = require_cuda()
+    B, T, D, H, W, lbs, ntok, Ld, Lh, qbs = {
+        "c3": (2, 16384, 1024, 16, 512, 256, 256, 64, 2, 0),
+        "c4": (4, 8192, 1024, 16, 256, 256, 128, 64, 2, 64)}[cfg_name]
+    shape = orc.BlockShape(d_model=D, n_heads=H, window=W, local_block_size=lbs, latent_tokens=ntok,
+                           latent_d_model=Ld, latent_heads=Lh, latent_query_block_size=qbs)
+    torch.manual_seed(3)
+    m = build_module(shape, None, dev)
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            p.normal_(0.0, 0.02) if name.endswith("weight") else p.normal_(0.0, 0.02)
+    x = torch.randn(B, T, D, device=dev).to(torch.bfloat16)
+    dout = torch.randn(B, T, D, device=dev)
+    _print_case(cfg_name, "full batch")
+    out, dx, grads = run_module(m, x, dout, autocast_bf16=True)
+    params = {n: p.detach().float().cpu() for n, p in m.named_parameters()}
+    for b in rows:
+        _print_case(cfg_name, "reference row", b)
+        o_ref, dx_ref, g_ref = torch_ref.block_forward_backward(params, x[b:b + 1].float().cpu(),
+                                                                dout[b:b + 1].float().cpu(), shape)
+        assert_bf16_close(out[b:b + 1], o_ref.numpy(), f"out[{b}]")
+        assert_bf16_close(dx[b:b + 1], dx_ref.numpy(), f"dx[{b}]")
+    return m, x, dout, params, shape
+
+
+def test_c3_long_context_rows_match_fp32_reference():
+    _config_row_check("c3", rows=(0, 1))
+
+
+def test_c4_macro_block_rows_match_fp32_reference():
+    _config_row_check("c4", rows=(0, 3))
