@@ -154,14 +154,15 @@ def cpu_baseline(cfg, budget_s: float):
                       f"torch CPU restatement of the reference PyTorch path, {el:.1f} s"}
 
 
-def read_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary, if present."""
+def read_traffic(config: str, kernel: str):
+    """HBM bytes per call of the entry point `kernel` at `config`, as measured by the rocprofv3 --pmc
+    FETCH_SIZE / WRITE_SIZE runs summarised in profiles/ (scaled by a plain copy), or None."""
     f = REPO / "profiles" / "pmc_traffic.json"
     if not f.exists():
         return None
     try:
-        return json.loads(f.read_text()).get(kernel)
-    except (ValueError, OSError):
+        return json.loads(f.read_text()).get(config, {}).get(kernel)
+    except (ValueError, OSError, AttributeError):
         return None
 
 
@@ -173,6 +174,9 @@ def main():
     ap.add_argument("--config", choices=sorted(CONFIGS), default="c2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run 3 plain device copies of MIB MiB each (scale factor for rocprofv3 FETCH_SIZE / "
+                         "WRITE_SIZE counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -182,6 +186,16 @@ def main():
 
     import torch
     from llattn_amd import ops as llops
+
+    if args.calibrate_copy:
+        n = args.calibrate_copy << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": n}), flush=True)
+        return
 
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda:0")
@@ -228,7 +242,7 @@ def main():
         kstats[name] = st
     dom = max((n for n in kstats if n in kb), key=lambda n: kstats[n]["avg_ms"] * kstats[n]["launches_per_step"])
     dom_ach = kstats[dom]["achieved_GBs"]
-    traffic = read_traffic(dom)
+    traffic = read_traffic(args.config, dom)
     for n, st in sorted(kstats.items(), key=lambda kv: -kv[1]["avg_ms"]):
         log(f"  {n:28s} {st}")
     log(f"step {ms:.3f} ms, HIP entry points {sum(s['avg_ms'] * s['launches_per_step'] for s in kstats.values()):.3f} ms")
