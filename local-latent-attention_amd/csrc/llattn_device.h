@@ -79,6 +79,27 @@ __device__ __forceinline__ void store4(T* p, const float v[4]) {
     *reinterpret_cast<uint2*>(p) = x;
   }
 }
+// 4 consecutive elements held as stored (8 bytes of bf16 / 16 bytes of fp32)
+// so a prefetched row costs half the registers in bf16; zero when !valid.
+template <typename T> struct Raw4;
+template <> struct Raw4<float> {
+  float4 v;
+  __device__ __forceinline__ void load(const float* p, bool valid) {
+    v = valid ? *reinterpret_cast<const float4*>(p) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  __device__ __forceinline__ void get(float o[4]) const { o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w; }
+};
+template <> struct Raw4<uint16_t> {
+  uint2 v;
+  __device__ __forceinline__ void load(const uint16_t* p, bool valid) {
+    v = valid ? *reinterpret_cast<const uint2*>(p) : make_uint2(0u, 0u);
+  }
+  __device__ __forceinline__ void get(float o[4]) const {
+    o[0] = __uint_as_float(v.x << 16); o[1] = __uint_as_float(v.x & 0xffff0000u);
+    o[2] = __uint_as_float(v.y << 16); o[3] = __uint_as_float(v.y & 0xffff0000u);
+  }
+};
+
 // ---- 16-byte copies (global <-> LDS) -----------------------------------------
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ void st16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
@@ -196,6 +217,143 @@ __device__ __forceinline__ void stage_rows(T* lds, const T* base, int64_t st, in
     st16(lds + row * P + col, x);
   }
 }
+
+// ---- col products with A read from a row-major LDS tile ------------------------
+// base = &tile[k0][m0] of a row-major tile with pitch P: A[m][k] = tile[k0 + k][m0 + m].
+// bf16: one ds_read_b64_tr_b16 gives lane (r, g) the four elements
+// tile[k0 + 4g + i][m0 + r], i = 0..3 (within each 16-lane group, lane j
+// supplies the address of row 4g + j/4, columns 4(j%4) .. 4(j%4)+3).
+template <int P>
+__device__ __forceinline__ f32x4 col_mma_rm(const uint16_t* base, const float b[4], f32x4 acc) {
+  typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const uint16_t* p = base + (4 * g + (j >> 2)) * P + 4 * (j & 3);
+  const bf16x4 av = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)(p));
+  i16x4 bv;
+  bv[0] = static_cast<short>(f2bf(b[0]));
+  bv[1] = static_cast<short>(f2bf(b[1]));
+  bv[2] = static_cast<short>(f2bf(b[2]));
+  bv[3] = static_cast<short>(f2bf(b[3]));
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, av), bv, acc, 0, 0, 0);
+}
+// fp32: four scalar LDS reads tile[k0 + 4g + i][m0 + r]; step i contracts k = 4g + i.
+template <int P>
+__device__ __forceinline__ f32x4 col_mma_rm(const float* base, const float b[4], f32x4 acc) {
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const float* p = base + (4 * g) * P + r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p[i * P], b[i], acc, 0, 0, 0);
+  return acc;
+}
+
+// ---- register-staged 64-row tiles ---------------------------------------------
+// A tile is copied global -> registers -> LDS in two steps so that every global
+// load of the tile is in flight at once (and the next tile's loads can overlap
+// the current tile's MFMA work): load() issues the loads, store*() writes LDS.
+//
+// RowTile: row-major [64][P] copy; consecutive threads take consecutive 16-byte
+// chunks of a row (coalesced reads).  Rows >= r_end and dims >= Dh are zero.
+template <typename T, int DHP>
+struct RowTile {
+  static constexpr int V = Vec16<T>::N, CPR = DHP / V, TASKS = 64 * CPR, IT = (TASKS + 255) / 256;
+  uint4 x[IT];
+  __device__ __forceinline__ void load(const T* base, int64_t st, int r0, int r_end, int Dh) {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int task = threadIdx.x + 256 * it, row = task / CPR, col = (task % CPR) * V, rr = r0 + row;
+      x[it] = make_uint4(0, 0, 0, 0);
+      if (task < TASKS && rr < r_end && col < Dh) x[it] = ld16(base + (int64_t)rr * st + col);
+    }
+  }
+  // rows (r0 + i) / div of the view (one row per latent query in macro-block
+  // mode); tile rows with r0 + i >= r_end are zero
+  __device__ __forceinline__ void load_div(const T* base, int64_t st, int r0, int r_end, int div, int Dh) {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int task = threadIdx.x + 256 * it, row = task / CPR, col = (task % CPR) * V, rr = r0 + row;
+      x[it] = make_uint4(0, 0, 0, 0);
+      if (task < TASKS && rr < r_end && col < Dh) x[it] = ld16(base + (int64_t)(rr / div) * st + col);
+    }
+  }
+  template <int P>
+  __device__ __forceinline__ void store(T* lds) const {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int task = threadIdx.x + 256 * it, row = task / CPR, col = (task % CPR) * V;
+      if (task < TASKS) st16(lds + row * P + col, x[it]);
+    }
+  }
+};
+
+// Coalesced copy of a row-major 64-row LDS tile (pitch P) to global rows
+// r0 + i (row stride st) for r0 + i < r_end and dims < Dh.
+template <typename T, int DHP, int P>
+__device__ __forceinline__ void store_tile(T* base, int64_t st, const T* lds, int r0, int r_end, int Dh) {
+  constexpr int V = Vec16<T>::N, CPR = DHP / V, TASKS = 64 * CPR, IT = (TASKS + 255) / 256;
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int task = threadIdx.x + 256 * it, row = task / CPR, col = (task % CPR) * V, rr = r0 + row;
+    if (task < TASKS && rr < r_end && col < Dh) st16(base + (int64_t)rr * st + col, ld16(lds + row * P + col));
+  }
+}
+
+// TransTile: the rows stored transposed into LDS [DHP][kTP] (row index
+// contiguous), and optionally row-major too.  The row index varies fastest
+// across threads so the transposed writes are whole dwords without bank
+// conflicts: a bf16 thread holds a pair of rows and packs the two rows'
+// elements of one dim into a dword.
+template <typename T, int DHP>
+struct TransTile {
+  static constexpr bool kF32 = std::is_same_v<T, float>;
+  static constexpr int V = Vec16<T>::N, CPR = DHP / V, RPT = kF32 ? 1 : 2, NR = 64 / RPT;
+  static constexpr int TASKS = NR * CPR, IT = (TASKS + 255) / 256;
+  uint4 x[IT][RPT];
+  __device__ __forceinline__ void load(const T* base, int64_t st, int r0, int r_end, int Dh) {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int task = threadIdx.x + 256 * it, row = RPT * (task % NR), col = (task / NR) * V, rr = r0 + row;
+#pragma unroll
+      for (int j = 0; j < RPT; ++j) {
+        x[it][j] = make_uint4(0, 0, 0, 0);
+        if (task < TASKS && col < Dh && rr + j < r_end) x[it][j] = ld16(base + (int64_t)(rr + j) * st + col);
+      }
+    }
+  }
+  template <int P>
+  __device__ __forceinline__ void store_rows(T* lds) const {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int task = threadIdx.x + 256 * it, row = RPT * (task % NR), col = (task / NR) * V;
+      if (task < TASKS) {
+#pragma unroll
+        for (int j = 0; j < RPT; ++j) st16(lds + (row + j) * P + col, x[it][j]);
+      }
+    }
+  }
+  __device__ __forceinline__ void store_t(T* lds_t) const {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int task = threadIdx.x + 256 * it, row = RPT * (task % NR), col = (task / NR) * V;
+      if (task >= TASKS) continue;
+      if constexpr (kF32) {
+        const uint4 v = x[it][0];
+        lds_t[(col + 0) * kTP + row] = __uint_as_float(v.x);
+        lds_t[(col + 1) * kTP + row] = __uint_as_float(v.y);
+        lds_t[(col + 2) * kTP + row] = __uint_as_float(v.z);
+        lds_t[(col + 3) * kTP + row] = __uint_as_float(v.w);
+      } else {
+        const uint4 x0 = x[it][0], x1 = x[it][1];
+        const uint32_t a[4] = {x0.x, x0.y, x0.z, x0.w}, b[4] = {x1.x, x1.y, x1.z, x1.w};
+        uint32_t* dst = reinterpret_cast<uint32_t*>(lds_t + col * kTP + row);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          dst[(2 * j) * (kTP / 2)] = (a[j] & 0xffffu) | (b[j] << 16);
+          dst[(2 * j + 1) * (kTP / 2)] = (a[j] >> 16) | (b[j] & 0xffff0000u);
+        }
+      }
+    }
+  }
+};
 
 // The same rows stored transposed into LDS [DHP][kTP] (row index contiguous),
 // and row-major into lds_rows as well when kRows.  Writes are whole dwords

@@ -42,111 +42,144 @@ struct LocalArgs {
 
 // ----------------------------------------------------------------------------
 // forward: local attention + gate mix
+//
+// Every global access is a coalesced copy of whole head rows (16-byte chunks,
+// consecutive lanes on consecutive chunks of a row) between HBM and a
+// row-major LDS tile; MFMA operands are read from the tiles: row operands with
+// ds_read_b128, column operands (V^T) with the transposing LDS read.
 // ----------------------------------------------------------------------------
 template <typename T, int DHP>
 __global__ __launch_bounds__(256) void local_fwd_kernel(const LocalArgs a) {
   constexpr int DQ = DHP / 4, NT = DHP / 16, KP = DHP + kRowPad<T>;
-  __shared__ __align__(16) T Ks[64 * KP];
-  __shared__ __align__(16) T Vt[DHP * kTP];
+  __shared__ __align__(16) T S0[64 * KP];  // query rows -> value rows -> remote rows -> y
+  __shared__ __align__(16) T S1[64 * KP];  // key rows -> o_local
+  __shared__ __align__(16) float gls[DHP], grs[DHP];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, g = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane & 15, g = lane >> 4;
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
   const int qt = bid % a.n_qt, bh = bid / a.n_qt, h = bh % a.H, b = bh / a.H;
-  const int T_ = a.T;
-  const int q0 = qt * 64, qw = q0 + wave * 16, qi = qw + r;
+  const int T_ = a.T, Dh = a.Dh;
+  const int q0 = qt * 64, qw = q0 + wave * 16, qi = qw + r, row = wave * 16 + r;
   const bool qv = qi < T_;
 
   const T* qbase = static_cast<const T*>(a.q) + b * a.q_sb + h * a.q_sh;
   const T* kbase = static_cast<const T*>(a.k) + b * a.k_sb + h * a.k_sh;
   const T* vbase = static_cast<const T*>(a.v) + b * a.v_sb + h * a.v_sh;
+  const T* rbase = static_cast<const T*>(a.rem) + b * a.r_sb + h * a.r_sh;
 
+  // every global read of the workgroup is issued before its first barrier
+  const int kbeg = max(0, q0 - a.W);
+  const int kend = min(T_, q0 + 64) - 1;  // exclusive
+  const int qend = min(T_, q0 + 64);
+  RowTile<T, DHP> qreg, kreg, vreg, rreg;
+  qreg.load(qbase, a.q_st, q0, qend, Dh);
+  kreg.load(kbase, a.k_st, kbeg, kend, Dh);
+  vreg.load(vbase, a.v_st, kbeg, kend, Dh);
+  rreg.load_div(rbase, a.r_sn, q0, qend, a.q_block, Dh);
+  for (int d = tid; d < DHP; d += 256) {
+    gls[d] = d < Dh ? a.gl[h * a.gate_hs + d] : 0.f;
+    grs[d] = d < Dh ? a.gr[h * a.gate_hs + d] : 0.f;
+  }
+  qreg.template store<KP>(S0);
+  kreg.template store<KP>(S1);
+  __syncthreads();
   RowFrag<T, DQ> qf;
-  qf.load(qbase + (int64_t)qi * a.q_st, g, a.Dh, qv);
+  qf.load_lds(S0 + row * KP, g);
+
   const int lo = qv ? key_lo(qi, a.W, a.bs) : INT_MAX;
   const int hi = qi - 1;
-
   float m_run = kNegInf, l_run = 0.f;
   f32x4 acc[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int kbeg = max(0, q0 - a.W);
-  const int kend = min(T_, q0 + 64) - 1;                     // exclusive
   const int wlo = max(0, qw - a.W), whi = min(qw + 15, T_ - 1) - 1;  // keys any query of this wave may use
   for (int k0 = kbeg; k0 < kend; k0 += 64) {
+    __syncthreads();  // S0 (queries / previous values) and S1 (previous keys) are free
+    vreg.template store<KP>(S0);
+    if (k0 != kbeg) kreg.template store<KP>(S1);
     __syncthreads();
-    stage_rows<T, DHP, KP>(Ks, kbase, a.k_st, k0, kend, a.Dh);
-    stage_rows_t<T, DHP, KP, false>(nullptr, Vt, vbase, a.v_st, k0, kend, a.Dh);
-    __syncthreads();
+    if (k0 + 64 < kend) {  // the next tile's loads overlap this tile's math
+      kreg.load(kbase, a.k_st, k0 + 64, kend, Dh);
+      vreg.load(vbase, a.v_st, k0 + 64, kend, Dh);
+    }
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const int s0 = k0 + 16 * st;
       if (s0 >= kend || s0 + 15 < wlo || s0 > whi) continue;  // uniform over the wave
       RowFrag<T, DQ> kf;
-      kf.load_lds(Ks + (16 * st + r) * KP, g);
+      kf.load_lds(S1 + (16 * st + r) * KP, g);
       const f32x4 s = row_mma(kf, qf, f32x4{0.f, 0.f, 0.f, 0.f});  // S^T[key 4g+i][query r]
-      bool ok[4];
+      float sv[4], mloc = kNegInf;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = s0 + 4 * g + i;
-        ok[i] = j >= lo && j <= hi;
+        sv[i] = (j >= lo && j <= hi) ? s[i] * a.scale_log2 : kNegInf;
+        mloc = fmaxf(mloc, sv[i]);
       }
-      online_softmax_pv<NT>(s, ok, a.scale_log2, m_run, l_run, acc, Vt + r * kTP + 16 * st + 4 * g);
+      mloc = max_groups(mloc);
+      const float m_new = fmaxf(m_run, mloc);
+      const float mu = (m_new == kNegInf) ? 0.f : m_new;
+      const float alpha = fast_exp2(m_run - mu);
+      float pv[4], ps = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pv[i] = fast_exp2(sv[i] - mu);
+        ps += pv[i];
+      }
+      l_run = l_run * alpha + ps;
+      m_run = m_new;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {  // O^T += V^T P^T, V^T read transposed from the value rows
+        acc[t] *= alpha;
+        acc[t] = col_mma_rm<KP>(S0 + (16 * st) * KP + 16 * t, pv, acc[t]);
+      }
     }
   }
+  __syncthreads();  // S0 / S1 free
+  rreg.template store<KP>(S0);
+  __syncthreads();
 
-  // ---- epilogue: normalise, gate, store ----
+  // ---- epilogue: normalise, gate, mix; rows go back through LDS ----
   const float l = sum_groups(l_run);
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  const float* glp = a.gl + h * a.gate_hs;
-  const float* grp = a.gr + h * a.gate_hs;
-  const int rrow = qv ? qi / a.q_block : 0;
-  const T* rp = static_cast<const T*>(a.rem) + b * a.r_sb + h * a.r_sh + (int64_t)rrow * a.r_sn;
   float o[NT][4], rv[NT][4];
   float sl = 0.f, sr = 0.f;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const int d = 16 * t + 4 * g;
-    const bool dok = qv && d < a.Dh;
-    float gl4[4] = {0.f, 0.f, 0.f, 0.f}, gr4[4] = {0.f, 0.f, 0.f, 0.f};
+    Raw4<T> rr4;
+    rr4.load(S0 + row * KP + d, true);
+    rr4.get(rv[t]);
+    const float4 gl4 = *reinterpret_cast<const float4*>(gls + d);
+    const float4 gr4 = *reinterpret_cast<const float4*>(grs + d);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) { o[t][i] = round_t<T>(acc[t][i] * inv); rv[t][i] = 0.f; }
-    if (dok) {
-      load4<T>(rp + d, rv[t]);
-      load4<float>(glp + d, gl4);
-      load4<float>(grp + d, gr4);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      sl += o[t][i] * gl4[i];
-      sr += rv[t][i] * gr4[i];
-    }
+    for (int i = 0; i < 4; ++i) o[t][i] = round_t<T>(acc[t][i] * inv);
+    sl += o[t][0] * gl4.x + o[t][1] * gl4.y + o[t][2] * gl4.z + o[t][3] * gl4.w;
+    sr += rv[t][0] * gr4.x + rv[t][1] * gr4.y + rv[t][2] * gr4.z + rv[t][3] * gr4.w;
   }
   sl = sum_groups(sl);
   sr = sum_groups(sr);
   const float mm = fmaxf(sl, sr);
   const float el = __expf(sl - mm), er = __expf(sr - mm);
   const float wl = el / (el + er), wr = er / (el + er);
-  if (qv) {
-    T* yp = static_cast<T*>(a.y) + b * a.y_sb + h * a.y_sh + (int64_t)qi * a.y_st;
-    T* op = static_cast<T*>(a.ol) + b * a.o_sb + h * a.o_sh + (int64_t)qi * a.o_st;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int d = 16 * t + 4 * g;
-      if (d < a.Dh) {
-        float yv[4];
+  for (int t = 0; t < NT; ++t) {  // each lane overwrites exactly the remote elements it read
+    const int d = 16 * t + 4 * g;
+    float yv[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) yv[i] = wl * o[t][i] + wr * rv[t][i];
-        store4<T>(yp + d, yv);
-        store4<T>(op + d, o[t]);
-      }
-    }
-    if (g == 0) {
-      const int64_t idx = ((int64_t)b * a.H + h) * T_ + qi;
-      a.lse[idx] = l > 0.f ? (m_run + __log2f(l)) * kLn2 : kNegInf;
-      a.w[idx] = wl;
-    }
+    for (int i = 0; i < 4; ++i) yv[i] = wl * o[t][i] + wr * rv[t][i];
+    store4<T>(S0 + row * KP + d, yv);
+    store4<T>(S1 + row * KP + d, o[t]);
   }
+  if (qv && g == 0) {
+    const int64_t idx = ((int64_t)b * a.H + h) * T_ + qi;
+    a.lse[idx] = l > 0.f ? (m_run + __log2f(l)) * kLn2 : kNegInf;
+    a.w[idx] = wl;
+  }
+  __syncthreads();
+  store_tile<T, DHP, KP>(static_cast<T*>(a.y) + b * a.y_sb + h * a.y_sh, a.y_st, S0, q0, qend, Dh);
+  store_tile<T, DHP, KP>(static_cast<T*>(a.ol) + b * a.o_sb + h * a.o_sh, a.o_st, S1, q0, qend, Dh);
 }
 
 // ----------------------------------------------------------------------------
@@ -156,66 +189,70 @@ __global__ __launch_bounds__(256) void local_fwd_kernel(const LocalArgs a) {
 template <typename T, int DHP>
 __global__ __launch_bounds__(256) void local_bwd_q_kernel(const LocalArgs a) {
   constexpr int DQ = DHP / 4, NT = DHP / 16, KP = DHP + kRowPad<T>;
-  __shared__ __align__(16) T Ks[64 * KP];
-  __shared__ __align__(16) T Kt[DHP * kTP];
-  __shared__ __align__(16) T Vs[64 * KP];
-  __shared__ __align__(16) T Ds[64 * KP];
+  __shared__ __align__(16) T S0[64 * KP];  // dy -> dO_local (kept: dO rows)            | loop: key rows
+  __shared__ __align__(16) T S1[64 * KP];  // o_local -> query rows                       | loop: value rows
+  __shared__ __align__(16) T S2[64 * KP];  // remote -> dremote                           | epilogue: dq
   __shared__ float gsum[4][2][DHP];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane & 15, g = lane >> 4;
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
   const int qt = bid % a.n_qt, bh = bid / a.n_qt, h = bh % a.H, b = bh / a.H;
   const int T_ = a.T, Dh = a.Dh;
-  const int q0 = qt * 64, qw = q0 + wave * 16, qi = qw + r;
+  const int q0 = qt * 64, qw = q0 + wave * 16, qi = qw + r, row = wave * 16 + r;
   const bool qv = qi < T_;
+  const int qend = min(T_, q0 + 64);
   const int64_t hrow = ((int64_t)b * a.H + h) * T_;
+  const T* qbase = static_cast<const T*>(a.q) + b * a.q_sb + h * a.q_sh;
+  const T* kbase = static_cast<const T*>(a.k) + b * a.k_sb + h * a.k_sh;
+  const T* vbase = static_cast<const T*>(a.v) + b * a.v_sb + h * a.v_sh;
 
-  // ---- phase 1: gate backward in the accumulator layout (dims 16t+4g+i) ----
+  // ---- phase 1: gate backward, in the accumulator layout (dims 16t+4g+i) ----
+  RowTile<T, DHP> dyreg, olreg, rreg, qreg;
+  dyreg.load(static_cast<const T*>(a.dy) + b * a.dy_sb + h * a.dy_sh, a.dy_st, q0, qend, Dh);
+  olreg.load(static_cast<const T*>(a.ol) + b * a.o_sb + h * a.o_sh, a.o_st, q0, qend, Dh);
+  rreg.load_div(static_cast<const T*>(a.rem) + b * a.r_sb + h * a.r_sh, a.r_sn, q0, qend, a.q_block, Dh);
+  qreg.load(qbase, a.q_st, q0, qend, Dh);
   const float wq = qv ? a.w[hrow + qi] : 0.f;
-  const T* dyp = static_cast<const T*>(a.dy) + b * a.dy_sb + h * a.dy_sh + (int64_t)qi * a.dy_st;
-  const T* olp = static_cast<const T*>(a.ol) + b * a.o_sb + h * a.o_sh + (int64_t)qi * a.o_st;
-  const int rrow = qv ? qi / a.q_block : 0;
-  const T* rp = static_cast<const T*>(a.rem) + b * a.r_sb + h * a.r_sh + (int64_t)rrow * a.r_sn;
+  const float lse_nat = qv ? a.lse[hrow + qi] : kNegInf;
+  dyreg.template store<KP>(S0);
+  olreg.template store<KP>(S1);
+  rreg.template store<KP>(S2);
+  __syncthreads();
+
   const float* glp = a.gl + h * a.gate_hs;
   const float* grp = a.gr + h * a.gate_hs;
-  float dyv[NT][4], olv[NT][4], rv[NT][4], gl4[NT][4], gr4[NT][4];
+  float dyv[NT][4], olv[NT][4], rv[NT][4];
   float dot1 = 0.f;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const int d = 16 * t + 4 * g;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dyv[t][i] = olv[t][i] = rv[t][i] = gl4[t][i] = gr4[t][i] = 0.f;
-    if (qv && d < Dh) {
-      load4<T>(dyp + d, dyv[t]);
-      load4<T>(olp + d, olv[t]);
-      load4<T>(rp + d, rv[t]);
-      load4<float>(glp + d, gl4[t]);
-      load4<float>(grp + d, gr4[t]);
-    }
+    Raw4<T> x;
+    x.load(S0 + row * KP + d, true); x.get(dyv[t]);
+    x.load(S1 + row * KP + d, true); x.get(olv[t]);
+    x.load(S2 + row * KP + d, true); x.get(rv[t]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) dot1 += dyv[t][i] * (olv[t][i] - rv[t][i]);
   }
   dot1 = sum_groups(dot1);
   const float delta = wq * (1.f - wq) * dot1;
   float Dq = 0.f;
-  T* drp = static_cast<T*>(a.dr) + b * a.dr_sb + h * a.dr_sh + (int64_t)qi * a.dr_st;
-  T* dop = static_cast<T*>(a.dO) + (((int64_t)b * T_ + qi) * a.H + h) * Dh;
-  T* dsrow = Ds + (wave * 16 + r) * KP;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const int d = 16 * t + 4 * g;
+    float gl4[4] = {0.f, 0.f, 0.f, 0.f}, gr4[4] = {0.f, 0.f, 0.f, 0.f};
+    if (d < Dh) {
+      load4<float>(glp + d, gl4);
+      load4<float>(grp + d, gr4);
+    }
     float dov[4], drv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      dov[i] = round_t<T>(wq * dyv[t][i] + delta * gl4[t][i]);
-      drv[i] = (1.f - wq) * dyv[t][i] - delta * gr4[t][i];
+      dov[i] = round_t<T>(wq * dyv[t][i] + delta * gl4[i]);
+      drv[i] = (1.f - wq) * dyv[t][i] - delta * gr4[i];
       Dq += dov[i] * olv[t][i];
     }
-    store4<T>(dsrow + d, dov);  // zero beyond Dh (all inputs were zero there)
-    if (qv && d < Dh) {
-      store4<T>(drp + d, drv);
-      store4<T>(dop + d, dov);
-    }
+    store4<T>(S0 + row * KP + d, dov);  // in place over the dy elements this lane read
+    store4<T>(S2 + row * KP + d, drv);  // in place over the remote elements
     // gate partial sums over the 16 queries of this wave
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -229,47 +266,56 @@ __global__ __launch_bounds__(256) void local_bwd_q_kernel(const LocalArgs a) {
   }
   Dq = sum_groups(Dq);
   if (qv && g == 0) a.Dsum[hrow + qi] = Dq;
-  __syncthreads();
+  __syncthreads();  // dO / dremote tiles complete; o_local no longer needed
+  qreg.template store<KP>(S1);
+  store_tile<T, DHP, KP>(static_cast<T*>(a.dO) + ((int64_t)b * T_ * a.H + h) * Dh, (int64_t)a.H * Dh, S0, q0, qend,
+                         Dh);
+  store_tile<T, DHP, KP>(static_cast<T*>(a.dr) + b * a.dr_sb + h * a.dr_sh, a.dr_st, S2, q0, qend, Dh);
   {
-    const int nrow = a.B * a.n_qt, row = b * a.n_qt + qt;
+    const int nrow = a.B * a.n_qt, prow = b * a.n_qt + qt;
     for (int idx = tid; idx < 2 * DHP; idx += 256) {
       const int which = idx / DHP, d = idx % DHP;
       if (d < Dh) {
-        const float s = gsum[0][which][d] + gsum[1][which][d] + gsum[2][which][d] + gsum[3][which][d];
-        a.gpart[(((int64_t)h * 2 + which) * Dh + d) * nrow + row] = s;
+        const float sum = gsum[0][which][d] + gsum[1][which][d] + gsum[2][which][d] + gsum[3][which][d];
+        a.gpart[(((int64_t)h * 2 + which) * Dh + d) * nrow + prow] = sum;
       }
     }
   }
+  // first key / value tile in flight while the fragments are read
+  const int kbeg = max(0, q0 - a.W);
+  const int kend = min(T_, q0 + 64) - 1;
+  RowTile<T, DHP> kreg, vreg;
+  kreg.load(kbase, a.k_st, kbeg, kend, Dh);
+  vreg.load(vbase, a.v_st, kbeg, kend, Dh);
+  __syncthreads();
+  RowFrag<T, DQ> qf, dof;
+  qf.load_lds(S1 + row * KP, g);
+  dof.load_lds(S0 + row * KP, g);
 
   // ---- phase 2: dQ = scale * sum_j dS_ij k_j ----
-  const T* qbase = static_cast<const T*>(a.q) + b * a.q_sb + h * a.q_sh;
-  const T* kbase = static_cast<const T*>(a.k) + b * a.k_sb + h * a.k_sh;
-  const T* vbase = static_cast<const T*>(a.v) + b * a.v_sb + h * a.v_sh;
-  RowFrag<T, DQ> qf, dof;
-  qf.load(qbase + (int64_t)qi * a.q_st, g, Dh, qv);
-  dof.load_lds(dsrow, g);  // same wave wrote it; the barrier above orders it
-  const float lse_nat = qv ? a.lse[hrow + qi] : kNegInf;
   const float lse2 = (lse_nat == kNegInf) ? 0.f : lse_nat * kLog2e;
   const int lo = qv ? key_lo(qi, a.W, a.bs) : INT_MAX;
   const int hi = qi - 1;
   f32x4 acc[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int kbeg = max(0, q0 - a.W);
-  const int kend = min(T_, q0 + 64) - 1;
   const int wlo = max(0, qw - a.W), whi = min(qw + 15, T_ - 1) - 1;
   for (int k0 = kbeg; k0 < kend; k0 += 64) {
+    __syncthreads();  // fragments read / previous tile consumed
+    kreg.template store<KP>(S0);
+    vreg.template store<KP>(S1);
     __syncthreads();
-    stage_rows_t<T, DHP, KP, true>(Ks, Kt, kbase, a.k_st, k0, kend, Dh);
-    stage_rows<T, DHP, KP>(Vs, vbase, a.v_st, k0, kend, Dh);
-    __syncthreads();
+    if (k0 + 64 < kend) {
+      kreg.load(kbase, a.k_st, k0 + 64, kend, Dh);
+      vreg.load(vbase, a.v_st, k0 + 64, kend, Dh);
+    }
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const int s0 = k0 + 16 * st;
       if (s0 >= kend || s0 + 15 < wlo || s0 > whi) continue;
       RowFrag<T, DQ> kf, vf;
-      kf.load_lds(Ks + (16 * st + r) * KP, g);
-      vf.load_lds(Vs + (16 * st + r) * KP, g);
+      kf.load_lds(S0 + (16 * st + r) * KP, g);
+      vf.load_lds(S1 + (16 * st + r) * KP, g);
       const f32x4 s = row_mma(kf, qf, f32x4{0.f, 0.f, 0.f, 0.f});    // S^T[key][query]
       const f32x4 dp = row_mma(vf, dof, f32x4{0.f, 0.f, 0.f, 0.f});  // dP^T[key][query]
       float ds[4];
@@ -280,22 +326,18 @@ __global__ __launch_bounds__(256) void local_bwd_q_kernel(const LocalArgs a) {
         ds[i] = p * (dp[i] - Dq);
       }
 #pragma unroll
-      for (int t = 0; t < NT; ++t) acc[t] = col_mma(Kt + (16 * t + r) * kTP + 16 * st + 4 * g, ds, acc[t]);
+      for (int t = 0; t < NT; ++t) acc[t] = col_mma_rm<KP>(S0 + (16 * st) * KP + 16 * t, ds, acc[t]);  // K^T dS^T
     }
   }
-  if (qv) {
-    T* dqp = static_cast<T*>(a.dq) + b * a.dq_sb + h * a.dq_sh + (int64_t)qi * a.dq_st;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int d = 16 * t + 4 * g;
-      if (d < Dh) {
-        float v4[4];
+  for (int t = 0; t < NT; ++t) {
+    float v4[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v4[i] = acc[t][i] * a.scale;
-        store4<T>(dqp + d, v4);
-      }
-    }
+    for (int i = 0; i < 4; ++i) v4[i] = acc[t][i] * a.scale;
+    store4<T>(S2 + row * KP + 16 * t + 4 * g, v4);  // S2 was last read before the loop's barriers
   }
+  __syncthreads();
+  store_tile<T, DHP, KP>(static_cast<T*>(a.dq) + b * a.dq_sb + h * a.dq_sh, a.dq_st, S2, q0, qend, Dh);
 }
 
 // ----------------------------------------------------------------------------
@@ -305,10 +347,8 @@ __global__ __launch_bounds__(256) void local_bwd_q_kernel(const LocalArgs a) {
 template <typename T, int DHP>
 __global__ __launch_bounds__(256) void local_bwd_kv_kernel(const LocalArgs a) {
   constexpr int DQ = DHP / 4, NT = DHP / 16, KP = DHP + kRowPad<T>;
-  __shared__ __align__(16) T Qs[64 * KP];
-  __shared__ __align__(16) T Qt[DHP * kTP];
-  __shared__ __align__(16) T Os[64 * KP];
-  __shared__ __align__(16) T Ot[DHP * kTP];
+  __shared__ __align__(16) T SQ[64 * KP];  // key rows -> query rows -> dk
+  __shared__ __align__(16) T SO[64 * KP];  // value rows -> dO rows -> dv
   __shared__ float lse2s[64], Dss[64];
   __shared__ int los[64];
 
@@ -316,51 +356,64 @@ __global__ __launch_bounds__(256) void local_bwd_kv_kernel(const LocalArgs a) {
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
   const int kt = bid % a.n_qt, bh = bid / a.n_qt, h = bh % a.H, b = bh / a.H;
   const int T_ = a.T, Dh = a.Dh;
-  const int j0 = kt * 64, kw = j0 + wave * 16, kj = kw + r;
+  const int j0 = kt * 64, kw = j0 + wave * 16, kj = kw + r, row = wave * 16 + r;
   const bool kv = kj < T_;
+  const int jend = min(T_, j0 + 64);
   const int64_t hrow = ((int64_t)b * a.H + h) * T_;
 
   const T* qbase = static_cast<const T*>(a.q) + b * a.q_sb + h * a.q_sh;
-  const T* kbase = static_cast<const T*>(a.k) + b * a.k_sb + h * a.k_sh;
-  const T* vbase = static_cast<const T*>(a.v) + b * a.v_sb + h * a.v_sh;
   const T* obase = static_cast<const T*>(a.dO) + (int64_t)b * T_ * a.H * Dh + (int64_t)h * Dh;
   const int64_t o_st = (int64_t)a.H * Dh;
 
+  const int qbeg = j0 + 1;
+  const int qend = (int)min((int64_t)T_, (int64_t)j0 + 64 + a.W);  // exclusive
+  RowTile<T, DHP> qreg, oreg;
+  float ls_r = 0.f, ds_r = 0.f;
+  auto load_tile = [&](int q0) {
+    qreg.load(qbase, a.q_st, q0, qend, Dh);
+    oreg.load(obase, o_st, q0, qend, Dh);
+    if (tid < 64 && q0 + tid < qend) {
+      ls_r = a.lse[hrow + q0 + tid];
+      ds_r = a.Dsum[hrow + q0 + tid];
+    }
+  };
+  {
+    RowTile<T, DHP> kreg, vreg;
+    kreg.load(static_cast<const T*>(a.k) + b * a.k_sb + h * a.k_sh, a.k_st, j0, jend, Dh);
+    vreg.load(static_cast<const T*>(a.v) + b * a.v_sb + h * a.v_sh, a.v_st, j0, jend, Dh);
+    if (qbeg < qend) load_tile(qbeg);
+    kreg.template store<KP>(SQ);
+    vreg.template store<KP>(SO);
+  }
+  __syncthreads();
   RowFrag<T, DQ> kf, vf;
-  kf.load(kbase + (int64_t)kj * a.k_st, g, Dh, kv);
-  vf.load(vbase + (int64_t)kj * a.v_st, g, Dh, kv);
+  kf.load_lds(SQ + row * KP, g);
+  vf.load_lds(SO + row * KP, g);
   f32x4 dk[NT], dv[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) dk[t] = dv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int qbeg = j0 + 1;
-  const int qend = (int)min((int64_t)T_, (int64_t)j0 + 64 + a.W);  // exclusive
   const int wqlo = kw + 1, wqhi = (int)min((int64_t)T_ - 1, (int64_t)kw + 15 + a.W);
   for (int q0 = qbeg; q0 < qend; q0 += 64) {
     __syncthreads();
-    stage_rows_t<T, DHP, KP, true>(Qs, Qt, qbase, a.q_st, q0, qend, Dh);
-    stage_rows_t<T, DHP, KP, true>(Os, Ot, obase, o_st, q0, qend, Dh);
+    qreg.template store<KP>(SQ);
+    oreg.template store<KP>(SO);
     if (tid < 64) {
       const int qq = q0 + tid;
-      if (qq < qend) {
-        const float ls = a.lse[hrow + qq];
-        lse2s[tid] = (ls == kNegInf) ? 0.f : ls * kLog2e;
-        Dss[tid] = a.Dsum[hrow + qq];
-        los[tid] = key_lo(qq, a.W, a.bs);
-      } else {
-        lse2s[tid] = 0.f;
-        Dss[tid] = 0.f;
-        los[tid] = INT_MAX;
-      }
+      const bool in = qq < qend;
+      lse2s[tid] = (!in || ls_r == kNegInf) ? 0.f : ls_r * kLog2e;
+      Dss[tid] = in ? ds_r : 0.f;
+      los[tid] = in ? key_lo(qq, a.W, a.bs) : INT_MAX;
     }
     __syncthreads();
+    if (q0 + 64 < qend) load_tile(q0 + 64);
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const int s0 = q0 + 16 * st;
       if (s0 >= qend || s0 + 15 < wqlo || s0 > wqhi) continue;
       RowFrag<T, DQ> qf, of;
-      qf.load_lds(Qs + (16 * st + r) * KP, g);
-      of.load_lds(Os + (16 * st + r) * KP, g);
+      qf.load_lds(SQ + (16 * st + r) * KP, g);
+      of.load_lds(SO + (16 * st + r) * KP, g);
       const f32x4 s = row_mma(qf, kf, f32x4{0.f, 0.f, 0.f, 0.f});   // S[query 4g+i][key r]
       const f32x4 dp = row_mma(of, vf, f32x4{0.f, 0.f, 0.f, 0.f});  // dP[query][key]
       float p[4], ds[4];
@@ -373,29 +426,26 @@ __global__ __launch_bounds__(256) void local_bwd_kv_kernel(const LocalArgs a) {
       }
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        dv[t] = col_mma(Ot + (16 * t + r) * kTP + 16 * st + 4 * g, p, dv[t]);   // dV^T[dim][key]
-        dk[t] = col_mma(Qt + (16 * t + r) * kTP + 16 * st + 4 * g, ds, dk[t]);  // dK^T[dim][key]
+        dv[t] = col_mma_rm<KP>(SO + (16 * st) * KP + 16 * t, p, dv[t]);   // dV^T = dO^T P
+        dk[t] = col_mma_rm<KP>(SQ + (16 * st) * KP + 16 * t, ds, dk[t]);  // dK^T = Q^T dS
       }
     }
   }
-  if (kv) {
-    T* dkp = static_cast<T*>(a.dk) + b * a.dk_sb + h * a.dk_sh + (int64_t)kj * a.dk_st;
-    T* dvp = static_cast<T*>(a.dv) + b * a.dv_sb + h * a.dv_sh + (int64_t)kj * a.dv_st;
+  __syncthreads();
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int d = 16 * t + 4 * g;
-      if (d < Dh) {
-        float kv4[4], vv4[4];
+  for (int t = 0; t < NT; ++t) {
+    float kv4[4], vv4[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          kv4[i] = dk[t][i] * a.scale;
-          vv4[i] = dv[t][i];
-        }
-        store4<T>(dkp + d, kv4);
-        store4<T>(dvp + d, vv4);
-      }
+    for (int i = 0; i < 4; ++i) {
+      kv4[i] = dk[t][i] * a.scale;
+      vv4[i] = dv[t][i];
     }
+    store4<T>(SQ + row * KP + 16 * t + 4 * g, kv4);
+    store4<T>(SO + row * KP + 16 * t + 4 * g, vv4);
   }
+  __syncthreads();
+  store_tile<T, DHP, KP>(static_cast<T*>(a.dk) + b * a.dk_sb + h * a.dk_sh, a.dk_st, SQ, j0, jend, Dh);
+  store_tile<T, DHP, KP>(static_cast<T*>(a.dv) + b * a.dv_sb + h * a.dv_sh, a.dv_st, SO, j0, jend, Dh);
 }
 
 // Ordered sum of the per-tile gate partials: dgate[h][d] = sum over (b, tile) of part[h][which][d][b*n_qt + tile].
