@@ -147,6 +147,35 @@ int32_t llattn_local_gate_bwd(const llattn_shape* s, const llattn_tensor* q, con
                               float* dgate_l, float* dgate_r, void* workspace, size_t workspace_bytes,
                               void* stream);
 
+/* Projection GEMM on bf16 MFMA: C[m][n] = sum_k A(m,k) B(n,k) (+ bias[n])
+ * (+ C[m][n] when accumulate).  A and B are bf16; each is stored
+ * k-contiguous (A[M][K] / B[N][K], trans = 0) or m/n-contiguous
+ * (A stored [K][M] / B stored [K][N], trans = 1), so the block's
+ * forward (x W^T + b), input-gradient (dy W) and weight-gradient (dy^T x)
+ * products all run without transpose copies.  C is bf16 or fp32; bias is
+ * fp32 [N] or NULL.  Leading dimensions are in elements.  split_k = 0 picks
+ * the number of K splits from the shape; more than one split writes fp32
+ * partials to the workspace (llattn_gemm_workspace_size bytes) and sums them
+ * in a fixed order.  Replaces the block's nn.Linear products and their
+ * autograd backward (reference models.py:80-84, 315, 333-353, 395, 462). */
+typedef struct llattn_gemm_desc {
+  int32_t M, N, K;
+  int32_t a_trans, b_trans;
+  const void* A;
+  int64_t lda;
+  const void* B;
+  int64_t ldb;
+  void* C;
+  int64_t ldc;
+  int32_t c_dtype;     /* LLATTN_BF16 or LLATTN_F32 */
+  int32_t accumulate;  /* 1: add into C */
+  const float* bias;   /* fp32 [N] or NULL */
+  int32_t split_k;     /* 0: automatic */
+} llattn_gemm_desc;
+
+size_t llattn_gemm_workspace_size(const llattn_gemm_desc* d);
+int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,443 @@
+// Projection GEMMs of the local+latent block on bf16 MFMA for gfx950.
+//
+// C[m][n] = sum_k A(m, k) * B(n, k)  (+ bias[n])  (+ C[m][n] when accumulating)
+//
+// A and B are bf16 and each is stored either k-contiguous ("A[M][K]",
+// "B[N][K]") or m/n-contiguous ("A[K][M]", "B[K][N]"), which covers every
+// projection of the block without a transpose copy:
+//   forward   y  = x W^T + b      A = x [M][K],   B = W [N][K]
+//   input grad dx = dy W          A = dy [M][K],  B = W stored [K][N]
+//   weight grad dW = dy^T x       A = dy stored [K][M], B = x stored [K][N]
+//
+// Tiling: a 256-thread workgroup (4 waves, 2 x 2) owns a 256 x 256 tile of C;
+// each wave owns 128 x 128 (64 accumulators of 16 x 16, v_mfma_f32_16x16x32_bf16,
+// held in AGPRs).  K advances in steps of 32 through four LDS stages of 32 KB.
+// Tiles move from HBM to LDS with buffer_load_dwordx4 ... lds (no register
+// staging); the loads of three steps are in flight while a step's 64 MFMAs per
+// wave run, and the next step's fragments are read from LDS meanwhile.
+//
+// LDS layouts (XOR-swizzled at 16-byte granularity, bank-conflict free):
+//   k-contiguous tile  [256 rows][32 k]:  chunk c (8 k) of row r at c ^ ((r >> 1) & 3)
+//   mn-contiguous tile [32 k][256 cols]:  chunk c (8 cols) of k-row k at c ^ 2(k & 3)
+// Operands of one MFMA: lane (r, g) (r = lane % 16, g = lane / 16) supplies
+// row r's eight k values 8g .. 8g+7 of the step -- one ds_read_b128 from a
+// k-contiguous tile, two ds_read_b64_tr_b16 from an mn-contiguous one.  Both
+// operands use the same k assignment, so the contraction is exact whichever
+// layout each comes from.
+//
+// Split-K (for the weight gradients, whose M x N is small and K = tokens is
+// large): split s covers k in [s*K/S, (s+1)*K/S) and writes fp32 partials; an
+// ordered reduction adds them (deterministic, no atomics).
+#include "llattn_abi.h"
+#include "llattn_device.h"
+
+namespace llattn {
+namespace gemm {
+
+constexpr int BM = 256, BN = 256, BK = 32, NST = 4;
+constexpr int TILE_BYTES = BM * BK * 2;        // 16 KB per operand per stage
+constexpr int STAGE_BYTES = 2 * TILE_BYTES;    // A + B
+constexpr int DMA_PER_TILE = TILE_BYTES / 1024 / 4;  // 1 KB blocks per wave per operand tile
+constexpr int DMA_PER_STEP = 2 * DMA_PER_TILE;       // per wave
+
+enum Epi { EPI_BF16 = 0, EPI_F32 = 1, EPI_PART = 2 };
+
+struct GemmArgs {
+  int M, N, K, k_split, tiles_m, tiles_n, accumulate;
+  const uint16_t* A; int64_t lda, a_bytes;
+  const uint16_t* B; int64_t ldb, b_bytes;
+  void* C; int64_t ldc;
+  const float* bias;
+  float* part;  // split-K partials [S][M][N]
+};
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) const void gbl_void;
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// LDS byte address of a pointer into shared memory
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, gfx9 family
+
+// One wave copies 64 x 16 bytes from global memory into the 1 KB LDS block at
+// `dst` (lane i lands at dst + 16 i) with buffer_load_dwordx4 ... lds: the
+// step's base address lives in the scalar buffer descriptor and each lane
+// adds its fixed 32-bit offset.  Offsets past the descriptor's extent read 0.
+// Written as inline asm so that the compiler does not see an LDS write in
+// flight: it would otherwise make every later LDS read wait for all of it
+// (vmcnt(0)), although the reads target another stage.  The main loop waits
+// for these loads itself (vmcnt) before the barrier that publishes them.
+__device__ __forceinline__ void dma_block(const i32x4& rs, uint32_t off, const unsigned char* dst) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(off), "s"(rs), "s"(lds_addr(dst))
+               : "memory", "m0");
+}
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt [3:0]+[15:14], expcnt [6:4], lgkmcnt [11:8]);
+// issued through the builtin so that the compiler's own wait insertion sees them.
+constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0070 | 0x0F00; }       // vmcnt(n)
+constexpr int wait_vm_lgkm0(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0070; }        // vmcnt(n) lgkmcnt(0)
+
+// Byte offsets (relative to the operand base at k = 0) of this lane's 16-byte
+// chunk in each of the wave's blocks of an operand tile (rows/cols
+// [o0, o0+256)).  Rows (k-contiguous) or columns (mn-contiguous) past `omax`
+// are clamped to a valid address; the outputs they feed are never stored.
+template <bool KMAJ>
+__device__ __forceinline__ void tile_offsets(uint32_t (&off)[DMA_PER_TILE], int64_t ld, int o0, int omax, int wave,
+                                             int lane) {
+#pragma unroll
+  for (int i = 0; i < DMA_PER_TILE; ++i) {
+    const int bi = wave * DMA_PER_TILE + i;
+    if constexpr (KMAJ) {  // block bi = rows 16bi .. 16bi+15, 4 chunks each
+      const int row = 16 * bi + (lane >> 2);
+      const int c = (lane & 3) ^ ((lane >> 3) & 3);  // (row >> 1) & 3 == (lane >> 3) & 3
+      const int gr = min(o0 + row, omax - 1);
+      off[i] = (uint32_t)(((int64_t)gr * ld + 8 * c) * 2);
+    } else {  // block bi = k-rows 2bi, 2bi+1, 32 chunks each
+      const int k = 2 * bi + (lane >> 5);
+      const int c = (lane & 31) ^ (2 * (k & 3));
+      const int col = min(o0 + 8 * c, omax - 8);
+      off[i] = (uint32_t)(((int64_t)k * ld + col) * 2);
+    }
+  }
+}
+
+// Issue this wave's share of one operand tile at k0 (`bytes`: storage extent of the operand).
+template <bool KMAJ>
+__device__ __forceinline__ void issue_tile(unsigned char* tile, const uint16_t* base, int64_t ld, int64_t bytes,
+                                           int k0, const uint32_t (&off)[DMA_PER_TILE], int wave) {
+  const int64_t skip = (KMAJ ? (int64_t)k0 : (int64_t)k0 * ld) * 2;
+  const uint64_t addr = reinterpret_cast<uint64_t>(base) + (uint64_t)skip;
+  const i32x4 rs = {(int)(uint32_t)addr, (int)((addr >> 32) & 0xffff), (int)(uint32_t)(bytes - skip), kRsrcWord3};
+#pragma unroll
+  for (int i = 0; i < DMA_PER_TILE; ++i) dma_block(rs, off[i], tile + (wave * DMA_PER_TILE + i) * 1024);
+}
+
+// 8 k values (8g .. 8g+7 of the step) of tile row/column o16 + r for lane (r, g).
+template <bool KMAJ>
+__device__ __forceinline__ bf16x8 frag(const unsigned char* tile, int o16, int r, int g) {
+  if constexpr (KMAJ) {
+    const int row = o16 + r;
+    return *reinterpret_cast<const bf16x8*>(tile + row * 64 + ((g ^ ((row >> 1) & 3)) << 4));
+  } else {
+    // transposing reads: the 16 lanes of group g supply rows kb + j/4, 8 bytes at
+    // column o16 + 4(j%4); lane r receives column o16 + r of those four rows
+    const int kb = 8 * g;
+    const int col = o16 + 4 * (r & 3), chunk = col >> 3, inner = (col & 7) << 1;
+    bf16x4 h[2];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int k = kb + 4 * half + (r >> 2);
+      const unsigned char* p = tile + k * 512 + ((chunk ^ (2 * (k & 3))) << 4) + inner;
+      h[half] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)(p));
+    }
+    return bf16x8{h[0][0], h[0][1], h[0][2], h[0][3], h[1][0], h[1][1], h[1][2], h[1][3]};
+  }
+}
+
+template <bool AK, bool BKM, int EPI>
+__global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
+  __shared__ __align__(1024) unsigned char smem[NST * STAGE_BYTES];
+  const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // workgroup -> (split, tile): contiguous ranges per XCD, then groups of 8 tile rows
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int tiles = a.tiles_m * a.tiles_n;
+  const int split = bid / tiles, t = bid % tiles;
+  constexpr int GM = 8;
+  const int group = t / (GM * a.tiles_n), first_m = group * GM;
+  const int gm = min(a.tiles_m - first_m, GM);
+  const int tm = first_m + (t % (GM * a.tiles_n)) % gm;
+  const int tn = (t % (GM * a.tiles_n)) / gm;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int kbeg = split * a.k_split, nk = a.k_split / BK;
+
+  f32x4 acc[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  uint32_t offa[DMA_PER_TILE], offb[DMA_PER_TILE];
+  tile_offsets<AK>(offa, a.lda, m0, a.M, wave, lane);
+  tile_offsets<BKM>(offb, a.ldb, n0, a.N, wave, lane);
+  auto issue = [&](int kt, int stage) {
+    unsigned char* st = smem + stage * STAGE_BYTES;
+    const int k0 = kbeg + kt * BK;
+    issue_tile<AK>(st, a.A, a.lda, a.a_bytes, k0, offa, wave);
+    issue_tile<BKM>(st + TILE_BYTES, a.B, a.ldb, a.b_bytes, k0, offb, wave);
+  };
+
+  // Pipeline over NST = 4 stages, one barrier per 32-k step.  Iteration kt:
+  //   wait until this wave's fragment reads of step kt and its DMA of step kt+1
+  //   are done; barrier (now every wave's DMA of step kt+1 has landed and no
+  //   wave reads stage kt%4 any more); read step kt+1's fragments; issue the DMA
+  //   of step kt+4 into stage kt%4; run step kt's 64 MFMAs per wave.
+  // Every iteration issues exactly one step of DMA (past the last step it
+  // reloads the last step into the free stage, which is never read again), so
+  // "step kt+1 landed" is always vmcnt <= 2 steps: vmcnt counts this wave's
+  // loads in issue order.  s_barrier is used without a fence: a fence would
+  // also wait for the DMA that is meant to stay in flight.
+  bf16x8 fa0[8], fb0[8], fa1[8], fb1[8];
+  auto read_step = [&](int stage, bf16x8 (&af)[8], bf16x8 (&bf)[8]) {
+    const unsigned char* As = smem + stage * STAGE_BYTES;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) af[i] = frag<AK>(As, wm * 128 + 16 * i, r, g);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) bf[j] = frag<BKM>(As + TILE_BYTES, wn * 128 + 16 * j, r, g);
+  };
+  auto mma_step = [&](const bf16x8 (&af)[8], const bf16x8 (&bf)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)  // B first: lane (r, g) accumulates C[m = r][n = 4g + e]
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[j], af[i], acc[i][j], 0, 0, 0);
+  };
+  auto step = [&](int kt, const bf16x8 (&ca)[8], const bf16x8 (&cb)[8], bf16x8 (&na)[8], bf16x8 (&nb)[8]) {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(2 * DMA_PER_STEP));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    read_step((kt + 1) % NST, na, nb);  // past the last step: unused data
+    __builtin_amdgcn_sched_barrier(0);
+    issue(min(kt + NST, nk - 1), kt % NST);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_step(ca, cb);
+  };
+
+#pragma unroll
+  for (int s = 0; s < NST; ++s) issue(min(s, nk - 1), s);
+  __builtin_amdgcn_s_waitcnt(wait_vm((NST - 1) * DMA_PER_STEP));
+  __builtin_amdgcn_s_barrier();
+  read_step(0, fa0, fb0);
+  for (int kt = 0; kt < nk; kt += 2) {  // nk is even; fragment buffers alternate between steps
+    step(kt, fa0, fb0, fa1, fb1);
+    step(kt + 1, fa1, fb1, fa0, fb0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));  // no DMA may land after the workgroup exits
+
+  // ---- epilogue ----
+  // Lane (r, g) holds C[m0 + wm*128 + 16i + r][n0 + wn*128 + 16j + 4g + e].  The
+  // values (+ bias) go through LDS so that global writes are whole 16-byte
+  // chunks of contiguous rows: each wave stages its 128 x 128 block in its own
+  // 32 KB of LDS (bf16: one pass; fp32: two passes of 64 rows) and writes it back
+  // row by row.  Every wave's MFMA operand reads are complete (lgkmcnt above);
+  // the barrier makes sure no other wave still reads the stages.
+  __builtin_amdgcn_s_barrier();
+  unsigned char* stg = smem + wave * 32768;
+  const int row0 = m0 + wm * 128, col0 = n0 + wn * 128;
+  float4 bias4[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int col = col0 + 16 * j + 4 * g;
+    bias4[j] = (EPI != EPI_PART && a.bias && col < a.N) ? *reinterpret_cast<const float4*>(a.bias + col)
+                                                        : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if constexpr (EPI == EPI_BF16) {
+    // bf16 rows of 256 B; 8-byte unit u of row rl stored at u ^ (rl & 15)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int rl = 16 * i + r;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float v[4] = {acc[i][j][0] + bias4[j].x, acc[i][j][1] + bias4[j].y, acc[i][j][2] + bias4[j].z,
+                            acc[i][j][3] + bias4[j].w};
+        uint2 x;
+        x.x = static_cast<uint32_t>(f2bf(v[0])) | (static_cast<uint32_t>(f2bf(v[1])) << 16);
+        x.y = static_cast<uint32_t>(f2bf(v[2])) | (static_cast<uint32_t>(f2bf(v[3])) << 16);
+        *reinterpret_cast<uint2*>(stg + rl * 256 + (((4 * j + g) ^ (rl & 15)) << 3)) = x;
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));  // this wave's staging writes are visible to itself
+#pragma unroll 4
+    for (int it = 0; it < 32; ++it) {  // 4 rows x 16 chunks of 16 B per instruction
+      const int idx = it * 64 + lane, rl = idx >> 4, c = idx & 15;
+      const int row = row0 + rl, col = col0 + 8 * c;
+      // units 2c, 2c+1 sit in one 16-byte slot, swapped when rl is odd
+      uint4 x = *reinterpret_cast<const uint4*>(stg + rl * 256 + (((2 * c) ^ (rl & 14)) << 3));
+      if (rl & 1) x = make_uint4(x.z, x.w, x.x, x.y);
+      if (row < a.M && col < a.N) {
+        uint16_t* p = static_cast<uint16_t*>(a.C) + (int64_t)row * a.ldc + col;
+        if (a.accumulate) {
+          const uint4 o = ld16(p);
+          const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, os[4] = {o.x, o.y, o.z, o.w};
+          uint32_t rs[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float lo = __uint_as_float(xs[e] << 16) + __uint_as_float(os[e] << 16);
+            const float hi = __uint_as_float(xs[e] & 0xffff0000u) + __uint_as_float(os[e] & 0xffff0000u);
+            rs[e] = static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
+          }
+          x = make_uint4(rs[0], rs[1], rs[2], rs[3]);
+        }
+        st16(p, x);
+      }
+    }
+  } else {
+    // fp32 rows of 512 B in two passes of 64 rows; 16-byte chunk c of row rl at c ^ (rl & 7)
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+      if (pass) __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));  // first pass's readback is done
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int i = 4 * pass + ii, rl = 16 * ii + r;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float4 v = make_float4(acc[i][j][0] + bias4[j].x, acc[i][j][1] + bias4[j].y,
+                                       acc[i][j][2] + bias4[j].z, acc[i][j][3] + bias4[j].w);
+          *reinterpret_cast<float4*>(stg + rl * 512 + (((4 * j + g) ^ (rl & 7)) << 4)) = v;
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));
+#pragma unroll 4
+      for (int it = 0; it < 32; ++it) {  // 2 rows x 32 chunks per instruction
+        const int idx = it * 64 + lane, rl = idx >> 5, c = idx & 31;
+        const int row = row0 + 64 * pass + rl, col = col0 + 4 * c;
+        float4 v = *reinterpret_cast<const float4*>(stg + rl * 512 + ((c ^ (rl & 7)) << 4));
+        if (row < a.M && col < a.N) {
+          float* p = EPI == EPI_PART ? a.part + ((int64_t)split * a.M + row) * a.N + col
+                                     : static_cast<float*>(a.C) + (int64_t)row * a.ldc + col;
+          if (EPI == EPI_F32 && a.accumulate) {
+            const float4 o = *reinterpret_cast<const float4*>(p);
+            v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
+          }
+          *reinterpret_cast<float4*>(p) = v;
+        }
+      }
+    }
+  }
+}
+
+// C = sum over splits of the partials (+ bias) (+ C), 4 columns per thread.
+template <int EPI>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs a, int S) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;  // quad index over M x N/4
+  const int nq = a.N / 4;
+  if (q >= (int64_t)a.M * nq) return;
+  const int row = (int)(q / nq), col = (int)(q % nq) * 4;
+  const int64_t mn = (int64_t)a.M * a.N;
+  const float* p = a.part + (int64_t)row * a.N + col;
+  float4 s = *reinterpret_cast<const float4*>(p);
+  for (int i = 1; i < S; ++i) {
+    const float4 x = *reinterpret_cast<const float4*>(p + i * mn);
+    s.x += x.x; s.y += x.y; s.z += x.z; s.w += x.w;
+  }
+  float v[4] = {s.x, s.y, s.z, s.w};
+  if (a.bias) {
+    const float4 b4 = *reinterpret_cast<const float4*>(a.bias + col);
+    v[0] += b4.x; v[1] += b4.y; v[2] += b4.z; v[3] += b4.w;
+  }
+  if constexpr (EPI == EPI_F32) {
+    float* c = static_cast<float*>(a.C) + (int64_t)row * a.ldc + col;
+    if (a.accumulate) {
+      const float4 o = *reinterpret_cast<const float4*>(c);
+      v[0] += o.x; v[1] += o.y; v[2] += o.z; v[3] += o.w;
+    }
+    *reinterpret_cast<float4*>(c) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    uint16_t* c = static_cast<uint16_t*>(a.C) + (int64_t)row * a.ldc + col;
+    if (a.accumulate) {
+      float o[4];
+      load4<uint16_t>(c, o);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += o[e];
+    }
+    store4<uint16_t>(c, v);
+  }
+}
+
+template <bool AK, bool BKM>
+void launch(const GemmArgs& a, int S, int c_dtype, hipStream_t st) {
+  const dim3 grid(a.tiles_m * a.tiles_n * S), block(256);
+  if (S > 1) {
+    hipLaunchKernelGGL((gemm_kernel<AK, BKM, EPI_PART>), grid, block, 0, st, a);
+    const int64_t quads = (int64_t)a.M * (a.N / 4);
+    const dim3 rg((unsigned)((quads + 255) / 256));
+    if (c_dtype == LLATTN_F32)
+      hipLaunchKernelGGL((splitk_reduce_kernel<EPI_F32>), rg, block, 0, st, a, S);
+    else
+      hipLaunchKernelGGL((splitk_reduce_kernel<EPI_BF16>), rg, block, 0, st, a, S);
+  } else if (c_dtype == LLATTN_F32) {
+    hipLaunchKernelGGL((gemm_kernel<AK, BKM, EPI_F32>), grid, block, 0, st, a);
+  } else {
+    hipLaunchKernelGGL((gemm_kernel<AK, BKM, EPI_BF16>), grid, block, 0, st, a);
+  }
+}
+
+// Number of K splits: 1 when the output tiles alone fill the chip, otherwise
+// the smallest power of two that gives at least one workgroup per CU while
+// every split keeps a whole number of 64-wide k steps.
+int resolve_split(const llattn_gemm_desc* d) {
+  if (d->split_k > 0) return d->split_k;
+  const int64_t tiles = (int64_t)((d->M + BM - 1) / BM) * ((d->N + BN - 1) / BN);
+  int s = 1;
+  while (tiles * s < 224 && d->K % (4 * s * BK) == 0 && d->K / (2 * s) >= 8 * BK) s *= 2;
+  return s;
+}
+
+}  // namespace gemm
+}  // namespace llattn
+
+using namespace llattn;
+using namespace llattn::gemm;
+
+extern "C" size_t llattn_gemm_workspace_size(const llattn_gemm_desc* d) {
+  if (!d) return 0;
+  const int S = resolve_split(d);
+  return S > 1 ? (size_t)S * d->M * d->N * sizeof(float) : 0;
+}
+
+extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!d) return fail(LLATTN_ERR_SHAPE, "llattn_gemm: null descriptor");
+  if (d->M <= 0 || d->N <= 0 || d->K <= 0)
+    return fail(LLATTN_ERR_SHAPE, "llattn_gemm: sizes must be positive (M=%d N=%d K=%d)", d->M, d->N, d->K);
+  if (d->c_dtype != LLATTN_BF16 && d->c_dtype != LLATTN_F32)
+    return fail(LLATTN_ERR_DTYPE, "llattn_gemm: unknown output dtype %d", d->c_dtype);
+  const int S = resolve_split(d);
+  if (S < 1 || d->K % (S * 2 * BK) != 0)
+    return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: K=%d must be a multiple of %d (%d x %d splits)", d->K,
+                S * 2 * BK, 2 * BK, S);
+  if (d->N % 8 != 0 || (d->a_trans && d->M % 8 != 0))
+    return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: N (and M of a transposed A) must be multiples of 8 (M=%d N=%d)",
+                d->M, d->N);
+  if (!d->A || !d->B || !d->C || !aligned16(d->A) || !aligned16(d->B) || !aligned16(d->C) ||
+      (d->bias && !aligned16(d->bias)))
+    return fail(LLATTN_ERR_LAYOUT, "llattn_gemm: operands must be non-null and 16-byte aligned");
+  if (d->lda % 8 || d->ldb % 8 || d->ldc % 8)
+    return fail(LLATTN_ERR_LAYOUT, "llattn_gemm: lda, ldb and ldc must be multiples of 8 elements");
+  if (d->lda < (d->a_trans ? d->M : d->K) || d->ldb < (d->b_trans ? d->N : d->K) || d->ldc < d->N)
+    return fail(LLATTN_ERR_LAYOUT, "llattn_gemm: leading dimensions smaller than the rows they hold");
+  // storage extents of the operands (the last row ends at its used width)
+  const int64_t a_bytes = (d->a_trans ? (int64_t)(d->K - 1) * d->lda + d->M : (int64_t)(d->M - 1) * d->lda + d->K) * 2;
+  const int64_t b_bytes = (d->b_trans ? (int64_t)(d->K - 1) * d->ldb + d->N : (int64_t)(d->N - 1) * d->ldb + d->K) * 2;
+  if (a_bytes >= (int64_t(1) << 32) || b_bytes >= (int64_t(1) << 32))
+    return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: operands of 4 GiB or more are not supported");
+  const size_t need = llattn_gemm_workspace_size(d);
+  if (need && (!workspace || workspace_bytes < need || !aligned16(workspace)))
+    return fail(LLATTN_ERR_WORKSPACE, "llattn_gemm: %d K splits need %zu workspace bytes (got %zu)", S, need,
+                workspace_bytes);
+  GemmArgs a{};
+  a.M = d->M; a.N = d->N; a.K = d->K; a.k_split = d->K / S;
+  a.tiles_m = (d->M + BM - 1) / BM; a.tiles_n = (d->N + BN - 1) / BN;
+  a.accumulate = d->accumulate;
+  a.A = static_cast<const uint16_t*>(d->A); a.lda = d->lda; a.a_bytes = a_bytes;
+  a.B = static_cast<const uint16_t*>(d->B); a.ldb = d->ldb; a.b_bytes = b_bytes;
+  a.C = d->C; a.ldc = d->ldc;
+  a.bias = d->bias;
+  a.part = static_cast<float*>(workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (!d->a_trans && !d->b_trans) launch<true, true>(a, S, d->c_dtype, st);
+  else if (!d->a_trans && d->b_trans) launch<true, false>(a, S, d->c_dtype, st);
+  else if (d->a_trans && d->b_trans) launch<false, false>(a, S, d->c_dtype, st);
+  else launch<false, true>(a, S, d->c_dtype, st);
+  return check_launch("llattn_gemm");
+}

@@ -36,8 +36,16 @@ class LlattnShape(ctypes.Structure):
         "gate_per_head")]
 
 
+class LlattnGemmDesc(ctypes.Structure):
+    _fields_ = [("M", ctypes.c_int32), ("N", ctypes.c_int32), ("K", ctypes.c_int32), ("a_trans", ctypes.c_int32),
+                ("b_trans", ctypes.c_int32), ("A", ctypes.c_void_p), ("lda", ctypes.c_int64), ("B", ctypes.c_void_p),
+                ("ldb", ctypes.c_int64), ("C", ctypes.c_void_p), ("ldc", ctypes.c_int64), ("c_dtype", ctypes.c_int32),
+                ("accumulate", ctypes.c_int32), ("bias", ctypes.c_void_p), ("split_k", ctypes.c_int32)]
+
+
 _P = ctypes.c_void_p
 _T = ctypes.POINTER(LlattnTensor)
+_G = ctypes.POINTER(LlattnGemmDesc)
 _S = ctypes.POINTER(LlattnShape)
 _I32, _I64, _SZ = ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
 
@@ -52,6 +60,8 @@ SIGNATURES = {
     "llattn_latent_bwd": (_I32, [_S, _T, _T, _T, _P, _T, _T, _T, _T, _P, _SZ, _P]),
     "llattn_local_gate_fwd": (_I32, [_S, _T, _T, _T, _T, _P, _P, _T, _T, _P, _P, _P]),
     "llattn_local_gate_bwd": (_I32, [_S, _T, _T, _T, _T, _P, _P, _T, _P, _P, _T, _T, _T, _T, _T, _P, _P, _P, _SZ, _P]),
+    "llattn_gemm_workspace_size": (_SZ, [_G]),
+    "llattn_gemm": (_I32, [_G, _P, _SZ, _P]),
 }
 
 _lib = None

@@ -1,0 +1,89 @@
+"""Projection GEMMs on the gfx950 MFMA kernel (``llattn_gemm`` of the C ABI).
+
+Three products cover every projection of the block and its backward without a
+transpose copy (all operands bf16, fp32 accumulation):
+
+* :func:`linear` -- ``y = x W^T (+ b)`` (``nn.Linear`` forward; reference models.py:315, 348, 395, 462);
+* :func:`matmul_nn` -- ``dx = dy W`` (input gradient);
+* :func:`matmul_tn` -- ``dW = dy^T x`` (weight gradient, fp32 output, split over tokens).
+
+Each takes 2-D views whose innermost dimension is contiguous; outputs may be
+passed in (``out=``) and accumulated into (``accumulate=True``).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib as L
+
+
+def _check2d(name: str, t: torch.Tensor) -> None:
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be a 2-D view with a contiguous inner dimension, got shape "
+                         f"{tuple(t.shape)} strides {t.stride()}")
+    if t.dtype != torch.bfloat16:
+        raise ValueError(f"{name} must be bfloat16 (got {t.dtype})")
+
+
+def _run(M: int, N: int, K: int, A: torch.Tensor, a_trans: bool, B: torch.Tensor, b_trans: bool, C: torch.Tensor,
+         bias: torch.Tensor | None, accumulate: bool, split_k: int = 0) -> None:
+    L.require_gpu(A, B, C)
+    if C.dim() != 2 or C.stride(1) != 1 or C.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("output must be a 2-D bf16 / fp32 view with a contiguous inner dimension")
+    if bias is not None and (bias.dtype != torch.float32 or not bias.is_contiguous() or bias.numel() != N):
+        raise ValueError(f"bias must be a contiguous fp32 vector of {N} elements")
+    desc = L.LlattnGemmDesc(M, N, K, int(a_trans), int(b_trans), A.data_ptr(), A.stride(0), B.data_ptr(),
+                            B.stride(0), C.data_ptr(), C.stride(0), L.dtype_code(C.dtype), int(accumulate),
+                            None if bias is None else bias.data_ptr(), split_k)
+    lib = L.load()
+    nws = lib.llattn_gemm_workspace_size(ctypes.byref(desc))
+    ws = torch.empty((max(nws, 1),), dtype=torch.uint8, device=C.device) if nws else None
+    from .ops import _call
+    _call("llattn_gemm", ctypes.byref(desc), None if ws is None else ws.data_ptr(), nws, L.stream_ptr(C.device))
+
+
+def linear(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None, out: torch.Tensor | None = None,
+           accumulate: bool = False) -> torch.Tensor:
+    """``x [M, K] @ w [N, K]^T (+ bias fp32 [N])`` -> bf16 ``[M, N]``."""
+    _check2d("x", x)
+    _check2d("w", w)
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError(f"x is [{M}, {K}] but w is {tuple(w.shape)}")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    _run(M, N, K, x, False, w, False, out, bias, accumulate)
+    return out
+
+
+def matmul_nn(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None,
+              accumulate: bool = False) -> torch.Tensor:
+    """``a [M, K] @ b [K, N]`` -> bf16 ``[M, N]`` (b read row-major, no transpose copy)."""
+    _check2d("a", a)
+    _check2d("b", b)
+    M, K = a.shape
+    N = b.shape[1]
+    if b.shape[0] != K:
+        raise ValueError(f"a is [{M}, {K}] but b is {tuple(b.shape)}")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    _run(M, N, K, a, False, b, True, out, None, accumulate)
+    return out
+
+
+def matmul_tn(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None, accumulate: bool = False,
+              split_k: int = 0) -> torch.Tensor:
+    """``a [K, M]^T @ b [K, N]`` -> fp32 ``[M, N]`` (weight gradients: K = tokens)."""
+    _check2d("a", a)
+    _check2d("b", b)
+    K, M = a.shape
+    N = b.shape[1]
+    if b.shape[0] != K:
+        raise ValueError(f"a is [{K}, {M}] but b is {tuple(b.shape)}")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=a.device)
+    _run(M, N, K, a, True, b, True, out, None, accumulate, split_k)
+    return out

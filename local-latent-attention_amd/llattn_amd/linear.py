@@ -1,0 +1,91 @@
+"""bf16 projections of the block with fp32 master weights (the autocast training path).
+
+:func:`project` computes ``x @ cat(W_i)^T + cat(b_i)`` for one or more
+``nn.Linear`` parameter pairs that read the same input (the block's ``qkv_proj``
+and token-wise ``rq_proj``, reference models.py:315, 348) as ONE bf16 GEMM, and
+its backward writes every weight gradient in fp32 straight from the gfx950
+split-K MFMA kernel (:func:`llattn_amd.gemm.matmul_tn`), so no bf16 weight
+gradient is materialised and cast.  It is what ``F.linear`` under
+``torch.autocast(dtype=bfloat16)`` computes (bf16 operands, fp32 accumulation,
+bf16 output), with the weight gradient accumulated in fp32 instead of being
+rounded to bf16 first.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from . import gemm
+
+BF16 = torch.bfloat16
+
+
+def tn_supported(k: int, m: int, n: int) -> bool:
+    """Shapes the weight-gradient kernel takes: the token count is split into whole 64-wide steps and the
+    output widths are multiples of 8."""
+    return k % 64 == 0 and m % 8 == 0 and n % 8 == 0
+
+
+def weight_grad(dy2: torch.Tensor, x2: torch.Tensor) -> torch.Tensor:
+    """fp32 ``dy2^T @ x2`` for bf16 ``dy2 [K, N]``, ``x2 [K, D]`` (K = tokens)."""
+    K, N = dy2.shape
+    D = x2.shape[1]
+    if tn_supported(K, N, D) and dy2.stride(1) == 1 and x2.stride(1) == 1:
+        return gemm.matmul_tn(dy2, x2)
+    # shapes the MFMA kernel does not tile (token counts that are not a multiple of 64): library GEMM
+    return torch.mm(dy2.t(), x2).float()
+
+
+class _Project(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, *params):
+        ws, bs = params[0::2], params[1::2]
+        has_bias = bs[0] is not None
+        K = x.shape[-1]
+        rows = [w.shape[0] for w in ws]
+        with torch.autocast(device_type="cuda", enabled=False):
+            x2 = x.reshape(-1, K).to(BF16)
+            if not x2.is_contiguous():
+                x2 = x2.contiguous()
+            wcat = torch.empty((sum(rows), K), dtype=BF16, device=x.device)
+            bcat = torch.empty((sum(rows),), dtype=BF16, device=x.device) if has_bias else None
+            o = 0
+            for w, b, n in zip(ws, bs, rows):
+                wcat[o:o + n].copy_(w)
+                if has_bias:
+                    bcat[o:o + n].copy_(b)
+                o += n
+            y = F.linear(x2, wcat, bcat)
+        ctx.save_for_backward(x2, wcat)
+        ctx.meta = (tuple(x.shape[:-1]), rows, has_bias, [w.dtype for w in ws], [None if b is None else b.dtype
+                                                                                 for b in bs], x.dtype)
+        return y.view(*x.shape[:-1], sum(rows))
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, wcat = ctx.saved_tensors
+        lead, rows, has_bias, wdt, bdt, xdt = ctx.meta
+        N = sum(rows)
+        with torch.autocast(device_type="cuda", enabled=False):
+            dy2 = dy.reshape(-1, N).to(BF16)
+            if not dy2.is_contiguous():
+                dy2 = dy2.contiguous()
+            dx = torch.mm(dy2, wcat).view(*lead, x2.shape[1]).to(xdt) if ctx.needs_input_grad[0] else None
+            dw = weight_grad(dy2, x2)
+            db = dy2.sum(0, dtype=torch.float32) if has_bias else None
+        grads = []
+        o = 0
+        for n, wd, bd in zip(rows, wdt, bdt):
+            grads.append(dw[o:o + n].to(wd))
+            grads.append(None if db is None else db[o:o + n].to(bd))
+            o += n
+        return (dx, *grads)
+
+
+def project(x: torch.Tensor, *linears: torch.nn.Linear) -> torch.Tensor:
+    """bf16 ``x @ [W_1; W_2; ...]^T + [b_1; b_2; ...]`` (all layers share the input width); backward gives
+    fp32 weight and bias gradients in the parameters' dtypes."""
+    params = []
+    for lin in linears:
+        params += [lin.weight, lin.bias]
+    return _Project.apply(x, *params)

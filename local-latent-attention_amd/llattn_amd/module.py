@@ -10,7 +10,8 @@ Data flow of one forward (B, T, D = batch, tokens, d_model):
 
 1. ``qkvr = x @ [W_qkv; W_rq]^T + b`` -- one GEMM for q|k|v and the token-wise
    latent queries (macro-block mode: ``qkv`` GEMM, HIP query-block pooling,
-   ``rq_proj`` GEMM);
+   ``rq_proj`` GEMM); under bf16 autocast through :func:`~llattn_amd.linear.project`,
+   whose weight gradients come from the gfx950 MFMA kernel in fp32;
 2. ``pooled = chunk means of x`` (HIP) and ``gkgv = rkv_proj(pooled)`` (GEMM);
 3. :class:`~llattn_amd.ops.LLAttnCore` -- HIP latent attention, ``r_out``
    GEMM, HIP windowed attention with the gate mix fused in its epilogue;
@@ -26,6 +27,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _lib as L
+from .linear import project
 from .ops import LLAttnCore, _Prof, pool
 
 
@@ -109,9 +111,15 @@ class LocalLatentAttentionTriton(nn.Module):
         if prof is not None:
             prof.start()
         macro = self.latent_query_block_size > 1
+        # bf16 autocast (the reference trainer's mode): projections in bf16 with fp32 weight gradients
+        bf16 = torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
         if macro:
-            qkvr = self.qkv_proj(x)
-            rq = self.rq_proj(pool(x, lay.q_block, lay.n_q, L.DIV_SEG))
+            qkvr = project(x, self.qkv_proj) if bf16 else self.qkv_proj(x)
+            pq = pool(x, lay.q_block, lay.n_q, L.DIV_SEG)
+            rq = project(pq, self.rq_proj) if bf16 else self.rq_proj(pq)
+        elif bf16:
+            qkvr = project(x, self.qkv_proj, self.rq_proj)
+            rq = None
         else:
             w = torch.cat([self.qkv_proj.weight, self.rq_proj.weight], dim=0)
             b = None if self.qkv_proj.bias is None else torch.cat([self.qkv_proj.bias, self.rq_proj.bias], dim=0)
@@ -129,7 +137,7 @@ class LocalLatentAttentionTriton(nn.Module):
             # the gate mix runs in the local kernel's epilogue: its time is in local_attention_ms
             prof.t["gate_mix_ms"] = 0.0
             self._record_profile(prof, lay)
-        return self.out(y)
+        return project(y, self.out) if bf16 else self.out(y)
 
     def _record_profile(self, prof, lay: L.Layout) -> None:
         t = prof.t

@@ -24,6 +24,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib as L
+from .linear import weight_grad
 
 _byref = ctypes.byref
 
@@ -197,7 +198,8 @@ def _core_backward(lay: L.Layout, dy, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, 
     with torch.autocast(device_type="cuda", enabled=False):
         dR2 = dR.view(B * lay.n_q, D)
         dlat = torch.mm(dR2, r_w.to(dt)).view(B, lay.n_q, Lh, Ldh)
-        dr_w = torch.mm(dR2.t(), lat.view(B * lay.n_q, Ld))
+        dr_w = weight_grad(dR2, lat.view(B * lay.n_q, Ld)) if dt == torch.bfloat16 else \
+            torch.mm(dR2.t(), lat.view(B * lay.n_q, Ld))
         dr_b = dR2.sum(dim=0, dtype=torch.float32) if has_rb else None
     ws2 = _empty((L.workspace_bytes(shape, L.WS_LATENT_BWD),), torch.uint8, device)
     _call("llattn_latent_bwd", _byref(shape), _byref(rq), _byref(gk), _byref(gv), lse_lat.data_ptr(),

@@ -24,7 +24,7 @@ def _declared_functions():
 def test_library_exports_every_declared_symbol():
     L, lib = _lib()
     names = _declared_functions()
-    assert len(names) == 9, names
+    assert len(names) == 11, names
     for n in names:
         assert hasattr(lib, n), n
         assert n in L.SIGNATURES, f"{n} has no ctypes signature"
@@ -113,6 +113,47 @@ def test_workspace_too_small_is_runtime_error():
     assert rc == L.ERR_WORKSPACE
     with pytest.raises(RuntimeError, match="workspace"):
         L.check(rc, "llattn_local_gate_bwd")
+
+
+def _gemm_desc(L, **kw):
+    base = dict(M=512, N=256, K=128, a_trans=0, b_trans=0, A=0x1000, lda=128, B=0x2000, ldb=128, C=0x3000, ldc=256,
+                c_dtype=L.BF16, accumulate=0, bias=None, split_k=0)
+    base.update(kw)
+    return L.LlattnGemmDesc(**base)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(M=0), 1, b"sizes must be positive"),
+    (dict(c_dtype=7), 2, b"unknown output dtype"),
+    (dict(K=96), 4, b"must be a multiple of 64"),
+    (dict(N=250, ldc=256), 4, b"multiples of 8"),
+    (dict(a_trans=1, M=100, lda=104), 4, b"multiples of 8"),
+    (dict(A=0x1004), 3, b"16-byte aligned"),
+    (dict(lda=100), 3, b"multiples of 8 elements"),
+    (dict(lda=64), 3, b"leading dimensions"),
+    (dict(ldc=128), 3, b"leading dimensions"),
+    (dict(split_k=4, K=128), 4, b"multiple of 256"),
+])
+def test_gemm_validation_codes(kw, code, msg):
+    L, lib = _lib()
+    d = _gemm_desc(L, **kw)
+    rc = lib.llattn_gemm(ctypes.byref(d), None, 0, None)
+    assert rc == code, lib.llattn_last_error()
+    assert msg in lib.llattn_last_error()
+
+
+def test_gemm_split_k_needs_workspace():
+    L, lib = _lib()
+    # weight-gradient shape: a small output, K = tokens -> the automatic split count is > 1
+    d = _gemm_desc(L, M=1408, N=1408, K=32768, a_trans=1, b_trans=1, lda=1408, ldb=1408, ldc=1408, c_dtype=L.F32)
+    need = lib.llattn_gemm_workspace_size(ctypes.byref(d))
+    assert need > 0 and need % (1408 * 1408 * 4) == 0
+    assert need // (1408 * 1408 * 4) in (2, 4, 8, 16)
+    rc = lib.llattn_gemm(ctypes.byref(d), None, 0, None)
+    assert rc == L.ERR_WORKSPACE and b"workspace" in lib.llattn_last_error()
+    # a full-chip output needs no split
+    d = _gemm_desc(L, M=32768, N=4736, K=1408, lda=1408, ldb=1408, ldc=4736)
+    assert lib.llattn_gemm_workspace_size(ctypes.byref(d)) == 0
 
 
 # ---------------------------------------------------------------- host logic

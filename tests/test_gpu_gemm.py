@@ -1,0 +1,116 @@
+"""GPU parity of the gfx950 projection GEMM (``llattn_gemm`` through the C ABI) against a float32 torch
+product of the same bf16 operands.
+
+Tolerances: bf16 output within 1e-2 of max(1, max|ref|) (one bf16 rounding of the result is 2^-8
+relative); fp32 output within 1e-4 of max(1, max|ref|) (fp32 accumulation over up to 32k terms).
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from gpu_helpers import require_cuda
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL, FP32_TOL = 1e-2, 1e-4
+
+
+def _err(got, ref):
+    return float((got.float() - ref).abs().max()) / max(1.0, float(ref.abs().max()))
+
+
+def _rand(*shape, gen, dev):
+    return torch.randn(*shape, device=dev, generator=gen).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 64), (300, 264, 128), (97, 40, 192), (1000, 1408, 512),
+                                   (32768, 4736, 1408)])
+def test_linear_with_bias(M, N, K):
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: linear", M, N, K, flush=True)
+    g = torch.Generator(device=dev).manual_seed(M + N + K)
+    x, w = _rand(M, K, gen=g, dev=dev), _rand(N, K, gen=g, dev=dev)
+    b = torch.randn(N, device=dev, generator=g)
+    ref = x.float() @ w.float().T + b
+    assert _err(gemm.linear(x, w, b), ref) < BF16_TOL
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 64), (300, 264, 128), (1000, 1408, 512)])
+def test_matmul_nn(M, N, K):
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: nn", M, N, K, flush=True)
+    g = torch.Generator(device=dev).manual_seed(7 * M + N)
+    a, b = _rand(M, K, gen=g, dev=dev), _rand(K, N, gen=g, dev=dev)
+    assert _err(gemm.matmul_nn(a, b), a.float() @ b.float()) < BF16_TOL
+
+
+@pytest.mark.parametrize("K,M,N,S", [(64, 256, 256, 1), (1024, 264, 136, 0), (4096, 1408, 512, 4),
+                                     (2048, 40, 96, 2), (32768, 1408, 1408, 0), (32768, 4736, 1408, 0)])
+def test_matmul_tn_fp32_out(K, M, N, S):
+    """Weight-gradient products, including split-K (S > 1 or automatic) at the config-2 shapes."""
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: tn", K, M, N, S, flush=True)
+    g = torch.Generator(device=dev).manual_seed(K + M)
+    a, b = _rand(K, M, gen=g, dev=dev), _rand(K, N, gen=g, dev=dev)
+    got = gemm.matmul_tn(a, b, split_k=S)
+    assert got.dtype == torch.float32
+    assert _err(got, a.float().T @ b.float()) < FP32_TOL
+
+
+def test_accumulate_and_strided_views():
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: accumulate", flush=True)
+    g = torch.Generator(device=dev).manual_seed(3)
+    big = _rand(512, 200, gen=g, dev=dev)
+    x = big[:, 8:136]                      # row stride 200, 128 columns
+    w = _rand(256, 128, gen=g, dev=dev)
+    c0 = _rand(512, 256, gen=g, dev=dev)
+    out = c0.clone()
+    gemm.linear(x, w, out=out, accumulate=True)
+    assert _err(out, c0.float() + x.float() @ w.float().T) < BF16_TOL
+    acc = torch.randn(256, 128, device=dev, generator=g)
+    dy = _rand(1024, 256, gen=g, dev=dev)
+    xx = _rand(1024, 128, gen=g, dev=dev)
+    ref = acc + dy.float().T @ xx.float()
+    gemm.matmul_tn(dy, xx, out=acc, accumulate=True)
+    assert _err(acc, ref) < FP32_TOL
+
+
+def test_deterministic_split_k():
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: split-K determinism", flush=True)
+    g = torch.Generator(device=dev).manual_seed(11)
+    a, b = _rand(32768, 512, gen=g, dev=dev), _rand(32768, 1408, gen=g, dev=dev)
+    torch.testing.assert_close(gemm.matmul_tn(a, b), gemm.matmul_tn(a, b), rtol=0, atol=0)
+
+
+def test_project_matches_fp32_linear():
+    """The bf16 projection autograd function (shared-input layers in one GEMM) vs fp32 F.linear on the same
+    bf16-rounded input: output, input gradient, fp32 weight and bias gradients."""
+    from llattn_amd.linear import project
+    dev = require_cuda()
+    print("case: project", flush=True)
+    torch.manual_seed(0)
+    l1, l2 = torch.nn.Linear(256, 384).to(dev), torch.nn.Linear(256, 64).to(dev)
+    x = torch.randn(2, 512, 256, device=dev).to(torch.bfloat16).requires_grad_(True)
+    dy = torch.randn(2, 512, 448, device=dev)
+    with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        y = project(x, l1, l2)
+    y.backward(dy.to(y.dtype))
+    xr = x.detach().float().requires_grad_(True)
+    # fp32 leaves holding the bf16-rounded weights, so the reference gradients are not rounded to bf16
+    wr = torch.cat([l1.weight, l2.weight]).detach().to(torch.bfloat16).float().requires_grad_(True)
+    br = torch.cat([l1.bias, l2.bias]).detach().to(torch.bfloat16).float().requires_grad_(True)
+    yr = torch.nn.functional.linear(xr, wr, br)
+    yr.backward(dy.to(torch.bfloat16).float())
+    assert y.dtype == torch.bfloat16 and l1.weight.grad.dtype == torch.float32
+    assert _err(y, yr) < BF16_TOL
+    assert _err(x.grad, xr.grad) < BF16_TOL
+    assert _err(torch.cat([l1.weight.grad, l2.weight.grad]), wr.grad) < 1e-3
+    assert _err(torch.cat([l1.bias.grad, l2.bias.grad]), br.grad) < 1e-3
