@@ -108,15 +108,12 @@ __device__ __forceinline__ void tile_offsets(uint32_t (&off)[DMA_PER_TILE], int6
   }
 }
 
-// Issue this wave's share of one operand tile at k0 (`bytes`: storage extent of the operand).
+// Buffer descriptor of an operand from step k0 on (`bytes`: storage extent of the operand).
 template <bool KMAJ>
-__device__ __forceinline__ void issue_tile(unsigned char* tile, const uint16_t* base, int64_t ld, int64_t bytes,
-                                           int k0, const uint32_t (&off)[DMA_PER_TILE], int wave) {
+__device__ __forceinline__ i32x4 step_rsrc(const uint16_t* base, int64_t ld, int64_t bytes, int k0) {
   const int64_t skip = (KMAJ ? (int64_t)k0 : (int64_t)k0 * ld) * 2;
   const uint64_t addr = reinterpret_cast<uint64_t>(base) + (uint64_t)skip;
-  const i32x4 rs = {(int)(uint32_t)addr, (int)((addr >> 32) & 0xffff), (int)(uint32_t)(bytes - skip), kRsrcWord3};
-#pragma unroll
-  for (int i = 0; i < DMA_PER_TILE; ++i) dma_block(rs, off[i], tile + (wave * DMA_PER_TILE + i) * 1024);
+  return i32x4{(int)(uint32_t)addr, (int)((addr >> 32) & 0xffff), (int)(uint32_t)(bytes - skip), kRsrcWord3};
 }
 
 // 8 k values (8g .. 8g+7 of the step) of tile row/column o16 + r for lane (r, g).
@@ -169,55 +166,66 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
   uint32_t offa[DMA_PER_TILE], offb[DMA_PER_TILE];
   tile_offsets<AK>(offa, a.lda, m0, a.M, wave, lane);
   tile_offsets<BKM>(offb, a.ldb, n0, a.N, wave, lane);
-  auto issue = [&](int kt, int stage) {
+  // DMA of this wave's block q (0..3: operand A, 4..7: operand B) of step kt into `stage`
+  auto dma = [&](const i32x4& rsa, const i32x4& rsb, int stage, int q) {
     unsigned char* st = smem + stage * STAGE_BYTES;
+    if (q < DMA_PER_TILE) dma_block(rsa, offa[q], st + (wave * DMA_PER_TILE + q) * 1024);
+    else dma_block(rsb, offb[q - DMA_PER_TILE], st + TILE_BYTES + (wave * DMA_PER_TILE + q - DMA_PER_TILE) * 1024);
+  };
+  auto step_rsrcs = [&](int kt, i32x4& rsa, i32x4& rsb) {
     const int k0 = kbeg + kt * BK;
-    issue_tile<AK>(st, a.A, a.lda, a.a_bytes, k0, offa, wave);
-    issue_tile<BKM>(st + TILE_BYTES, a.B, a.ldb, a.b_bytes, k0, offb, wave);
+    rsa = step_rsrc<AK>(a.A, a.lda, a.a_bytes, k0);
+    rsb = step_rsrc<BKM>(a.B, a.ldb, a.b_bytes, k0);
   };
 
   // Pipeline over NST = 4 stages, one barrier per 32-k step.  Iteration kt:
   //   wait until this wave's fragment reads of step kt and its DMA of step kt+1
   //   are done; barrier (now every wave's DMA of step kt+1 has landed and no
-  //   wave reads stage kt%4 any more); read step kt+1's fragments; issue the DMA
-  //   of step kt+4 into stage kt%4; run step kt's 64 MFMAs per wave.
+  //   wave reads stage kt%4 any more); then step kt's 64 MFMAs per wave, with
+  //   the 16 fragment reads of step kt+1 and the 8 DMA blocks of step kt+4 (into
+  //   stage kt%4) interleaved between them so that the LDS and address queues
+  //   drain while the MFMA pipe stays busy.
   // Every iteration issues exactly one step of DMA (past the last step it
   // reloads the last step into the free stage, which is never read again), so
   // "step kt+1 landed" is always vmcnt <= 2 steps: vmcnt counts this wave's
   // loads in issue order.  s_barrier is used without a fence: a fence would
   // also wait for the DMA that is meant to stay in flight.
   bf16x8 fa0[8], fb0[8], fa1[8], fb1[8];
-  auto read_step = [&](int stage, bf16x8 (&af)[8], bf16x8 (&bf)[8]) {
-    const unsigned char* As = smem + stage * STAGE_BYTES;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) af[i] = frag<AK>(As, wm * 128 + 16 * i, r, g);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) bf[j] = frag<BKM>(As + TILE_BYTES, wn * 128 + 16 * j, r, g);
-  };
-  auto mma_step = [&](const bf16x8 (&af)[8], const bf16x8 (&bf)[8]) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int j = 0; j < 8; ++j)  // B first: lane (r, g) accumulates C[m = r][n = 4g + e]
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[j], af[i], acc[i][j], 0, 0, 0);
-  };
   auto step = [&](int kt, const bf16x8 (&ca)[8], const bf16x8 (&cb)[8], bf16x8 (&na)[8], bf16x8 (&nb)[8]) {
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(2 * DMA_PER_STEP));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    read_step((kt + 1) % NST, na, nb);  // past the last step: unused data
-    __builtin_amdgcn_sched_barrier(0);
-    issue(min(kt + NST, nk - 1), kt % NST);
-    __builtin_amdgcn_sched_barrier(0);
-    mma_step(ca, cb);
+    const unsigned char* Ns = smem + ((kt + 1) % NST) * STAGE_BYTES;  // past the last step: unused data
+    i32x4 rsa, rsb;
+    step_rsrcs(min(kt + NST, nk - 1), rsa, rsb);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      if (q < 8) na[q] = frag<AK>(Ns, wm * 128 + 16 * q, r, g);
+      else nb[q - 8] = frag<BKM>(Ns + TILE_BYTES, wn * 128 + 16 * (q - 8), r, g);
+      if (q & 1) dma(rsa, rsb, kt % NST, q >> 1);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {  // B first: lane (r, g) accumulates C[m = r][n = 4g + e]
+        const int n = 4 * q + u, i = n >> 3, j = n & 7;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cb[j], ca[i], acc[i][j], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
 
 #pragma unroll
-  for (int s = 0; s < NST; ++s) issue(min(s, nk - 1), s);
+  for (int s = 0; s < NST; ++s) {
+    i32x4 rsa, rsb;
+    step_rsrcs(min(s, nk - 1), rsa, rsb);
+#pragma unroll
+    for (int q = 0; q < DMA_PER_STEP; ++q) dma(rsa, rsb, s, q);
+  }
   __builtin_amdgcn_s_waitcnt(wait_vm((NST - 1) * DMA_PER_STEP));
   __builtin_amdgcn_s_barrier();
-  read_step(0, fa0, fb0);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) fa0[i] = frag<AK>(smem, wm * 128 + 16 * i, r, g);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) fb0[j] = frag<BKM>(smem + TILE_BYTES, wn * 128 + 16 * j, r, g);
   for (int kt = 0; kt < nk; kt += 2) {  // nk is even; fragment buffers alternate between steps
     step(kt, fa0, fb0, fa1, fb1);
     step(kt + 1, fa1, fb1, fa0, fb0);

@@ -26,6 +26,26 @@ def tn_supported(k: int, m: int, n: int) -> bool:
     return k % 64 == 0 and m % 8 == 0 and n % 8 == 0
 
 
+def mfma_supported(k: int, n: int) -> bool:
+    """Shapes the forward / input-gradient kernel takes: the contraction in whole 64-wide steps and an
+    output width that is a multiple of 8."""
+    return k % 64 == 0 and n % 8 == 0
+
+
+def linear_fwd(x2: torch.Tensor, w: torch.Tensor, b32: torch.Tensor | None, library: bool = False) -> torch.Tensor:
+    """bf16 ``x2 @ w^T + b`` (fp32 bias added before the bf16 rounding of the output)."""
+    if not library and mfma_supported(x2.shape[1], w.shape[0]):
+        return gemm.linear(x2, w, b32)
+    return F.linear(x2, w, None if b32 is None else b32.to(BF16))
+
+
+def input_grad(dy2: torch.Tensor, w: torch.Tensor, library: bool = False) -> torch.Tensor:
+    """bf16 ``dy2 @ w`` (w [N, K] read row-major)."""
+    if not library and mfma_supported(dy2.shape[1], w.shape[1]):
+        return gemm.matmul_nn(dy2, w)
+    return torch.mm(dy2, w)
+
+
 def weight_grad(dy2: torch.Tensor, x2: torch.Tensor) -> torch.Tensor:
     """fp32 ``dy2^T @ x2`` for bf16 ``dy2 [K, N]``, ``x2 [K, D]`` (K = tokens)."""
     K, N = dy2.shape
@@ -38,7 +58,7 @@ def weight_grad(dy2: torch.Tensor, x2: torch.Tensor) -> torch.Tensor:
 
 class _Project(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, *params):
+    def forward(ctx, x, library, *params):
         ws, bs = params[0::2], params[1::2]
         has_bias = bs[0] is not None
         K = x.shape[-1]
@@ -48,29 +68,29 @@ class _Project(torch.autograd.Function):
             if not x2.is_contiguous():
                 x2 = x2.contiguous()
             wcat = torch.empty((sum(rows), K), dtype=BF16, device=x.device)
-            bcat = torch.empty((sum(rows),), dtype=BF16, device=x.device) if has_bias else None
+            bcat = torch.empty((sum(rows),), dtype=torch.float32, device=x.device) if has_bias else None
             o = 0
             for w, b, n in zip(ws, bs, rows):
                 wcat[o:o + n].copy_(w)
                 if has_bias:
                     bcat[o:o + n].copy_(b)
                 o += n
-            y = F.linear(x2, wcat, bcat)
+            y = linear_fwd(x2, wcat, bcat, library)
         ctx.save_for_backward(x2, wcat)
         ctx.meta = (tuple(x.shape[:-1]), rows, has_bias, [w.dtype for w in ws], [None if b is None else b.dtype
-                                                                                 for b in bs], x.dtype)
+                                                                                 for b in bs], x.dtype, library)
         return y.view(*x.shape[:-1], sum(rows))
 
     @staticmethod
     def backward(ctx, dy):
         x2, wcat = ctx.saved_tensors
-        lead, rows, has_bias, wdt, bdt, xdt = ctx.meta
+        lead, rows, has_bias, wdt, bdt, xdt, library = ctx.meta
         N = sum(rows)
         with torch.autocast(device_type="cuda", enabled=False):
             dy2 = dy.reshape(-1, N).to(BF16)
             if not dy2.is_contiguous():
                 dy2 = dy2.contiguous()
-            dx = torch.mm(dy2, wcat).view(*lead, x2.shape[1]).to(xdt) if ctx.needs_input_grad[0] else None
+            dx = input_grad(dy2, wcat, library).view(*lead, x2.shape[1]).to(xdt) if ctx.needs_input_grad[0] else None
             dw = weight_grad(dy2, x2)
             db = dy2.sum(0, dtype=torch.float32) if has_bias else None
         grads = []
@@ -79,13 +99,16 @@ class _Project(torch.autograd.Function):
             grads.append(dw[o:o + n].to(wd))
             grads.append(None if db is None else db[o:o + n].to(bd))
             o += n
-        return (dx, *grads)
+        return (dx, None, *grads)
 
 
-def project(x: torch.Tensor, *linears: torch.nn.Linear) -> torch.Tensor:
+def project(x: torch.Tensor, *linears: torch.nn.Linear, library: bool = False) -> torch.Tensor:
     """bf16 ``x @ [W_1; W_2; ...]^T + [b_1; b_2; ...]`` (all layers share the input width); backward gives
-    fp32 weight and bias gradients in the parameters' dtypes."""
+    fp32 weight and bias gradients in the parameters' dtypes.  ``library=True`` keeps the forward and
+    input-gradient products on hipBLASLt (the weight gradient always runs on the MFMA kernel when its shape
+    allows): at the block's widest projection (config 2: 32768 x 4736 x 1408) the library kernel is still
+    the faster of the two."""
     params = []
     for lin in linears:
         params += [lin.weight, lin.bias]
-    return _Project.apply(x, *params)
+    return _Project.apply(x, library, *params)

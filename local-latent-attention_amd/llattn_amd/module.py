@@ -114,11 +114,11 @@ class LocalLatentAttentionTriton(nn.Module):
         # bf16 autocast (the reference trainer's mode): projections in bf16 with fp32 weight gradients
         bf16 = torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
         if macro:
-            qkvr = project(x, self.qkv_proj) if bf16 else self.qkv_proj(x)
+            qkvr = project(x, self.qkv_proj, library=True) if bf16 else self.qkv_proj(x)
             pq = pool(x, lay.q_block, lay.n_q, L.DIV_SEG)
             rq = project(pq, self.rq_proj) if bf16 else self.rq_proj(pq)
         elif bf16:
-            qkvr = project(x, self.qkv_proj, self.rq_proj)
+            qkvr = project(x, self.qkv_proj, self.rq_proj, library=True)
             rq = None
         else:
             w = torch.cat([self.qkv_proj.weight, self.rq_proj.weight], dim=0)

@@ -24,7 +24,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib as L
-from .linear import weight_grad
+from .linear import input_grad, linear_fwd, weight_grad
 
 _byref = ctypes.byref
 
@@ -156,7 +156,11 @@ def _core_forward(lay: L.Layout, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, r_b, 
     _call("llattn_latent_fwd", _byref(shape), _byref(rq), _byref(gk), _byref(gv), _byref(L.view_bnhd(lat)),
           lse_lat.data_ptr(), stream)
     with torch.autocast(device_type="cuda", enabled=False):
-        R = F.linear(lat.view(B, lay.n_q, Ld), r_w.to(dt), None if r_b is None else r_b.to(dt))
+        if dt == torch.bfloat16:
+            R = linear_fwd(lat.view(B * lay.n_q, Ld), r_w.to(dt), None if r_b is None else r_b.float()).view(
+                B, lay.n_q, D)
+        else:
+            R = F.linear(lat.view(B, lay.n_q, Ld), r_w.to(dt), None if r_b is None else r_b.to(dt))
     if prof is not None:
         prof.lap("latent_attention_ms")
     y = _empty((B, T, H, Dh), dt, device)
@@ -197,7 +201,8 @@ def _core_backward(lay: L.Layout, dy, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, 
         dR = drem
     with torch.autocast(device_type="cuda", enabled=False):
         dR2 = dR.view(B * lay.n_q, D)
-        dlat = torch.mm(dR2, r_w.to(dt)).view(B, lay.n_q, Lh, Ldh)
+        dlat = (input_grad(dR2, r_w.to(dt)) if dt == torch.bfloat16 else torch.mm(dR2, r_w.to(dt))).view(
+            B, lay.n_q, Lh, Ldh)
         dr_w = weight_grad(dR2, lat.view(B * lay.n_q, Ld)) if dt == torch.bfloat16 else \
             torch.mm(dR2.t(), lat.view(B * lay.n_q, Ld))
         dr_b = dR2.sum(dim=0, dtype=torch.float32) if has_rb else None

@@ -139,6 +139,19 @@ def _op_case(B, T, H, Dh, Lh, Ldh, W, lbs, chunk, qbs, seed, dtype, per_head_gat
     dq, dk, dv = orc.local_attention_backward(arr["Q"], arr["K"], arr["V"], O, LSE, dO, lay)
     ref = dict(out=Y, Q=dq, K=dk, V=dv, GQ=drq, GK=dgk, GV=dgv, gl=dgl, gr=dgr,
                rw=np.einsum("bsk,bsl->kl", dR_q, L_flat), rb=dR_q.sum((0, 1)))
+    if dtype == torch.bfloat16:
+        # Precision floor of the gate gradients: the same sums over O and R rounded to bf16, the storage
+        # type the bf16 path (like the reference under autocast) keeps them in.  These are sums over all
+        # tokens of delta * O with cancellation, so their relative error is set by that rounding.
+        def bf(a):
+            return torch.tensor(a).to(torch.bfloat16).double().numpy()
+        Ob, Rb = bf(O), bf(R_tok)
+        wb = 1.0 / (1.0 + np.exp(-(np.einsum("bhtd,hd->bht", Ob, gl) - np.einsum("bhtd,hd->bht", Rb, gr))))
+        db = wb * (1 - wb) * np.einsum("bhtd,bhtd->bht", dOut, Ob - Rb)
+        fl, fr = np.einsum("bht,bhtd->hd", db, Ob), -np.einsum("bht,bhtd->hd", db, Rb)
+        if not per_head_gate:
+            fl, fr = fl.sum(0, keepdims=True), fr.sum(0, keepdims=True)
+        ref["_floor"] = {"gl": err_stats(fl, dgl), "gr": err_stats(fr, dgr)}
     return got, ref
 
 
@@ -170,8 +183,9 @@ def test_op_fp32_matches_oracle(case):
 def test_op_bf16_matches_oracle(case):
     _print_case("op bf16", case)
     got, ref = _op_case(*case, seed=hash(case) % 1000 + 1, dtype=torch.bfloat16)
+    floor = ref.pop("_floor")
     for k in ref:
-        assert_bf16_close(got[k], ref[k], k)
+        assert_bf16_close(got[k], ref[k], k, floor=floor.get(k))
 
 
 def test_op_per_head_gate():
