@@ -171,6 +171,8 @@ typedef struct llattn_gemm_desc {
   int32_t accumulate;  /* 1: add into C */
   const float* bias;   /* fp32 [N] or NULL */
   int32_t split_k;     /* 0: automatic */
+  float* a_colsum;     /* NULL, or fp32 [M] receiving sum_k A(m, k) (a_trans = 1 only): the bias gradient
+                          of a weight-gradient product, from the same pass over A */
 } llattn_gemm_desc;
 
 size_t llattn_gemm_workspace_size(const llattn_gemm_desc* d);

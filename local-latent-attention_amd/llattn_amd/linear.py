@@ -46,14 +46,16 @@ def input_grad(dy2: torch.Tensor, w: torch.Tensor, library: bool = False) -> tor
     return torch.mm(dy2, w)
 
 
-def weight_grad(dy2: torch.Tensor, x2: torch.Tensor) -> torch.Tensor:
-    """fp32 ``dy2^T @ x2`` for bf16 ``dy2 [K, N]``, ``x2 [K, D]`` (K = tokens)."""
+def weight_grad(dy2: torch.Tensor, x2: torch.Tensor, bias_grad: bool = False):
+    """fp32 ``dy2^T @ x2`` for bf16 ``dy2 [K, N]``, ``x2 [K, D]`` (K = tokens), and with ``bias_grad`` also the
+    fp32 column sums of ``dy2`` (the bias gradient, from the same pass over ``dy2``): returns ``(dW, db)``."""
     K, N = dy2.shape
     D = x2.shape[1]
     if tn_supported(K, N, D) and dy2.stride(1) == 1 and x2.stride(1) == 1:
-        return gemm.matmul_tn(dy2, x2)
+        db = torch.empty((N,), dtype=torch.float32, device=dy2.device) if bias_grad else None
+        return gemm.matmul_tn(dy2, x2, colsum=db), db
     # shapes the MFMA kernel does not tile (token counts that are not a multiple of 64): library GEMM
-    return torch.mm(dy2.t(), x2).float()
+    return torch.mm(dy2.t(), x2).float(), (dy2.sum(0, dtype=torch.float32) if bias_grad else None)
 
 
 class _Project(torch.autograd.Function):
@@ -91,8 +93,7 @@ class _Project(torch.autograd.Function):
             if not dy2.is_contiguous():
                 dy2 = dy2.contiguous()
             dx = input_grad(dy2, wcat, library).view(*lead, x2.shape[1]).to(xdt) if ctx.needs_input_grad[0] else None
-            dw = weight_grad(dy2, x2)
-            db = dy2.sum(0, dtype=torch.float32) if has_bias else None
+            dw, db = weight_grad(dy2, x2, has_bias)
         grads = []
         o = 0
         for n, wd, bd in zip(rows, wdt, bdt):

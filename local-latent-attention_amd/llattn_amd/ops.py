@@ -203,9 +203,11 @@ def _core_backward(lay: L.Layout, dy, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, 
         dR2 = dR.view(B * lay.n_q, D)
         dlat = (input_grad(dR2, r_w.to(dt)) if dt == torch.bfloat16 else torch.mm(dR2, r_w.to(dt))).view(
             B, lay.n_q, Lh, Ldh)
-        dr_w = weight_grad(dR2, lat.view(B * lay.n_q, Ld)) if dt == torch.bfloat16 else \
-            torch.mm(dR2.t(), lat.view(B * lay.n_q, Ld))
-        dr_b = dR2.sum(dim=0, dtype=torch.float32) if has_rb else None
+        if dt == torch.bfloat16:
+            dr_w, dr_b = weight_grad(dR2, lat.view(B * lay.n_q, Ld), has_rb)
+        else:
+            dr_w = torch.mm(dR2.t(), lat.view(B * lay.n_q, Ld))
+            dr_b = dR2.sum(dim=0, dtype=torch.float32) if has_rb else None
     ws2 = _empty((L.workspace_bytes(shape, L.WS_LATENT_BWD),), torch.uint8, device)
     _call("llattn_latent_bwd", _byref(shape), _byref(rq), _byref(gk), _byref(gv), lse_lat.data_ptr(),
           _byref(L.view_bnhd(dlat)), _byref(drq), _byref(dgk), _byref(dgv), ws2.data_ptr(), ws2.numel(), stream)

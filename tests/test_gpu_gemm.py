@@ -56,9 +56,11 @@ def test_matmul_tn_fp32_out(K, M, N, S):
     print("case: tn", K, M, N, S, flush=True)
     g = torch.Generator(device=dev).manual_seed(K + M)
     a, b = _rand(K, M, gen=g, dev=dev), _rand(K, N, gen=g, dev=dev)
-    got = gemm.matmul_tn(a, b, split_k=S)
+    cs = torch.empty(M, device=dev)
+    got = gemm.matmul_tn(a, b, split_k=S, colsum=cs)
     assert got.dtype == torch.float32
     assert _err(got, a.float().T @ b.float()) < FP32_TOL
+    assert _err(cs, a.float().sum(0)) < FP32_TOL      # column sums (bias gradient) from the same pass
 
 
 def test_accumulate_and_strided_views():
