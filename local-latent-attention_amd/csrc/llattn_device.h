@@ -189,6 +189,15 @@ __device__ __forceinline__ float max_groups(float x) {
   x = fmaxf(x, __shfl_xor(x, 32));
   return x;
 }
+// sum over the 16 lanes of a group (same g), valid in the group's last lane
+// (r = 15): a DPP row_shr ladder (VALU; out-of-row sources read 0)
+__device__ __forceinline__ float sum_rows16_last(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x111, 0xf, 0xf, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x112, 0xf, 0xf, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x114, 0xf, 0xf, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x118, 0xf, 0xf, true));
+  return x;
+}
 // sum over the 16 lanes of a group (same g)
 __device__ __forceinline__ float sum_rows16(float x) {
   x += __shfl_xor(x, 1);
@@ -253,14 +262,14 @@ __device__ __forceinline__ f32x4 col_mma_rm(const float* base, const float b[4],
 //
 // RowTile: row-major [64][P] copy; consecutive threads take consecutive 16-byte
 // chunks of a row (coalesced reads).  Rows >= r_end and dims >= Dh are zero.
-template <typename T, int DHP>
+template <typename T, int DHP, int NTHR = 256>
 struct RowTile {
-  static constexpr int V = Vec16<T>::N, CPR = DHP / V, TASKS = 64 * CPR, IT = (TASKS + 255) / 256;
+  static constexpr int V = Vec16<T>::N, CPR = DHP / V, TASKS = 64 * CPR, IT = (TASKS + NTHR - 1) / NTHR;
   uint4 x[IT];
   __device__ __forceinline__ void load(const T* base, int64_t st, int r0, int r_end, int Dh) {
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-      const int task = threadIdx.x + 256 * it, row = task / CPR, col = (task % CPR) * V, rr = r0 + row;
+      const int task = threadIdx.x + NTHR * it, row = task / CPR, col = (task % CPR) * V, rr = r0 + row;
       x[it] = make_uint4(0, 0, 0, 0);
       if (task < TASKS && rr < r_end && col < Dh) x[it] = ld16(base + (int64_t)rr * st + col);
     }
@@ -270,7 +279,7 @@ struct RowTile {
   __device__ __forceinline__ void load_div(const T* base, int64_t st, int r0, int r_end, int div, int Dh) {
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-      const int task = threadIdx.x + 256 * it, row = task / CPR, col = (task % CPR) * V, rr = r0 + row;
+      const int task = threadIdx.x + NTHR * it, row = task / CPR, col = (task % CPR) * V, rr = r0 + row;
       x[it] = make_uint4(0, 0, 0, 0);
       if (task < TASKS && rr < r_end && col < Dh) x[it] = ld16(base + (int64_t)(rr / div) * st + col);
     }
@@ -279,7 +288,7 @@ struct RowTile {
   __device__ __forceinline__ void store(T* lds) const {
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-      const int task = threadIdx.x + 256 * it, row = task / CPR, col = (task % CPR) * V;
+      const int task = threadIdx.x + NTHR * it, row = task / CPR, col = (task % CPR) * V;
       if (task < TASKS) st16(lds + row * P + col, x[it]);
     }
   }
@@ -287,12 +296,12 @@ struct RowTile {
 
 // Coalesced copy of a row-major 64-row LDS tile (pitch P) to global rows
 // r0 + i (row stride st) for r0 + i < r_end and dims < Dh.
-template <typename T, int DHP, int P>
+template <typename T, int DHP, int P, int NTHR = 256>
 __device__ __forceinline__ void store_tile(T* base, int64_t st, const T* lds, int r0, int r_end, int Dh) {
-  constexpr int V = Vec16<T>::N, CPR = DHP / V, TASKS = 64 * CPR, IT = (TASKS + 255) / 256;
+  constexpr int V = Vec16<T>::N, CPR = DHP / V, TASKS = 64 * CPR, IT = (TASKS + NTHR - 1) / NTHR;
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
-    const int task = threadIdx.x + 256 * it, row = task / CPR, col = (task % CPR) * V, rr = r0 + row;
+    const int task = threadIdx.x + NTHR * it, row = task / CPR, col = (task % CPR) * V, rr = r0 + row;
     if (task < TASKS && rr < r_end && col < Dh) st16(base + (int64_t)rr * st + col, ld16(lds + row * P + col));
   }
 }

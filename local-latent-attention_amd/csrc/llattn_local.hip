@@ -256,9 +256,9 @@ __global__ __launch_bounds__(256) void local_bwd_q_kernel(const LocalArgs a) {
     // gate partial sums over the 16 queries of this wave
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float pl = sum_rows16(delta * olv[t][i]);
-      const float pr = sum_rows16(-delta * rv[t][i]);
-      if (r == 0) {
+      const float pl = sum_rows16_last(delta * olv[t][i]);
+      const float pr = sum_rows16_last(-delta * rv[t][i]);
+      if (r == 15) {
         gsum[wave][0][d + i] = pl;
         gsum[wave][1][d + i] = pr;
       }
@@ -448,6 +448,333 @@ __global__ __launch_bounds__(256) void local_bwd_kv_kernel(const LocalArgs a) {
   store_tile<T, DHP, KP>(static_cast<T*>(a.dv) + b * a.dv_sb + h * a.dv_sh, a.dv_st, SO, j0, jend, Dh);
 }
 
+// ----------------------------------------------------------------------------
+// fused backward for windows W <= 64, bf16: one workgroup walks a segment of
+// kSegTiles query tiles of one (batch, head) in order.  With W <= 64 the keys of
+// query tile qt lie in key tiles qt-1 and qt, and key tile qt gets its queries
+// from query tiles qt and qt+1, so after step qt key tile qt-1 is complete.
+// Every row of q, k, v, dy, o_local and remote is read from HBM once per
+// segment (plus one tile of halo at each end), dO never leaves LDS, and each
+// output row is written once.  512 threads in two roles that share a SIMD:
+//   query waves 0-3 (16 queries each): gate backward (dO, D, dremote, gate
+//     partials), then dQ over key tiles qt-1 and qt;
+//   key waves 4-7 (16 keys each of tiles qt-1 and qt): dK / dV contributions
+//     of the step's queries, concurrently with the query waves' dQ.  The
+//     partial dK / dV of key tile qt is parked in LDS (fp32, in the
+//     accumulator layout, read back by the same lane) until step qt+1
+//     completes it, so only one key tile's accumulators are live at a time.
+// The segment's last key tile needs the queries of the next segment's first
+// tile: an extra step at the end gates that tile and adds its contributions
+// (its own outputs belong to the next segment).  No atomics: every output has
+// one writer.
+// ----------------------------------------------------------------------------
+constexpr int kSegTiles = 8;
+
+template <int DHP>
+__global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a) {
+  using T = uint16_t;
+  constexpr int NTHR = 512;
+  constexpr int DQ = DHP / 4, NT = DHP / 16, KP = DHP + kRowPad<T>;
+  __shared__ __align__(16) T SQ[64 * KP];     // query rows of the step's tile -> dq staging
+  __shared__ __align__(16) T SO[64 * KP];     // dy -> dO rows
+  __shared__ __align__(16) T SK[2][64 * KP];  // key rows by tile parity (o_local while gating; dk staging)
+  __shared__ __align__(16) T SV[2][64 * KP];  // value rows by tile parity (remote -> dremote while gating; dv staging)
+  __shared__ __align__(16) T SDK[64 * KP];    // finished dk rows of key tile qt-1
+  __shared__ __align__(16) T SDV[64 * KP];    // finished dv rows of key tile qt-1
+  __shared__ __align__(16) f32x4 PKV[4][2 * NT][64];  // key waves: partial dk (t < NT) / dv of key tile qt
+  __shared__ float gsum[4][2][DHP];
+  __shared__ __align__(16) float gls[DHP], grs[DHP];
+  __shared__ float lse2s[64], Dss[64];
+  __shared__ int los[64];
+
+  const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool qrole = wave < 4;
+  const int w4 = wave & 3, row = w4 * 16 + r;  // query row (query waves) or key row (key waves)
+  const int n_seg = (a.n_qt + kSegTiles - 1) / kSegTiles;
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int seg = bid % n_seg, bh = bid / n_seg, h = bh % a.H, b = bh / a.H;
+  const int t0 = seg * kSegTiles, t1 = min(a.n_qt, t0 + kSegTiles);
+  const int tlast = min(t1, a.n_qt - 1);  // the extra step runs when t1 < n_qt
+  const int T_ = a.T, Dh = a.Dh;
+  const int64_t hrow = ((int64_t)b * a.H + h) * T_;
+  const T* qbase = static_cast<const T*>(a.q) + b * a.q_sb + h * a.q_sh;
+  const T* kbase = static_cast<const T*>(a.k) + b * a.k_sb + h * a.k_sh;
+  const T* vbase = static_cast<const T*>(a.v) + b * a.v_sb + h * a.v_sh;
+  const T* dybase = static_cast<const T*>(a.dy) + b * a.dy_sb + h * a.dy_sh;
+  const T* olbase = static_cast<const T*>(a.ol) + b * a.o_sb + h * a.o_sh;
+  const T* rbase = static_cast<const T*>(a.rem) + b * a.r_sb + h * a.r_sh;
+
+  for (int d = tid; d < DHP; d += NTHR) {
+    gls[d] = d < Dh ? a.gl[h * a.gate_hs + d] : 0.f;
+    grs[d] = d < Dh ? a.gr[h * a.gate_hs + d] : 0.f;
+  }
+  RowTile<T, DHP, NTHR> rdy, rol, rrm, rq, rk, rv;
+  float nw = 0.f, nlse = kNegInf;  // the query waves' next w and lse
+  auto load_step = [&](int qt) {
+    const int q0 = qt * 64, qend = min(T_, q0 + 64);
+    rdy.load(dybase, a.dy_st, q0, qend, Dh);
+    rol.load(olbase, a.o_st, q0, qend, Dh);
+    rrm.load_div(rbase, a.r_sn, q0, qend, a.q_block, Dh);
+    rq.load(qbase, a.q_st, q0, qend, Dh);
+    if (qt < t1) {  // the extra step needs no keys of its own tile
+      rk.load(kbase, a.k_st, q0, qend, Dh);
+      rv.load(vbase, a.v_st, q0, qend, Dh);
+    }
+    const int qi = q0 + row;
+    if (qrole && qi < T_) {
+      nw = a.w[hrow + qi];
+      nlse = a.lse[hrow + qi];
+    }
+  };
+  if (t0 > 0) {  // keys of tile t0-1 for the first step's dQ
+    const int p0 = (t0 - 1) * 64;
+    rk.load(kbase, a.k_st, p0, p0 + 64, Dh);
+    rv.load(vbase, a.v_st, p0, p0 + 64, Dh);
+    rk.template store<KP>(SK[(t0 - 1) & 1]);
+    rv.template store<KP>(SV[(t0 - 1) & 1]);
+  }
+  load_step(t0);
+
+  for (int qt = t0; qt <= tlast; ++qt) {
+    const bool full = qt < t1;
+    const bool own_prev = qt - 1 >= t0;
+    const int cur = qt & 1, prv = cur ^ 1;
+    const int q0 = qt * 64, qend = min(T_, q0 + 64);
+    const int qw = q0 + w4 * 16, qi = qw + r;
+    const bool qv = qi < T_;
+    const float wq = qv ? nw : 0.f, lse_nat = qv ? nlse : kNegInf;
+
+    // ---- stage the step's rows (o_local and remote in SDK / SDV, free until the key waves finish
+    //      key tile qt-1), then put the next step's loads in flight for the whole step ----
+    __syncthreads();  // the previous step's write-back is done with SQ, SDK, SDV; SO, SK[cur], SV[cur] are free
+    rdy.template store<KP>(SO);
+    rol.template store<KP>(SDK);
+    rrm.template store<KP>(SDV);
+    rq.template store<KP>(SQ);
+    if (full) {
+      rk.template store<KP>(SK[cur]);
+      rv.template store<KP>(SV[cur]);
+    }
+    if (qt + 1 <= tlast) load_step(qt + 1);
+    __syncthreads();
+
+    // ---- query waves: gate backward in the accumulator layout (dims 16t+4g+i) ----
+    float Dq = 0.f;
+    if (qrole) {
+      // two passes over the staged rows (re-read from LDS) keep the register footprint small
+      float dot1 = 0.f;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int d = 16 * t + 4 * g;
+        float dyv[4], olv[4], rv4[4];
+        Raw4<T> x;
+        x.load(SO + row * KP + d, true); x.get(dyv);
+        x.load(SDK + row * KP + d, true); x.get(olv);
+        x.load(SDV + row * KP + d, true); x.get(rv4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dot1 += dyv[i] * (olv[i] - rv4[i]);
+      }
+      dot1 = sum_groups(dot1);
+      const float delta = wq * (1.f - wq) * dot1;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int d = 16 * t + 4 * g;
+        float dyv[4], olv[4], rv4[4];
+        Raw4<T> x;
+        x.load(SO + row * KP + d, true); x.get(dyv);
+        x.load(SDK + row * KP + d, true); x.get(olv);
+        x.load(SDV + row * KP + d, true); x.get(rv4);
+        const float4 gl4 = *reinterpret_cast<const float4*>(gls + d);
+        const float4 gr4 = *reinterpret_cast<const float4*>(grs + d);
+        const float glv[4] = {gl4.x, gl4.y, gl4.z, gl4.w}, grv[4] = {gr4.x, gr4.y, gr4.z, gr4.w};
+        float dov[4], drv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          dov[i] = round_t<T>(wq * dyv[i] + delta * glv[i]);
+          drv[i] = (1.f - wq) * dyv[i] - delta * grv[i];
+          Dq += dov[i] * olv[i];
+        }
+        store4<T>(SO + row * KP + d, dov);  // in place over the dy elements this lane read
+        if (full && qv && d < Dh)            // dremote straight from the accumulator layout
+          store4<T>(static_cast<T*>(a.dr) + b * a.dr_sb + h * a.dr_sh + (int64_t)qi * a.dr_st + d, drv);
+        if (full) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {  // gate partial sums over the 16 queries of this wave
+            const float pl = sum_rows16_last(delta * olv[i]);
+            const float pr = sum_rows16_last(-delta * rv4[i]);
+            if (r == 15) {
+              gsum[w4][0][d + i] = pl;
+              gsum[w4][1][d + i] = pr;
+            }
+          }
+        }
+      }
+      Dq = sum_groups(Dq);
+      if (g == 0) {
+        Dss[row] = qv ? Dq : 0.f;
+        lse2s[row] = (!qv || lse_nat == kNegInf) ? 0.f : lse_nat * kLog2e;
+        los[row] = qv ? key_lo(qi, a.W, a.bs) : INT_MAX;
+      }
+    }
+    __syncthreads();  // dO and the per-query stats are complete; o_local / remote (SDK / SDV) are consumed
+    if (full) {
+      const int nrow = a.B * a.n_qt, prow = b * a.n_qt + qt;
+      for (int idx = tid; idx < 2 * DHP; idx += NTHR) {
+        const int which = idx / DHP, d = idx % DHP;
+        if (d < Dh) {
+          const float sum = gsum[0][which][d] + gsum[1][which][d] + gsum[2][which][d] + gsum[3][which][d];
+          a.gpart[(((int64_t)h * 2 + which) * Dh + d) * nrow + prow] = sum;
+        }
+      }
+    }
+
+    f32x4 dq[NT];  // query waves
+#pragma unroll
+    for (int t = 0; t < NT; ++t) dq[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (qrole) {
+      // ---- dQ = scale * sum_j dS_ij k_j over key tiles qt-1 and qt ----
+      if (full) {
+        RowFrag<T, DQ> qf, dof;
+        qf.load_lds(SQ + row * KP, g);
+        dof.load_lds(SO + row * KP, g);
+        const float lse2 = (lse_nat == kNegInf) ? 0.f : lse_nat * kLog2e;
+        const int lo = qv ? key_lo(qi, a.W, a.bs) : INT_MAX;
+        const int hi = qi - 1;
+        const int wlo = max(0, qw - a.W), whi = min(qw + 15, T_ - 1) - 1;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int kt = qt - 1 + half;
+          const T* Ks = SK[half ? cur : prv];
+          const T* Vs = SV[half ? cur : prv];
+#pragma unroll
+          for (int st = 0; st < 4; ++st) {
+            const int s0 = kt * 64 + 16 * st;
+            if (s0 + 15 < wlo || s0 > whi) continue;  // uniform over the wave (also skips tile -1)
+            RowFrag<T, DQ> kf, vf;
+            kf.load_lds(Ks + (16 * st + r) * KP, g);
+            vf.load_lds(Vs + (16 * st + r) * KP, g);
+            const f32x4 sv = row_mma(kf, qf, f32x4{0.f, 0.f, 0.f, 0.f});    // S^T[key][query]
+            const f32x4 dp = row_mma(vf, dof, f32x4{0.f, 0.f, 0.f, 0.f});  // dP^T[key][query]
+            float ds[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int j = s0 + 4 * g + i;
+              const float pj = (j >= lo && j <= hi) ? fast_exp2(sv[i] * a.scale_log2 - lse2) : 0.f;
+              ds[i] = pj * (dp[i] - Dq);
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) dq[t] = col_mma_rm<KP>(Ks + (16 * st) * KP + 16 * t, ds, dq[t]);
+          }
+        }
+      }
+    } else {
+      // ---- dK / dV of this wave's 16 keys of tiles qt-1 (if owned: finished into SDK / SDV)
+      //      and qt (if full: parked in PKV) ----
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int kt = qt - 1 + half;
+        if (half == 0 ? !own_prev : !full) continue;  // uniform
+        const int kw = kt * 64 + w4 * 16, kj = kw + r;
+        const bool kv = kj < T_;
+        const int wqlo = kw + 1, wqhi = (int)min((int64_t)T_ - 1, (int64_t)kw + 15 + a.W);
+        f32x4 dk[NT], dv[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          dk[t] = half == 0 ? PKV[w4][t][lane] : f32x4{0.f, 0.f, 0.f, 0.f};
+          dv[t] = half == 0 ? PKV[w4][NT + t][lane] : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        RowFrag<T, DQ> kf, vf;
+        kf.load_lds((half ? SK[cur] : SK[prv]) + row * KP, g);
+        vf.load_lds((half ? SV[cur] : SV[prv]) + row * KP, g);
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const int s0 = q0 + 16 * st;
+          if (s0 >= qend || s0 + 15 < wqlo || s0 > wqhi) continue;  // uniform
+          RowFrag<T, DQ> qf, of;
+          qf.load_lds(SQ + (16 * st + r) * KP, g);
+          of.load_lds(SO + (16 * st + r) * KP, g);
+          const f32x4 sv = row_mma(qf, kf, f32x4{0.f, 0.f, 0.f, 0.f});  // S[query 4g+i][key r]
+          const f32x4 dp = row_mma(of, vf, f32x4{0.f, 0.f, 0.f, 0.f});  // dP[query][key]
+          float pp[4], ds[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int ql = 16 * st + 4 * g + i, qq = q0 + ql;
+            const bool ok = kv && kj >= los[ql] && kj <= qq - 1;
+            pp[i] = ok ? fast_exp2(sv[i] * a.scale_log2 - lse2s[ql]) : 0.f;
+            ds[i] = pp[i] * (dp[i] - Dss[ql]);
+          }
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            dv[t] = col_mma_rm<KP>(SO + (16 * st) * KP + 16 * t, pp, dv[t]);  // dV^T = dO^T P
+            dk[t] = col_mma_rm<KP>(SQ + (16 * st) * KP + 16 * t, ds, dk[t]);  // dK^T = Q^T dS
+          }
+        }
+        if (half == 0) {
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            float k4[4], v4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              k4[i] = dk[t][i] * a.scale;
+              v4[i] = dv[t][i];
+            }
+            store4<T>(SDK + row * KP + 16 * t + 4 * g, k4);
+            store4<T>(SDV + row * KP + 16 * t + 4 * g, v4);
+          }
+        } else {
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            PKV[w4][t][lane] = dk[t];
+            PKV[w4][NT + t][lane] = dv[t];
+          }
+        }
+      }
+    }
+
+    // ---- write-back: dq of this tile, dk / dv of key tile qt-1 (complete now) ----
+    __syncthreads();  // every wave is done reading SQ; SDK / SDV are complete
+    if (qrole && full) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        float v4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v4[i] = dq[t][i] * a.scale;
+        store4<T>(SQ + row * KP + 16 * t + 4 * g, v4);
+      }
+    }
+    __syncthreads();
+    if (full) store_tile<T, DHP, KP, NTHR>(static_cast<T*>(a.dq) + b * a.dq_sb + h * a.dq_sh, a.dq_st, SQ, q0, qend, Dh);
+    if (own_prev) {
+      const int p0 = q0 - 64;
+      store_tile<T, DHP, KP, NTHR>(static_cast<T*>(a.dk) + b * a.dk_sb + h * a.dk_sh, a.dk_st, SDK, p0, p0 + 64, Dh);
+      store_tile<T, DHP, KP, NTHR>(static_cast<T*>(a.dv) + b * a.dv_sb + h * a.dv_sh, a.dv_st, SDV, p0, p0 + 64, Dh);
+    }
+  }
+  // a segment that ends the sequence finishes its last key tile here (no next queries)
+  if (t1 == a.n_qt) {
+    const int p0 = (t1 - 1) * 64;
+    __syncthreads();  // the last step's stores from SDK / SDV are done
+    if (!qrole) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const f32x4 dk = PKV[w4][t][lane], dv = PKV[w4][NT + t][lane];
+        float k4[4], v4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          k4[i] = dk[i] * a.scale;
+          v4[i] = dv[i];
+        }
+        store4<T>(SDK + row * KP + 16 * t + 4 * g, k4);
+        store4<T>(SDV + row * KP + 16 * t + 4 * g, v4);
+      }
+    }
+    __syncthreads();
+    store_tile<T, DHP, KP, NTHR>(static_cast<T*>(a.dk) + b * a.dk_sb + h * a.dk_sh, a.dk_st, SDK, p0, T_, Dh);
+    store_tile<T, DHP, KP, NTHR>(static_cast<T*>(a.dv) + b * a.dv_sb + h * a.dv_sh, a.dv_st, SDV, p0, T_, Dh);
+  }
+}
+
 // Ordered sum of the per-tile gate partials: dgate[h][d] = sum over (b, tile) of part[h][which][d][b*n_qt + tile].
 // One wave per output: lanes stride over the contiguous partials, then a fixed butterfly.
 __global__ __launch_bounds__(256) void gate_reduce_kernel(const float* __restrict__ part, float* dgl, float* dgr,
@@ -477,6 +804,13 @@ void launch_fwd(const LocalArgs& a, hipStream_t stream) {
 }
 template <typename T, int DHP>
 void launch_bwd(const LocalArgs& a, hipStream_t stream) {
+  if constexpr (std::is_same_v<T, uint16_t> && DHP <= 96) {
+    if (a.W <= 64) {  // one pass: keys of a query tile span two key tiles
+      const int n_seg = (a.n_qt + kSegTiles - 1) / kSegTiles;
+      hipLaunchKernelGGL((local_bwd_fused_kernel<DHP>), dim3(a.B * a.H * n_seg), dim3(512), 0, stream, a);
+      return;
+    }
+  }
   hipLaunchKernelGGL((local_bwd_q_kernel<T, DHP>), dim3(a.B * a.H * a.n_qt), dim3(256), 0, stream, a);
   hipLaunchKernelGGL((local_bwd_kv_kernel<T, DHP>), dim3(a.B * a.H * a.n_qt), dim3(256), 0, stream, a);
 }
