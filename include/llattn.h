@@ -171,12 +171,19 @@ typedef struct llattn_gemm_desc {
   int32_t accumulate;  /* 1: add into C */
   const float* bias;   /* fp32 [N] or NULL */
   int32_t split_k;     /* 0: automatic */
-  float* a_colsum;     /* NULL, or fp32 [M] receiving sum_k A(m, k) (a_trans = 1 only): the bias gradient
-                          of a weight-gradient product, from the same pass over A */
 } llattn_gemm_desc;
 
 size_t llattn_gemm_workspace_size(const llattn_gemm_desc* d);
 int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Column sums out[n] = sum_m x[m][n] in fp32 of a bf16 matrix x (M rows of
+ * leading dimension ld): the bias gradient of a projection (sum over tokens of
+ * its output gradient).  Two passes through a workspace of
+ * llattn_colsum_workspace_size(M, N) bytes; deterministic.  Replaces the bias
+ * gradients of the block's nn.Linear layers (reference models.py:80-84). */
+size_t llattn_colsum_workspace_size(int32_t M, int32_t N);
+int32_t llattn_colsum(const void* x, int64_t ld, int32_t M, int32_t N, float* out, void* workspace,
+                      size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

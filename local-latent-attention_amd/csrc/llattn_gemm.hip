@@ -28,12 +28,6 @@
 // Split-K (for the weight gradients, whose M x N is small and K = tokens is
 // large): split s covers k in [s*K/S, (s+1)*K/S) and writes fp32 partials; an
 // ordered reduction adds them (deterministic, no atomics).
-//
-// Column sums (the bias gradient of a weight-gradient product, sum over tokens
-// of dy): with an m-contiguous A, each wave also adds up half of the A
-// fragments it feeds to the MFMAs (wave column wn takes fragments 4wn..4wn+3;
-// one v_dot2_f32_bf16 against (1, 1) per group of four MFMAs), so
-// sum_k A(m, k) comes out of the same pass over A at a balanced cost.
 #include "llattn_abi.h"
 #include "llattn_device.h"
 
@@ -54,8 +48,7 @@ struct GemmArgs {
   const uint16_t* B; int64_t ldb, b_bytes;
   void* C; int64_t ldc;
   const float* bias;
-  float* part;    // split-K partials [S][M][N]
-  float* colsum;  // sum_k A(m, k): [M] (one split) or per-split partials [S][M] after `part`
+  float* part;  // split-K partials [S][M][N]
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -198,14 +191,6 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
   // loads in issue order.  s_barrier is used without a fence: a fence would
   // also wait for the DMA that is meant to stay in flight.
   bf16x8 fa0[8], fb0[8], fa1[8], fb1[8];
-  // column sums of A over this split's k range (m-contiguous A only): this wave sums
-  // fragments i = 4wn .. 4wn+3, i.e. rows m0 + wm*128 + 16i + r
-  const bool do_cs = !AK && a.colsum != nullptr;
-  float cs[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) cs[i] = 0.f;
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
   auto step = [&](int kt, const bf16x8 (&ca)[8], const bf16x8 (&cb)[8], bf16x8 (&na)[8], bf16x8 (&nb)[8]) {
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(2 * DMA_PER_STEP));
@@ -223,12 +208,6 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
       for (int u = 0; u < 4; ++u) {  // B first: lane (r, g) accumulates C[m = r][n = 4g + e]
         const int n = 4 * q + u, i = n >> 3, j = n & 7;
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cb[j], ca[i], acc[i][j], 0, 0, 0);
-      }
-      if (!AK && do_cs) {  // k values 2h, 2h+1 (h = q % 4) of fragment 4wn + q/4
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-        const int f0 = q >> 2, h = q & 3;
-        const uint32_t u = wn ? __builtin_bit_cast(u32x4, ca[4 + f0])[h] : __builtin_bit_cast(u32x4, ca[f0])[h];
-        cs[f0] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u), ones, cs[f0], false);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -253,18 +232,6 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
   }
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));  // no DMA may land after the workgroup exits
-  if (do_cs) {  // lanes (r, g = 0..3) hold disjoint k subsets of row 16i + r: fixed-order butterfly
-    const int S = gridDim.x / tiles;
-    float* dst = S > 1 ? a.colsum + (int64_t)split * a.M : a.colsum;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float v = cs[i];
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
-      const int row = m0 + wm * 128 + 16 * (4 * wn + i) + r;
-      if (g == 0 && row < a.M) dst[row] = v;
-    }
-  }
 
   // ---- epilogue ----
   // Lane (r, g) holds C[m0 + wm*128 + 16i + r][n0 + wn*128 + 16j + 4g + e].  The
@@ -396,22 +363,11 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs a, in
   }
 }
 
-// colsum[m] = sum over splits of the per-split column sums (fixed order).
-__global__ __launch_bounds__(256) void colsum_reduce_kernel(const float* __restrict__ part, float* out, int M, int S) {
-  const int m = blockIdx.x * 256 + threadIdx.x;
-  if (m >= M) return;
-  float s = part[m];
-  for (int i = 1; i < S; ++i) s += part[(int64_t)i * M + m];
-  out[m] = s;
-}
-
 template <bool AK, bool BKM>
-void launch(const GemmArgs& a, int S, int c_dtype, float* colsum_out, hipStream_t st) {
+void launch(const GemmArgs& a, int S, int c_dtype, hipStream_t st) {
   const dim3 grid(a.tiles_m * a.tiles_n * S), block(256);
   if (S > 1) {
     hipLaunchKernelGGL((gemm_kernel<AK, BKM, EPI_PART>), grid, block, 0, st, a);
-    if (colsum_out)
-      hipLaunchKernelGGL(colsum_reduce_kernel, dim3((a.M + 255) / 256), block, 0, st, a.colsum, colsum_out, a.M, S);
     const int64_t quads = (int64_t)a.M * (a.N / 4);
     const dim3 rg((unsigned)((quads + 255) / 256));
     if (c_dtype == LLATTN_F32)
@@ -445,10 +401,7 @@ using namespace llattn::gemm;
 extern "C" size_t llattn_gemm_workspace_size(const llattn_gemm_desc* d) {
   if (!d) return 0;
   const int S = resolve_split(d);
-  if (S <= 1) return 0;
-  // C partials [S][M][N], then column-sum partials [S][M] (256-byte aligned)
-  const size_t part = ((size_t)S * d->M * d->N * sizeof(float) + 255) & ~size_t(255);
-  return part + (d->a_colsum ? (size_t)S * d->M * sizeof(float) : 0);
+  return S > 1 ? (size_t)S * d->M * d->N * sizeof(float) : 0;
 }
 
 extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_t workspace_bytes, void* stream) {
@@ -467,8 +420,6 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
   if (!d->A || !d->B || !d->C || !aligned16(d->A) || !aligned16(d->B) || !aligned16(d->C) ||
       (d->bias && !aligned16(d->bias)))
     return fail(LLATTN_ERR_LAYOUT, "llattn_gemm: operands must be non-null and 16-byte aligned");
-  if (d->a_colsum && !d->a_trans)
-    return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: column sums need an m-contiguous A (a_trans = 1)");
   if (d->lda % 8 || d->ldb % 8 || d->ldc % 8)
     return fail(LLATTN_ERR_LAYOUT, "llattn_gemm: lda, ldb and ldc must be multiples of 8 elements");
   if (d->lda < (d->a_trans ? d->M : d->K) || d->ldb < (d->b_trans ? d->N : d->K) || d->ldc < d->N)
@@ -491,20 +442,10 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
   a.C = d->C; a.ldc = d->ldc;
   a.bias = d->bias;
   a.part = static_cast<float*>(workspace);
-  float* cs_out = nullptr;
-  if (d->a_colsum) {
-    if (S > 1) {
-      a.colsum = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                          (((size_t)S * d->M * d->N * sizeof(float) + 255) & ~size_t(255)));
-      cs_out = d->a_colsum;
-    } else {
-      a.colsum = d->a_colsum;
-    }
-  }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (!d->a_trans && !d->b_trans) launch<true, true>(a, S, d->c_dtype, cs_out, st);
-  else if (!d->a_trans && d->b_trans) launch<true, false>(a, S, d->c_dtype, cs_out, st);
-  else if (d->a_trans && d->b_trans) launch<false, false>(a, S, d->c_dtype, cs_out, st);
-  else launch<false, true>(a, S, d->c_dtype, cs_out, st);
+  if (!d->a_trans && !d->b_trans) launch<true, true>(a, S, d->c_dtype, st);
+  else if (!d->a_trans && d->b_trans) launch<true, false>(a, S, d->c_dtype, st);
+  else if (d->a_trans && d->b_trans) launch<false, false>(a, S, d->c_dtype, st);
+  else launch<false, true>(a, S, d->c_dtype, st);
   return check_launch("llattn_gemm");
 }

@@ -40,8 +40,7 @@ class LlattnGemmDesc(ctypes.Structure):
     _fields_ = [("M", ctypes.c_int32), ("N", ctypes.c_int32), ("K", ctypes.c_int32), ("a_trans", ctypes.c_int32),
                 ("b_trans", ctypes.c_int32), ("A", ctypes.c_void_p), ("lda", ctypes.c_int64), ("B", ctypes.c_void_p),
                 ("ldb", ctypes.c_int64), ("C", ctypes.c_void_p), ("ldc", ctypes.c_int64), ("c_dtype", ctypes.c_int32),
-                ("accumulate", ctypes.c_int32), ("bias", ctypes.c_void_p), ("split_k", ctypes.c_int32),
-                ("a_colsum", ctypes.c_void_p)]
+                ("accumulate", ctypes.c_int32), ("bias", ctypes.c_void_p), ("split_k", ctypes.c_int32)]
 
 
 _P = ctypes.c_void_p
@@ -63,6 +62,8 @@ SIGNATURES = {
     "llattn_local_gate_bwd": (_I32, [_S, _T, _T, _T, _T, _P, _P, _T, _P, _P, _T, _T, _T, _T, _T, _P, _P, _P, _SZ, _P]),
     "llattn_gemm_workspace_size": (_SZ, [_G]),
     "llattn_gemm": (_I32, [_G, _P, _SZ, _P]),
+    "llattn_colsum_workspace_size": (_SZ, [_I32, _I32]),
+    "llattn_colsum": (_I32, [_P, _I64, _I32, _I32, _P, _P, _SZ, _P]),
 }
 
 _lib = None

@@ -28,18 +28,15 @@ def _check2d(name: str, t: torch.Tensor) -> None:
 
 
 def _run(M: int, N: int, K: int, A: torch.Tensor, a_trans: bool, B: torch.Tensor, b_trans: bool, C: torch.Tensor,
-         bias: torch.Tensor | None, accumulate: bool, split_k: int = 0, colsum: torch.Tensor | None = None) -> None:
+         bias: torch.Tensor | None, accumulate: bool, split_k: int = 0) -> None:
     L.require_gpu(A, B, C)
     if C.dim() != 2 or C.stride(1) != 1 or C.dtype not in (torch.bfloat16, torch.float32):
         raise ValueError("output must be a 2-D bf16 / fp32 view with a contiguous inner dimension")
     if bias is not None and (bias.dtype != torch.float32 or not bias.is_contiguous() or bias.numel() != N):
         raise ValueError(f"bias must be a contiguous fp32 vector of {N} elements")
-    if colsum is not None and (colsum.dtype != torch.float32 or not colsum.is_contiguous() or colsum.numel() != M):
-        raise ValueError(f"colsum must be a contiguous fp32 vector of {M} elements")
     desc = L.LlattnGemmDesc(M, N, K, int(a_trans), int(b_trans), A.data_ptr(), A.stride(0), B.data_ptr(),
                             B.stride(0), C.data_ptr(), C.stride(0), L.dtype_code(C.dtype), int(accumulate),
-                            None if bias is None else bias.data_ptr(), split_k,
-                            None if colsum is None else colsum.data_ptr())
+                            None if bias is None else bias.data_ptr(), split_k)
     lib = L.load()
     nws = lib.llattn_gemm_workspace_size(ctypes.byref(desc))
     ws = torch.empty((max(nws, 1),), dtype=torch.uint8, device=C.device) if nws else None
@@ -78,9 +75,8 @@ def matmul_nn(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None,
 
 
 def matmul_tn(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None, accumulate: bool = False,
-              split_k: int = 0, colsum: torch.Tensor | None = None) -> torch.Tensor:
-    """``a [K, M]^T @ b [K, N]`` -> fp32 ``[M, N]`` (weight gradients: K = tokens).  With ``colsum`` (fp32
-    ``[M]``), also writes ``a.sum(0)`` -- the bias gradient -- from the same pass over ``a``."""
+              split_k: int = 0) -> torch.Tensor:
+    """``a [K, M]^T @ b [K, N]`` -> fp32 ``[M, N]`` (weight gradients: K = tokens)."""
     _check2d("a", a)
     _check2d("b", b)
     K, M = a.shape
@@ -89,5 +85,20 @@ def matmul_tn(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None,
         raise ValueError(f"a is [{K}, {M}] but b is {tuple(b.shape)}")
     if out is None:
         out = torch.empty((M, N), dtype=torch.float32, device=a.device)
-    _run(M, N, K, a, True, b, True, out, None, accumulate, split_k, colsum)
+    _run(M, N, K, a, True, b, True, out, None, accumulate, split_k)
+    return out
+
+
+def colsum(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 ``x.sum(0)`` of a bf16 ``[M, N]`` view (the bias gradient of a projection)."""
+    _check2d("x", x)
+    L.require_gpu(x)
+    M, N = x.shape
+    if out is None:
+        out = torch.empty((N,), dtype=torch.float32, device=x.device)
+    lib = L.load()
+    nws = lib.llattn_colsum_workspace_size(M, N)
+    ws = torch.empty((max(nws, 1),), dtype=torch.uint8, device=x.device)
+    from .ops import _call
+    _call("llattn_colsum", x.data_ptr(), x.stride(0), M, N, out.data_ptr(), ws.data_ptr(), nws, L.stream_ptr(x.device))
     return out

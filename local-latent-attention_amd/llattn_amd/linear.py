@@ -48,12 +48,11 @@ def input_grad(dy2: torch.Tensor, w: torch.Tensor, library: bool = False) -> tor
 
 def weight_grad(dy2: torch.Tensor, x2: torch.Tensor, bias_grad: bool = False):
     """fp32 ``dy2^T @ x2`` for bf16 ``dy2 [K, N]``, ``x2 [K, D]`` (K = tokens), and with ``bias_grad`` also the
-    fp32 column sums of ``dy2`` (the bias gradient, from the same pass over ``dy2``): returns ``(dW, db)``."""
+    fp32 column sums of ``dy2`` (the bias gradient): returns ``(dW, db)``."""
     K, N = dy2.shape
     D = x2.shape[1]
     if tn_supported(K, N, D) and dy2.stride(1) == 1 and x2.stride(1) == 1:
-        db = torch.empty((N,), dtype=torch.float32, device=dy2.device) if bias_grad else None
-        return gemm.matmul_tn(dy2, x2, colsum=db), db
+        return gemm.matmul_tn(dy2, x2), (gemm.colsum(dy2) if bias_grad else None)
     # shapes the MFMA kernel does not tile (token counts that are not a multiple of 64): library GEMM
     return torch.mm(dy2.t(), x2).float(), (dy2.sum(0, dtype=torch.float32) if bias_grad else None)
 

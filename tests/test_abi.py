@@ -24,7 +24,7 @@ def _declared_functions():
 def test_library_exports_every_declared_symbol():
     L, lib = _lib()
     names = _declared_functions()
-    assert len(names) == 11, names
+    assert len(names) == 13, names
     for n in names:
         assert hasattr(lib, n), n
         assert n in L.SIGNATURES, f"{n} has no ctypes signature"
@@ -154,6 +154,18 @@ def test_gemm_split_k_needs_workspace():
     # a full-chip output needs no split
     d = _gemm_desc(L, M=32768, N=4736, K=1408, lda=1408, ldb=1408, ldc=4736)
     assert lib.llattn_gemm_workspace_size(ctypes.byref(d)) == 0
+
+
+def test_colsum_validation():
+    L, lib = _lib()
+    assert lib.llattn_colsum_workspace_size(32768, 1408) == 64 * 1408 * 4
+    assert lib.llattn_colsum_workspace_size(10, 16) == 1 * 16 * 4
+    rc = lib.llattn_colsum(ctypes.c_void_p(0x1000), 16, 0, 16, ctypes.c_void_p(0x2000), None, 0, None)
+    assert rc == L.ERR_SHAPE
+    rc = lib.llattn_colsum(ctypes.c_void_p(0x1000), 12, 4, 12, ctypes.c_void_p(0x2000), None, 0, None)
+    assert rc == L.ERR_LAYOUT and b"multiples of 8" in lib.llattn_last_error()
+    rc = lib.llattn_colsum(ctypes.c_void_p(0x1000), 16, 4, 16, ctypes.c_void_p(0x2000), None, 0, None)
+    assert rc == L.ERR_WORKSPACE
 
 
 # ---------------------------------------------------------------- host logic

@@ -56,11 +56,23 @@ def test_matmul_tn_fp32_out(K, M, N, S):
     print("case: tn", K, M, N, S, flush=True)
     g = torch.Generator(device=dev).manual_seed(K + M)
     a, b = _rand(K, M, gen=g, dev=dev), _rand(K, N, gen=g, dev=dev)
-    cs = torch.empty(M, device=dev)
-    got = gemm.matmul_tn(a, b, split_k=S, colsum=cs)
+    got = gemm.matmul_tn(a, b, split_k=S)
     assert got.dtype == torch.float32
     assert _err(got, a.float().T @ b.float()) < FP32_TOL
-    assert _err(cs, a.float().sum(0)) < FP32_TOL      # column sums (bias gradient) from the same pass
+
+
+@pytest.mark.parametrize("M,N", [(1, 8), (97, 40), (1000, 136), (32768, 1408), (32768, 4736)])
+def test_colsum(M, N):
+    """Bias-gradient column sums, including ragged stripes and row blocks, and their determinism."""
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: colsum", M, N, flush=True)
+    g = torch.Generator(device=dev).manual_seed(M + N)
+    big = _rand(M, N + 16, gen=g, dev=dev)
+    x = big[:, 8:8 + N]                       # strided view
+    got = gemm.colsum(x)
+    assert _err(got, x.float().sum(0)) < FP32_TOL
+    torch.testing.assert_close(got, gemm.colsum(x), rtol=0, atol=0)
 
 
 def test_accumulate_and_strided_views():
