@@ -59,7 +59,8 @@ def weight_grad(dy2: torch.Tensor, x2: torch.Tensor, bias_grad: bool = False):
 
 class _Project(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, library, *params):
+    def forward(ctx, x, library, pools, *params):
+        ctx.set_materialize_grads(False)
         ws, bs = params[0::2], params[1::2]
         has_bias = bs[0] is not None
         K = x.shape[-1]
@@ -77,38 +78,67 @@ class _Project(torch.autograd.Function):
                     bcat[o:o + n].copy_(b)
                 o += n
             y = linear_fwd(x2, wcat, bcat, library)
+            pooled = []
+            if pools:
+                from .ops import _contig, pool_fwd_into
+                xc = x2.view(x.shape) if x.dtype == BF16 else _contig(x)
+                for seg, n_seg, divisor in pools:
+                    p = torch.empty((x.shape[0], n_seg, K), dtype=x.dtype, device=x.device)
+                    pool_fwd_into(xc, p, seg, n_seg, divisor)
+                    pooled.append(p)
         ctx.save_for_backward(x2, wcat)
         ctx.meta = (tuple(x.shape[:-1]), rows, has_bias, [w.dtype for w in ws], [None if b is None else b.dtype
-                                                                                 for b in bs], x.dtype, library)
-        return y.view(*x.shape[:-1], sum(rows))
+                                                                                 for b in bs], x.dtype, library,
+                    tuple(pools))
+        return (y.view(*x.shape[:-1], sum(rows)), *pooled)
 
     @staticmethod
-    def backward(ctx, dy):
+    def backward(ctx, dy, *dpooled):
         x2, wcat = ctx.saved_tensors
-        lead, rows, has_bias, wdt, bdt, xdt, library = ctx.meta
+        lead, rows, has_bias, wdt, bdt, xdt, library, pools = ctx.meta
         N = sum(rows)
+        K = x2.shape[1]
+        dx = dw = db = None
         with torch.autocast(device_type="cuda", enabled=False):
-            dy2 = dy.reshape(-1, N).to(BF16)
-            if not dy2.is_contiguous():
-                dy2 = dy2.contiguous()
-            dx = input_grad(dy2, wcat, library).view(*lead, x2.shape[1]).to(xdt) if ctx.needs_input_grad[0] else None
-            dw, db = weight_grad(dy2, x2, has_bias)
+            if dy is not None:
+                dy2 = dy.reshape(-1, N).to(BF16)
+                if not dy2.is_contiguous():
+                    dy2 = dy2.contiguous()
+                if ctx.needs_input_grad[0]:
+                    dx = input_grad(dy2, wcat, library).view(*lead, K).to(xdt)
+                dw, db = weight_grad(dy2, x2, has_bias)
+            if ctx.needs_input_grad[0] and any(g is not None for g in dpooled):
+                # pooling backward accumulates straight into the projection's input gradient
+                from .ops import _contig, pool_bwd_into
+                if dx is None:
+                    dx = torch.zeros((*lead, K), dtype=xdt, device=x2.device)
+                elif not dx.is_contiguous():
+                    dx = dx.contiguous()
+                for g, (seg, n_seg, divisor) in zip(dpooled, pools):
+                    if g is not None:
+                        pool_bwd_into(_contig(g.to(xdt)), dx, seg, n_seg, divisor, accumulate=True)
         grads = []
         o = 0
         for n, wd, bd in zip(rows, wdt, bdt):
-            grads.append(dw[o:o + n].to(wd))
+            grads.append(None if dw is None else dw[o:o + n].to(wd))
             grads.append(None if db is None else db[o:o + n].to(bd))
             o += n
-        return (dx, None, *grads)
+        return (dx, None, None, *grads)
 
 
-def project(x: torch.Tensor, *linears: torch.nn.Linear, library: bool = False) -> torch.Tensor:
+def project(x: torch.Tensor, *linears: torch.nn.Linear, library: bool = False, pools=()):
     """bf16 ``x @ [W_1; W_2; ...]^T + [b_1; b_2; ...]`` (all layers share the input width); backward gives
     fp32 weight and bias gradients in the parameters' dtypes.  ``library=True`` keeps the forward and
     input-gradient products on hipBLASLt (the weight gradient always runs on the MFMA kernel when its shape
     allows): at the block's widest projection (config 2: 32768 x 4736 x 1408) the library kernel is still
-    the faster of the two."""
+    the faster of the two.
+
+    ``pools``: ``(seg, n_seg, divisor)`` segment poolings of the same ``x [B, T, K]`` (as
+    :func:`llattn_amd.ops.pool`) returned after the projection, ``(y, pooled_1, ...)``; their backward adds
+    into the projection's input gradient in place, so the block's input gradient is formed once.  Without
+    ``pools`` the projection alone is returned."""
     params = []
     for lin in linears:
         params += [lin.weight, lin.bias]
-    return _Project.apply(x, library, *params)
+    out = _Project.apply(x, library, tuple(pools), *params)
+    return out if pools else out[0]

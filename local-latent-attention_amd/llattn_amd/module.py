@@ -113,12 +113,18 @@ class LocalLatentAttentionTriton(nn.Module):
         macro = self.latent_query_block_size > 1
         # bf16 autocast (the reference trainer's mode): projections in bf16 with fp32 weight gradients
         bf16 = torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
-        if macro:
-            qkvr = project(x, self.qkv_proj, library=True) if bf16 else self.qkv_proj(x)
-            pq = pool(x, lay.q_block, lay.n_q, L.DIV_SEG)
-            rq = project(pq, self.rq_proj) if bf16 else self.rq_proj(pq)
+        latents = (lay.chunk, lay.n_chunks, L.DIV_COUNT)
+        pooled = None
+        if macro and bf16:
+            # both poolings of x ride on the projection, whose backward adds their gradients in place
+            qkvr, pq, pooled = project(x, self.qkv_proj, library=True,
+                                       pools=[(lay.q_block, lay.n_q, L.DIV_SEG), latents])
+            rq = project(pq, self.rq_proj)
+        elif macro:
+            qkvr = self.qkv_proj(x)
+            rq = self.rq_proj(pool(x, lay.q_block, lay.n_q, L.DIV_SEG))
         elif bf16:
-            qkvr = project(x, self.qkv_proj, self.rq_proj, library=True)
+            qkvr, pooled = project(x, self.qkv_proj, self.rq_proj, library=True, pools=[latents])
             rq = None
         else:
             w = torch.cat([self.qkv_proj.weight, self.rq_proj.weight], dim=0)
@@ -127,7 +133,7 @@ class LocalLatentAttentionTriton(nn.Module):
             rq = None
         if prof is not None:
             prof.lap("qkv_ms")
-        gkgv = self.rkv_proj(pool(x, lay.chunk, lay.n_chunks, L.DIV_COUNT))
+        gkgv = self.rkv_proj(pool(x, *latents) if pooled is None else pooled)
         if prof is not None:
             prof.lap("pool_ms")
         rqc = None if rq is None else rq.to(qkvr.dtype)

@@ -128,3 +128,35 @@ def test_project_matches_fp32_linear():
     assert _err(x.grad, xr.grad) < BF16_TOL
     assert _err(torch.cat([l1.weight.grad, l2.weight.grad]), wr.grad) < 1e-3
     assert _err(torch.cat([l1.bias.grad, l2.bias.grad]), br.grad) < 1e-3
+
+
+def test_project_with_pools_matches_fp32():
+    """Poolings that ride on the projection: forward values and the input gradient, which sums the
+    projection's and both poolings' gradients in place (ragged last segment in the second pooling)."""
+    from llattn_amd import _lib as L
+    from llattn_amd.linear import project
+    dev = require_cuda()
+    print("case: project+pools", flush=True)
+    torch.manual_seed(1)
+    lin = torch.nn.Linear(256, 320).to(dev)
+    B, T, K = 2, 512, 256
+    x = torch.randn(B, T, K, device=dev).to(torch.bfloat16).requires_grad_(True)
+    pools = [(64, 8, L.DIV_COUNT), (100, 6, L.DIV_SEG)]
+    with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        y, p1, p2 = project(x, lin, library=False, pools=pools)
+    dy = torch.randn_like(y, dtype=torch.float32).to(torch.bfloat16)
+    d1 = torch.randn_like(p1, dtype=torch.float32).to(torch.bfloat16)
+    d2 = torch.randn_like(p2, dtype=torch.float32).to(torch.bfloat16)
+    torch.autograd.backward([y, p1, p2], [dy, d1, d2])
+
+    xr = x.detach().float().requires_grad_(True)
+    wr = lin.weight.detach().to(torch.bfloat16).float()
+    br = lin.bias.detach().to(torch.bfloat16).float()
+    yr = torch.nn.functional.linear(xr, wr, br)
+    r1 = xr.view(B, 8, 64, K).mean(2)
+    pad = torch.nn.functional.pad(xr, (0, 0, 0, 600 - T))
+    r2 = pad.view(B, 6, 100, K).sum(2) / 100
+    torch.autograd.backward([yr, r1, r2], [dy.float(), d1.float(), d2.float()])
+    assert _err(y, yr) < BF16_TOL
+    assert _err(p1, r1) < BF16_TOL and _err(p2, r2) < BF16_TOL
+    assert _err(x.grad, xr.grad) < BF16_TOL
