@@ -189,6 +189,18 @@ __device__ __forceinline__ float max_groups(float x) {
   x = fmaxf(x, __shfl_xor(x, 32));
   return x;
 }
+// Workgroup barrier that orders LDS only: the fences are limited to the local
+// address space, so the wave waits for its own LDS operations (lgkmcnt(0)) but
+// global loads and stores stay in flight across it (a full __syncthreads also
+// waits for vmcnt(0), which would drain every prefetch issued before it).  Only
+// for kernels in which no wave reads global memory that another wave of the
+// workgroup wrote.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // sum over the 16 lanes of a group (same g), valid in the group's last lane
 // (r = 15): a DPP row_shr ladder (VALU; out-of-row sources read 0)
 __device__ __forceinline__ float sum_rows16_last(float x) {
@@ -196,6 +208,14 @@ __device__ __forceinline__ float sum_rows16_last(float x) {
   x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x112, 0xf, 0xf, true));
   x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x114, 0xf, 0xf, true));
   x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x118, 0xf, 0xf, true));
+  return x;
+}
+// sum over each aligned group of 8 lanes, in every lane of the group: quad
+// swaps (quad_perm [1,0,3,2], [2,3,0,1]) then row_half_mirror (lane i <- 7-i)
+__device__ __forceinline__ float sum_lanes8(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xB1, 0xf, 0xf, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x4E, 0xf, 0xf, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x141, 0xf, 0xf, true));
   return x;
 }
 // sum over the 16 lanes of a group (same g)
@@ -232,6 +252,25 @@ __device__ __forceinline__ void stage_rows(T* lds, const T* base, int64_t st, in
 // bf16: one ds_read_b64_tr_b16 gives lane (r, g) the four elements
 // tile[k0 + 4g + i][m0 + r], i = 0..3 (within each 16-lane group, lane j
 // supplies the address of row 4g + j/4, columns 4(j%4) .. 4(j%4)+3).
+// two floats -> packed bf16 pair (round to nearest even; one v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+}
+__device__ __forceinline__ i16x4 pack_bf16x4(const float b[4]) {
+  const uint2 u = make_uint2(pack_bf16x2(b[0], b[1]), pack_bf16x2(b[2], b[3]));
+  return __builtin_bit_cast(i16x4, u);
+}
+// col_mma_rm with the lane's four B values already packed (convert once, use for every t)
+template <int P>
+__device__ __forceinline__ f32x4 col_mma_rm(const uint16_t* base, const i16x4 bv, f32x4 acc) {
+  typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const uint16_t* p = base + (4 * g + (j >> 2)) * P + 4 * (j & 3);
+  const bf16x4 av = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)(p));
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, av), bv, acc, 0, 0, 0);
+}
 template <int P>
 __device__ __forceinline__ f32x4 col_mma_rm(const uint16_t* base, const float b[4], f32x4 acc) {
   typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));

@@ -26,7 +26,7 @@
 // layout each comes from.
 //
 // Split-K (for the weight gradients, whose M x N is small and K = tokens is
-// large): split s covers k in [s*K/S, (s+1)*K/S) and writes fp32 partials; an
+// large): split s covers the 64-wide k steps [s*P/S, (s+1)*P/S) of P and writes fp32 partials; an
 // ordered reduction adds them (deterministic, no atomics).
 #include "llattn_abi.h"
 #include "llattn_device.h"
@@ -43,7 +43,7 @@ constexpr int DMA_PER_STEP = 2 * DMA_PER_TILE;       // per wave
 enum Epi { EPI_BF16 = 0, EPI_F32 = 1, EPI_PART = 2 };
 
 struct GemmArgs {
-  int M, N, K, k_split, tiles_m, tiles_n, accumulate;
+  int M, N, K, k_pairs, n_split, tiles_m, tiles_n, accumulate;  // k_pairs: 64-wide k steps
   const uint16_t* A; int64_t lda, a_bytes;
   const uint16_t* B; int64_t ldb, b_bytes;
   void* C; int64_t ldc;
@@ -155,7 +155,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
   const int tm = first_m + (t % (GM * a.tiles_n)) % gm;
   const int tn = (t % (GM * a.tiles_n)) / gm;
   const int m0 = tm * BM, n0 = tn * BN;
-  const int kbeg = split * a.k_split, nk = a.k_split / BK;
+  // split s takes 64-wide steps [s P / S, (s+1) P / S): uneven by at most one step
+  const int p0 = split * a.k_pairs / a.n_split, p1 = (split + 1) * a.k_pairs / a.n_split;
+  const int kbeg = p0 * 2 * BK, nk = 2 * (p1 - p0);
 
   f32x4 acc[8][8];
 #pragma unroll
@@ -335,7 +337,15 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs a, in
   const int64_t mn = (int64_t)a.M * a.N;
   const float* p = a.part + (int64_t)row * a.N + col;
   float4 s = *reinterpret_cast<const float4*>(p);
-  for (int i = 1; i < S; ++i) {
+  int i = 1;
+  for (; i + 4 <= S; i += 4) {  // four partials in flight, added in split order
+    float4 x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) x[u] = *reinterpret_cast<const float4*>(p + (i + u) * mn);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) { s.x += x[u].x; s.y += x[u].y; s.z += x[u].z; s.w += x[u].w; }
+  }
+  for (; i < S; ++i) {
     const float4 x = *reinterpret_cast<const float4*>(p + i * mn);
     s.x += x.x; s.y += x.y; s.z += x.z; s.w += x.w;
   }
@@ -381,15 +391,16 @@ void launch(const GemmArgs& a, int S, int c_dtype, hipStream_t st) {
   }
 }
 
-// Number of K splits: 1 when the output tiles alone fill the chip, otherwise
-// the smallest power of two that gives at least one workgroup per CU while
-// every split keeps a whole number of 64-wide k steps.
+// Number of K splits: 1 when the output tiles alone fill most of the chip,
+// otherwise as many as keep every workgroup in ONE round on the 256 CUs (one
+// 128 KB workgroup per CU) with at least four 64-wide k steps per split.  A
+// second, mostly idle round of workgroups costs more than the partials.
 int resolve_split(const llattn_gemm_desc* d) {
   if (d->split_k > 0) return d->split_k;
   const int64_t tiles = (int64_t)((d->M + BM - 1) / BM) * ((d->N + BN - 1) / BN);
-  int s = 1;
-  while (tiles * s < 224 && d->K % (4 * s * BK) == 0 && d->K / (2 * s) >= 8 * BK) s *= 2;
-  return s;
+  if (tiles >= 224 || d->K % (2 * BK)) return 1;
+  const int64_t s = std::min<int64_t>(256 / tiles, d->K / (2 * BK) / 4);
+  return s < 1 ? 1 : (int)s;
 }
 
 }  // namespace gemm
@@ -411,9 +422,11 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
   if (d->c_dtype != LLATTN_BF16 && d->c_dtype != LLATTN_F32)
     return fail(LLATTN_ERR_DTYPE, "llattn_gemm: unknown output dtype %d", d->c_dtype);
   const int S = resolve_split(d);
-  if (S < 1 || d->K % (S * 2 * BK) != 0)
-    return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: K=%d must be a multiple of %d (%d x %d splits)", d->K,
-                S * 2 * BK, 2 * BK, S);
+  if (d->K % (2 * BK) != 0)
+    return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: K=%d must be a multiple of %d", d->K, 2 * BK);
+  if (S < 1 || S > d->K / (2 * BK))
+    return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: %d K splits for K=%d: at most one per %d-wide k step", S, d->K,
+                2 * BK);
   if (d->N % 8 != 0 || (d->a_trans && d->M % 8 != 0))
     return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: N (and M of a transposed A) must be multiples of 8 (M=%d N=%d)",
                 d->M, d->N);
@@ -434,7 +447,7 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
     return fail(LLATTN_ERR_WORKSPACE, "llattn_gemm: %d K splits need %zu workspace bytes (got %zu)", S, need,
                 workspace_bytes);
   GemmArgs a{};
-  a.M = d->M; a.N = d->N; a.K = d->K; a.k_split = d->K / S;
+  a.M = d->M; a.N = d->N; a.K = d->K; a.k_pairs = d->K / (2 * BK); a.n_split = S;
   a.tiles_m = (d->M + BM - 1) / BM; a.tiles_n = (d->N + BN - 1) / BN;
   a.accumulate = d->accumulate;
   a.A = static_cast<const uint16_t*>(d->A); a.lda = d->lda; a.a_bytes = a_bytes;

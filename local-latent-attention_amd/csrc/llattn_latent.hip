@@ -70,10 +70,10 @@ __global__ __launch_bounds__(256) void latent_fwd_kernel(const LatentArgs a) {
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int n0 = 0; n0 < nmax; n0 += 64) {
-    __syncthreads();
+    lds_barrier();
     stage_rows<T, DHP, KP>(Ks, gkb, a.gk_sn, n0, nmax, a.Ldh);
     stage_rows_t<T, DHP, KP, false>(nullptr, Vt, gvb, a.gv_sn, n0, nmax, a.Ldh);
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const int s0 = n0 + 16 * st;
@@ -135,14 +135,14 @@ __global__ __launch_bounds__(256) void latent_bwd_q_kernel(const LatentArgs a) {
   // pass 1: D = sum_n P_n dP_n
   float D = 0.f;
   for (int n0 = 0; n0 < nmax; n0 += 64) {
-    __syncthreads();
+    lds_barrier();
     if (single) {
       stage_rows_t<T, DHP, KP, true>(Ks, Kt, gkb, a.gk_sn, n0, nmax, a.Ldh);
     } else {
       stage_rows<T, DHP, KP>(Ks, gkb, a.gk_sn, n0, nmax, a.Ldh);
     }
     stage_rows<T, DHP, KP>(Vs, gvb, a.gv_sn, n0, nmax, a.Ldh);
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const int s0 = n0 + 16 * st;
@@ -166,10 +166,10 @@ __global__ __launch_bounds__(256) void latent_bwd_q_kernel(const LatentArgs a) {
   for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int n0 = 0; n0 < nmax; n0 += 64) {
     if (!single) {
-      __syncthreads();
+      lds_barrier();
       stage_rows_t<T, DHP, KP, true>(Ks, Kt, gkb, a.gk_sn, n0, nmax, a.Ldh);
       stage_rows<T, DHP, KP>(Vs, gvb, a.gv_sn, n0, nmax, a.Ldh);
-      __syncthreads();
+      lds_barrier();
     }
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
@@ -242,7 +242,7 @@ __global__ __launch_bounds__(256) void latent_bwd_kv_kernel(const LatentArgs a) 
   const int qbeg = max(seg * kSeg, s_first);
   const int qend = min((seg + 1) * kSeg, a.n_q);
   for (int q0 = qbeg; q0 < qend; q0 += 64) {
-    __syncthreads();
+    lds_barrier();
     stage_rows_t<T, DHP, KP, true>(Qs, Qt, rqb, a.rq_sn, q0, qend, a.Ldh);
     stage_rows_t<T, DHP, KP, true>(Os, Ot, dlb, a.do_sn, q0, qend, a.Ldh);
     if (tid < 64) {
@@ -258,7 +258,7 @@ __global__ __launch_bounds__(256) void latent_bwd_kv_kernel(const LatentArgs a) 
         vis[tid] = 0;
       }
     }
-    __syncthreads();
+    lds_barrier();
     const int s0 = q0 + 16 * wave;  // each wave takes one 16-query sub-tile
     if (s0 < qend) {
       RowFrag<T, DQ> qf, of;
@@ -282,7 +282,7 @@ __global__ __launch_bounds__(256) void latent_bwd_kv_kernel(const LatentArgs a) 
   }
   // sum the four waves in order: red[which][dim][latent]
   for (int w = 0; w < 4; ++w) {
-    __syncthreads();
+    lds_barrier();
     if (wave == w) {
 #pragma unroll
       for (int t = 0; t < NT; ++t)
@@ -296,7 +296,7 @@ __global__ __launch_bounds__(256) void latent_bwd_kv_kernel(const LatentArgs a) 
         }
     }
   }
-  __syncthreads();
+  lds_barrier();
   float* part = a.part + ((((int64_t)b * a.Lh + lh) * a.n_seg + seg) * a.n_lt * 16) * 2 * a.Ldh;
   for (int idx = tid; idx < 16 * 2 * a.Ldh; idx += 256) {
     const int n = idx / (2 * a.Ldh), which = (idx / a.Ldh) % 2, d = idx % a.Ldh;

@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void local_fwd_kernel(const LocalArgs a) {
   }
   qreg.template store<KP>(S0);
   kreg.template store<KP>(S1);
-  __syncthreads();
+  lds_barrier();
   RowFrag<T, DQ> qf;
   qf.load_lds(S0 + row * KP, g);
 
@@ -95,10 +95,10 @@ __global__ __launch_bounds__(256) void local_fwd_kernel(const LocalArgs a) {
 
   const int wlo = max(0, qw - a.W), whi = min(qw + 15, T_ - 1) - 1;  // keys any query of this wave may use
   for (int k0 = kbeg; k0 < kend; k0 += 64) {
-    __syncthreads();  // S0 (queries / previous values) and S1 (previous keys) are free
+    lds_barrier();  // S0 (queries / previous values) and S1 (previous keys) are free
     vreg.template store<KP>(S0);
     if (k0 != kbeg) kreg.template store<KP>(S1);
-    __syncthreads();
+    lds_barrier();
     if (k0 + 64 < kend) {  // the next tile's loads overlap this tile's math
       kreg.load(kbase, a.k_st, k0 + 64, kend, Dh);
       vreg.load(vbase, a.v_st, k0 + 64, kend, Dh);
@@ -136,9 +136,9 @@ __global__ __launch_bounds__(256) void local_fwd_kernel(const LocalArgs a) {
       }
     }
   }
-  __syncthreads();  // S0 / S1 free
+  lds_barrier();  // S0 / S1 free
   rreg.template store<KP>(S0);
-  __syncthreads();
+  lds_barrier();
 
   // ---- epilogue: normalise, gate, mix; rows go back through LDS ----
   const float l = sum_groups(l_run);
@@ -177,7 +177,7 @@ __global__ __launch_bounds__(256) void local_fwd_kernel(const LocalArgs a) {
     a.lse[idx] = l > 0.f ? (m_run + __log2f(l)) * kLn2 : kNegInf;
     a.w[idx] = wl;
   }
-  __syncthreads();
+  lds_barrier();
   store_tile<T, DHP, KP>(static_cast<T*>(a.y) + b * a.y_sb + h * a.y_sh, a.y_st, S0, q0, qend, Dh);
   store_tile<T, DHP, KP>(static_cast<T*>(a.ol) + b * a.o_sb + h * a.o_sh, a.o_st, S1, q0, qend, Dh);
 }
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(256) void local_bwd_q_kernel(const LocalArgs a) {
   dyreg.template store<KP>(S0);
   olreg.template store<KP>(S1);
   rreg.template store<KP>(S2);
-  __syncthreads();
+  lds_barrier();
 
   const float* glp = a.gl + h * a.gate_hs;
   const float* grp = a.gr + h * a.gate_hs;
@@ -266,7 +266,7 @@ __global__ __launch_bounds__(256) void local_bwd_q_kernel(const LocalArgs a) {
   }
   Dq = sum_groups(Dq);
   if (qv && g == 0) a.Dsum[hrow + qi] = Dq;
-  __syncthreads();  // dO / dremote tiles complete; o_local no longer needed
+  lds_barrier();  // dO / dremote tiles complete; o_local no longer needed
   qreg.template store<KP>(S1);
   store_tile<T, DHP, KP>(static_cast<T*>(a.dO) + ((int64_t)b * T_ * a.H + h) * Dh, (int64_t)a.H * Dh, S0, q0, qend,
                          Dh);
@@ -287,7 +287,7 @@ __global__ __launch_bounds__(256) void local_bwd_q_kernel(const LocalArgs a) {
   RowTile<T, DHP> kreg, vreg;
   kreg.load(kbase, a.k_st, kbeg, kend, Dh);
   vreg.load(vbase, a.v_st, kbeg, kend, Dh);
-  __syncthreads();
+  lds_barrier();
   RowFrag<T, DQ> qf, dof;
   qf.load_lds(S1 + row * KP, g);
   dof.load_lds(S0 + row * KP, g);
@@ -301,10 +301,10 @@ __global__ __launch_bounds__(256) void local_bwd_q_kernel(const LocalArgs a) {
   for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int wlo = max(0, qw - a.W), whi = min(qw + 15, T_ - 1) - 1;
   for (int k0 = kbeg; k0 < kend; k0 += 64) {
-    __syncthreads();  // fragments read / previous tile consumed
+    lds_barrier();  // fragments read / previous tile consumed
     kreg.template store<KP>(S0);
     vreg.template store<KP>(S1);
-    __syncthreads();
+    lds_barrier();
     if (k0 + 64 < kend) {
       kreg.load(kbase, a.k_st, k0 + 64, kend, Dh);
       vreg.load(vbase, a.v_st, k0 + 64, kend, Dh);
@@ -336,7 +336,7 @@ __global__ __launch_bounds__(256) void local_bwd_q_kernel(const LocalArgs a) {
     for (int i = 0; i < 4; ++i) v4[i] = acc[t][i] * a.scale;
     store4<T>(S2 + row * KP + 16 * t + 4 * g, v4);  // S2 was last read before the loop's barriers
   }
-  __syncthreads();
+  lds_barrier();
   store_tile<T, DHP, KP>(static_cast<T*>(a.dq) + b * a.dq_sb + h * a.dq_sh, a.dq_st, S2, q0, qend, Dh);
 }
 
@@ -385,7 +385,7 @@ __global__ __launch_bounds__(256) void local_bwd_kv_kernel(const LocalArgs a) {
     kreg.template store<KP>(SQ);
     vreg.template store<KP>(SO);
   }
-  __syncthreads();
+  lds_barrier();
   RowFrag<T, DQ> kf, vf;
   kf.load_lds(SQ + row * KP, g);
   vf.load_lds(SO + row * KP, g);
@@ -395,7 +395,7 @@ __global__ __launch_bounds__(256) void local_bwd_kv_kernel(const LocalArgs a) {
 
   const int wqlo = kw + 1, wqhi = (int)min((int64_t)T_ - 1, (int64_t)kw + 15 + a.W);
   for (int q0 = qbeg; q0 < qend; q0 += 64) {
-    __syncthreads();
+    lds_barrier();
     qreg.template store<KP>(SQ);
     oreg.template store<KP>(SO);
     if (tid < 64) {
@@ -405,7 +405,7 @@ __global__ __launch_bounds__(256) void local_bwd_kv_kernel(const LocalArgs a) {
       Dss[tid] = in ? ds_r : 0.f;
       los[tid] = in ? key_lo(qq, a.W, a.bs) : INT_MAX;
     }
-    __syncthreads();
+    lds_barrier();
     if (q0 + 64 < qend) load_tile(q0 + 64);
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
@@ -431,7 +431,7 @@ __global__ __launch_bounds__(256) void local_bwd_kv_kernel(const LocalArgs a) {
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     float kv4[4], vv4[4];
@@ -443,58 +443,57 @@ __global__ __launch_bounds__(256) void local_bwd_kv_kernel(const LocalArgs a) {
     store4<T>(SQ + row * KP + 16 * t + 4 * g, kv4);
     store4<T>(SO + row * KP + 16 * t + 4 * g, vv4);
   }
-  __syncthreads();
+  lds_barrier();
   store_tile<T, DHP, KP>(static_cast<T*>(a.dk) + b * a.dk_sb + h * a.dk_sh, a.dk_st, SQ, j0, jend, Dh);
   store_tile<T, DHP, KP>(static_cast<T*>(a.dv) + b * a.dv_sb + h * a.dv_sh, a.dv_st, SO, j0, jend, Dh);
 }
 
 // ----------------------------------------------------------------------------
 // fused backward for windows W <= 64, bf16: one workgroup walks a segment of
-// kSegTiles query tiles of one (batch, head) in order.  With W <= 64 the keys of
-// query tile qt lie in key tiles qt-1 and qt, and key tile qt gets its queries
-// from query tiles qt and qt+1, so after step qt key tile qt-1 is complete.
-// Every row of q, k, v, dy, o_local and remote is read from HBM once per
-// segment (plus one tile of halo at each end), dO never leaves LDS, and each
-// output row is written once.  512 threads in two roles that share a SIMD:
-//   query waves 0-3 (16 queries each): gate backward (dO, D, dremote, gate
-//     partials), then dQ over key tiles qt-1 and qt;
-//   key waves 4-7 (16 keys each of tiles qt-1 and qt): dK / dV contributions
-//     of the step's queries, concurrently with the query waves' dQ.  The
-//     partial dK / dV of key tile qt is parked in LDS (fp32, in the
-//     accumulator layout, read back by the same lane) until step qt+1
-//     completes it, so only one key tile's accumulators are live at a time.
+// query tiles of one (batch, head) in order.  With W <= 64 the keys of query
+// tile qt lie in key tiles qt-1 and qt, and key tile qt gets its queries from
+// query tiles qt and qt+1, so after step qt key tile qt-1 is complete.  Every
+// row of q, k, v, dy, o_local and remote is read from HBM once per segment
+// (plus one tile of halo at each end), dO never leaves LDS, and each output
+// row is written once, straight from registers.  Two LDS barriers per step:
+//   1. stage q / k / v of the step (prefetched into registers one step ahead),
+//      and gate backward by all 512 threads, eight per query row (dO into LDS,
+//      D, dremote to HBM, gate partial sums kept per thread in LDS across the
+//      segment); then the next step's loads are put in flight;
+//   2. query waves 0-3 (16 queries each): dQ over key tiles qt-1 and qt;
+//      key waves 4-7 (16 keys each): dK / dV contributions of the step's
+//      queries to key tiles qt-1 (then complete and stored) and qt (kept in
+//      registers for the next step).
 // The segment's last key tile needs the queries of the next segment's first
 // tile: an extra step at the end gates that tile and adds its contributions
-// (its own outputs belong to the next segment).  No atomics: every output has
-// one writer.
+// (its own outputs belong to the next segment).  The gate partial sums of the
+// segment are added over its rows in a fixed order at the end.  No atomics:
+// every output has one writer.
 // ----------------------------------------------------------------------------
-constexpr int kSegTiles = 8;
-
 template <int DHP>
-__global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a) {
+__global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a, int seg_tiles) {
   using T = uint16_t;
   constexpr int NTHR = 512;
   constexpr int DQ = DHP / 4, NT = DHP / 16, KP = DHP + kRowPad<T>;
-  __shared__ __align__(16) T SQ[64 * KP];     // query rows of the step's tile -> dq staging
-  __shared__ __align__(16) T SO[64 * KP];     // dy -> dO rows
-  __shared__ __align__(16) T SK[2][64 * KP];  // key rows by tile parity (o_local while gating; dk staging)
-  __shared__ __align__(16) T SV[2][64 * KP];  // value rows by tile parity (remote -> dremote while gating; dv staging)
-  __shared__ __align__(16) T SDK[64 * KP];    // finished dk rows of key tile qt-1
-  __shared__ __align__(16) T SDV[64 * KP];    // finished dv rows of key tile qt-1
-  __shared__ __align__(16) f32x4 PKV[4][2 * NT][64];  // key waves: partial dk (t < NT) / dv of key tile qt
-  __shared__ float gsum[4][2][DHP];
+  constexpr int GS = DHP / 8, GV = GS / 4;  // gate layout: 8 threads per row, GS dims each, GV groups of 4
+  __shared__ __align__(16) T SQ[64 * KP];     // query rows of the step
+  __shared__ __align__(16) T SO[64 * KP];     // dO rows of the step
+  __shared__ __align__(16) T SK[2][64 * KP];  // key rows by tile parity
+  __shared__ __align__(16) T SV[2][64 * KP];  // value rows by tile parity
+  __shared__ __align__(16) f32x4 GACC[2 * GV][NTHR];  // per-thread gate partials: [l groups | r groups][thread]
   __shared__ __align__(16) float gls[DHP], grs[DHP];
-  __shared__ float lse2s[64], Dss[64];
-  __shared__ int los[64];
+  __shared__ __align__(16) float lse2s[64], Dss[64];
+  __shared__ __align__(16) int los[64];
 
   const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool qrole = wave < 4;
-  const int w4 = wave & 3, row = w4 * 16 + r;  // query row (query waves) or key row (key waves)
-  const int n_seg = (a.n_qt + kSegTiles - 1) / kSegTiles;
+  const int w4 = wave & 3, row = w4 * 16 + r;       // query row (query waves) or key row (key waves)
+  const int grow = tid >> 3, gd0 = (tid & 7) * GS;  // gate layout: row and first dim
+  const int n_seg = (a.n_qt + seg_tiles - 1) / seg_tiles;
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
   const int seg = bid % n_seg, bh = bid / n_seg, h = bh % a.H, b = bh / a.H;
-  const int t0 = seg * kSegTiles, t1 = min(a.n_qt, t0 + kSegTiles);
+  const int t0 = seg * seg_tiles, t1 = min(a.n_qt, t0 + seg_tiles);
   const int tlast = min(t1, a.n_qt - 1);  // the extra step runs when t1 < n_qt
   const int T_ = a.T, Dh = a.Dh;
   const int64_t hrow = ((int64_t)b * a.H + h) * T_;
@@ -504,144 +503,140 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a)
   const T* dybase = static_cast<const T*>(a.dy) + b * a.dy_sb + h * a.dy_sh;
   const T* olbase = static_cast<const T*>(a.ol) + b * a.o_sb + h * a.o_sh;
   const T* rbase = static_cast<const T*>(a.rem) + b * a.r_sb + h * a.r_sh;
+  T* dqbase = static_cast<T*>(a.dq) + b * a.dq_sb + h * a.dq_sh;
+  T* dkbase = static_cast<T*>(a.dk) + b * a.dk_sb + h * a.dk_sh;
+  T* dvbase = static_cast<T*>(a.dv) + b * a.dv_sb + h * a.dv_sh;
+  T* drbase = static_cast<T*>(a.dr) + b * a.dr_sb + h * a.dr_sh;
+  // row strides fit in 32 bits (checked by the launcher); fewer live scalar registers
+  const int q_st = (int)a.q_st, k_st = (int)a.k_st, v_st = (int)a.v_st, dy_st = (int)a.dy_st, o_st = (int)a.o_st;
+  const int r_sn = (int)a.r_sn, dq_st = (int)a.dq_st, dk_st = (int)a.dk_st, dv_st = (int)a.dv_st, dr_st = (int)a.dr_st;
 
   for (int d = tid; d < DHP; d += NTHR) {
     gls[d] = d < Dh ? a.gl[h * a.gate_hs + d] : 0.f;
     grs[d] = d < Dh ? a.gr[h * a.gate_hs + d] : 0.f;
   }
-  RowTile<T, DHP, NTHR> rdy, rol, rrm, rq, rk, rv;
-  float nw = 0.f, nlse = kNegInf;  // the query waves' next w and lse
+#pragma unroll
+  for (int j = 0; j < 2 * GV; ++j) GACC[j][tid] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // prefetch: q / k / v rows of a tile (row-tile layout) and the gate inputs of its rows (gate layout)
+  RowTile<T, DHP, NTHR> rq, rk, rv;
+  Raw4<T> pdy[GV], pol[GV], prm[GV];
+  float pw = 0.f, plse = kNegInf;
   auto load_step = [&](int qt) {
     const int q0 = qt * 64, qend = min(T_, q0 + 64);
-    rdy.load(dybase, a.dy_st, q0, qend, Dh);
-    rol.load(olbase, a.o_st, q0, qend, Dh);
-    rrm.load_div(rbase, a.r_sn, q0, qend, a.q_block, Dh);
-    rq.load(qbase, a.q_st, q0, qend, Dh);
+    rq.load(qbase, q_st, q0, qend, Dh);
     if (qt < t1) {  // the extra step needs no keys of its own tile
-      rk.load(kbase, a.k_st, q0, qend, Dh);
-      rv.load(vbase, a.v_st, q0, qend, Dh);
+      rk.load(kbase, k_st, q0, qend, Dh);
+      rv.load(vbase, v_st, q0, qend, Dh);
     }
-    const int qi = q0 + row;
-    if (qrole && qi < T_) {
-      nw = a.w[hrow + qi];
-      nlse = a.lse[hrow + qi];
+    const int qi = q0 + grow;
+    const bool ok = qi < T_;
+#pragma unroll
+    for (int j = 0; j < GV; ++j) {
+      const int d = gd0 + 4 * j;
+      const bool v = ok && d < Dh;
+      pdy[j].load(dybase + (int64_t)qi * dy_st + d, v);
+      pol[j].load(olbase + (int64_t)qi * o_st + d, v);
+      prm[j].load(rbase + (int64_t)(qi / a.q_block) * r_sn + d, v);
     }
+    pw = ok ? a.w[hrow + qi] : 0.f;
+    plse = ok ? a.lse[hrow + qi] : kNegInf;
   };
   if (t0 > 0) {  // keys of tile t0-1 for the first step's dQ
     const int p0 = (t0 - 1) * 64;
-    rk.load(kbase, a.k_st, p0, p0 + 64, Dh);
-    rv.load(vbase, a.v_st, p0, p0 + 64, Dh);
+    rk.load(kbase, k_st, p0, p0 + 64, Dh);
+    rv.load(vbase, v_st, p0, p0 + 64, Dh);
     rk.template store<KP>(SK[(t0 - 1) & 1]);
     rv.template store<KP>(SV[(t0 - 1) & 1]);
   }
   load_step(t0);
+
+  f32x4 pk[NT], pv[NT];  // key waves: partial dK / dV of this wave's 16 keys of key tile qt-1
+#pragma unroll
+  for (int t = 0; t < NT; ++t) pk[t] = pv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   for (int qt = t0; qt <= tlast; ++qt) {
     const bool full = qt < t1;
     const bool own_prev = qt - 1 >= t0;
     const int cur = qt & 1, prv = cur ^ 1;
     const int q0 = qt * 64, qend = min(T_, q0 + 64);
-    const int qw = q0 + w4 * 16, qi = qw + r;
-    const bool qv = qi < T_;
-    const float wq = qv ? nw : 0.f, lse_nat = qv ? nlse : kNegInf;
 
-    // ---- stage the step's rows (o_local and remote in SDK / SDV, free until the key waves finish
-    //      key tile qt-1), then put the next step's loads in flight for the whole step ----
-    __syncthreads();  // the previous step's write-back is done with SQ, SDK, SDV; SO, SK[cur], SV[cur] are free
-    rdy.template store<KP>(SO);
-    rol.template store<KP>(SDK);
-    rrm.template store<KP>(SDV);
+    // ---- 1. stage the step's rows; gate backward in the gate layout ----
+    lds_barrier();  // the previous step is done with SQ, SO, SK[cur], SV[cur] and the per-query stats
     rq.template store<KP>(SQ);
     if (full) {
       rk.template store<KP>(SK[cur]);
       rv.template store<KP>(SV[cur]);
     }
-    if (qt + 1 <= tlast) load_step(qt + 1);
-    __syncthreads();
-
-    // ---- query waves: gate backward in the accumulator layout (dims 16t+4g+i) ----
-    float Dq = 0.f;
-    if (qrole) {
-      // two passes over the staged rows (re-read from LDS) keep the register footprint small
+    {
+      const int qi = q0 + grow;
+      const bool qv = qi < T_;
+      const float wq = pw;
+      float dyv[GS], olv[GS], rmv[GS];
+#pragma unroll
+      for (int j = 0; j < GV; ++j) {
+        pdy[j].get(dyv + 4 * j);
+        pol[j].get(olv + 4 * j);
+        prm[j].get(rmv + 4 * j);
+      }
       float dot1 = 0.f;
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const int d = 16 * t + 4 * g;
-        float dyv[4], olv[4], rv4[4];
-        Raw4<T> x;
-        x.load(SO + row * KP + d, true); x.get(dyv);
-        x.load(SDK + row * KP + d, true); x.get(olv);
-        x.load(SDV + row * KP + d, true); x.get(rv4);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dot1 += dyv[i] * (olv[i] - rv4[i]);
-      }
-      dot1 = sum_groups(dot1);
+      for (int e = 0; e < GS; ++e) dot1 += dyv[e] * (olv[e] - rmv[e]);
+      dot1 = sum_lanes8(dot1);
       const float delta = wq * (1.f - wq) * dot1;
+      float Dp = 0.f;
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const int d = 16 * t + 4 * g;
-        float dyv[4], olv[4], rv4[4];
-        Raw4<T> x;
-        x.load(SO + row * KP + d, true); x.get(dyv);
-        x.load(SDK + row * KP + d, true); x.get(olv);
-        x.load(SDV + row * KP + d, true); x.get(rv4);
+      for (int j = 0; j < GV; ++j) {
+        const int d = gd0 + 4 * j;
         const float4 gl4 = *reinterpret_cast<const float4*>(gls + d);
         const float4 gr4 = *reinterpret_cast<const float4*>(grs + d);
         const float glv[4] = {gl4.x, gl4.y, gl4.z, gl4.w}, grv[4] = {gr4.x, gr4.y, gr4.z, gr4.w};
         float dov[4], drv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          dov[i] = round_t<T>(wq * dyv[i] + delta * glv[i]);
-          drv[i] = (1.f - wq) * dyv[i] - delta * grv[i];
-          Dq += dov[i] * olv[i];
+          const int e = 4 * j + i;
+          dov[i] = round_t<T>(wq * dyv[e] + delta * glv[i]);
+          drv[i] = (1.f - wq) * dyv[e] - delta * grv[i];
+          Dp += dov[i] * olv[e];
         }
-        store4<T>(SO + row * KP + d, dov);  // in place over the dy elements this lane read
-        if (full && qv && d < Dh)            // dremote straight from the accumulator layout
-          store4<T>(static_cast<T*>(a.dr) + b * a.dr_sb + h * a.dr_sh + (int64_t)qi * a.dr_st + d, drv);
+        store4<T>(SO + grow * KP + d, dov);
         if (full) {
+          if (qv && d < Dh)
+            store4<T>(drbase + (int64_t)qi * dr_st + d, drv);
+          f32x4 al = GACC[j][tid], ar = GACC[GV + j][tid];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {  // gate partial sums over the 16 queries of this wave
-            const float pl = sum_rows16_last(delta * olv[i]);
-            const float pr = sum_rows16_last(-delta * rv4[i]);
-            if (r == 15) {
-              gsum[w4][0][d + i] = pl;
-              gsum[w4][1][d + i] = pr;
-            }
+          for (int i = 0; i < 4; ++i) {
+            al[i] += delta * olv[4 * j + i];
+            ar[i] -= delta * rmv[4 * j + i];
           }
+          GACC[j][tid] = al;
+          GACC[GV + j][tid] = ar;
         }
       }
-      Dq = sum_groups(Dq);
-      if (g == 0) {
-        Dss[row] = qv ? Dq : 0.f;
-        lse2s[row] = (!qv || lse_nat == kNegInf) ? 0.f : lse_nat * kLog2e;
-        los[row] = qv ? key_lo(qi, a.W, a.bs) : INT_MAX;
+      Dp = sum_lanes8(Dp);
+      if ((tid & 7) == 0) {
+        Dss[grow] = qv ? Dp : 0.f;
+        lse2s[grow] = (!qv || plse == kNegInf) ? 0.f : plse * kLog2e;
+        los[grow] = qv ? key_lo(qi, a.W, a.bs) : INT_MAX;
       }
     }
-    __syncthreads();  // dO and the per-query stats are complete; o_local / remote (SDK / SDV) are consumed
-    if (full) {
-      const int nrow = a.B * a.n_qt, prow = b * a.n_qt + qt;
-      for (int idx = tid; idx < 2 * DHP; idx += NTHR) {
-        const int which = idx / DHP, d = idx % DHP;
-        if (d < Dh) {
-          const float sum = gsum[0][which][d] + gsum[1][which][d] + gsum[2][which][d] + gsum[3][which][d];
-          a.gpart[(((int64_t)h * 2 + which) * Dh + d) * nrow + prow] = sum;
-        }
-      }
-    }
+    if (qt + 1 <= tlast) load_step(qt + 1);
+    lds_barrier();  // dO, the staged rows and the per-query stats are complete
 
-    f32x4 dq[NT];  // query waves
-#pragma unroll
-    for (int t = 0; t < NT; ++t) dq[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // ---- 2. dQ (query waves) and dK / dV (key waves) ----
     if (qrole) {
-      // ---- dQ = scale * sum_j dS_ij k_j over key tiles qt-1 and qt ----
       if (full) {
+        const int qw = q0 + w4 * 16, qi = qw + r;
+        const bool qv = qi < T_;
         RowFrag<T, DQ> qf, dof;
         qf.load_lds(SQ + row * KP, g);
         dof.load_lds(SO + row * KP, g);
-        const float lse2 = (lse_nat == kNegInf) ? 0.f : lse_nat * kLog2e;
-        const int lo = qv ? key_lo(qi, a.W, a.bs) : INT_MAX;
-        const int hi = qi - 1;
+        const float lse2 = lse2s[row], Dq = Dss[row];
+        const int lo = los[row], hi = qi - 1;
         const int wlo = max(0, qw - a.W), whi = min(qw + 15, T_ - 1) - 1;
+        f32x4 dq[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) dq[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
           const int kt = qt - 1 + half;
@@ -660,29 +655,39 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const int j = s0 + 4 * g + i;
-              const float pj = (j >= lo && j <= hi) ? fast_exp2(sv[i] * a.scale_log2 - lse2) : 0.f;
-              ds[i] = pj * (dp[i] - Dq);
+              const float p = fast_exp2(sv[i] * a.scale_log2 - lse2);
+              ds[i] = (j >= lo && j <= hi) ? p * (dp[i] - Dq) : 0.f;
             }
+            const i16x4 dsb = pack_bf16x4(ds);
 #pragma unroll
-            for (int t = 0; t < NT; ++t) dq[t] = col_mma_rm<KP>(Ks + (16 * st) * KP + 16 * t, ds, dq[t]);
+            for (int t = 0; t < NT; ++t) dq[t] = col_mma_rm<KP>(Ks + (16 * st) * KP + 16 * t, dsb, dq[t]);
+          }
+        }
+        if (qv) {  // lane holds dQ[query qi][16t + 4g + i]
+          T* p = dqbase + (int64_t)qi * dq_st;
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            const int d = 16 * t + 4 * g;
+            float v4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v4[i] = dq[t][i] * a.scale;
+            if (d < Dh) store4<T>(p + d, v4);
           }
         }
       }
     } else {
-      // ---- dK / dV of this wave's 16 keys of tiles qt-1 (if owned: finished into SDK / SDV)
-      //      and qt (if full: parked in PKV) ----
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        const int kt = qt - 1 + half;
         if (half == 0 ? !own_prev : !full) continue;  // uniform
+        const int kt = qt - 1 + half;
         const int kw = kt * 64 + w4 * 16, kj = kw + r;
         const bool kv = kj < T_;
         const int wqlo = kw + 1, wqhi = (int)min((int64_t)T_ - 1, (int64_t)kw + 15 + a.W);
         f32x4 dk[NT], dv[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          dk[t] = half == 0 ? PKV[w4][t][lane] : f32x4{0.f, 0.f, 0.f, 0.f};
-          dv[t] = half == 0 ? PKV[w4][NT + t][lane] : f32x4{0.f, 0.f, 0.f, 0.f};
+          dk[t] = half == 0 ? pk[t] : f32x4{0.f, 0.f, 0.f, 0.f};
+          dv[t] = half == 0 ? pv[t] : f32x4{0.f, 0.f, 0.f, 0.f};
         }
         RowFrag<T, DQ> kf, vf;
         kf.load_lds((half ? SK[cur] : SK[prv]) + row * KP, g);
@@ -694,88 +699,105 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a)
           RowFrag<T, DQ> qf, of;
           qf.load_lds(SQ + (16 * st + r) * KP, g);
           of.load_lds(SO + (16 * st + r) * KP, g);
+          const int ql = 16 * st + 4 * g;  // this lane's four queries (rows of the step's tile)
+          const int4 lo4 = *reinterpret_cast<const int4*>(los + ql);
+          const float4 l4 = *reinterpret_cast<const float4*>(lse2s + ql);
+          const float4 D4 = *reinterpret_cast<const float4*>(Dss + ql);
+          const int lov[4] = {lo4.x, lo4.y, lo4.z, lo4.w};
+          const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, Dv[4] = {D4.x, D4.y, D4.z, D4.w};
           const f32x4 sv = row_mma(qf, kf, f32x4{0.f, 0.f, 0.f, 0.f});  // S[query 4g+i][key r]
           const f32x4 dp = row_mma(of, vf, f32x4{0.f, 0.f, 0.f, 0.f});  // dP[query][key]
           float pp[4], ds[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int ql = 16 * st + 4 * g + i, qq = q0 + ql;
-            const bool ok = kv && kj >= los[ql] && kj <= qq - 1;
-            pp[i] = ok ? fast_exp2(sv[i] * a.scale_log2 - lse2s[ql]) : 0.f;
-            ds[i] = pp[i] * (dp[i] - Dss[ql]);
+            const int qq = q0 + ql + i;
+            const bool ok = kv && kj >= lov[i] && kj <= qq - 1;
+            const float p = fast_exp2(sv[i] * a.scale_log2 - lv[i]);
+            pp[i] = ok ? p : 0.f;
+            ds[i] = pp[i] * (dp[i] - Dv[i]);
           }
+          const i16x4 ppb = pack_bf16x4(pp), dsb = pack_bf16x4(ds);
 #pragma unroll
           for (int t = 0; t < NT; ++t) {
-            dv[t] = col_mma_rm<KP>(SO + (16 * st) * KP + 16 * t, pp, dv[t]);  // dV^T = dO^T P
-            dk[t] = col_mma_rm<KP>(SQ + (16 * st) * KP + 16 * t, ds, dk[t]);  // dK^T = Q^T dS
+            dv[t] = col_mma_rm<KP>(SO + (16 * st) * KP + 16 * t, ppb, dv[t]);  // dV^T = dO^T P
+            dk[t] = col_mma_rm<KP>(SQ + (16 * st) * KP + 16 * t, dsb, dk[t]);  // dK^T = Q^T dS
           }
         }
-        if (half == 0) {
+        if (half == 0) {  // key tile qt-1 is complete: lane holds dK / dV[key kj][16t + 4g + i]
+          if (kv) {
+            T* pkp = dkbase + (int64_t)kj * dk_st;
+            T* pvp = dvbase + (int64_t)kj * dv_st;
 #pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            float k4[4], v4[4];
+            for (int t = 0; t < NT; ++t) {
+              const int d = 16 * t + 4 * g;
+              float k4[4], v4[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              k4[i] = dk[t][i] * a.scale;
-              v4[i] = dv[t][i];
+              for (int i = 0; i < 4; ++i) {
+                k4[i] = dk[t][i] * a.scale;
+                v4[i] = dv[t][i];
+              }
+              if (d < Dh) {
+                store4<T>(pkp + d, k4);
+                store4<T>(pvp + d, v4);
+              }
             }
-            store4<T>(SDK + row * KP + 16 * t + 4 * g, k4);
-            store4<T>(SDV + row * KP + 16 * t + 4 * g, v4);
           }
         } else {
 #pragma unroll
           for (int t = 0; t < NT; ++t) {
-            PKV[w4][t][lane] = dk[t];
-            PKV[w4][NT + t][lane] = dv[t];
+            pk[t] = dk[t];
+            pv[t] = dv[t];
           }
         }
       }
     }
-
-    // ---- write-back: dq of this tile, dk / dv of key tile qt-1 (complete now) ----
-    __syncthreads();  // every wave is done reading SQ; SDK / SDV are complete
-    if (qrole && full) {
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        float v4[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v4[i] = dq[t][i] * a.scale;
-        store4<T>(SQ + row * KP + 16 * t + 4 * g, v4);
-      }
-    }
-    __syncthreads();
-    if (full) store_tile<T, DHP, KP, NTHR>(static_cast<T*>(a.dq) + b * a.dq_sb + h * a.dq_sh, a.dq_st, SQ, q0, qend, Dh);
-    if (own_prev) {
-      const int p0 = q0 - 64;
-      store_tile<T, DHP, KP, NTHR>(static_cast<T*>(a.dk) + b * a.dk_sb + h * a.dk_sh, a.dk_st, SDK, p0, p0 + 64, Dh);
-      store_tile<T, DHP, KP, NTHR>(static_cast<T*>(a.dv) + b * a.dv_sb + h * a.dv_sh, a.dv_st, SDV, p0, p0 + 64, Dh);
-    }
   }
-  // a segment that ends the sequence finishes its last key tile here (no next queries)
-  if (t1 == a.n_qt) {
-    const int p0 = (t1 - 1) * 64;
-    __syncthreads();  // the last step's stores from SDK / SDV are done
-    if (!qrole) {
+  // a segment that ends the sequence: its last key tile gets no more queries
+  if (!qrole && t1 == a.n_qt) {
+    const int kj = (t1 - 1) * 64 + row;
+    if (kj < T_) {
+      T* pkp = dkbase + (int64_t)kj * dk_st;
+      T* pvp = dvbase + (int64_t)kj * dv_st;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const f32x4 dk = PKV[w4][t][lane], dv = PKV[w4][NT + t][lane];
+        const int d = 16 * t + 4 * g;
         float k4[4], v4[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          k4[i] = dk[i] * a.scale;
-          v4[i] = dv[i];
+          k4[i] = pk[t][i] * a.scale;
+          v4[i] = pv[t][i];
         }
-        store4<T>(SDK + row * KP + 16 * t + 4 * g, k4);
-        store4<T>(SDV + row * KP + 16 * t + 4 * g, v4);
+        if (d < Dh) {
+          store4<T>(pkp + d, k4);
+          store4<T>(pvp + d, v4);
+        }
       }
     }
-    __syncthreads();
-    store_tile<T, DHP, KP, NTHR>(static_cast<T*>(a.dk) + b * a.dk_sb + h * a.dk_sh, a.dk_st, SDK, p0, T_, Dh);
-    store_tile<T, DHP, KP, NTHR>(static_cast<T*>(a.dv) + b * a.dv_sb + h * a.dv_sh, a.dv_st, SDV, p0, T_, Dh);
+  }
+  // gate partials of the segment: the 64 row threads of each dim added in row order
+  lds_barrier();
+  const int nrow = a.B * n_seg, prow = b * n_seg + seg;
+  for (int idx = tid; idx < 2 * DHP; idx += NTHR) {
+    const int which = idx / DHP, d = idx % DHP;
+    if (d < Dh) {
+      const int sg = d / GS, e = d % GS;
+      const int j = which * GV + e / 4, i = e % 4;
+      float s = 0.f;
+      for (int rr = 0; rr < 64; ++rr) s += GACC[j][rr * 8 + sg][i];
+      a.gpart[(((int64_t)h * 2 + which) * Dh + d) * nrow + prow] = s;
+    }
   }
 }
 
-// Ordered sum of the per-tile gate partials: dgate[h][d] = sum over (b, tile) of part[h][which][d][b*n_qt + tile].
+// Query tiles per workgroup of the fused backward: enough workgroups for one
+// per CU (256) where the (batch, head) count allows, otherwise whole sequences.
+int fused_seg_tiles(const LocalArgs& a) {
+  const int bh = a.B * a.H;
+  const int want = max(1, (256 + bh - 1) / bh);
+  return max(2, (a.n_qt + want - 1) / want);
+}
+
+// Ordered sum of the gate partials: dgate[h][d] = sum over the nrow partial rows of part[h][which][d][row].
 // One wave per output: lanes stride over the contiguous partials, then a fixed butterfly.
 __global__ __launch_bounds__(256) void gate_reduce_kernel(const float* __restrict__ part, float* dgl, float* dgr,
                                                           int H, int Dh, int nrow) {
@@ -802,12 +824,23 @@ template <typename T, int DHP>
 void launch_fwd(const LocalArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL((local_fwd_kernel<T, DHP>), dim3(a.B * a.H * a.n_qt), dim3(256), 0, stream, a);
 }
+// The fused one-pass backward covers bf16 with padded head dims up to 96,
+// windows up to 64 (keys of a query tile span two key tiles) and row strides
+// below 2^31 elements.
+bool fused_bwd(const LocalArgs& a, int dtype, int dhp) {
+  const int64_t lim = INT32_MAX;
+  const bool st32 = a.q_st <= lim && a.k_st <= lim && a.v_st <= lim && a.dy_st <= lim && a.o_st <= lim &&
+                    a.r_sn <= lim && a.dq_st <= lim && a.dk_st <= lim && a.dv_st <= lim && a.dr_st <= lim;
+  return dtype == LLATTN_BF16 && dhp <= 96 && a.W <= 64 && st32;
+}
+
 template <typename T, int DHP>
 void launch_bwd(const LocalArgs& a, hipStream_t stream) {
   if constexpr (std::is_same_v<T, uint16_t> && DHP <= 96) {
-    if (a.W <= 64) {  // one pass: keys of a query tile span two key tiles
-      const int n_seg = (a.n_qt + kSegTiles - 1) / kSegTiles;
-      hipLaunchKernelGGL((local_bwd_fused_kernel<DHP>), dim3(a.B * a.H * n_seg), dim3(512), 0, stream, a);
+    if (fused_bwd(a, LLATTN_BF16, DHP)) {
+      const int seg_tiles = fused_seg_tiles(a);
+      const int n_seg = (a.n_qt + seg_tiles - 1) / seg_tiles;
+      hipLaunchKernelGGL((local_bwd_fused_kernel<DHP>), dim3(a.B * a.H * n_seg), dim3(512), 0, stream, a, seg_tiles);
       return;
     }
   }
@@ -925,7 +958,10 @@ extern "C" int32_t llattn_local_gate_bwd(const llattn_shape* s, const llattn_ten
   const bool ok =
       s->dtype == LLATTN_F32 ? dispatch<float>(dhp, false, a, st) : dispatch<uint16_t>(dhp, false, a, st);
   if (!ok) return fail(LLATTN_ERR_UNSUPPORTED, "head_dim %d unsupported", s->Dh);
+  // gate partial rows: one per (batch, segment) from the fused kernel, one per (batch, query tile) otherwise
+  const int seg_tiles = fused_seg_tiles(a);
+  const int nrow = fused_bwd(a, s->dtype, dhp) ? s->B * ((a.n_qt + seg_tiles - 1) / seg_tiles) : s->B * a.n_qt;
   hipLaunchKernelGGL(gate_reduce_kernel, dim3((s->H * 2 * s->Dh + 3) / 4), dim3(256), 0, st, a.gpart, dgate_l, dgate_r,
-                     s->H, s->Dh, s->B * a.n_qt);
+                     s->H, s->Dh, nrow);
   return check_launch("llattn_local_gate_bwd");
 }

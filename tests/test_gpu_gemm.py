@@ -48,7 +48,8 @@ def test_matmul_nn(M, N, K):
 
 
 @pytest.mark.parametrize("K,M,N,S", [(64, 256, 256, 1), (1024, 264, 136, 0), (4096, 1408, 512, 4),
-                                     (2048, 40, 96, 2), (32768, 1408, 1408, 0), (32768, 4736, 1408, 0)])
+                                     (2048, 40, 96, 2), (4096, 264, 136, 3), (32768, 1408, 1408, 0),
+                                     (32768, 4736, 1408, 0), (32768, 1408, 512, 0)])
 def test_matmul_tn_fp32_out(K, M, N, S):
     """Weight-gradient products, including split-K (S > 1 or automatic) at the config-2 shapes."""
     from llattn_amd import gemm
