@@ -81,6 +81,10 @@ __device__ __forceinline__ void store4(T* p, const float v[4]) {
 }
 // 4 consecutive elements held as stored (8 bytes of bf16 / 16 bytes of fp32)
 // so a prefetched row costs half the registers in bf16; zero when !valid.
+__device__ __forceinline__ void unpack_bf16x4(uint2 v, float o[4]) {
+  o[0] = __uint_as_float(v.x << 16); o[1] = __uint_as_float(v.x & 0xffff0000u);
+  o[2] = __uint_as_float(v.y << 16); o[3] = __uint_as_float(v.y & 0xffff0000u);
+}
 template <typename T> struct Raw4;
 template <> struct Raw4<float> {
   float4 v;
@@ -328,6 +332,52 @@ struct RowTile {
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
       const int task = threadIdx.x + NTHR * it, row = task / CPR, col = (task % CPR) * V;
+      if (task < TASKS) st16(lds + row * P + col, x[it]);
+    }
+  }
+};
+
+// ---- buffer loads (range-checked: an offset past the resource's extent reads zero) ----
+constexpr uint32_t kOffOOB = 0x80000000u;  // an offset beyond every extent used here (< 2 GiB)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
+  const int n = bytes <= 0 ? 0 : (bytes >= (int64_t)kOffOOB ? (int)(kOffOOB - 16) : (int)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, n, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ uint2 buf_ld8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
+
+// BufTile: a bf16 RowTile read with buffer loads.  Each thread's byte offsets
+// within a tile are fixed (set once by init for the view's row stride), the
+// tile's rows come from a resource that ends with the last valid row, so
+// rows past the end and padding dims read as zero without branches.
+// Offsets are 32-bit: 64 rows of the view must span less than 2 GiB.
+template <int DHP, int NTHR>
+struct BufTile {
+  static constexpr int CPR = DHP / 8, TASKS = 64 * CPR, IT = (TASKS + NTHR - 1) / NTHR;
+  uint4 x[IT];
+  uint32_t off[IT];
+  __device__ __forceinline__ void init(int st, int Dh) {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int task = threadIdx.x + NTHR * it, row = task / CPR, col = (task % CPR) * 8;
+      off[it] = (task < TASKS && col < Dh) ? (uint32_t)(row * st + col) * 2u : kOffOOB;
+    }
+  }
+  // rows [r0, r_end) of the view at base (row stride st elements)
+  __device__ __forceinline__ void load(const uint16_t* base, int st, int r0, int r_end, int Dh) {
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(base + (int64_t)r0 * st, ((int64_t)(r_end - r0 - 1) * st + Dh) * 2);
+#pragma unroll
+    for (int it = 0; it < IT; ++it) x[it] = buf_ld16(rs, off[it]);
+  }
+  template <int P>
+  __device__ __forceinline__ void store(uint16_t* lds) const {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int task = threadIdx.x + NTHR * it, row = task / CPR, col = (task % CPR) * 8;
       if (task < TASKS) st16(lds + row * P + col, x[it]);
     }
   }

@@ -507,7 +507,7 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
   T* dkbase = static_cast<T*>(a.dk) + b * a.dk_sb + h * a.dk_sh;
   T* dvbase = static_cast<T*>(a.dv) + b * a.dv_sb + h * a.dv_sh;
   T* drbase = static_cast<T*>(a.dr) + b * a.dr_sb + h * a.dr_sh;
-  // row strides fit in 32 bits (checked by the launcher); fewer live scalar registers
+  // row strides below 2^24 (checked by the launcher); fewer live scalar registers
   const int q_st = (int)a.q_st, k_st = (int)a.k_st, v_st = (int)a.v_st, dy_st = (int)a.dy_st, o_st = (int)a.o_st;
   const int r_sn = (int)a.r_sn, dq_st = (int)a.dq_st, dk_st = (int)a.dk_st, dv_st = (int)a.dv_st, dr_st = (int)a.dr_st;
 
@@ -519,8 +519,21 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
   for (int j = 0; j < 2 * GV; ++j) GACC[j][tid] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // prefetch: q / k / v rows of a tile (row-tile layout) and the gate inputs of its rows (gate layout)
-  RowTile<T, DHP, NTHR> rq, rk, rv;
-  Raw4<T> pdy[GV], pol[GV], prm[GV];
+  BufTile<DHP, NTHR> rq, rk, rv;
+  rq.init(q_st, Dh);
+  rk.init(k_st, Dh);
+  rv.init(v_st, Dh);
+  // gate rows: this thread's 8-byte groups at fixed offsets within a tile (out of range: zero)
+  uint32_t odyo[GV], orem[GV];  // dy and o_local share one offset when their strides agree
+  const bool same_st = dy_st == o_st;
+#pragma unroll
+  for (int j = 0; j < GV; ++j) {
+    const int d = gd0 + 4 * j;
+    odyo[j] = d < Dh ? (uint32_t)(grow * dy_st + d) * 2u : kOffOOB;
+    orem[j] = d < Dh ? (uint32_t)(grow * r_sn + d) * 2u : kOffOOB;
+  }
+  const bool qb1 = a.q_block == 1;
+  uint2 pdy[GV], pol[GV], prm[GV];
   float pw = 0.f, plse = kNegInf;
   auto load_step = [&](int qt) {
     const int q0 = qt * 64, qend = min(T_, q0 + 64);
@@ -529,16 +542,30 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
       rk.load(kbase, k_st, q0, qend, Dh);
       rv.load(vbase, v_st, q0, qend, Dh);
     }
-    const int qi = q0 + grow;
-    const bool ok = qi < T_;
+    const int rows = qend - q0;
+    const auto rdy = make_rsrc(dybase + (int64_t)q0 * dy_st, ((int64_t)(rows - 1) * dy_st + Dh) * 2);
+    const auto rol = make_rsrc(olbase + (int64_t)q0 * o_st, ((int64_t)(rows - 1) * o_st + Dh) * 2);
 #pragma unroll
     for (int j = 0; j < GV; ++j) {
-      const int d = gd0 + 4 * j;
-      const bool v = ok && d < Dh;
-      pdy[j].load(dybase + (int64_t)qi * dy_st + d, v);
-      pol[j].load(olbase + (int64_t)qi * o_st + d, v);
-      prm[j].load(rbase + (int64_t)(qi / a.q_block) * r_sn + d, v);
+      pdy[j] = buf_ld8(rdy, odyo[j]);
+      pol[j] = buf_ld8(rol, same_st ? odyo[j] : (gd0 + 4 * j < Dh ? (uint32_t)(grow * o_st + gd0 + 4 * j) * 2u
+                                                                   : kOffOOB));
     }
+    if (qb1) {  // one remote row per token
+      const auto rrm = make_rsrc(rbase + (int64_t)q0 * r_sn, ((int64_t)(rows - 1) * r_sn + Dh) * 2);
+#pragma unroll
+      for (int j = 0; j < GV; ++j) prm[j] = buf_ld8(rrm, orem[j]);
+    } else {  // one remote row per latent query of q_block tokens
+      const int qi = q0 + grow;
+      const int64_t rr = qi < T_ ? qi / a.q_block : -1;
+#pragma unroll
+      for (int j = 0; j < GV; ++j) {
+        const int d = gd0 + 4 * j;
+        prm[j] = (rr >= 0 && d < Dh) ? *reinterpret_cast<const uint2*>(rbase + rr * r_sn + d) : make_uint2(0u, 0u);
+      }
+    }
+    const int qi = q0 + grow;
+    const bool ok = qi < T_;
     pw = ok ? a.w[hrow + qi] : 0.f;
     plse = ok ? a.lse[hrow + qi] : kNegInf;
   };
@@ -575,9 +602,9 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
       float dyv[GS], olv[GS], rmv[GS];
 #pragma unroll
       for (int j = 0; j < GV; ++j) {
-        pdy[j].get(dyv + 4 * j);
-        pol[j].get(olv + 4 * j);
-        prm[j].get(rmv + 4 * j);
+        unpack_bf16x4(pdy[j], dyv + 4 * j);
+        unpack_bf16x4(pol[j], olv + 4 * j);
+        unpack_bf16x4(prm[j], rmv + 4 * j);
       }
       float dot1 = 0.f;
 #pragma unroll
@@ -826,9 +853,10 @@ void launch_fwd(const LocalArgs& a, hipStream_t stream) {
 }
 // The fused one-pass backward covers bf16 with padded head dims up to 96,
 // windows up to 64 (keys of a query tile span two key tiles) and row strides
-// below 2^31 elements.
+// below 2^24 elements (its buffer loads address a 64-row tile with 32-bit
+// byte offsets).
 bool fused_bwd(const LocalArgs& a, int dtype, int dhp) {
-  const int64_t lim = INT32_MAX;
+  const int64_t lim = int64_t(1) << 24;
   const bool st32 = a.q_st <= lim && a.k_st <= lim && a.v_st <= lim && a.dy_st <= lim && a.o_st <= lim &&
                     a.r_sn <= lim && a.dq_st <= lim && a.dk_st <= lim && a.dv_st <= lim && a.dr_st <= lim;
   return dtype == LLATTN_BF16 && dhp <= 96 && a.W <= 64 && st32;
