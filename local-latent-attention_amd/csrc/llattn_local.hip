@@ -555,13 +555,14 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
       const auto rrm = make_rsrc(rbase + (int64_t)q0 * r_sn, ((int64_t)(rows - 1) * r_sn + Dh) * 2);
 #pragma unroll
       for (int j = 0; j < GV; ++j) prm[j] = buf_ld8(rrm, orem[j]);
-    } else {  // one remote row per latent query of q_block tokens
-      const int qi = q0 + grow;
-      const int64_t rr = qi < T_ ? qi / a.q_block : -1;
+    } else {  // one remote row per latent query of q_block tokens: rows counted from the tile's first one
+      const int qi = q0 + grow, rq0 = q0 / a.q_block;
+      const int rrel = (qi - rq0 * a.q_block) / a.q_block, rlast = (qend - 1) / a.q_block - rq0;
+      const auto rrm = make_rsrc(rbase + (int64_t)rq0 * r_sn, ((int64_t)rlast * r_sn + Dh) * 2);
 #pragma unroll
       for (int j = 0; j < GV; ++j) {
         const int d = gd0 + 4 * j;
-        prm[j] = (rr >= 0 && d < Dh) ? *reinterpret_cast<const uint2*>(rbase + rr * r_sn + d) : make_uint2(0u, 0u);
+        prm[j] = buf_ld8(rrm, (qi < T_ && d < Dh) ? (uint32_t)(rrel * r_sn + d) * 2u : kOffOOB);
       }
     }
     const int qi = q0 + grow;
@@ -683,7 +684,7 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
             for (int i = 0; i < 4; ++i) {
               const int j = s0 + 4 * g + i;
               const float p = fast_exp2(sv[i] * a.scale_log2 - lse2);
-              ds[i] = (j >= lo && j <= hi) ? p * (dp[i] - Dq) : 0.f;
+              ds[i] = ((j >= lo) & (j <= hi)) ? p * (dp[i] - Dq) : 0.f;
             }
             const i16x4 dsb = pack_bf16x4(ds);
 #pragma unroll
@@ -738,7 +739,7 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int qq = q0 + ql + i;
-            const bool ok = kv && kj >= lov[i] && kj <= qq - 1;
+            const bool ok = kv & (kj >= lov[i]) & (kj <= qq - 1);  // no short circuit: plain selects
             const float p = fast_exp2(sv[i] * a.scale_log2 - lv[i]);
             pp[i] = ok ? p : 0.f;
             ds[i] = pp[i] * (dp[i] - Dv[i]);
