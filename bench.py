@@ -10,8 +10,10 @@ weights (how the reference trainer runs it).  The default workload is
 the 0.55b-preset layer at B=16, T=2048.
 
 Prints ONE JSON line.  Besides the driver's fields it carries
-``roofline`` (the dominant HIP kernel against HBM peak, its duration measured
-with HIP events on the launch stream inside the timed region),
+``roofline`` (the C-ABI entry point with the most time per step, priced
+against bf16 MFMA peak for the projection GEMM and against HBM peak for the
+attention kernels; durations measured with HIP events on the launch stream
+inside the timed region),
 ``mfma_frac_module`` (algorithmic module FLOPs / step time / bf16 dense
 peak), per-kernel event timings, and ``cpu_baseline`` (the reference
 PyTorch path restated in fp32, timed on the host cores on a bounded
@@ -84,6 +86,10 @@ def module_flops(lay):
                + 2 * T * D * D            # out
                + 4 * Dh * T * H)          # gate dots
     return 3 * fwd
+
+
+# entry points priced against MFMA peak (their calls state algorithmic FLOPs); the rest against HBM
+FLOP_ENTRY_POINTS = ("llattn_gemm",)
 
 
 def kernel_bytes(lay, es):
@@ -228,21 +234,34 @@ def main():
     ms = (t1 - t0) * 1000.0 / args.steps
     tokens = cfg["B"] * cfg["T"]
     flops = module_flops(lay)
-    per_kernel = {}
-    for name, s, e in events:
+    per_kernel, per_work = {}, {}
+    for name, s, e, work in events:
         per_kernel.setdefault(name, []).append(s.elapsed_time(e))
+        if work is not None:
+            per_work[name] = per_work.get(name, 0) + work
     kb = kernel_bytes(lay, 2)
     kstats = {}
     for name, ts in per_kernel.items():
         avg = sum(ts) / len(ts)
         st = {"avg_ms": round(avg, 4), "launches_per_step": len(ts) / args.steps}
-        if name in kb:
-            st["alg_bytes"] = kb[name]
-            st["achieved_GBs"] = round(kb[name] / (avg * 1e-3) / 1e9, 1)
+        if name in FLOP_ENTRY_POINTS and name in per_work:  # MFMA-bound: algorithmic FLOPs per launch
+            st["alg_tflop"] = round(per_work[name] / len(ts) / 1e12, 6)
+            st["achieved_TFLOPs"] = round(per_work[name] / (sum(ts) * 1e-3) / 1e12, 1)
+        elif name in kb or name in per_work:  # HBM-bound: algorithmic bytes per launch
+            st["alg_bytes"] = kb[name] if name in kb else int(per_work[name] / len(ts))
+            st["achieved_GBs"] = round(st["alg_bytes"] / (avg * 1e-3) / 1e9, 1)
         kstats[name] = st
-    dom = max((n for n in kstats if n in kb), key=lambda n: kstats[n]["avg_ms"] * kstats[n]["launches_per_step"])
-    dom_ach = kstats[dom]["achieved_GBs"]
+    # the dominant entry point: most time per step
+    dom = max(kstats, key=lambda n: kstats[n]["avg_ms"] * kstats[n]["launches_per_step"])
     traffic = read_traffic(args.config, dom)
+    if "achieved_TFLOPs" in kstats[dom]:
+        ach = kstats[dom]["achieved_TFLOPs"]
+        roof = {"kernel": dom, "bound": "mfma", "achieved": ach, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
+                "frac": round(ach * 1e12 / MFMA_BF16_PEAK, 4), "traffic": traffic}
+    else:
+        ach = kstats[dom]["achieved_GBs"]
+        roof = {"kernel": dom, "bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic}
     for n, st in sorted(kstats.items(), key=lambda kv: -kv[1]["avg_ms"]):
         log(f"  {n:28s} {st}")
     log(f"step {ms:.3f} ms, HIP entry points {sum(s['avg_ms'] * s['launches_per_step'] for s in kstats.values()):.3f} ms")
@@ -267,8 +286,7 @@ def main():
                    "precision": "bf16 autocast, fp32 master weights"},
         "mfma_frac_module": round(flops / (ms * 1e-3) / MFMA_BF16_PEAK, 4),
         "module_tflop_per_step": round(flops / 1e12, 4),
-        "roofline": {"kernel": dom, "bound": "hbm", "achieved": dom_ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dom_ach / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "roofline": roof,
         "kernels": kstats,
     }
     if not args.no_cpu_baseline:

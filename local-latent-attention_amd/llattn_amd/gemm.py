@@ -41,7 +41,8 @@ def _run(M: int, N: int, K: int, A: torch.Tensor, a_trans: bool, B: torch.Tensor
     nws = lib.llattn_gemm_workspace_size(ctypes.byref(desc))
     ws = torch.empty((max(nws, 1),), dtype=torch.uint8, device=C.device) if nws else None
     from .ops import _call
-    _call("llattn_gemm", ctypes.byref(desc), None if ws is None else ws.data_ptr(), nws, L.stream_ptr(C.device))
+    _call("llattn_gemm", ctypes.byref(desc), None if ws is None else ws.data_ptr(), nws, L.stream_ptr(C.device),
+          work=2 * M * N * K)
 
 
 def linear(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None, out: torch.Tensor | None = None,
@@ -100,5 +101,6 @@ def colsum(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     nws = lib.llattn_colsum_workspace_size(M, N)
     ws = torch.empty((max(nws, 1),), dtype=torch.uint8, device=x.device)
     from .ops import _call
-    _call("llattn_colsum", x.data_ptr(), x.stride(0), M, N, out.data_ptr(), ws.data_ptr(), nws, L.stream_ptr(x.device))
+    _call("llattn_colsum", x.data_ptr(), x.stride(0), M, N, out.data_ptr(), ws.data_ptr(), nws, L.stream_ptr(x.device),
+          work=M * N * 2 + N * 4)
     return out

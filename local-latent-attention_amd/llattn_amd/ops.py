@@ -28,12 +28,13 @@ from .linear import input_grad, linear_fwd, weight_grad
 
 _byref = ctypes.byref
 
-# When set to a list, every C-ABI call appends (entry point, start event, end event) recorded on
+# When set to a list, every C-ABI call appends (entry point, start event, end event, work) recorded on
 # the stream the call launches on; a benchmark turns this on to time kernels inside its timed region.
+# `work` is the call's algorithmic FLOPs (GEMMs) or bytes (column sums) when the caller states it.
 EVENT_LOG = None
 
 
-def _call(name: str, *args) -> None:
+def _call(name: str, *args, work=None) -> None:
     fn = getattr(L.load(), name)
     if EVENT_LOG is None:
         rc = fn(*args)
@@ -42,7 +43,7 @@ def _call(name: str, *args) -> None:
         start.record()
         rc = fn(*args)
         end.record()
-        EVENT_LOG.append((name, start, end))
+        EVENT_LOG.append((name, start, end, work))
     L.check(rc, name)
 
 
