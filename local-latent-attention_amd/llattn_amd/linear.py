@@ -60,6 +60,7 @@ def weight_grad(dy2: torch.Tensor, x2: torch.Tensor, bias_grad: bool = False):
 class _Project(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, library, pools, *params):
+        # library: (forward on hipBLASLt, input gradient on hipBLASLt)
         ctx.set_materialize_grads(False)
         ws, bs = params[0::2], params[1::2]
         has_bias = bs[0] is not None
@@ -77,7 +78,7 @@ class _Project(torch.autograd.Function):
                 if has_bias:
                     bcat[o:o + n].copy_(b)
                 o += n
-            y = linear_fwd(x2, wcat, bcat, library)
+            y = linear_fwd(x2, wcat, bcat, library[0])
             pooled = []
             if pools:
                 from .ops import _contig, pool_fwd_into
@@ -105,7 +106,7 @@ class _Project(torch.autograd.Function):
                 if not dy2.is_contiguous():
                     dy2 = dy2.contiguous()
                 if ctx.needs_input_grad[0]:
-                    dx = input_grad(dy2, wcat, library).view(*lead, K).to(xdt)
+                    dx = input_grad(dy2, wcat, library[1]).view(*lead, K).to(xdt)
                 dw, db = weight_grad(dy2, x2, has_bias)
             if ctx.needs_input_grad[0] and any(g is not None for g in dpooled):
                 # pooling backward accumulates straight into the projection's input gradient
@@ -126,12 +127,12 @@ class _Project(torch.autograd.Function):
         return (dx, None, None, *grads)
 
 
-def project(x: torch.Tensor, *linears: torch.nn.Linear, library: bool = False, pools=()):
+def project(x: torch.Tensor, *linears: torch.nn.Linear, library_fwd: bool = False, library_dx: bool = False,
+            pools=()):
     """bf16 ``x @ [W_1; W_2; ...]^T + [b_1; b_2; ...]`` (all layers share the input width); backward gives
-    fp32 weight and bias gradients in the parameters' dtypes.  ``library=True`` keeps the forward and
-    input-gradient products on hipBLASLt (the weight gradient always runs on the MFMA kernel when its shape
-    allows): at the block's widest projection (config 2: 32768 x 4736 x 1408) the library kernel is still
-    the faster of the two.
+    fp32 weight and bias gradients in the parameters' dtypes.  ``library_fwd`` / ``library_dx`` put the
+    forward / input-gradient product on hipBLASLt instead of the MFMA kernel (the weight gradient always
+    runs on the MFMA kernel when its shape allows); the block picks per projection whichever is faster.
 
     ``pools``: ``(seg, n_seg, divisor)`` segment poolings of the same ``x [B, T, K]`` (as
     :func:`llattn_amd.ops.pool`) returned after the projection, ``(y, pooled_1, ...)``; their backward adds
@@ -140,5 +141,5 @@ def project(x: torch.Tensor, *linears: torch.nn.Linear, library: bool = False, p
     params = []
     for lin in linears:
         params += [lin.weight, lin.bias]
-    out = _Project.apply(x, library, tuple(pools), *params)
+    out = _Project.apply(x, (library_fwd, library_dx), tuple(pools), *params)
     return out if pools else out[0]

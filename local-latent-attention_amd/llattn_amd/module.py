@@ -30,6 +30,12 @@ from . import _lib as L
 from .linear import project
 from .ops import LLAttnCore, _Prof, pool
 
+# Which bf16 projection products run on hipBLASLt rather than the MFMA kernel (measured at config 2,
+# whole step): the two forwards with K = 1408 are about 1% faster on the library; every input and
+# weight gradient is faster on the MFMA kernel (qkv input gradient by about 15%).
+QKV_FWD_LIBRARY = True
+OUT_FWD_LIBRARY = True
+
 
 class LocalLatentAttentionTriton(nn.Module):
     """``LocalLatentAttentionTriton(d_model, n_heads, latent_heads, latent_dim, n_latents, window,
@@ -117,14 +123,14 @@ class LocalLatentAttentionTriton(nn.Module):
         pooled = None
         if macro and bf16:
             # both poolings of x ride on the projection, whose backward adds their gradients in place
-            qkvr, pq, pooled = project(x, self.qkv_proj, library=True,
+            qkvr, pq, pooled = project(x, self.qkv_proj, library_fwd=QKV_FWD_LIBRARY,
                                        pools=[(lay.q_block, lay.n_q, L.DIV_SEG), latents])
             rq = project(pq, self.rq_proj)
         elif macro:
             qkvr = self.qkv_proj(x)
             rq = self.rq_proj(pool(x, lay.q_block, lay.n_q, L.DIV_SEG))
         elif bf16:
-            qkvr, pooled = project(x, self.qkv_proj, self.rq_proj, library=True, pools=[latents])
+            qkvr, pooled = project(x, self.qkv_proj, self.rq_proj, library_fwd=QKV_FWD_LIBRARY, pools=[latents])
             rq = None
         else:
             w = torch.cat([self.qkv_proj.weight, self.rq_proj.weight], dim=0)
@@ -143,7 +149,7 @@ class LocalLatentAttentionTriton(nn.Module):
             # the gate mix runs in the local kernel's epilogue: its time is in local_attention_ms
             prof.t["gate_mix_ms"] = 0.0
             self._record_profile(prof, lay)
-        return project(y, self.out) if bf16 else self.out(y)
+        return project(y, self.out, library_fwd=OUT_FWD_LIBRARY) if bf16 else self.out(y)
 
     def _record_profile(self, prof, lay: L.Layout) -> None:
         t = prof.t
