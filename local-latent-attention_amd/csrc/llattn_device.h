@@ -350,8 +350,8 @@ __device__ __forceinline__ uint2 buf_ld8(__amdgpu_buffer_rsrc_t r, uint32_t off)
   return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
 }
 
-// BufTile: a bf16 RowTile read with buffer loads.  Each thread's byte offsets
-// within a tile are fixed (set once by init for the view's row stride), the
+// BufTile: a bf16 RowTile read with buffer loads.  Each thread's byte offset
+// within a tile is a fixed function of its index and the row stride; the
 // tile's rows come from a resource that ends with the last valid row, so
 // rows past the end and padding dims read as zero without branches.
 // Offsets are 32-bit: 64 rows of the view must span less than 2 GiB.
@@ -359,25 +359,23 @@ template <int DHP, int NTHR>
 struct BufTile {
   static constexpr int CPR = DHP / 8, TASKS = 64 * CPR, IT = (TASKS + NTHR - 1) / NTHR;
   uint4 x[IT];
-  uint32_t off[IT];
-  __device__ __forceinline__ void init(int st, int Dh) {
-#pragma unroll
-    for (int it = 0; it < IT; ++it) {
-      const int task = threadIdx.x + NTHR * it, row = task / CPR, col = (task % CPR) * 8;
-      off[it] = (task < TASKS && col < Dh) ? (uint32_t)(row * st + col) * 2u : kOffOOB;
-    }
-  }
   // rows [r0, r_end) of the view at base (row stride st elements)
   __device__ __forceinline__ void load(const uint16_t* base, int st, int r0, int r_end, int Dh) {
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(base + (int64_t)r0 * st, ((int64_t)(r_end - r0 - 1) * st + Dh) * 2);
 #pragma unroll
-    for (int it = 0; it < IT; ++it) x[it] = buf_ld16(rs, off[it]);
+    for (int it = 0; it < IT; ++it) {
+      const int task = threadIdx.x + NTHR * it, row = task / CPR, col = (task % CPR) * 8;
+      x[it] = buf_ld16(rs, (task < TASKS && col < Dh) ? (uint32_t)(row * st + col) * 2u : kOffOOB);
+    }
   }
   template <int P>
   __device__ __forceinline__ void store(uint16_t* lds) const {
+    // the thread's LDS offsets are recomputed here rather than kept live across a caller's loop
+    int zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-      const int task = threadIdx.x + NTHR * it, row = task / CPR, col = (task % CPR) * 8;
+      const int task = threadIdx.x + zero + NTHR * it, row = task / CPR, col = (task % CPR) * 8;
       if (task < TASKS) st16(lds + row * P + col, x[it]);
     }
   }

@@ -459,7 +459,7 @@ __global__ __launch_bounds__(256) void local_bwd_kv_kernel(const LocalArgs a) {
 //   1. stage q / k / v of the step (prefetched into registers one step ahead),
 //      and gate backward by all 512 threads, eight per query row (dO into LDS,
 //      D, dremote to HBM, gate partial sums kept per thread in LDS across the
-//      segment); then the next step's loads are put in flight;
+//      segment); the next step's q / k / v loads go out before the gate, its gate rows after;
 //   2. query waves 0-3 (16 queries each): dQ over key tiles qt-1 and qt;
 //      key waves 4-7 (16 keys each): dK / dV contributions of the step's
 //      queries to key tiles qt-1 (then complete and stored) and qt (kept in
@@ -503,13 +503,16 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
   const T* dybase = static_cast<const T*>(a.dy) + b * a.dy_sb + h * a.dy_sh;
   const T* olbase = static_cast<const T*>(a.ol) + b * a.o_sb + h * a.o_sh;
   const T* rbase = static_cast<const T*>(a.rem) + b * a.r_sb + h * a.r_sh;
-  T* dqbase = static_cast<T*>(a.dq) + b * a.dq_sb + h * a.dq_sh;
-  T* dkbase = static_cast<T*>(a.dk) + b * a.dk_sb + h * a.dk_sh;
-  T* dvbase = static_cast<T*>(a.dv) + b * a.dv_sb + h * a.dv_sh;
-  T* drbase = static_cast<T*>(a.dr) + b * a.dr_sb + h * a.dr_sh;
-  // row strides below 2^24 (checked by the launcher); fewer live scalar registers
+  // row strides below 2^24 and (batch, head) slabs below 2^30 elements (checked by the launcher)
   const int q_st = (int)a.q_st, k_st = (int)a.k_st, v_st = (int)a.v_st, dy_st = (int)a.dy_st, o_st = (int)a.o_st;
   const int r_sn = (int)a.r_sn, dq_st = (int)a.dq_st, dk_st = (int)a.dk_st, dv_st = (int)a.dv_st, dr_st = (int)a.dr_st;
+  // Outputs and the per-row stats go through range-checked buffer accesses over this (batch, head)
+  // slab: a masked-off access is an offset past the extent, never a skipped instruction, so every
+  // step issues the same memory operations and the compiler's wait counts stay exact.
+  auto slab = [&](const void* base, int st) { return make_rsrc(base, ((int64_t)(T_ - 1) * st + Dh) * 2); };
+  const auto rdr = slab(static_cast<T*>(a.dr) + b * a.dr_sb + h * a.dr_sh, dr_st);
+  const float* wrow = a.w + hrow;
+  const float* lrow = a.lse + hrow;
 
   for (int d = tid; d < DHP; d += NTHR) {
     gls[d] = d < Dh ? a.gl[h * a.gate_hs + d] : 0.f;
@@ -520,43 +523,33 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
 
   // prefetch: q / k / v rows of a tile (row-tile layout) and the gate inputs of its rows (gate layout)
   BufTile<DHP, NTHR> rq, rk, rv;
-  rq.init(q_st, Dh);
-  rk.init(k_st, Dh);
-  rv.init(v_st, Dh);
-  // gate rows: this thread's 8-byte groups at fixed offsets within a tile (out of range: zero)
-  uint32_t odyo[GV], orem[GV];  // dy and o_local share one offset when their strides agree
-  const bool same_st = dy_st == o_st;
-#pragma unroll
-  for (int j = 0; j < GV; ++j) {
-    const int d = gd0 + 4 * j;
-    odyo[j] = d < Dh ? (uint32_t)(grow * dy_st + d) * 2u : kOffOOB;
-    orem[j] = d < Dh ? (uint32_t)(grow * r_sn + d) * 2u : kOffOOB;
-  }
+  // gate rows: this thread's 8-byte groups at offsets within a tile (out of range: zero)
+  auto goff = [&](int st, int j) { return gd0 + 4 * j < Dh ? (uint32_t)(grow * st + gd0 + 4 * j) * 2u : kOffOOB; };
   const bool qb1 = a.q_block == 1;
   uint2 pdy[GV], pol[GV], prm[GV];
-  float pw = 0.f, plse = kNegInf;
-  auto load_step = [&](int qt) {
+  float pw = 0.f, plse = 0.f;
+  auto load_tiles = [&](int qt) {  // q / k / v rows of tile qt (zero past the sequence)
     const int q0 = qt * 64, qend = min(T_, q0 + 64);
     rq.load(qbase, q_st, q0, qend, Dh);
-    if (qt < t1) {  // the extra step needs no keys of its own tile
-      rk.load(kbase, k_st, q0, qend, Dh);
-      rv.load(vbase, v_st, q0, qend, Dh);
-    }
-    const int rows = qend - q0;
+    rk.load(kbase, k_st, q0, qend, Dh);
+    rv.load(vbase, v_st, q0, qend, Dh);
+  };
+  auto load_gate = [&](int qt) {  // dy / o_local / remote rows, w and lse of tile qt (gate layout)
+    const int q0 = qt * 64, qend = min(T_, q0 + 64), rows = qend - q0;
     const auto rdy = make_rsrc(dybase + (int64_t)q0 * dy_st, ((int64_t)(rows - 1) * dy_st + Dh) * 2);
     const auto rol = make_rsrc(olbase + (int64_t)q0 * o_st, ((int64_t)(rows - 1) * o_st + Dh) * 2);
 #pragma unroll
     for (int j = 0; j < GV; ++j) {
-      pdy[j] = buf_ld8(rdy, odyo[j]);
-      pol[j] = buf_ld8(rol, same_st ? odyo[j] : (gd0 + 4 * j < Dh ? (uint32_t)(grow * o_st + gd0 + 4 * j) * 2u
-                                                                   : kOffOOB));
+      pdy[j] = buf_ld8(rdy, goff(dy_st, j));
+      pol[j] = buf_ld8(rol, goff(o_st, j));
     }
+    const int qi = q0 + grow;
     if (qb1) {  // one remote row per token
       const auto rrm = make_rsrc(rbase + (int64_t)q0 * r_sn, ((int64_t)(rows - 1) * r_sn + Dh) * 2);
 #pragma unroll
-      for (int j = 0; j < GV; ++j) prm[j] = buf_ld8(rrm, orem[j]);
+      for (int j = 0; j < GV; ++j) prm[j] = buf_ld8(rrm, goff(r_sn, j));
     } else {  // one remote row per latent query of q_block tokens: rows counted from the tile's first one
-      const int qi = q0 + grow, rq0 = q0 / a.q_block;
+      const int rq0 = q0 / a.q_block;
       const int rrel = (qi - rq0 * a.q_block) / a.q_block, rlast = (qend - 1) / a.q_block - rq0;
       const auto rrm = make_rsrc(rbase + (int64_t)rq0 * r_sn, ((int64_t)rlast * r_sn + Dh) * 2);
 #pragma unroll
@@ -565,11 +558,17 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
         prm[j] = buf_ld8(rrm, (qi < T_ && d < Dh) ? (uint32_t)(rrel * r_sn + d) * 2u : kOffOOB);
       }
     }
-    const int qi = q0 + grow;
-    const bool ok = qi < T_;
-    pw = ok ? a.w[hrow + qi] : 0.f;
-    plse = ok ? a.lse[hrow + qi] : kNegInf;
+    const int qc = min(qi, T_ - 1);  // always one load each (rows past the end are masked by the gate)
+    pw = wrow[qc];
+    plse = lrow[qc];
   };
+  // 4 values of a row as bf16 through a buffer store (offset past the extent: dropped)
+  auto store4 = [&](__amdgpu_buffer_rsrc_t rs, uint32_t off, const float v[4]) {
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 x = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    __builtin_amdgcn_raw_buffer_store_b64(x, rs, off, 0, 0);
+  };
+
   if (t0 > 0) {  // keys of tile t0-1 for the first step's dQ
     const int p0 = (t0 - 1) * 64;
     rk.load(kbase, k_st, p0, p0 + 64, Dh);
@@ -577,94 +576,98 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
     rk.template store<KP>(SK[(t0 - 1) & 1]);
     rv.template store<KP>(SV[(t0 - 1) & 1]);
   }
-  load_step(t0);
+  load_tiles(t0);
+  load_gate(t0);
 
-  f32x4 pk[NT], pv[NT];  // key waves: partial dK / dV of this wave's 16 keys of key tile qt-1
-#pragma unroll
-  for (int t = 0; t < NT; ++t) pk[t] = pv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  for (int qt = t0; qt <= tlast; ++qt) {
+  // ---- 1. stage the step's rows; gate backward in the gate layout (every thread) ----
+  auto stage_and_gate = [&](int qt) {
     const bool full = qt < t1;
-    const bool own_prev = qt - 1 >= t0;
-    const int cur = qt & 1, prv = cur ^ 1;
-    const int q0 = qt * 64, qend = min(T_, q0 + 64);
-
-    // ---- 1. stage the step's rows; gate backward in the gate layout ----
+    const int cur = qt & 1, q0 = qt * 64;
     lds_barrier();  // the previous step is done with SQ, SO, SK[cur], SV[cur] and the per-query stats
     rq.template store<KP>(SQ);
     if (full) {
       rk.template store<KP>(SK[cur]);
       rv.template store<KP>(SV[cur]);
     }
-    {
-      const int qi = q0 + grow;
-      const bool qv = qi < T_;
-      const float wq = pw;
-      float dyv[GS], olv[GS], rmv[GS];
+    // the next step's q / k / v loads go out now (their registers are free); its gate rows after the
+    // gate, which still reads this step's
+    load_tiles(qt + 1);
+    const int qi = q0 + grow;
+    const bool qv = qi < T_;
+    const float wq = qv ? pw : 0.f, lse_nat = qv ? plse : kNegInf;
+    const int qb0 = q0 / a.bs, qr0 = q0 - qb0 * a.bs;  // block of the tile's first row (uniform)
+    float dyv[GS], olv[GS], rmv[GS];
 #pragma unroll
-      for (int j = 0; j < GV; ++j) {
-        unpack_bf16x4(pdy[j], dyv + 4 * j);
-        unpack_bf16x4(pol[j], olv + 4 * j);
-        unpack_bf16x4(prm[j], rmv + 4 * j);
+    for (int j = 0; j < GV; ++j) {
+      unpack_bf16x4(pdy[j], dyv + 4 * j);
+      unpack_bf16x4(pol[j], olv + 4 * j);
+      unpack_bf16x4(prm[j], rmv + 4 * j);
+    }
+    float dot1 = 0.f;
+#pragma unroll
+    for (int e = 0; e < GS; ++e) dot1 += dyv[e] * (olv[e] - rmv[e]);
+    dot1 = sum_lanes8(dot1);
+    const float delta = wq * (1.f - wq) * dot1;
+    float Dp = 0.f;
+#pragma unroll
+    for (int j = 0; j < GV; ++j) {
+      const int d = gd0 + 4 * j;
+      const float4 gl4 = *reinterpret_cast<const float4*>(gls + d);
+      const float4 gr4 = *reinterpret_cast<const float4*>(grs + d);
+      const float glv[4] = {gl4.x, gl4.y, gl4.z, gl4.w}, grv[4] = {gr4.x, gr4.y, gr4.z, gr4.w};
+      float dov[4], drv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = 4 * j + i;
+        dov[i] = round_t<T>(wq * dyv[e] + delta * glv[i]);
+        drv[i] = (1.f - wq) * dyv[e] - delta * grv[i];
+        Dp += dov[i] * olv[e];
       }
-      float dot1 = 0.f;
-#pragma unroll
-      for (int e = 0; e < GS; ++e) dot1 += dyv[e] * (olv[e] - rmv[e]);
-      dot1 = sum_lanes8(dot1);
-      const float delta = wq * (1.f - wq) * dot1;
-      float Dp = 0.f;
-#pragma unroll
-      for (int j = 0; j < GV; ++j) {
-        const int d = gd0 + 4 * j;
-        const float4 gl4 = *reinterpret_cast<const float4*>(gls + d);
-        const float4 gr4 = *reinterpret_cast<const float4*>(grs + d);
-        const float glv[4] = {gl4.x, gl4.y, gl4.z, gl4.w}, grv[4] = {gr4.x, gr4.y, gr4.z, gr4.w};
-        float dov[4], drv[4];
+      ::llattn::store4<T>(SO + grow * KP + d, dov);
+      store4(rdr, (full && qv && d < Dh) ? (uint32_t)(qi * dr_st + d) * 2u : kOffOOB, drv);
+      if (full) {
+        f32x4 al = GACC[j][tid], ar = GACC[GV + j][tid];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int e = 4 * j + i;
-          dov[i] = round_t<T>(wq * dyv[e] + delta * glv[i]);
-          drv[i] = (1.f - wq) * dyv[e] - delta * grv[i];
-          Dp += dov[i] * olv[e];
+          al[i] += delta * olv[4 * j + i];
+          ar[i] -= delta * rmv[4 * j + i];
         }
-        store4<T>(SO + grow * KP + d, dov);
-        if (full) {
-          if (qv && d < Dh)
-            store4<T>(drbase + (int64_t)qi * dr_st + d, drv);
-          f32x4 al = GACC[j][tid], ar = GACC[GV + j][tid];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            al[i] += delta * olv[4 * j + i];
-            ar[i] -= delta * rmv[4 * j + i];
-          }
-          GACC[j][tid] = al;
-          GACC[GV + j][tid] = ar;
-        }
-      }
-      Dp = sum_lanes8(Dp);
-      if ((tid & 7) == 0) {
-        Dss[grow] = qv ? Dp : 0.f;
-        lse2s[grow] = (!qv || plse == kNegInf) ? 0.f : plse * kLog2e;
-        los[grow] = qv ? key_lo(qi, a.W, a.bs) : INT_MAX;
+        GACC[j][tid] = al;
+        GACC[GV + j][tid] = ar;
       }
     }
-    if (qt + 1 <= tlast) load_step(qt + 1);
+    Dp = sum_lanes8(Dp);
+    if ((tid & 7) == 0) {
+      Dss[grow] = qv ? Dp : 0.f;
+      lse2s[grow] = (!qv || lse_nat == kNegInf) ? 0.f : lse_nat * kLog2e;
+      // key_lo without a division: the launcher guarantees bs >= 64, so the block of row q0 + grow is
+      // the tile's first block or the next one
+      const int blk = (qb0 + (qr0 + grow >= a.bs)) * a.bs;
+      los[grow] = qv ? max(max(0, qi - a.W), blk - a.W + 1) : INT_MAX;
+    }
+    load_gate(qt + 1);
     lds_barrier();  // dO, the staged rows and the per-query stats are complete
+  };
 
-    // ---- 2. dQ (query waves) and dK / dV (key waves) ----
-    if (qrole) {
+  if (qrole) {
+    // ---- 2q. dQ = scale * sum_j dS_ij k_j over key tiles qt-1 and qt ----
+    const auto rdq = slab(static_cast<T*>(a.dq) + b * a.dq_sb + h * a.dq_sh, dq_st);
+    for (int qt = t0; qt <= tlast; ++qt) {
+      stage_and_gate(qt);
+      const bool full = qt < t1;
+      const int cur = qt & 1, prv = cur ^ 1;
+      const int qw = qt * 64 + w4 * 16, qi = qw + r;
+      const bool qv = qi < T_;
+      f32x4 dq[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) dq[t] = f32x4{0.f, 0.f, 0.f, 0.f};
       if (full) {
-        const int qw = q0 + w4 * 16, qi = qw + r;
-        const bool qv = qi < T_;
         RowFrag<T, DQ> qf, dof;
         qf.load_lds(SQ + row * KP, g);
         dof.load_lds(SO + row * KP, g);
         const float lse2 = lse2s[row], Dq = Dss[row];
         const int lo = los[row], hi = qi - 1;
         const int wlo = max(0, qw - a.W), whi = min(qw + 15, T_ - 1) - 1;
-        f32x4 dq[NT];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) dq[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
           const int kt = qt - 1 + half;
@@ -691,22 +694,32 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
             for (int t = 0; t < NT; ++t) dq[t] = col_mma_rm<KP>(Ks + (16 * st) * KP + 16 * t, dsb, dq[t]);
           }
         }
-        if (qv) {  // lane holds dQ[query qi][16t + 4g + i]
-          T* p = dqbase + (int64_t)qi * dq_st;
-#pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            const int d = 16 * t + 4 * g;
-            float v4[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) v4[i] = dq[t][i] * a.scale;
-            if (d < Dh) store4<T>(p + d, v4);
-          }
-        }
       }
-    } else {
+      // lane holds dQ[query qi][16t + 4g + i]
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int d = 16 * t + 4 * g;
+        float v4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v4[i] = dq[t][i] * a.scale;
+        store4(rdq, (full && qv && d < Dh) ? (uint32_t)(qi * dq_st + d) * 2u : kOffOOB, v4);
+      }
+    }
+  } else {
+    // ---- 2k. dK / dV of this wave's 16 keys of tiles qt-1 (if owned: then complete) and qt ----
+    const auto rdk = slab(static_cast<T*>(a.dk) + b * a.dk_sb + h * a.dk_sh, dk_st);
+    const auto rdv = slab(static_cast<T*>(a.dv) + b * a.dv_sb + h * a.dv_sh, dv_st);
+    f32x4 pk[NT], pv[NT];  // partial dK / dV of this wave's keys of key tile qt-1
+#pragma unroll
+    for (int t = 0; t < NT; ++t) pk[t] = pv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int qt = t0; qt <= tlast; ++qt) {
+      stage_and_gate(qt);
+      const bool full = qt < t1, own_prev = qt - 1 >= t0;
+      const int cur = qt & 1, prv = cur ^ 1;
+      const int q0 = qt * 64, qend = min(T_, q0 + 64);
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        if (half == 0 ? !own_prev : !full) continue;  // uniform
+        const bool active = half == 0 ? own_prev : full;  // uniform
         const int kt = qt - 1 + half;
         const int kw = kt * 64 + w4 * 16, kj = kw + r;
         const bool kv = kj < T_;
@@ -717,58 +730,55 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
           dk[t] = half == 0 ? pk[t] : f32x4{0.f, 0.f, 0.f, 0.f};
           dv[t] = half == 0 ? pv[t] : f32x4{0.f, 0.f, 0.f, 0.f};
         }
-        RowFrag<T, DQ> kf, vf;
-        kf.load_lds((half ? SK[cur] : SK[prv]) + row * KP, g);
-        vf.load_lds((half ? SV[cur] : SV[prv]) + row * KP, g);
+        if (active) {
+          RowFrag<T, DQ> kf, vf;
+          kf.load_lds((half ? SK[cur] : SK[prv]) + row * KP, g);
+          vf.load_lds((half ? SV[cur] : SV[prv]) + row * KP, g);
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-          const int s0 = q0 + 16 * st;
-          if (s0 >= qend || s0 + 15 < wqlo || s0 > wqhi) continue;  // uniform
-          RowFrag<T, DQ> qf, of;
-          qf.load_lds(SQ + (16 * st + r) * KP, g);
-          of.load_lds(SO + (16 * st + r) * KP, g);
-          const int ql = 16 * st + 4 * g;  // this lane's four queries (rows of the step's tile)
-          const int4 lo4 = *reinterpret_cast<const int4*>(los + ql);
-          const float4 l4 = *reinterpret_cast<const float4*>(lse2s + ql);
-          const float4 D4 = *reinterpret_cast<const float4*>(Dss + ql);
-          const int lov[4] = {lo4.x, lo4.y, lo4.z, lo4.w};
-          const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, Dv[4] = {D4.x, D4.y, D4.z, D4.w};
-          const f32x4 sv = row_mma(qf, kf, f32x4{0.f, 0.f, 0.f, 0.f});  // S[query 4g+i][key r]
-          const f32x4 dp = row_mma(of, vf, f32x4{0.f, 0.f, 0.f, 0.f});  // dP[query][key]
-          float pp[4], ds[4];
+          for (int st = 0; st < 4; ++st) {
+            const int s0 = q0 + 16 * st;
+            if (s0 >= qend || s0 + 15 < wqlo || s0 > wqhi) continue;  // uniform
+            RowFrag<T, DQ> qf, of;
+            qf.load_lds(SQ + (16 * st + r) * KP, g);
+            of.load_lds(SO + (16 * st + r) * KP, g);
+            const int ql = 16 * st + 4 * g;  // this lane's four queries (rows of the step's tile)
+            const int4 lo4 = *reinterpret_cast<const int4*>(los + ql);
+            const float4 l4 = *reinterpret_cast<const float4*>(lse2s + ql);
+            const float4 D4 = *reinterpret_cast<const float4*>(Dss + ql);
+            const int lov[4] = {lo4.x, lo4.y, lo4.z, lo4.w};
+            const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, Dv[4] = {D4.x, D4.y, D4.z, D4.w};
+            const f32x4 sv = row_mma(qf, kf, f32x4{0.f, 0.f, 0.f, 0.f});  // S[query 4g+i][key r]
+            const f32x4 dp = row_mma(of, vf, f32x4{0.f, 0.f, 0.f, 0.f});  // dP[query][key]
+            float pp[4], ds[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int qq = q0 + ql + i;
-            const bool ok = kv & (kj >= lov[i]) & (kj <= qq - 1);  // no short circuit: plain selects
-            const float p = fast_exp2(sv[i] * a.scale_log2 - lv[i]);
-            pp[i] = ok ? p : 0.f;
-            ds[i] = pp[i] * (dp[i] - Dv[i]);
-          }
-          const i16x4 ppb = pack_bf16x4(pp), dsb = pack_bf16x4(ds);
+            for (int i = 0; i < 4; ++i) {
+              const int qq = q0 + ql + i;
+              const bool ok = kv & (kj >= lov[i]) & (kj <= qq - 1);  // no short circuit: plain selects
+              const float p = fast_exp2(sv[i] * a.scale_log2 - lv[i]);
+              pp[i] = ok ? p : 0.f;
+              ds[i] = pp[i] * (dp[i] - Dv[i]);
+            }
+            const i16x4 ppb = pack_bf16x4(pp), dsb = pack_bf16x4(ds);
 #pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            dv[t] = col_mma_rm<KP>(SO + (16 * st) * KP + 16 * t, ppb, dv[t]);  // dV^T = dO^T P
-            dk[t] = col_mma_rm<KP>(SQ + (16 * st) * KP + 16 * t, dsb, dk[t]);  // dK^T = Q^T dS
+            for (int t = 0; t < NT; ++t) {
+              dv[t] = col_mma_rm<KP>(SO + (16 * st) * KP + 16 * t, ppb, dv[t]);  // dV^T = dO^T P
+              dk[t] = col_mma_rm<KP>(SQ + (16 * st) * KP + 16 * t, dsb, dk[t]);  // dK^T = Q^T dS
+            }
           }
         }
         if (half == 0) {  // key tile qt-1 is complete: lane holds dK / dV[key kj][16t + 4g + i]
-          if (kv) {
-            T* pkp = dkbase + (int64_t)kj * dk_st;
-            T* pvp = dvbase + (int64_t)kj * dv_st;
+          const bool st_ok = own_prev && kv;
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-              const int d = 16 * t + 4 * g;
-              float k4[4], v4[4];
+          for (int t = 0; t < NT; ++t) {
+            const int d = 16 * t + 4 * g;
+            float k4[4], v4[4];
 #pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                k4[i] = dk[t][i] * a.scale;
-                v4[i] = dv[t][i];
-              }
-              if (d < Dh) {
-                store4<T>(pkp + d, k4);
-                store4<T>(pvp + d, v4);
-              }
+            for (int i = 0; i < 4; ++i) {
+              k4[i] = dk[t][i] * a.scale;
+              v4[i] = dv[t][i];
             }
+            store4(rdk, (st_ok && d < Dh) ? (uint32_t)(kj * dk_st + d) * 2u : kOffOOB, k4);
+            store4(rdv, (st_ok && d < Dh) ? (uint32_t)(kj * dv_st + d) * 2u : kOffOOB, v4);
           }
         } else {
 #pragma unroll
@@ -779,13 +789,9 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
         }
       }
     }
-  }
-  // a segment that ends the sequence: its last key tile gets no more queries
-  if (!qrole && t1 == a.n_qt) {
-    const int kj = (t1 - 1) * 64 + row;
-    if (kj < T_) {
-      T* pkp = dkbase + (int64_t)kj * dk_st;
-      T* pvp = dvbase + (int64_t)kj * dv_st;
+    // a segment that ends the sequence: its last key tile gets no more queries
+    if (t1 == a.n_qt) {
+      const int kj = (t1 - 1) * 64 + row;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const int d = 16 * t + 4 * g;
@@ -795,10 +801,8 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
           k4[i] = pk[t][i] * a.scale;
           v4[i] = pv[t][i];
         }
-        if (d < Dh) {
-          store4<T>(pkp + d, k4);
-          store4<T>(pvp + d, v4);
-        }
+        store4(rdk, (kj < T_ && d < Dh) ? (uint32_t)(kj * dk_st + d) * 2u : kOffOOB, k4);
+        store4(rdv, (kj < T_ && d < Dh) ? (uint32_t)(kj * dv_st + d) * 2u : kOffOOB, v4);
       }
     }
   }
@@ -853,14 +857,19 @@ void launch_fwd(const LocalArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL((local_fwd_kernel<T, DHP>), dim3(a.B * a.H * a.n_qt), dim3(256), 0, stream, a);
 }
 // The fused one-pass backward covers bf16 with padded head dims up to 96,
-// windows up to 64 (keys of a query tile span two key tiles) and row strides
+// windows up to 64 (keys of a query tile span two key tiles), local blocks of
+// at least 64 tokens (a tile spans at most two blocks), row strides
 // below 2^24 elements (its buffer loads address a 64-row tile with 32-bit
-// byte offsets).
+// byte offsets) and output slabs of T rows below 2^30 elements.
 bool fused_bwd(const LocalArgs& a, int dtype, int dhp) {
   const int64_t lim = int64_t(1) << 24;
   const bool st32 = a.q_st <= lim && a.k_st <= lim && a.v_st <= lim && a.dy_st <= lim && a.o_st <= lim &&
                     a.r_sn <= lim && a.dq_st <= lim && a.dk_st <= lim && a.dv_st <= lim && a.dr_st <= lim;
-  return dtype == LLATTN_BF16 && dhp <= 96 && a.W <= 64 && st32;
+  // outputs are addressed with 32-bit byte offsets over a (batch, head) slab of T rows
+  const int64_t slab = int64_t(1) << 30;
+  const bool slab32 = (int64_t)a.T * a.dq_st < slab && (int64_t)a.T * a.dk_st < slab &&
+                      (int64_t)a.T * a.dv_st < slab && (int64_t)a.T * a.dr_st < slab;
+  return dtype == LLATTN_BF16 && dhp <= 96 && a.W <= 64 && a.bs >= 64 && st32 && slab32;
 }
 
 template <typename T, int DHP>
