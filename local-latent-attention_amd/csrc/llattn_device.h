@@ -360,22 +360,23 @@ struct BufTile {
   static constexpr int CPR = DHP / 8, TASKS = 64 * CPR, IT = (TASKS + NTHR - 1) / NTHR;
   uint4 x[IT];
   // rows [r0, r_end) of the view at base (row stride st elements)
-  __device__ __forceinline__ void load(const uint16_t* base, int st, int r0, int r_end, int Dh) {
+  __device__ __forceinline__ void load(const uint16_t* base, int st, int r0, int r_end, int Dh, int tid) {
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(base + (int64_t)r0 * st, ((int64_t)(r_end - r0 - 1) * st + Dh) * 2);
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-      const int task = threadIdx.x + NTHR * it, row = task / CPR, col = (task % CPR) * 8;
+      const int task = tid + NTHR * it, row = task / CPR, col = (task % CPR) * 8;
       x[it] = buf_ld16(rs, (task < TASKS && col < Dh) ? (uint32_t)(row * st + col) * 2u : kOffOOB);
     }
   }
+  // tid: the thread's index among the NTHR threads that share the tile
   template <int P>
-  __device__ __forceinline__ void store(uint16_t* lds) const {
+  __device__ __forceinline__ void store(uint16_t* lds, int tid) const {
     // the thread's LDS offsets are recomputed here rather than kept live across a caller's loop
     int zero;
     asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-      const int task = threadIdx.x + zero + NTHR * it, row = task / CPR, col = (task % CPR) * 8;
+      const int task = tid + zero + NTHR * it, row = task / CPR, col = (task % CPR) * 8;
       if (task < TASKS) st16(lds + row * P + col, x[it]);
     }
   }

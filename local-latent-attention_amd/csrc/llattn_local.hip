@@ -455,41 +455,43 @@ __global__ __launch_bounds__(256) void local_bwd_kv_kernel(const LocalArgs a) {
 // query tiles qt and qt+1, so after step qt key tile qt-1 is complete.  Every
 // row of q, k, v, dy, o_local and remote is read from HBM once per segment
 // (plus one tile of halo at each end), dO never leaves LDS, and each output
-// row is written once, straight from registers.  Two LDS barriers per step:
-//   1. stage q / k / v of the step (prefetched into registers one step ahead),
-//      and gate backward by all 512 threads, eight per query row (dO into LDS,
-//      D, dremote to HBM, gate partial sums kept per thread in LDS across the
-//      segment); the next step's q / k / v loads go out before the gate, its gate rows after;
-//   2. query waves 0-3 (16 queries each): dQ over key tiles qt-1 and qt;
-//      key waves 4-7 (16 keys each): dK / dV contributions of the step's
-//      queries to key tiles qt-1 (then complete and stored) and qt (kept in
-//      registers for the next step).
+// row is written once, straight from registers.
+//
+// The two roles work one tile apart, with ONE LDS barrier per step:
+//   query waves 0-3: gate backward of tile qt+1 (8 threads per row, 2 rows per
+//     thread: dO into LDS, D / lse / key bounds, dremote to HBM, gate partial
+//     sums kept per thread in LDS for the segment), then dQ of tile qt over key
+//     tiles qt-1 and qt (16 queries per wave);
+//   key waves 4-7: stage q / k / v of tile qt+1 into LDS (prefetched one step
+//     ahead), then the dK / dV contributions of tile qt's queries to key tiles
+//     qt-1 (then complete and stored) and qt (kept in registers).
+// q and dO are double-buffered by tile parity, k and v triple-buffered, so the
+// tile being produced never overwrites one being read.  Different work on the
+// two waves of each SIMD (VALU-heavy gate, LDS/MFMA-bound products) overlaps.
 // The segment's last key tile needs the queries of the next segment's first
-// tile: an extra step at the end gates that tile and adds its contributions
-// (its own outputs belong to the next segment).  The gate partial sums of the
-// segment are added over its rows in a fixed order at the end.  No atomics:
-// every output has one writer.
+// tile: an extra step at the end adds their contributions (that tile's own
+// outputs belong to the next segment).  Every step issues the same memory
+// operations (masked lanes use out-of-range buffer offsets), so the compiler's
+// vmcnt waits are exact.  No atomics: every output has one writer.
 // ----------------------------------------------------------------------------
 template <int DHP>
 __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a, int seg_tiles) {
   using T = uint16_t;
-  constexpr int NTHR = 512;
-  constexpr int DQ = DHP / 4, NT = DHP / 16, KP = DHP + kRowPad<T>;
+  constexpr int DQ = DHP / 4, NT = DHP / 16, KP = DHP + kRowPad<T>, TILE = 64 * KP;
   constexpr int GS = DHP / 8, GV = GS / 4;  // gate layout: 8 threads per row, GS dims each, GV groups of 4
-  __shared__ __align__(16) T SQ[64 * KP];     // query rows of the step
-  __shared__ __align__(16) T SO[64 * KP];     // dO rows of the step
-  __shared__ __align__(16) T SK[2][64 * KP];  // key rows by tile parity
-  __shared__ __align__(16) T SV[2][64 * KP];  // value rows by tile parity
-  __shared__ __align__(16) f32x4 GACC[2 * GV][NTHR];  // per-thread gate partials: [l groups | r groups][thread]
+  __shared__ __align__(16) T SQ[2 * TILE];  // query rows by tile parity
+  __shared__ __align__(16) T SO[2 * TILE];  // dO rows by tile parity
+  __shared__ __align__(16) T SK[3 * TILE];  // key rows by tile index mod 3
+  __shared__ __align__(16) T SV[3 * TILE];  // value rows by tile index mod 3
   __shared__ __align__(16) float gls[DHP], grs[DHP];
-  __shared__ __align__(16) float lse2s[64], Dss[64];
-  __shared__ __align__(16) int los[64];
+  __shared__ __align__(16) float lse2s[2][64], Dss[2][64];
+  __shared__ __align__(16) int los[2][64];
 
   const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool qrole = wave < 4;
-  const int w4 = wave & 3, row = w4 * 16 + r;       // query row (query waves) or key row (key waves)
-  const int grow = tid >> 3, gd0 = (tid & 7) * GS;  // gate layout: row and first dim
+  const int w4 = wave & 3, row = w4 * 16 + r;  // query row (query waves) or key row (key waves)
+  const int rtid = tid & 255;                  // thread index within the role
   const int n_seg = (a.n_qt + seg_tiles - 1) / seg_tiles;
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
   const int seg = bid % n_seg, bh = bid / n_seg, h = bh % a.H, b = bh / a.H;
@@ -497,71 +499,10 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
   const int tlast = min(t1, a.n_qt - 1);  // the extra step runs when t1 < n_qt
   const int T_ = a.T, Dh = a.Dh;
   const int64_t hrow = ((int64_t)b * a.H + h) * T_;
-  const T* qbase = static_cast<const T*>(a.q) + b * a.q_sb + h * a.q_sh;
-  const T* kbase = static_cast<const T*>(a.k) + b * a.k_sb + h * a.k_sh;
-  const T* vbase = static_cast<const T*>(a.v) + b * a.v_sb + h * a.v_sh;
-  const T* dybase = static_cast<const T*>(a.dy) + b * a.dy_sb + h * a.dy_sh;
-  const T* olbase = static_cast<const T*>(a.ol) + b * a.o_sb + h * a.o_sh;
-  const T* rbase = static_cast<const T*>(a.rem) + b * a.r_sb + h * a.r_sh;
   // row strides below 2^24 and (batch, head) slabs below 2^30 elements (checked by the launcher)
   const int q_st = (int)a.q_st, k_st = (int)a.k_st, v_st = (int)a.v_st, dy_st = (int)a.dy_st, o_st = (int)a.o_st;
   const int r_sn = (int)a.r_sn, dq_st = (int)a.dq_st, dk_st = (int)a.dk_st, dv_st = (int)a.dv_st, dr_st = (int)a.dr_st;
-  // Outputs and the per-row stats go through range-checked buffer accesses over this (batch, head)
-  // slab: a masked-off access is an offset past the extent, never a skipped instruction, so every
-  // step issues the same memory operations and the compiler's wait counts stay exact.
   auto slab = [&](const void* base, int st) { return make_rsrc(base, ((int64_t)(T_ - 1) * st + Dh) * 2); };
-  const auto rdr = slab(static_cast<T*>(a.dr) + b * a.dr_sb + h * a.dr_sh, dr_st);
-  const float* wrow = a.w + hrow;
-  const float* lrow = a.lse + hrow;
-
-  for (int d = tid; d < DHP; d += NTHR) {
-    gls[d] = d < Dh ? a.gl[h * a.gate_hs + d] : 0.f;
-    grs[d] = d < Dh ? a.gr[h * a.gate_hs + d] : 0.f;
-  }
-#pragma unroll
-  for (int j = 0; j < 2 * GV; ++j) GACC[j][tid] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // prefetch: q / k / v rows of a tile (row-tile layout) and the gate inputs of its rows (gate layout)
-  BufTile<DHP, NTHR> rq, rk, rv;
-  // gate rows: this thread's 8-byte groups at offsets within a tile (out of range: zero)
-  auto goff = [&](int st, int j) { return gd0 + 4 * j < Dh ? (uint32_t)(grow * st + gd0 + 4 * j) * 2u : kOffOOB; };
-  const bool qb1 = a.q_block == 1;
-  uint2 pdy[GV], pol[GV], prm[GV];
-  float pw = 0.f, plse = 0.f;
-  auto load_tiles = [&](int qt) {  // q / k / v rows of tile qt (zero past the sequence)
-    const int q0 = qt * 64, qend = min(T_, q0 + 64);
-    rq.load(qbase, q_st, q0, qend, Dh);
-    rk.load(kbase, k_st, q0, qend, Dh);
-    rv.load(vbase, v_st, q0, qend, Dh);
-  };
-  auto load_gate = [&](int qt) {  // dy / o_local / remote rows, w and lse of tile qt (gate layout)
-    const int q0 = qt * 64, qend = min(T_, q0 + 64), rows = qend - q0;
-    const auto rdy = make_rsrc(dybase + (int64_t)q0 * dy_st, ((int64_t)(rows - 1) * dy_st + Dh) * 2);
-    const auto rol = make_rsrc(olbase + (int64_t)q0 * o_st, ((int64_t)(rows - 1) * o_st + Dh) * 2);
-#pragma unroll
-    for (int j = 0; j < GV; ++j) {
-      pdy[j] = buf_ld8(rdy, goff(dy_st, j));
-      pol[j] = buf_ld8(rol, goff(o_st, j));
-    }
-    const int qi = q0 + grow;
-    if (qb1) {  // one remote row per token
-      const auto rrm = make_rsrc(rbase + (int64_t)q0 * r_sn, ((int64_t)(rows - 1) * r_sn + Dh) * 2);
-#pragma unroll
-      for (int j = 0; j < GV; ++j) prm[j] = buf_ld8(rrm, goff(r_sn, j));
-    } else {  // one remote row per latent query of q_block tokens: rows counted from the tile's first one
-      const int rq0 = q0 / a.q_block;
-      const int rrel = (qi - rq0 * a.q_block) / a.q_block, rlast = (qend - 1) / a.q_block - rq0;
-      const auto rrm = make_rsrc(rbase + (int64_t)rq0 * r_sn, ((int64_t)rlast * r_sn + Dh) * 2);
-#pragma unroll
-      for (int j = 0; j < GV; ++j) {
-        const int d = gd0 + 4 * j;
-        prm[j] = buf_ld8(rrm, (qi < T_ && d < Dh) ? (uint32_t)(rrel * r_sn + d) * 2u : kOffOOB);
-      }
-    }
-    const int qc = min(qi, T_ - 1);  // always one load each (rows past the end are masked by the gate)
-    pw = wrow[qc];
-    plse = lrow[qc];
-  };
   // 4 values of a row as bf16 through a buffer store (offset past the extent: dropped)
   auto store4 = [&](__amdgpu_buffer_rsrc_t rs, uint32_t off, const float v[4]) {
     typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
@@ -569,93 +510,167 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
     __builtin_amdgcn_raw_buffer_store_b64(x, rs, off, 0, 0);
   };
 
-  if (t0 > 0) {  // keys of tile t0-1 for the first step's dQ
-    const int p0 = (t0 - 1) * 64;
-    rk.load(kbase, k_st, p0, p0 + 64, Dh);
-    rv.load(vbase, v_st, p0, p0 + 64, Dh);
-    rk.template store<KP>(SK[(t0 - 1) & 1]);
-    rv.template store<KP>(SV[(t0 - 1) & 1]);
+  for (int d = tid; d < DHP; d += 512) {
+    gls[d] = d < Dh ? a.gl[h * a.gate_hs + d] : 0.f;
+    grs[d] = d < Dh ? a.gr[h * a.gate_hs + d] : 0.f;
   }
-  load_tiles(t0);
-  load_gate(t0);
+  lds_barrier();  // the gate vectors are read by every query thread from the prologue on
 
-  // ---- 1. stage the step's rows; gate backward in the gate layout (every thread) ----
-  auto stage_and_gate = [&](int qt) {
-    const bool full = qt < t1;
-    const int cur = qt & 1, q0 = qt * 64;
-    lds_barrier();  // the previous step is done with SQ, SO, SK[cur], SV[cur] and the per-query stats
-    rq.template store<KP>(SQ);
-    if (full) {
-      rk.template store<KP>(SK[cur]);
-      rv.template store<KP>(SV[cur]);
-    }
-    // the next step's q / k / v loads go out now (their registers are free); its gate rows after the
-    // gate, which still reads this step's
-    load_tiles(qt + 1);
-    const int qi = q0 + grow;
-    const bool qv = qi < T_;
-    const float wq = qv ? pw : 0.f, lse_nat = qv ? plse : kNegInf;
-    const int qb0 = q0 / a.bs, qr0 = q0 - qb0 * a.bs;  // block of the tile's first row (uniform)
-    float dyv[GS], olv[GS], rmv[GS];
+  // ---- query role: gate backward of one tile (rows gr0 and gr0 + 32, 8 threads per row) ----
+  const T* dybase = static_cast<const T*>(a.dy) + b * a.dy_sb + h * a.dy_sh;
+  const T* olbase = static_cast<const T*>(a.ol) + b * a.o_sb + h * a.o_sh;
+  const T* rbase = static_cast<const T*>(a.rem) + b * a.r_sb + h * a.r_sh;
+  const float* wrow = a.w + hrow;
+  const float* lrow = a.lse + hrow;
+  const int gr0 = rtid >> 3, gd0 = (rtid & 7) * GS;
+  const bool qb1 = a.q_block == 1;
+  uint2 pdy[2][GV], pol[2][GV], prm[2][GV];
+  float pw[2], plse[2];
+  // this thread's gate partial sums (over the segment's rows it gates)
+  float accl[GS], accr[GS];
+  auto goff = [&](int grow, int st, int j) {
+    return gd0 + 4 * j < Dh ? (uint32_t)(grow * st + gd0 + 4 * j) * 2u : kOffOOB;
+  };
+  auto load_gate = [&](int qt) {  // dy / o_local / remote rows, w and lse of tile qt (zero past the end)
+    const int q0 = qt * 64, qend = min(T_, q0 + 64), rows = qend - q0;
+    const auto rdy = make_rsrc(dybase + (int64_t)q0 * dy_st, ((int64_t)(rows - 1) * dy_st + Dh) * 2);
+    const auto rol = make_rsrc(olbase + (int64_t)q0 * o_st, ((int64_t)(rows - 1) * o_st + Dh) * 2);
 #pragma unroll
-    for (int j = 0; j < GV; ++j) {
-      unpack_bf16x4(pdy[j], dyv + 4 * j);
-      unpack_bf16x4(pol[j], olv + 4 * j);
-      unpack_bf16x4(prm[j], rmv + 4 * j);
-    }
-    float dot1 = 0.f;
+    for (int u = 0; u < 2; ++u) {
+      const int grow = gr0 + 32 * u, qi = q0 + grow;
 #pragma unroll
-    for (int e = 0; e < GS; ++e) dot1 += dyv[e] * (olv[e] - rmv[e]);
-    dot1 = sum_lanes8(dot1);
-    const float delta = wq * (1.f - wq) * dot1;
-    float Dp = 0.f;
-#pragma unroll
-    for (int j = 0; j < GV; ++j) {
-      const int d = gd0 + 4 * j;
-      const float4 gl4 = *reinterpret_cast<const float4*>(gls + d);
-      const float4 gr4 = *reinterpret_cast<const float4*>(grs + d);
-      const float glv[4] = {gl4.x, gl4.y, gl4.z, gl4.w}, grv[4] = {gr4.x, gr4.y, gr4.z, gr4.w};
-      float dov[4], drv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int e = 4 * j + i;
-        dov[i] = round_t<T>(wq * dyv[e] + delta * glv[i]);
-        drv[i] = (1.f - wq) * dyv[e] - delta * grv[i];
-        Dp += dov[i] * olv[e];
+      for (int j = 0; j < GV; ++j) {
+        pdy[u][j] = buf_ld8(rdy, goff(grow, dy_st, j));
+        pol[u][j] = buf_ld8(rol, goff(grow, o_st, j));
       }
-      ::llattn::store4<T>(SO + grow * KP + d, dov);
-      store4(rdr, (full && qv && d < Dh) ? (uint32_t)(qi * dr_st + d) * 2u : kOffOOB, drv);
-      if (full) {
-        f32x4 al = GACC[j][tid], ar = GACC[GV + j][tid];
+      if (qb1) {  // one remote row per token
+        const auto rrm = make_rsrc(rbase + (int64_t)q0 * r_sn, ((int64_t)(rows - 1) * r_sn + Dh) * 2);
+#pragma unroll
+        for (int j = 0; j < GV; ++j) prm[u][j] = buf_ld8(rrm, goff(grow, r_sn, j));
+      } else {  // one remote row per latent query of q_block tokens: rows counted from the tile's first one
+        const int rq0 = q0 / a.q_block;
+        const int rrel = (qi - rq0 * a.q_block) / a.q_block, rlast = (qend - 1) / a.q_block - rq0;
+        const auto rrm = make_rsrc(rbase + (int64_t)rq0 * r_sn, ((int64_t)rlast * r_sn + Dh) * 2);
+#pragma unroll
+        for (int j = 0; j < GV; ++j) {
+          const int d = gd0 + 4 * j;
+          prm[u][j] = buf_ld8(rrm, (qi < T_ && d < Dh) ? (uint32_t)(rrel * r_sn + d) * 2u : kOffOOB);
+        }
+      }
+      const int qc = min(qi, T_ - 1);  // always one load each (rows past the end are masked by the gate)
+      pw[u] = wrow[qc];
+      plse[u] = lrow[qc];
+    }
+  };
+  auto gate = [&](int qt, const __amdgpu_buffer_rsrc_t& rdr) {  // gate backward of tile qt (prefetched rows)
+    const bool full = qt < t1;  // the extra step's tile belongs to the next segment: no outputs of its own
+    const int q0 = qt * 64, par = qt & 1;
+    const int qb0 = q0 / a.bs, qr0 = q0 - qb0 * a.bs;  // block of the tile's first row (uniform)
+    T* so = SO + par * TILE;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int grow = gr0 + 32 * u, qi = q0 + grow;
+      const bool qv = qi < T_;
+      const float wq = qv ? pw[u] : 0.f, lse_nat = qv ? plse[u] : kNegInf;
+      float dyv[GS], olv[GS], rmv[GS];
+#pragma unroll
+      for (int j = 0; j < GV; ++j) {
+        unpack_bf16x4(pdy[u][j], dyv + 4 * j);
+        unpack_bf16x4(pol[u][j], olv + 4 * j);
+        unpack_bf16x4(prm[u][j], rmv + 4 * j);
+      }
+      float dot1 = 0.f;
+#pragma unroll
+      for (int e = 0; e < GS; ++e) dot1 += dyv[e] * (olv[e] - rmv[e]);
+      dot1 = sum_lanes8(dot1);
+      const float delta = wq * (1.f - wq) * dot1;
+      float Dp = 0.f;
+#pragma unroll
+      for (int j = 0; j < GV; ++j) {
+        const int d = gd0 + 4 * j;
+        const float4 gl4 = *reinterpret_cast<const float4*>(gls + d);
+        const float4 gr4 = *reinterpret_cast<const float4*>(grs + d);
+        const float glv[4] = {gl4.x, gl4.y, gl4.z, gl4.w}, grv[4] = {gr4.x, gr4.y, gr4.z, gr4.w};
+        float dov[4], drv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          al[i] += delta * olv[4 * j + i];
-          ar[i] -= delta * rmv[4 * j + i];
+          const int e = 4 * j + i;
+          dov[i] = round_t<T>(wq * dyv[e] + delta * glv[i]);
+          drv[i] = (1.f - wq) * dyv[e] - delta * grv[i];
+          Dp += dov[i] * olv[e];
         }
-        GACC[j][tid] = al;
-        GACC[GV + j][tid] = ar;
+        ::llattn::store4<T>(so + grow * KP + d, dov);
+        store4(rdr, (full && qv && d < Dh) ? (uint32_t)(qi * dr_st + d) * 2u : kOffOOB, drv);
+        if (full) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            accl[4 * j + i] += delta * olv[4 * j + i];
+            accr[4 * j + i] -= delta * rmv[4 * j + i];
+          }
+        }
+      }
+      Dp = sum_lanes8(Dp);
+      if ((rtid & 7) == 0) {
+        Dss[par][grow] = qv ? Dp : 0.f;
+        lse2s[par][grow] = (!qv || lse_nat == kNegInf) ? 0.f : lse_nat * kLog2e;
+        // key_lo without a division: bs >= 64 (launcher), so row q0 + grow lies in the tile's first
+        // block or the next one
+        const int blk = (qb0 + (qr0 + grow >= a.bs)) * a.bs;
+        los[par][grow] = qv ? max(max(0, qi - a.W), blk - a.W + 1) : INT_MAX;
       }
     }
-    Dp = sum_lanes8(Dp);
-    if ((tid & 7) == 0) {
-      Dss[grow] = qv ? Dp : 0.f;
-      lse2s[grow] = (!qv || lse_nat == kNegInf) ? 0.f : lse_nat * kLog2e;
-      // key_lo without a division: the launcher guarantees bs >= 64, so the block of row q0 + grow is
-      // the tile's first block or the next one
-      const int blk = (qb0 + (qr0 + grow >= a.bs)) * a.bs;
-      los[grow] = qv ? max(max(0, qi - a.W), blk - a.W + 1) : INT_MAX;
-    }
-    load_gate(qt + 1);
-    lds_barrier();  // dO, the staged rows and the per-query stats are complete
   };
 
+  // ---- key role: q / k / v rows of one tile, staged through registers ----
+  const T* qbase = static_cast<const T*>(a.q) + b * a.q_sb + h * a.q_sh;
+  const T* kbase = static_cast<const T*>(a.k) + b * a.k_sb + h * a.k_sh;
+  const T* vbase = static_cast<const T*>(a.v) + b * a.v_sb + h * a.v_sh;
+  BufTile<DHP, 256> rq, rk, rv;
+  auto load_tiles = [&](int qt) {  // zero past the sequence
+    const int q0 = qt * 64, qend = min(T_, q0 + 64);
+    rq.load(qbase, q_st, q0, qend, Dh, rtid);
+    rk.load(kbase, k_st, q0, qend, Dh, rtid);
+    rv.load(vbase, v_st, q0, qend, Dh, rtid);
+  };
+  auto store_tiles = [&](int qt) {
+    rq.template store<KP>(SQ + (qt & 1) * TILE, rtid);
+    rk.template store<KP>(SK + (qt % 3) * TILE, rtid);
+    rv.template store<KP>(SV + (qt % 3) * TILE, rtid);
+  };
+
+  // ---- prologue: tile t0 staged and gated, keys of tile t0-1 staged ----
   if (qrole) {
-    // ---- 2q. dQ = scale * sum_j dS_ij k_j over key tiles qt-1 and qt ----
+#pragma unroll
+    for (int e = 0; e < GS; ++e) accl[e] = accr[e] = 0.f;
+    load_gate(t0);
+    gate(t0, slab(static_cast<T*>(a.dr) + b * a.dr_sb + h * a.dr_sh, dr_st));
+    load_gate(t0 + 1);
+  } else {
+    if (t0 > 0) {
+      const int p0 = (t0 - 1) * 64;
+      rk.load(kbase, k_st, p0, p0 + 64, Dh, rtid);
+      rv.load(vbase, v_st, p0, p0 + 64, Dh, rtid);
+      rk.template store<KP>(SK + ((t0 - 1) % 3) * TILE, rtid);
+      rv.template store<KP>(SV + ((t0 - 1) % 3) * TILE, rtid);
+    }
+    load_tiles(t0);
+    store_tiles(t0);
+    load_tiles(t0 + 1);
+  }
+  lds_barrier();
+
+  if (qrole) {
+    const auto rdr = slab(static_cast<T*>(a.dr) + b * a.dr_sb + h * a.dr_sh, dr_st);
     const auto rdq = slab(static_cast<T*>(a.dq) + b * a.dq_sb + h * a.dq_sh, dq_st);
     for (int qt = t0; qt <= tlast; ++qt) {
-      stage_and_gate(qt);
+      // gate of the next tile (its rows were prefetched last step), then the loads of the one after
+      if (qt + 1 <= tlast) gate(qt + 1, rdr);
+      load_gate(qt + 2);
+      // ---- dQ = scale * sum_j dS_ij k_j over key tiles qt-1 and qt ----
       const bool full = qt < t1;
-      const int cur = qt & 1, prv = cur ^ 1;
+      const int par = qt & 1;
+      const T* sq = SQ + par * TILE;
+      const T* so = SO + par * TILE;
       const int qw = qt * 64 + w4 * 16, qi = qw + r;
       const bool qv = qi < T_;
       f32x4 dq[NT];
@@ -663,16 +678,16 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
       for (int t = 0; t < NT; ++t) dq[t] = f32x4{0.f, 0.f, 0.f, 0.f};
       if (full) {
         RowFrag<T, DQ> qf, dof;
-        qf.load_lds(SQ + row * KP, g);
-        dof.load_lds(SO + row * KP, g);
-        const float lse2 = lse2s[row], Dq = Dss[row];
-        const int lo = los[row], hi = qi - 1;
+        qf.load_lds(sq + row * KP, g);
+        dof.load_lds(so + row * KP, g);
+        const float lse2 = lse2s[par][row], Dq = Dss[par][row];
+        const int lo = los[par][row], hi = qi - 1;
         const int wlo = max(0, qw - a.W), whi = min(qw + 15, T_ - 1) - 1;
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
           const int kt = qt - 1 + half;
-          const T* Ks = SK[half ? cur : prv];
-          const T* Vs = SV[half ? cur : prv];
+          const T* Ks = SK + ((kt + 3) % 3) * TILE;
+          const T* Vs = SV + ((kt + 3) % 3) * TILE;
 #pragma unroll
           for (int st = 0; st < 4; ++st) {
             const int s0 = kt * 64 + 16 * st;
@@ -704,18 +719,23 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
         for (int i = 0; i < 4; ++i) v4[i] = dq[t][i] * a.scale;
         store4(rdq, (full && qv && d < Dh) ? (uint32_t)(qi * dq_st + d) * 2u : kOffOOB, v4);
       }
+      lds_barrier();  // tile qt+1 is staged and gated; every wave is done with tile qt-1's buffers
     }
   } else {
-    // ---- 2k. dK / dV of this wave's 16 keys of tiles qt-1 (if owned: then complete) and qt ----
     const auto rdk = slab(static_cast<T*>(a.dk) + b * a.dk_sb + h * a.dk_sh, dk_st);
     const auto rdv = slab(static_cast<T*>(a.dv) + b * a.dv_sb + h * a.dv_sh, dv_st);
     f32x4 pk[NT], pv[NT];  // partial dK / dV of this wave's keys of key tile qt-1
 #pragma unroll
     for (int t = 0; t < NT; ++t) pk[t] = pv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int qt = t0; qt <= tlast; ++qt) {
-      stage_and_gate(qt);
+      // stage the next tile (prefetched last step), then the loads of the one after
+      if (qt + 1 <= tlast) store_tiles(qt + 1);
+      load_tiles(qt + 2);
+      // ---- dK / dV of this wave's 16 keys of tiles qt-1 (if owned: then complete) and qt ----
       const bool full = qt < t1, own_prev = qt - 1 >= t0;
-      const int cur = qt & 1, prv = cur ^ 1;
+      const int par = qt & 1;
+      const T* sq = SQ + par * TILE;
+      const T* so = SO + par * TILE;
       const int q0 = qt * 64, qend = min(T_, q0 + 64);
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
@@ -732,19 +752,19 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
         }
         if (active) {
           RowFrag<T, DQ> kf, vf;
-          kf.load_lds((half ? SK[cur] : SK[prv]) + row * KP, g);
-          vf.load_lds((half ? SV[cur] : SV[prv]) + row * KP, g);
+          kf.load_lds(SK + ((kt + 3) % 3) * TILE + row * KP, g);
+          vf.load_lds(SV + ((kt + 3) % 3) * TILE + row * KP, g);
 #pragma unroll
           for (int st = 0; st < 4; ++st) {
             const int s0 = q0 + 16 * st;
             if (s0 >= qend || s0 + 15 < wqlo || s0 > wqhi) continue;  // uniform
             RowFrag<T, DQ> qf, of;
-            qf.load_lds(SQ + (16 * st + r) * KP, g);
-            of.load_lds(SO + (16 * st + r) * KP, g);
+            qf.load_lds(sq + (16 * st + r) * KP, g);
+            of.load_lds(so + (16 * st + r) * KP, g);
             const int ql = 16 * st + 4 * g;  // this lane's four queries (rows of the step's tile)
-            const int4 lo4 = *reinterpret_cast<const int4*>(los + ql);
-            const float4 l4 = *reinterpret_cast<const float4*>(lse2s + ql);
-            const float4 D4 = *reinterpret_cast<const float4*>(Dss + ql);
+            const int4 lo4 = *reinterpret_cast<const int4*>(&los[par][ql]);
+            const float4 l4 = *reinterpret_cast<const float4*>(&lse2s[par][ql]);
+            const float4 D4 = *reinterpret_cast<const float4*>(&Dss[par][ql]);
             const int lov[4] = {lo4.x, lo4.y, lo4.z, lo4.w};
             const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, Dv[4] = {D4.x, D4.y, D4.z, D4.w};
             const f32x4 sv = row_mma(qf, kf, f32x4{0.f, 0.f, 0.f, 0.f});  // S[query 4g+i][key r]
@@ -761,8 +781,8 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
             const i16x4 ppb = pack_bf16x4(pp), dsb = pack_bf16x4(ds);
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-              dv[t] = col_mma_rm<KP>(SO + (16 * st) * KP + 16 * t, ppb, dv[t]);  // dV^T = dO^T P
-              dk[t] = col_mma_rm<KP>(SQ + (16 * st) * KP + 16 * t, dsb, dk[t]);  // dK^T = Q^T dS
+              dv[t] = col_mma_rm<KP>(so + (16 * st) * KP + 16 * t, ppb, dv[t]);  // dV^T = dO^T P
+              dk[t] = col_mma_rm<KP>(sq + (16 * st) * KP + 16 * t, dsb, dk[t]);  // dK^T = Q^T dS
             }
           }
         }
@@ -788,6 +808,7 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
           }
         }
       }
+      lds_barrier();  // tile qt+1 is staged and gated; every wave is done with tile qt-1's buffers
     }
     // a segment that ends the sequence: its last key tile gets no more queries
     if (t1 == a.n_qt) {
@@ -806,16 +827,24 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
       }
     }
   }
-  // gate partials of the segment: the 64 row threads of each dim added in row order
+  // gate partials of the segment: the 32 row threads of each dim (two rows each) added in order,
+  // through LDS that no wave reads any more (the key tiles)
+  float* gacc = reinterpret_cast<float*>(SK);  // [l | r][256 threads][GS]
+  if (qrole) {
+#pragma unroll
+    for (int e = 0; e < GS; ++e) {
+      gacc[rtid * GS + e] = accl[e];
+      gacc[(256 + rtid) * GS + e] = accr[e];
+    }
+  }
   lds_barrier();
   const int nrow = a.B * n_seg, prow = b * n_seg + seg;
-  for (int idx = tid; idx < 2 * DHP; idx += NTHR) {
+  for (int idx = tid; idx < 2 * DHP; idx += 512) {
     const int which = idx / DHP, d = idx % DHP;
     if (d < Dh) {
       const int sg = d / GS, e = d % GS;
-      const int j = which * GV + e / 4, i = e % 4;
       float s = 0.f;
-      for (int rr = 0; rr < 64; ++rr) s += GACC[j][rr * 8 + sg][i];
+      for (int rr = 0; rr < 32; ++rr) s += gacc[(which * 256 + rr * 8 + sg) * GS + e];
       a.gpart[(((int64_t)h * 2 + which) * Dh + d) * nrow + prow] = s;
     }
   }
