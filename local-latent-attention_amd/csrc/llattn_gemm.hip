@@ -28,6 +28,8 @@
 // Split-K (for the weight gradients, whose M x N is small and K = tokens is
 // large): split s covers the 64-wide k steps [s*P/S, (s+1)*P/S) of P and writes fp32 partials; an
 // ordered reduction adds them (deterministic, no atomics).
+#include <type_traits>
+
 #include "llattn_abi.h"
 #include "llattn_device.h"
 
@@ -88,7 +90,14 @@ constexpr int wait_vm_lgkm0(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0070
 // chunk in each of the wave's blocks of an operand tile (rows/cols
 // [o0, o0+256)).  Rows (k-contiguous) or columns (mn-contiguous) past `omax`
 // are clamped to a valid address; the outputs they feed are never stored.
-template <bool KMAJ>
+// k-contiguous tiles: chunk c of row `row` sits at c ^ swz(row).  PERM selects the swizzle of the
+// B operand whose fragments read rows in the permuted order of frag<KMAJ, true> (conflict-free for it).
+template <bool PERM>
+__device__ __forceinline__ int kswz(int row) {
+  return PERM ? (((row >> 1) & 1) | (((row >> 3) & 1) << 1)) : ((row >> 1) & 3);
+}
+
+template <bool KMAJ, bool PERM = false>
 __device__ __forceinline__ void tile_offsets(uint32_t (&off)[DMA_PER_TILE], int64_t ld, int o0, int omax, int wave,
                                              int lane) {
 #pragma unroll
@@ -96,7 +105,7 @@ __device__ __forceinline__ void tile_offsets(uint32_t (&off)[DMA_PER_TILE], int6
     const int bi = wave * DMA_PER_TILE + i;
     if constexpr (KMAJ) {  // block bi = rows 16bi .. 16bi+15, 4 chunks each
       const int row = 16 * bi + (lane >> 2);
-      const int c = (lane & 3) ^ ((lane >> 3) & 3);  // (row >> 1) & 3 == (lane >> 3) & 3
+      const int c = (lane & 3) ^ kswz<PERM>(row);
       const int gr = min(o0 + row, omax - 1);
       off[i] = (uint32_t)(((int64_t)gr * ld + 8 * c) * 2);
     } else {  // block bi = k-rows 2bi, 2bi+1, 32 chunks each
@@ -116,12 +125,14 @@ __device__ __forceinline__ i32x4 step_rsrc(const uint16_t* base, int64_t ld, int
   return i32x4{(int)(uint32_t)addr, (int)((addr >> 32) & 0xffff), (int)(uint32_t)(bytes - skip), kRsrcWord3};
 }
 
-// 8 k values (8g .. 8g+7 of the step) of tile row/column o16 + r for lane (r, g).
-template <bool KMAJ>
+// 8 k values (8g .. 8g+7 of the step) of tile row/column o16 + r for lane (r, g).  PERM (k-contiguous
+// B only): lane r reads row o16 + 8(r/4) + r%4 instead, so that with o16 = 32p + 4u the output
+// columns a lane accumulates for the block pair (u = 0, 1) are 8 consecutive ones, 32p + 8g + 0..7.
+template <bool KMAJ, bool PERM = false>
 __device__ __forceinline__ bf16x8 frag(const unsigned char* tile, int o16, int r, int g) {
   if constexpr (KMAJ) {
-    const int row = o16 + r;
-    return *reinterpret_cast<const bf16x8*>(tile + row * 64 + ((g ^ ((row >> 1) & 3)) << 4));
+    const int row = PERM ? o16 + 8 * (r >> 2) + (r & 3) : o16 + r;
+    return *reinterpret_cast<const bf16x8*>(tile + row * 64 + ((g ^ kswz<PERM>(row)) << 4));
   } else {
     // transposing reads: the 16 lanes of group g supply rows kb + j/4, 8 bytes at
     // column o16 + 4(j%4); lane r receives column o16 + r of those four rows
@@ -140,6 +151,8 @@ __device__ __forceinline__ bf16x8 frag(const unsigned char* tile, int o16, int r
 
 template <bool AK, bool BKM, int EPI>
 __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
+  // bf16 output from a k-contiguous B: permuted B fragments, so each lane writes 16-byte rows directly
+  constexpr bool PB = BKM && EPI == EPI_BF16;
   __shared__ __align__(1024) unsigned char smem[NST * STAGE_BYTES];
   const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -165,9 +178,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // first B row / column of fragment block j (PB: block pairs interleave in groups of four)
+  auto bcol = [&](int j) { return PB ? wn * 128 + 32 * (j >> 1) + 4 * (j & 1) : wn * 128 + 16 * j; };
   uint32_t offa[DMA_PER_TILE], offb[DMA_PER_TILE];
   tile_offsets<AK>(offa, a.lda, m0, a.M, wave, lane);
-  tile_offsets<BKM>(offb, a.ldb, n0, a.N, wave, lane);
+  tile_offsets<BKM, PB>(offb, a.ldb, n0, a.N, wave, lane);
   // DMA of this wave's block q (0..3: operand A, 4..7: operand B) of step kt into `stage`
   auto dma = [&](const i32x4& rsa, const i32x4& rsb, int stage, int q) {
     unsigned char* st = smem + stage * STAGE_BYTES;
@@ -204,7 +219,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
       if (q < 8) na[q] = frag<AK>(Ns, wm * 128 + 16 * q, r, g);
-      else nb[q - 8] = frag<BKM>(Ns + TILE_BYTES, wn * 128 + 16 * (q - 8), r, g);
+      else nb[q - 8] = frag<BKM, PB>(Ns + TILE_BYTES, bcol(q - 8), r, g);
       if (q & 1) dma(rsa, rsb, kt % NST, q >> 1);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {  // B first: lane (r, g) accumulates C[m = r][n = 4g + e]
@@ -227,7 +242,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) fa0[i] = frag<AK>(smem, wm * 128 + 16 * i, r, g);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) fb0[j] = frag<BKM>(smem + TILE_BYTES, wn * 128 + 16 * j, r, g);
+  for (int j = 0; j < 8; ++j) fb0[j] = frag<BKM, PB>(smem + TILE_BYTES, bcol(j), r, g);
   for (int kt = 0; kt < nk; kt += 2) {  // nk is even; fragment buffers alternate between steps
     step(kt, fa0, fb0, fa1, fb1);
     step(kt + 1, fa1, fb1, fa0, fb0);
@@ -236,6 +251,41 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
   __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));  // no DMA may land after the workgroup exits
 
   // ---- epilogue ----
+  if constexpr (PB) {
+    // Lane (r, g) holds C[m0 + wm*128 + 16i + r][n0 + wn*128 + 32p + 8g + e'] for e' = 0..7 in
+    // acc[i][2p] (e' < 4) and acc[i][2p+1] (e' >= 4): one 16-byte store per (i, p), 16 rows x 64
+    // contiguous bytes per instruction, straight from the accumulators.
+    const int rowb = m0 + wm * 128 + r, colb = n0 + wn * 128 + 8 * g;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int col = colb + 32 * p;
+      float4 b0 = make_float4(0.f, 0.f, 0.f, 0.f), b1 = b0;
+      if (a.bias && col < a.N) {
+        b0 = *reinterpret_cast<const float4*>(a.bias + col);
+        b1 = *reinterpret_cast<const float4*>(a.bias + col + 4);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int row = rowb + 16 * i;
+        if (row >= a.M || col >= a.N) continue;
+        const f32x4 u = acc[i][2 * p], w = acc[i][2 * p + 1];
+        float v[8] = {u[0] + b0.x, u[1] + b0.y, u[2] + b0.z, u[3] + b0.w,
+                      w[0] + b1.x, w[1] + b1.y, w[2] + b1.z, w[3] + b1.w};
+        uint16_t* pc = static_cast<uint16_t*>(a.C) + (int64_t)row * a.ldc + col;
+        if (a.accumulate) {
+          const uint4 o = ld16(pc);
+          const uint32_t os[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[2 * e] += __uint_as_float(os[e] << 16);
+            v[2 * e + 1] += __uint_as_float(os[e] & 0xffff0000u);
+          }
+        }
+        st16(pc, make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                            pack_bf16x2(v[6], v[7])));
+      }
+    }
+  } else {
   // Lane (r, g) holds C[m0 + wm*128 + 16i + r][n0 + wn*128 + 16j + 4g + e].  The
   // values (+ bias) go through LDS so that global writes are whole 16-byte
   // chunks of contiguous rows: each wave stages its 128 x 128 block in its own
@@ -325,6 +375,213 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
       }
     }
   }
+  }
+}
+
+// Persistent variant for bf16 C = A Bᵀ (+ bias) with k-contiguous A and B and no K split: one
+// workgroup per CU walks tiles v = blockIdx.x, + gridDim.x, ...  The 4-stage DMA ring runs on
+// across tiles (the last four k steps of a tile fetch the first four of the next), and the
+// epilogue stores straight from the accumulators (permuted B fragments give each lane 8
+// consecutive columns), so a tile's output drains to memory while the next tile's MFMAs run
+// instead of in a burst that every CU pays at the same moment.
+//
+// Memory operations per tile boundary are fixed (one DMA of the next tile's bias slice into LDS,
+// 32 stores; masked lanes use out-of-range buffer offsets, and the first tile issues the same 33
+// with nothing to store), so the vmcnt immediates below are exact: the first three k steps after
+// a boundary wait with 49 younger operations in flight, the others with 16.
+constexpr int EPI_OPS = 1 + 32;  // bias DMA + stores per tile boundary
+
+// Byte offsets relative to the tile origin (row/column 0 of the tile, k = 0) of this lane's
+// 16-byte chunk in each of the wave's blocks of a k-contiguous operand tile.
+template <bool PERM>
+__device__ __forceinline__ void tile_rel_offsets(uint32_t (&off)[DMA_PER_TILE], int64_t ld, int wave, int lane) {
+#pragma unroll
+  for (int i = 0; i < DMA_PER_TILE; ++i) {
+    const int row = 16 * (wave * DMA_PER_TILE + i) + (lane >> 2);
+    const int c = (lane & 3) ^ kswz<PERM>(row);
+    off[i] = (uint32_t)(((int64_t)row * ld + 8 * c) * 2);
+  }
+}
+
+// Buffer descriptor of a k-contiguous operand from row o0 and step k0 on.  Rows past the operand
+// read zero (their offsets are past `bytes`); they only feed outputs that are never stored.
+__device__ __forceinline__ i32x4 tile_rsrc(const uint16_t* base, int64_t ld, int64_t bytes, int o0, int k0) {
+  const int64_t skip = ((int64_t)o0 * ld + k0) * 2;
+  const uint64_t addr = reinterpret_cast<uint64_t>(base) + (uint64_t)skip;
+  return i32x4{(int)(uint32_t)addr, (int)((addr >> 32) & 0xffff), (int)(uint32_t)(bytes - skip), kRsrcWord3};
+}
+
+// tile v -> origin: contiguous tile ranges per XCD, then groups of 8 tile rows
+__device__ __forceinline__ void tile_origin(const GemmArgs& a, int v, int total, int& m0, int& n0) {
+  const int t = xcd_remap(v, total);
+  constexpr int GM = 8;
+  const int group = t / (GM * a.tiles_n), first_m = group * GM;
+  const int gm = min(a.tiles_m - first_m, GM);
+  m0 = (first_m + (t % (GM * a.tiles_n)) % gm) * BM;
+  n0 = ((t % (GM * a.tiles_n)) / gm) * BN;
+}
+
+__global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) {
+  __shared__ __align__(1024) unsigned char smem[NST * STAGE_BYTES];
+  __shared__ __align__(16) float sbias[2][BN];  // bias of the tile being finished / fetched, by tile parity
+  const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int total = a.tiles_m * a.tiles_n, nk = a.K / BK;  // nk >= 4 and even (launcher)
+
+  auto bcol = [&](int j) { return wn * 128 + 32 * (j >> 1) + 4 * (j & 1); };
+  auto opaque_lane = [&]() {
+    int zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+    return lane + zero;
+  };
+  // Per-lane offsets are recomputed in every step from an opaque copy of the lane index rather
+  // than kept live across the tile loop: with 256 accumulators and two fragment buffers the
+  // register file is full, and a spilled offset would be reloaded with a vmcnt wait that drains
+  // the previous tile's stores.
+  auto dma = [&](const i32x4& rsa, const i32x4& rsb, int stage, int q, int ln) {
+    unsigned char* st = smem + stage * STAGE_BYTES;
+    uint32_t off[DMA_PER_TILE];
+    if (q < DMA_PER_TILE) {
+      tile_rel_offsets<false>(off, a.lda, wave, ln);
+      dma_block(rsa, off[q], st + (wave * DMA_PER_TILE + q) * 1024);
+    } else {
+      tile_rel_offsets<true>(off, a.ldb, wave, ln);
+      dma_block(rsb, off[q - DMA_PER_TILE], st + TILE_BYTES + (wave * DMA_PER_TILE + q - DMA_PER_TILE) * 1024);
+    }
+  };
+
+  // C through a range-checked buffer (a masked lane's offset is past the extent)
+  const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.C, ((int64_t)(a.M - 1) * a.ldc + a.N) * 2);
+  // this wave's 64-column slice of a tile's bias into sbias[slot] (lanes 0..15, 16 bytes each;
+  // columns past N, or no bias: zero)
+  auto bias_dma = [&](int n0t, int slot) {
+    const uint64_t addr = reinterpret_cast<uint64_t>(a.bias) + (uint64_t)n0t * 4;
+    const int64_t bytes = a.bias ? (int64_t)(a.N - n0t) * 4 : 0;
+    const i32x4 rs{(int)(uint32_t)addr, (int)((addr >> 32) & 0xffff), (int)(uint32_t)bytes, kRsrcWord3};
+    const int ln = opaque_lane();
+    if (ln < 16) dma_block(rs, (uint32_t)(wave * 256 + ln * 16), reinterpret_cast<const unsigned char*>(&sbias[slot][wave * 64]));
+  };
+
+  int v = blockIdx.x, m0, n0;
+  tile_origin(a, v, total, m0, n0);
+  // the tile whose steps the DMA ring fetches after this one, if any
+  int vn = v + gridDim.x, m0n = 0, n0n = 0;
+  if (vn < total) tile_origin(a, vn, total, m0n, n0n);
+
+  f32x4 acc[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // prologue: steps 0..3 of the first tile, then the boundary's 40 operations with nothing to move
+#pragma unroll
+  for (int s = 0; s < NST; ++s) {
+    const i32x4 rsa = tile_rsrc(a.A, a.lda, a.a_bytes, m0, s * BK), rsb = tile_rsrc(a.B, a.ldb, a.b_bytes, n0, s * BK);
+#pragma unroll
+    for (int q = 0; q < DMA_PER_STEP; ++q) dma(rsa, rsb, s, q, lane);
+  }
+  bias_dma(n0, 0);
+#pragma unroll
+  for (int u = 0; u < 32; ++u) __builtin_amdgcn_raw_buffer_store_b128(i32x4{0, 0, 0, 0}, rc, kOffOOB, 0, 0);
+  __builtin_amdgcn_s_waitcnt(wait_vm((NST - 1) * DMA_PER_STEP + EPI_OPS));
+  __builtin_amdgcn_s_barrier();
+  bf16x8 fa0[8], fb0[8], fa1[8], fb1[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) fa0[i] = frag<true>(smem, wm * 128 + 16 * i, r, g);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) fb0[j] = frag<true, true>(smem + TILE_BYTES, bcol(j), r, g);
+
+  int gs = 0;    // global step index of the tile's step 0 (stage of step kt: (gs + kt) % 4)
+  int slot = 0;  // sbias slot of the current tile
+  // One k step (see gemm_kernel); WAIT: the vmcnt immediate (younger operations allowed in flight).
+  // The DMA of global step gs+kt+4 fetches the tile's step kt+4, else the next tile's step
+  // kt+4-nk, else (last tile) reloads the last step into the free stage.
+  int tln = lane;  // the lane index as seen by this tile's steps (re-derived per tile, see dma)
+  auto step = [&](auto wait_tag, int kt, const bf16x8 (&ca)[8], const bf16x8 (&cb)[8], bf16x8 (&na)[8],
+                  bf16x8 (&nb)[8]) {
+    constexpr int WAIT = decltype(wait_tag)::value;
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(WAIT));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    const unsigned char* Ns = smem + ((gs + kt + 1) % NST) * STAGE_BYTES;
+    const int ka = kt + NST;
+    i32x4 rsa, rsb;
+    if (ka < nk) {
+      rsa = tile_rsrc(a.A, a.lda, a.a_bytes, m0, ka * BK);
+      rsb = tile_rsrc(a.B, a.ldb, a.b_bytes, n0, ka * BK);
+    } else if (vn < total) {
+      rsa = tile_rsrc(a.A, a.lda, a.a_bytes, m0n, (ka - nk) * BK);
+      rsb = tile_rsrc(a.B, a.ldb, a.b_bytes, n0n, (ka - nk) * BK);
+    } else {
+      rsa = tile_rsrc(a.A, a.lda, a.a_bytes, m0, (nk - 1) * BK);
+      rsb = tile_rsrc(a.B, a.ldb, a.b_bytes, n0, (nk - 1) * BK);
+    }
+    const int dstage = (gs + kt) % NST;
+    const int ln = tln, rr = ln & 15, gg = ln >> 4;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      if (q < 8) na[q] = frag<true>(Ns, wm * 128 + 16 * q, rr, gg);
+      else nb[q - 8] = frag<true, true>(Ns + TILE_BYTES, bcol(q - 8), rr, gg);
+      if (q & 1) dma(rsa, rsb, dstage, q >> 1, ln);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int n = 4 * q + u, i = n >> 3, j = n & 7;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cb[j], ca[i], acc[i][j], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  using W56 = std::integral_constant<int, 2 * DMA_PER_STEP + EPI_OPS>;
+  using W16 = std::integral_constant<int, 2 * DMA_PER_STEP>;
+
+  while (true) {
+    tln = opaque_lane();
+    step(W56{}, 0, fa0, fb0, fa1, fb1);
+    step(W56{}, 1, fa1, fb1, fa0, fb0);
+    step(W56{}, 2, fa0, fb0, fa1, fb1);
+    step(W16{}, 3, fa1, fb1, fa0, fb0);
+    for (int kt = 4; kt < nk; kt += 2) {
+      step(W16{}, kt, fa0, fb0, fa1, fb1);
+      step(W16{}, kt + 1, fa1, fb1, fa0, fb0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    bias_dma(vn < total ? n0n : n0, slot ^ 1);  // the next tile's bias, after the DMA of its 4th step
+    // ---- epilogue: lane (r, g) holds C[m0 + wm*128 + 16i + r][n0 + wn*128 + 32p + 8g + e'],
+    //      e' = 0..7 in acc[i][2p] (e' < 4) and acc[i][2p+1] (e' >= 4) ----
+    const int eln = opaque_lane(), er = eln & 15, eg = eln >> 4;
+    const int rowb = m0 + wm * 128 + er, colb = n0 + wn * 128 + 8 * eg;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int col = colb + 32 * p;
+      const float* bl = &sbias[slot][wn * 128 + 32 * p + 8 * eg];
+      const float4 b0 = *reinterpret_cast<const float4*>(bl), b1 = *reinterpret_cast<const float4*>(bl + 4);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int row = rowb + 16 * i;
+        const f32x4 u = acc[i][2 * p], w = acc[i][2 * p + 1];
+        const uint4 x = make_uint4(pack_bf16x2(u[0] + b0.x, u[1] + b0.y), pack_bf16x2(u[2] + b0.z, u[3] + b0.w),
+                                   pack_bf16x2(w[0] + b1.x, w[1] + b1.y), pack_bf16x2(w[2] + b1.z, w[3] + b1.w));
+        const uint32_t oc = (row < a.M && col < a.N) ? (uint32_t)((int64_t)row * a.ldc + col) * 2u : kOffOOB;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, x), rc, oc, 0, 0);
+      }
+    }
+    if (vn >= total) break;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    gs += nk;
+    slot ^= 1;
+    v = vn;
+    m0 = m0n;
+    n0 = n0n;
+    vn = v + gridDim.x;
+    if (vn < total) tile_origin(a, vn, total, m0n, n0n);
+  }
+  __builtin_amdgcn_s_waitcnt(wait_vm(0));  // no DMA may land after the workgroup exits
 }
 
 // C = sum over splits of the partials (+ bias) (+ C), 4 columns per thread.
@@ -456,7 +713,16 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
   a.bias = d->bias;
   a.part = static_cast<float*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (!d->a_trans && !d->b_trans) launch<true, true>(a, S, d->c_dtype, st);
+  // bf16 x Wᵀ (+ bias) without K split or accumulation: the persistent kernel, one workgroup per CU
+  const int64_t c_bytes = ((int64_t)(d->M - 1) * d->ldc + d->N) * 2;
+  if (!d->a_trans && !d->b_trans && S == 1 && d->c_dtype == LLATTN_BF16 && !d->accumulate && d->K >= 4 * BK &&
+      c_bytes < (int64_t(1) << 31)) {
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      cus = 256;
+    const int tiles = a.tiles_m * a.tiles_n;
+    hipLaunchKernelGGL(gemm_persistent_kernel, dim3(std::min(tiles, cus)), dim3(256), 0, st, a);
+  } else if (!d->a_trans && !d->b_trans) launch<true, true>(a, S, d->c_dtype, st);
   else if (!d->a_trans && d->b_trans) launch<true, false>(a, S, d->c_dtype, st);
   else if (d->a_trans && d->b_trans) launch<false, false>(a, S, d->c_dtype, st);
   else launch<false, true>(a, S, d->c_dtype, st);

@@ -31,10 +31,10 @@ from .linear import project
 from .ops import LLAttnCore, _Prof, pool
 
 # Which bf16 projection products run on hipBLASLt rather than the MFMA kernel (measured at config 2,
-# whole step): the two forwards with K = 1408 are about 1% faster on the library; every input and
-# weight gradient is faster on the MFMA kernel (qkv input gradient by about 15%).
-QKV_FWD_LIBRARY = True
-OUT_FWD_LIBRARY = True
+# whole step): none -- with the persistent forward kernel every projection product of the block is
+# faster on the MFMA kernel (the two K = 1408 forwards by about 1% of the step).
+QKV_FWD_LIBRARY = False
+OUT_FWD_LIBRARY = False
 
 
 class LocalLatentAttentionTriton(nn.Module):

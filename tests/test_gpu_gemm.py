@@ -144,7 +144,7 @@ def test_project_with_pools_matches_fp32():
     x = torch.randn(B, T, K, device=dev).to(torch.bfloat16).requires_grad_(True)
     pools = [(64, 8, L.DIV_COUNT), (100, 6, L.DIV_SEG)]
     with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
-        y, p1, p2 = project(x, lin, library=False, pools=pools)
+        y, p1, p2 = project(x, lin, pools=pools)
     dy = torch.randn_like(y, dtype=torch.float32).to(torch.bfloat16)
     d1 = torch.randn_like(p1, dtype=torch.float32).to(torch.bfloat16)
     d2 = torch.randn_like(p2, dtype=torch.float32).to(torch.bfloat16)
