@@ -29,6 +29,10 @@ import sys
 import time
 from pathlib import Path
 
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
 REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO / "local-latent-attention_amd"))
 
@@ -47,6 +51,10 @@ CONFIGS = {
                latent_d_model=64, latent_heads=2, qbs=64,
                workload="macro-block latent query layer fwd+bwd (BASELINE config 4)"),
 }
+
+
+# config 5: the full LM (0.55b preset: reference train.py:73-82; vocab 32000, B16 T2048)
+LM_CONFIG = dict(B=16, T=2048, vocab=32000, n_layers=22, d_model=1408, d_ff=4096)
 
 
 def log(*a):
@@ -109,7 +117,6 @@ def kernel_bytes(lay, es):
 
 
 def make_module(cfg, dev):
-    import torch
     from llattn_amd import LocalLatentAttentionTriton
     torch.manual_seed(0)
     m = LocalLatentAttentionTriton(cfg["d_model"], cfg["n_heads"], cfg["latent_heads"], cfg["latent_d_model"],
@@ -129,7 +136,6 @@ def make_module(cfg, dev):
 def cpu_baseline(cfg, budget_s: float):
     """The reference PyTorch path (fp32 torch restatement, autograd backward) on the host cores, on one
     sequence of the workload, repeated until ``budget_s`` of CPU time."""
-    import torch
     from oracle import torch_ref
     from oracle.llattn_oracle import BlockShape
     torch.set_num_threads(os.cpu_count() or 1)
@@ -160,6 +166,199 @@ def cpu_baseline(cfg, budget_s: float):
                       f"torch CPU restatement of the reference PyTorch path, {el:.1f} s"}
 
 
+class TorchPathAttention(nn.Module):
+    """The reference's PyTorch attention block (reference models.py:61-462): SDPA per local block with an
+    additive float mask (cached per shape), eager latent attention, ``r_out``, the gate softmax and ``out``,
+    with the same parameters as the HIP block.  It is the comparison baseline of config 5 (the "PyTorch
+    SDPA + eager latent" path on the same GPU) and nothing else."""
+
+    def __init__(self, config):
+        super().__init__()
+        D, H, Ld = config.d_model, config.n_heads, config.latent_d_model
+        self.d_model, self.n_heads, self.head_dim = D, H, D // H
+        self.latent_heads, self.latent_head_dim = config.latent_heads, Ld // config.latent_heads
+        self.window, self.local_block_size = config.local_window, config.local_block_size
+        self.latent_tokens, self.latent_query_block_size = config.latent_tokens, config.latent_query_block_size
+        # names, shapes and creation order of reference models.py:80-90
+        self.qkv_proj = nn.Linear(D, 3 * D)
+        self.rq_proj = nn.Linear(D, Ld)
+        self.rkv_proj = nn.Linear(D, 2 * Ld)
+        self.r_out = nn.Linear(Ld, D)
+        self.out = nn.Linear(D, D)
+        self.gate_local = nn.Linear(self.head_dim, 1, bias=False)
+        self.gate_remote = nn.Linear(self.head_dim, 1, bias=False)
+        self._mask_cache = {}
+
+    def _pool_to_latents(self, x):  # reference models.py:159-214
+        B, T, D = x.shape
+        chunk = math.ceil(T / min(self.latent_tokens, T))
+        full, rem = T // chunk, T % chunk
+        parts = [x[:, :full * chunk, :].contiguous().view(B, full, chunk, D).mean(dim=2)] if full else []
+        if rem:
+            parts.append(x[:, full * chunk:, :].mean(dim=1, keepdim=True))
+        pooled = parts[0] if len(parts) == 1 else torch.cat(parts, dim=1)
+        ids = (torch.arange(T, device=x.device) // chunk).clamp(max=pooled.size(1) - 1)
+        return pooled, ids
+
+    def _pool_query_blocks(self, x, ids):  # reference models.py:216-230
+        B, T, D = x.shape
+        qb = min(T, self.latent_query_block_size)
+        n = math.ceil(T / qb)
+        if n * qb > T:
+            x = F.pad(x, (0, 0, 0, n * qb - T))
+        pooled = x.view(B, n, qb, D).mean(dim=2)
+        return pooled, torch.stack([ids[s:min(s + qb, T)].min() for s in range(0, T, qb)])
+
+    def _mask(self, nq, nk, left, device, dtype):  # reference models.py:278-305
+        key = (nq, nk, left, device)
+        m = self._mask_cache.get(key)
+        if m is None:
+            dist = (left + torch.arange(nq, device=device)).unsqueeze(1) - torch.arange(nk, device=device)
+            allowed = (dist > 0) & (dist <= self.window)
+            m = torch.full((nq, nk), float("-inf"), device=device).masked_fill(allowed, 0.0)
+            self._mask_cache[key] = m
+        return m.to(dtype=dtype)
+
+    @staticmethod
+    def _sdpa(q, k, v, mask):
+        """SDPA as the reference calls it.  On the GPU in bf16 the fused memory-efficient kernel is required:
+        bf16 batched products with a transposed right operand (what SDPA's math path and its backward issue)
+        have faulted MI355X boxes under this software stack."""
+        if q.is_cuda and q.dtype != torch.float32:
+            from torch.nn.attention import SDPBackend, sdpa_kernel
+            with sdpa_kernel([SDPBackend.EFFICIENT_ATTENTION]):
+                return F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+        return F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+
+    def _local_attention(self, q, k, v):  # reference models.py:232-276
+        B, _, T, _ = q.shape
+        bs = min(T, max(self.window, self.local_block_size))
+        out = q.new_empty(B, self.n_heads, T, self.head_dim)
+        for a in range(0, T, bs):
+            b = min(a + bs, T)
+            ka = max(0, a - self.window + 1)
+            out[:, :, a:b, :] = self._sdpa(q[:, :, a:b, :], k[:, :, ka:b, :], v[:, :, ka:b, :],
+                                           self._mask(b - a, b - ka, a - ka, q.device, q.dtype))
+        return out
+
+    def forward(self, x):  # reference models.py:307-462
+        B, T, D = x.shape
+        H, Dh, Lh, Ldh = self.n_heads, self.head_dim, self.latent_heads, self.latent_head_dim
+        q, k, v = (t.transpose(1, 2) for t in self.qkv_proj(x).view(B, T, 3, H, Dh).unbind(dim=2))
+        pooled, ids = self._pool_to_latents(x)
+        gk, gv = (t.transpose(1, 2) for t in self.rkv_proj(pooled).view(B, pooled.size(1), 2, Lh, Ldh)
+                  .unbind(dim=2))
+        if self.latent_query_block_size > 1:
+            qsrc, qids = self._pool_query_blocks(x, ids)
+        else:
+            qsrc, qids = x, ids
+        nq = qsrc.size(1)
+        rq = self.rq_proj(qsrc).view(B, nq, Lh, Ldh).transpose(1, 2)
+        local = self._local_attention(q, k, v)
+        # the latent products are tiny (Nc latents per query); they run in fp32 so that no bf16 batched product
+        # with a transposed operand is issued on the GPU (see _sdpa)
+        with torch.autocast(device_type=x.device.type, enabled=False):
+            wide = torch.promote_types(rq.dtype, torch.float32)
+            rq32, gk32, gv32 = rq.to(wide), gk.to(wide), gv.to(wide)
+            scores = torch.matmul(rq32, gk32.transpose(-2, -1)) / math.sqrt(Ldh)
+            causal = torch.arange(pooled.size(1), device=x.device).unsqueeze(0) >= qids.unsqueeze(1)
+            scores = scores.masked_fill(causal.unsqueeze(0).unsqueeze(0), float("-inf"))
+            valid = (~causal).any(dim=-1).view(1, 1, nq, 1)
+            scores = torch.where(valid, scores, torch.zeros_like(scores))
+            lat = torch.matmul(torch.softmax(scores, dim=-1) * valid, gv32).to(rq.dtype)
+        remote = self.r_out(lat.transpose(1, 2).contiguous().view(B, nq, Lh * Ldh))
+        if self.latent_query_block_size > 1:
+            qb = min(T, self.latent_query_block_size)
+            reps = torch.full((nq,), qb, dtype=torch.long, device=x.device)
+            if T % qb:
+                reps[-1] = T % qb
+            remote = torch.repeat_interleave(remote, reps, dim=1)
+        remote = remote.view(B, T, H, Dh).transpose(1, 2)
+        s_l, s_r = self.gate_local(local), self.gate_remote(remote)
+        m = torch.maximum(s_l, s_r)
+        e_l, e_r = torch.exp(s_l - m), torch.exp(s_r - m)
+        z = e_l + e_r
+        mixed = (e_l / z) * local + (e_r / z) * remote
+        return self.out(mixed.transpose(1, 2).contiguous().view(B, T, D))
+
+
+def lm_flops(c):
+    """Algorithmic FLOPs of one training step of the LM: 3 x forward (sum of 2 M N K over the contractions;
+    the attention layers as module_flops, the FFN, the tied head)."""
+    lay = layout(CONFIGS["c2"] | {k: c[k] for k in ("B", "T")})
+    tokens = c["B"] * c["T"]
+    ffn = 2 * 2 * c["d_model"] * c["d_ff"]
+    head = 2 * c["d_model"] * c["vocab"]
+    return c["n_layers"] * module_flops(lay) + 3 * tokens * (c["n_layers"] * ffn + head)
+
+
+def bench_lm(args):
+    """Config 5: one bf16 AdamW training step of the 0.55b LocalLatentLM (22 layers, the HIP block in every
+    layer), tokens/s, next to the same model with the PyTorch SDPA + eager latent block on the same GPU."""
+    from llattn_amd.lm import build_model, make_optimizer, train_step
+
+    c = LM_CONFIG
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(5)
+    tokens = torch.randint(0, c["vocab"], (c["B"], c["T"] + 1), device=dev, generator=g)
+    inputs, targets = tokens[:, :-1], tokens[:, 1:]
+    kw = dict(vocab_size=c["vocab"], max_seq_len=c["T"])
+
+    def run(model, label):
+        opt = make_optimizer(model)
+        first = float(train_step(model, opt, inputs, targets))
+        for _ in range(args.warmup - 1):
+            train_step(model, opt, inputs, targets)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            loss = train_step(model, opt, inputs, targets)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+        log(f"{label}: {ms:.2f} ms per step, first-step loss {first:.5f}, last loss {float(loss):.5f}, "
+            f"peak memory {torch.cuda.max_memory_allocated() / 2**30:.1f} GiB")
+        return ms, first
+
+    torch.manual_seed(0)
+    model = build_model("0.55b", **kw).to(dev)
+    init = {k: v.detach().clone() for k, v in model.state_dict().items()}
+    ms, first = run(model, "HIP block")
+    del model
+    torch.cuda.empty_cache()
+    torch.cuda.reset_peak_memory_stats()
+    ref = build_model("0.55b", attention_factory=TorchPathAttention, **kw).to(dev)
+    ref.load_state_dict(init)
+    del init
+    ms_ref, first_ref = run(ref, "PyTorch SDPA + eager latent block")
+    ntok = c["B"] * c["T"]
+    flops = lm_flops(c)
+    return {
+        "metric": "LocalLatentLM 0.55b bf16 training step tokens/s (forward, backward, AdamW)",
+        "value": round(ntok / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (tokens uniform in [0, 32000), seeded; next-token targets; LocalLatentLM init)",
+        "config": {"workload": "0.55b LocalLatentLM training step, HIP block in all 22 layers (BASELINE config 5)",
+                   "batch": c["B"], "seq_len": c["T"], "vocab": c["vocab"], "layers": c["n_layers"],
+                   "d_model": c["d_model"], "d_ff": c["d_ff"], "parallelism": "none (1 GPU)",
+                   "precision": "bf16 autocast, fp32 master weights, fused AdamW, grad clip 1.0"},
+        "mfma_frac_step": round(flops / (ms * 1e-3) / MFMA_BF16_PEAK, 4),
+        "step_tflop": round(flops / 1e12, 3),
+        "sdpa_baseline": {"value": round(ntok / (ms_ref * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms_ref, 3),
+                          "what": "same model and weights with the reference PyTorch attention block (SDPA + eager "
+                                  "latent) in every layer, same GPU, same run"},
+        "speedup_vs_sdpa": round(ms_ref / ms, 3),
+        "first_step_loss": {"hip": round(first, 5), "sdpa": round(first_ref, 5)},
+    }
+
+
 def read_traffic(config: str, kernel: str):
     """HBM bytes per call of the entry point `kernel` at `config`, as measured by the rocprofv3 --pmc
     FETCH_SIZE / WRITE_SIZE runs summarised in profiles/ (scaled by a plain copy), or None."""
@@ -177,7 +376,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", choices=sorted(CONFIGS), default="c2")
+    ap.add_argument("--config", choices=sorted(CONFIGS) + ["c5"], default="c2",
+                    help="c2 (default), c3, c4: one attention layer; c5: a full training step of the 0.55b LM")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -190,7 +390,6 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
-    import torch
     from llattn_amd import ops as llops
 
     if args.calibrate_copy:
@@ -203,6 +402,9 @@ def main():
         print(json.dumps({"calibrate_copy_bytes": n}), flush=True)
         return
 
+    if args.config == "c5":
+        print(json.dumps(bench_lm(args)), flush=True)
+        return
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda:0")
     lay = layout(cfg)

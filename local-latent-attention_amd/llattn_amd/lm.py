@@ -1,0 +1,177 @@
+"""The language model around the attention block, for full training steps with the HIP block in every layer.
+
+Module tree, parameter names, initialisation and forward follow the
+reference LM (reference models.py:40-58 ``RMSNorm`` / ``FeedForward``,
+:490-502 ``TransformerBlock``, :505-580 ``LocalLatentLM``), so its state
+dicts load here and the other way round.  The attention of every block is
+:func:`~llattn_amd.config.build_attention` (the gfx950 HIP block), as the
+reference builds it when ``use_triton_kernel`` is set (reference
+models.py:465-488).  ``attention_factory`` replaces it, e.g. with another
+implementation to compare against.
+
+:func:`lm_loss` is the token-level loss and metrics of the reference trainer
+(reference train.py:340-370, ``compute_loss_and_metrics`` for [B, T] targets),
+:func:`make_optimizer` its AdamW set-up (reference train.py:851-859) and
+:func:`train_step` one optimiser step as its loop runs it (reference
+train.py:960-1037, one micro-step, gradient clipping, no loss scaling in bf16).
+"""
+from __future__ import annotations
+
+import math
+from typing import Callable, Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from torch.utils.checkpoint import checkpoint
+
+from .config import MODEL_PRESETS, ModelConfig, build_attention
+
+
+class RMSNorm(nn.Module):
+    """reference models.py:40-47"""
+
+    def __init__(self, dim: int, eps: float = 1e-6) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim))
+        self.eps = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return F.rms_norm(x, (self.weight.shape[0],), self.weight, self.eps)
+
+
+class FeedForward(nn.Module):
+    """reference models.py:50-58 (``w2(gelu(w1 x))``; dropout 0 is the identity)."""
+
+    def __init__(self, config: ModelConfig) -> None:
+        super().__init__()
+        self.w1 = nn.Linear(config.d_model, config.d_ff)
+        self.w2 = nn.Linear(config.d_ff, config.d_model)
+        self.dropout = nn.Dropout(config.dropout)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.dropout(self.w2(F.gelu(self.w1(x))))
+
+
+class TransformerBlock(nn.Module):
+    """Pre-norm residual block (reference models.py:490-502)."""
+
+    def __init__(self, config: ModelConfig, attention_factory: Callable[[ModelConfig], nn.Module]) -> None:
+        super().__init__()
+        self.norm1 = RMSNorm(config.d_model)
+        self.norm2 = RMSNorm(config.d_model)
+        self.attn = attention_factory(config)
+        self.ff = FeedForward(config)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        x = x + self.attn(self.norm1(x))
+        return x + self.ff(self.norm2(x))
+
+
+class LocalLatentLM(nn.Module):
+    """Token + learned position embeddings, ``n_layers`` blocks, final norm, LM head tied to the token
+    embedding (reference models.py:505-580)."""
+
+    def __init__(self, config: ModelConfig,
+                 attention_factory: Optional[Callable[[ModelConfig], nn.Module]] = None) -> None:
+        super().__init__()
+        self.config = config
+        self.checkpoint_blocks = config.checkpoint_blocks
+        factory = attention_factory or build_attention
+        self.embedding = nn.Embedding(config.vocab_size, config.d_model)
+        self.position = nn.Embedding(config.max_seq_len, config.d_model)
+        self.blocks = nn.ModuleList([TransformerBlock(config, factory) for _ in range(config.n_layers)])
+        self.norm = RMSNorm(config.d_model)
+        self.lm_head = nn.Linear(config.d_model, config.vocab_size, bias=False)
+        self.lm_head.weight = self.embedding.weight
+        self._init_weights(config.n_layers)
+
+    def _init_weights(self, n_layers: int) -> None:
+        """N(0, 0.02) for every Linear and Embedding, zero biases, the residual output projections
+        (``out``, ``r_out``, ``w2``) scaled by 1/sqrt(2 n_layers); the tied head is skipped (reference
+        models.py:520-546).  The gate vectors are Linear layers too, so they get N(0, 0.02)."""
+        output_projs = {"out", "r_out", "w2"}
+        for name, module in self.named_modules():
+            if module is self.lm_head:
+                continue
+            if isinstance(module, nn.Linear):
+                nn.init.normal_(module.weight, mean=0.0, std=0.02)
+                if module.bias is not None:
+                    nn.init.zeros_(module.bias)
+                if name.rsplit(".", 1)[-1] in output_projs:
+                    module.weight.data.mul_(1.0 / math.sqrt(2 * n_layers))
+            elif isinstance(module, nn.Embedding):
+                nn.init.normal_(module.weight, mean=0.0, std=0.02)
+
+    # profiling API of the reference LM (reference models.py:548-565): per-block stats averaged
+    def set_profile(self, enabled: bool) -> None:
+        for block in self.blocks:
+            block.attn.set_profile(enabled)
+
+    def get_profile_stats(self) -> dict[str, float]:
+        totals: dict[str, float] = {}
+        count = 0
+        for block in self.blocks:
+            stats = block.attn.get_profile_stats()
+            if not stats:
+                continue
+            count += 1
+            for k, v in stats.items():
+                totals[k] = totals.get(k, 0.0) + v
+        return {k: v / count for k, v in totals.items()} if count else {}
+
+    def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
+        _, seq_len = input_ids.shape
+        pos = torch.arange(seq_len, device=input_ids.device)
+        x = self.embedding(input_ids) + self.position(pos).unsqueeze(0)
+        for block in self.blocks:
+            if self.checkpoint_blocks and self.training:
+                x = checkpoint(block, x, use_reentrant=False)
+            else:
+                x = block(x)
+        return self.lm_head(self.norm(x))
+
+
+def build_model(preset: Optional[str] = None, attention_factory=None, **overrides) -> LocalLatentLM:
+    """``LocalLatentLM`` from ``ModelConfig`` defaults, a trainer preset's architecture keys (reference
+    train.py:71-102) and explicit overrides, in that order of precedence (lowest first)."""
+    fields = dict(MODEL_PRESETS[preset]) if preset else {}
+    fields.update(overrides)
+    return LocalLatentLM(ModelConfig(**fields), attention_factory)
+
+
+def lm_loss(logits: torch.Tensor, targets: torch.Tensor):
+    """Mean next-token cross entropy over ``[B, T]`` targets and the trainer's metric tensors (no host
+    synchronisation), as reference train.py:354-370 computes them."""
+    flat = logits.reshape(-1, logits.size(-1))
+    loss = F.cross_entropy(flat, targets.reshape(-1))
+    acc = (logits.argmax(dim=-1) == targets).float().mean()
+    loss_det = loss.detach()
+    return loss, {"eval_loss": loss_det, "eval_acc": acc,
+                  "eval_perplexity": torch.exp(torch.clamp(loss_det, max=20.0)),
+                  "eval_bpt": loss_det / math.log(2.0)}
+
+
+def make_optimizer(model: nn.Module, lr: float = 3e-4) -> torch.optim.Optimizer:
+    """AdamW with weight decay 0.1 on matrices and 0 on vectors, betas (0.9, 0.95), fused on GPU (reference
+    train.py:851-859; default lr of reference train.py:159)."""
+    decay = [p for p in model.parameters() if p.ndim >= 2]
+    no_decay = [p for p in model.parameters() if p.ndim < 2]
+    fused = next(model.parameters()).device.type == "cuda"
+    return torch.optim.AdamW([{"params": decay, "weight_decay": 0.1}, {"params": no_decay, "weight_decay": 0.0}],
+                             lr=lr, betas=(0.9, 0.95), fused=fused)
+
+
+def train_step(model: nn.Module, optimizer: torch.optim.Optimizer, inputs: torch.Tensor, targets: torch.Tensor,
+               grad_clip: float = 1.0) -> torch.Tensor:
+    """One bf16-autocast optimiser step: forward, loss, backward, gradient clipping, AdamW update, gradients
+    cleared (reference train.py:960-1037 with one micro-step).  Returns the detached loss (no sync)."""
+    with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        logits = model(inputs)
+        loss, _ = lm_loss(logits, targets)
+        loss.backward()
+    if grad_clip > 0:
+        torch.nn.utils.clip_grad_norm_(model.parameters(), grad_clip)
+    optimizer.step()
+    optimizer.zero_grad(set_to_none=True)
+    return loss.detach()

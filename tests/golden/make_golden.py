@@ -25,7 +25,16 @@ pins on its own:
   ``dout = randn(2,512,256)`` -- and the file keeps per-tensor sums so a
   regeneration can be verified.
 
+* ``lm_tiny.npz``   -- a 2-layer ``LocalLatentLM`` (models.py:490-580) built
+  under ``torch.manual_seed(21)`` in float64: every initialised parameter,
+  input ids and next-token targets, logits, the mean cross entropy and the
+  autograd gradient of every parameter (the tied head shares the token
+  embedding's).  Pins the LM composition, the module / RNG order of its
+  initialisation and the state-dict keys.
+
 Only data is written here; nothing from the reference's source is kept.
+``python tests/golden/make_golden.py /root/reference lm`` rewrites only the
+LM fixture.
 """
 from __future__ import annotations
 
@@ -163,14 +172,43 @@ def write_c1(models):
     np.savez_compressed(OUT_DIR / "case_c1.npz", meta=json.dumps(meta), **arrays)
 
 
+LM_CASE = dict(vocab_size=96, max_seq_len=64, d_model=64, n_heads=2, n_layers=2, d_ff=128, local_window=16,
+               local_block_size=32, latent_tokens=6, latent_d_model=16, latent_heads=2, latent_query_block_size=0)
+
+
+def write_lm(models):
+    torch.manual_seed(21)
+    model = models.build_model(**LM_CASE).double()
+    g = torch.Generator().manual_seed(22)
+    ids = torch.randint(0, LM_CASE["vocab_size"], (2, 62), generator=g)
+    inputs, targets = ids[:, :-1], ids[:, 1:]
+    logits = model(inputs)
+    loss = torch.nn.functional.cross_entropy(logits.reshape(-1, logits.size(-1)), targets.reshape(-1))
+    loss.backward()
+    arrays = {"inputs": inputs.numpy(), "targets": targets.numpy(), "logits": logits.detach().numpy(),
+              "loss": loss.detach().numpy()}
+    for n, p in model.named_parameters():
+        arrays["p:" + n] = p.detach().numpy()
+        arrays["g:" + n] = p.grad.numpy()
+    meta = dict(LM_CASE, seed=21, ids_seed=22, dtype="float64", torch=torch.__version__,
+                state_dict_keys=list(model.state_dict().keys()),
+                param_order=[n for n, _ in model.named_parameters()])
+    np.savez_compressed(OUT_DIR / "lm_tiny.npz", meta=json.dumps(meta), **arrays)
+
+
 def main(argv):
     ref_root = Path(argv[1] if len(argv) > 1 else "/root/reference")
     torch.set_num_threads(8)
     models = _import_reference(ref_root)
+    if len(argv) > 2 and argv[2] == "lm":
+        write_lm(models)
+        print("lm_tiny.npz", (OUT_DIR / "lm_tiny.npz").stat().st_size)
+        return
     write_keysets(models)
     write_pools(models)
     write_e2e(models)
     write_c1(models)
+    write_lm(models)
     for f in sorted(OUT_DIR.glob("*.npz")):
         print(f.name, f.stat().st_size)
 

@@ -1,0 +1,172 @@
+"""The language model around the block (config 5): composition, initialisation and training step.
+
+CPU: the LM built by ``llattn_amd.lm`` against the reference LM's golden vectors (``tests/golden/lm_tiny.npz``,
+written by importing the reference ``models.py``): state-dict keys, every initialised parameter under the
+seed, and -- with the attention evaluated by the oracle -- logits, loss and every gradient.  The config-5
+comparison block of ``bench.py`` (the reference PyTorch attention path) against the block golden cases.
+
+GPU: the same LM with the HIP block in every layer against the golden vectors (fp32, 1e-4), and a bf16
+training step against the fp32 reference path.
+"""
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import E2E_CASES, GOLDEN, load_case
+
+LM_KEYS = ("vocab_size", "max_seq_len", "d_model", "n_heads", "n_layers", "d_ff", "local_window", "local_block_size",
+           "latent_tokens", "latent_d_model", "latent_heads", "latent_query_block_size")
+
+
+def _lm_golden():
+    z = np.load(GOLDEN / "lm_tiny.npz", allow_pickle=False)
+    meta = json.loads(str(z["meta"]))
+    params = {k[2:]: z[k] for k in z.files if k.startswith("p:")}
+    grads = {k[2:]: z[k] for k in z.files if k.startswith("g:")}
+    return meta, z, params, grads
+
+
+def _oracle_attention_factory():
+    """Attention evaluated by the oracle's torch restatement, with the HIP module's parameters."""
+    from llattn_amd import LocalLatentAttentionTriton
+    from oracle import torch_ref
+    from oracle.llattn_oracle import BlockShape
+
+    class OracleAttention(LocalLatentAttentionTriton):
+        def forward(self, x, _positions=None):
+            shape = BlockShape(d_model=self.d_model, n_heads=self.n_heads, window=self.window,
+                               local_block_size=self.local_block_size, latent_tokens=self.n_latents,
+                               latent_d_model=self.latent_dim, latent_heads=self.latent_heads,
+                               latent_query_block_size=self.latent_query_block_size)
+            return torch_ref.block_forward(dict(self.named_parameters()), x, shape)
+
+    def factory(cfg):
+        return OracleAttention(cfg.d_model, cfg.n_heads, cfg.latent_heads, cfg.latent_d_model, cfg.latent_tokens,
+                               cfg.local_window, local_block_size=cfg.local_block_size,
+                               latent_query_block_size=cfg.latent_query_block_size)
+    return factory
+
+
+def _build(meta, factory=None):
+    from llattn_amd.lm import build_model
+    torch.manual_seed(meta["seed"])
+    return build_model(attention_factory=factory, **{k: meta[k] for k in LM_KEYS})
+
+
+def test_lm_keys_and_init_match_reference_under_seed():
+    meta, _, params, _ = _lm_golden()
+    m = _build(meta)
+    assert list(m.state_dict().keys()) == meta["state_dict_keys"]
+    assert [n for n, _ in m.named_parameters()] == meta["param_order"]
+    assert m.lm_head.weight is m.embedding.weight
+    for n, p in m.named_parameters():
+        assert np.array_equal(p.detach().double().numpy(), params[n]), n
+
+
+def test_lm_forward_backward_matches_reference_with_oracle_attention():
+    meta, z, params, grads = _lm_golden()
+    m = _build(meta, _oracle_attention_factory()).double()
+    m.load_state_dict({k: torch.from_numpy(v) for k, v in params.items()}, strict=False)
+    from llattn_amd.lm import lm_loss
+    logits = m(torch.from_numpy(z["inputs"]))
+    loss, metrics = lm_loss(logits, torch.from_numpy(z["targets"]))
+    loss.backward()
+    np.testing.assert_allclose(logits.detach().numpy(), z["logits"], rtol=0, atol=1e-10)
+    assert abs(float(loss.detach()) - float(z["loss"])) < 1e-12
+    assert abs(float(metrics["eval_perplexity"]) - float(np.exp(z["loss"]))) < 1e-9
+    for n, p in m.named_parameters():
+        np.testing.assert_allclose(p.grad.numpy(), grads[n], rtol=0, atol=1e-10, err_msg=n)
+
+
+def test_lm_loss_metrics():
+    from llattn_amd.lm import lm_loss
+    g = torch.Generator().manual_seed(0)
+    logits = torch.randn(2, 5, 7, generator=g, dtype=torch.float64)
+    targets = torch.randint(0, 7, (2, 5), generator=g)
+    loss, mt = lm_loss(logits, targets)
+    lp = torch.log_softmax(logits, -1).gather(-1, targets[..., None])[..., 0]
+    assert abs(float(loss) + float(lp.mean())) < 1e-12
+    assert abs(float(mt["eval_acc"]) - float((logits.argmax(-1) == targets).double().mean())) < 1e-7
+    assert abs(float(mt["eval_bpt"]) - float(loss) / np.log(2.0)) < 1e-12
+
+
+@pytest.mark.parametrize("case", E2E_CASES)
+def test_config5_comparison_block_is_the_reference_path(case):
+    """bench.py's SDPA + eager latent block (the config-5 baseline) reproduces the reference block."""
+    import bench
+    from llattn_amd import ModelConfig
+    meta, x, dout, params, out_ref, dx_ref, grads_ref = load_case(case)
+    cfg = ModelConfig(d_model=meta["d_model"], n_heads=meta["n_heads"], local_window=meta["local_window"],
+                      local_block_size=meta["local_block_size"], latent_tokens=meta["latent_tokens"],
+                      latent_d_model=meta["latent_d_model"], latent_heads=meta["latent_heads"],
+                      latent_query_block_size=meta["latent_query_block_size"])
+    blk = bench.TorchPathAttention(cfg).double()
+    blk.load_state_dict({k: torch.from_numpy(v) for k, v in params.items()})
+    xt = torch.from_numpy(x).requires_grad_(True)
+    out = blk(xt)
+    out.backward(torch.from_numpy(dout))
+    np.testing.assert_allclose(out.detach().numpy(), out_ref, rtol=0, atol=1e-10)
+    np.testing.assert_allclose(xt.grad.numpy(), dx_ref, rtol=0, atol=1e-10)
+    for n, p in blk.named_parameters():
+        np.testing.assert_allclose(p.grad.numpy(), grads_ref[n], rtol=0, atol=1e-10, err_msg=n)
+
+
+@pytest.mark.gpu
+def test_lm_hip_block_matches_reference_fp32():
+    from gpu_helpers import assert_fp32_close, require_cuda
+    from llattn_amd.lm import lm_loss
+    dev = require_cuda()
+    meta, z, params, grads = _lm_golden()
+    m = _build(meta).to(dev)
+    m.load_state_dict({k: torch.tensor(v, dtype=torch.float32) for k, v in params.items()}, strict=False)
+    logits = m(torch.from_numpy(z["inputs"]).to(dev))
+    loss, _ = lm_loss(logits, torch.from_numpy(z["targets"]).to(dev))
+    loss.backward()
+    assert_fp32_close(logits.detach().cpu().double().numpy(), z["logits"], "logits")
+    assert abs(float(loss.detach()) - float(z["loss"])) < 1e-4
+    for n, p in m.named_parameters():
+        assert_fp32_close(p.grad.cpu().double().numpy(), grads[n], n)
+
+
+@pytest.mark.gpu
+def test_lm_bf16_training_step_against_fp32_reference_path():
+    """A bf16-autocast step of the LM with the HIP block: gradients against the same LM with the reference
+    PyTorch block in fp32 (bar raised to twice what that reference path itself reaches under bf16), then a
+    few optimiser steps that lower the loss."""
+    import bench
+    from gpu_helpers import assert_bf16_close, err_stats, require_cuda
+    from llattn_amd.lm import build_model, lm_loss, make_optimizer, train_step
+    dev = require_cuda()
+    kw = dict(vocab_size=256, max_seq_len=256, d_model=192, n_heads=2, n_layers=2, d_ff=384, local_window=32,
+              local_block_size=64, latent_tokens=8, latent_d_model=64, latent_heads=2)
+    torch.manual_seed(3)
+    hip = build_model(**kw).to(dev)
+    init = {k: v.detach().clone() for k, v in hip.state_dict().items()}
+    g = torch.Generator(device=dev).manual_seed(4)
+    ids = torch.randint(0, 256, (2, 257), device=dev, generator=g)
+    inputs, targets = ids[:, :-1], ids[:, 1:]
+
+    def grads_of(model, bf16):
+        model.zero_grad(set_to_none=True)
+        d = next(model.parameters()).device
+        with torch.autocast(device_type=d.type, dtype=torch.bfloat16, enabled=bf16):
+            loss, _ = lm_loss(model(inputs.to(d)), targets.to(d))
+            loss.backward()
+        return float(loss), {n: p.grad.detach().double().cpu().numpy() for n, p in model.named_parameters()}
+
+    # the reference path and its bf16 floor run on the CPU
+    ref = build_model(attention_factory=bench.TorchPathAttention, **kw)
+    ref.load_state_dict({k: v.cpu() for k, v in init.items()})
+    loss_ref, g_ref = grads_of(ref, False)
+    _, g_floor = grads_of(ref, True)
+    loss_hip, g_hip = grads_of(hip, True)
+    assert abs(loss_hip - loss_ref) < 2e-2
+    for n in g_ref:
+        assert_bf16_close(g_hip[n], g_ref[n], n, floor=err_stats(g_floor[n], g_ref[n]))
+    opt = make_optimizer(hip, lr=1e-3)
+    losses = [float(train_step(hip, opt, inputs, targets)) for _ in range(4)]
+    assert all(np.isfinite(losses)) and losses[-1] < losses[0], losses
