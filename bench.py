@@ -282,6 +282,19 @@ class TorchPathAttention(nn.Module):
         return self.out(mixed.transpose(1, 2).contiguous().view(B, T, D))
 
 
+class TorchRMSNorm(nn.Module):
+    """The reference's RMSNorm (reference models.py:40-47, ``F.rms_norm``): the norm of the config-5
+    comparison model."""
+
+    def __init__(self, dim: int, eps: float = 1e-6) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim))
+        self.eps = eps
+
+    def forward(self, x):
+        return F.rms_norm(x, (self.weight.shape[0],), self.weight, self.eps)
+
+
 def lm_flops(c):
     """Algorithmic FLOPs of one training step of the LM: 3 x forward (sum of 2 M N K over the contractions;
     the attention layers as module_flops, the FFN, the tied head)."""
@@ -293,8 +306,9 @@ def lm_flops(c):
 
 
 def bench_lm(args):
-    """Config 5: one bf16 AdamW training step of the 0.55b LocalLatentLM (22 layers, the HIP block in every
-    layer), tokens/s, next to the same model with the PyTorch SDPA + eager latent block on the same GPU."""
+    """Config 5: one bf16 AdamW training step of the 0.55b LocalLatentLM (22 layers, the HIP block and the
+    HIP RMSNorm in every layer), tokens/s, next to the reference model (PyTorch SDPA + eager latent block,
+    torch RMSNorm) with the same weights on the same GPU."""
     from llattn_amd.lm import build_model, make_optimizer, train_step
 
     c = LM_CONFIG
@@ -323,16 +337,19 @@ def bench_lm(args):
     model = build_model("0.55b", **kw).to(dev)
     init = {k: v.detach().clone() for k, v in model.state_dict().items()}
     ms, first = run(model, "HIP block")
-    del model
-    torch.cuda.empty_cache()
-    torch.cuda.reset_peak_memory_stats()
-    ref = build_model("0.55b", attention_factory=TorchPathAttention, **kw).to(dev)
-    ref.load_state_dict(init)
-    del init
-    ms_ref, first_ref = run(ref, "PyTorch SDPA + eager latent block")
     ntok = c["B"] * c["T"]
     flops = lm_flops(c)
-    return {
+    if args.no_sdpa_baseline:
+        ms_ref = first_ref = None
+    else:
+        del model
+        torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats()
+        ref = build_model("0.55b", attention_factory=TorchPathAttention, norm_factory=TorchRMSNorm, **kw).to(dev)
+        ref.load_state_dict(init)
+        del init
+        ms_ref, first_ref = run(ref, "PyTorch SDPA + eager latent block")
+    result = {
         "metric": "LocalLatentLM 0.55b bf16 training step tokens/s (forward, backward, AdamW)",
         "value": round(ntok / (ms * 1e-3), 1),
         "unit": "tokens/s",
@@ -351,12 +368,15 @@ def bench_lm(args):
                    "precision": "bf16 autocast, fp32 master weights, fused AdamW, grad clip 1.0"},
         "mfma_frac_step": round(flops / (ms * 1e-3) / MFMA_BF16_PEAK, 4),
         "step_tflop": round(flops / 1e12, 3),
-        "sdpa_baseline": {"value": round(ntok / (ms_ref * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms_ref, 3),
-                          "what": "same model and weights with the reference PyTorch attention block (SDPA + eager "
-                                  "latent) in every layer, same GPU, same run"},
-        "speedup_vs_sdpa": round(ms_ref / ms, 3),
-        "first_step_loss": {"hip": round(first, 5), "sdpa": round(first_ref, 5)},
     }
+    if ms_ref is not None:
+        result["sdpa_baseline"] = {
+            "value": round(ntok / (ms_ref * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms_ref, 3),
+            "what": "same model and weights with the reference PyTorch attention block (SDPA + eager latent) and "
+                    "torch RMSNorm in every layer, same GPU, same run"}
+        result["speedup_vs_sdpa"] = round(ms_ref / ms, 3)
+        result["first_step_loss"] = {"hip": round(first, 5), "sdpa": round(first_ref, 5)}
+    return result
 
 
 def read_traffic(config: str, kernel: str):
@@ -379,6 +399,7 @@ def main():
     ap.add_argument("--config", choices=sorted(CONFIGS) + ["c5"], default="c2",
                     help="c2 (default), c3, c4: one attention layer; c5: a full training step of the 0.55b LM")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-sdpa-baseline", action="store_true", help="c5: time the HIP model only")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 3 plain device copies of MIB MiB each (scale factor for rocprofv3 FETCH_SIZE / "

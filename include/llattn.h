@@ -185,6 +185,28 @@ size_t llattn_colsum_workspace_size(int32_t M, int32_t N);
 int32_t llattn_colsum(const void* x, int64_t ld, int32_t M, int32_t N, float* out, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/* RMSNorm of the residual stream around the block (reference models.py:40-47,
+ * F.rms_norm(x, (D,), w, eps), the LM's norm1 / norm2 / norm of reference
+ * models.py:493-494, 513):
+ *   y = x * rstd * w,  rstd[m] = 1 / sqrt(mean_d x[m][d]^2 + eps).
+ * x, y: M rows of D elements (leading dimensions ldx / ldy in elements; rows
+ * 16-byte (fp32) or 8-byte (bf16) aligned), each LLATTN_F32 or LLATTN_BF16 --
+ * y in bf16 feeds the block's bf16 projections without a cast.  weight fp32
+ * [D] (16-byte aligned); rstd fp32 [M] is written for the backward.
+ * D must be a multiple of 4 and at most 4096. */
+int32_t llattn_rmsnorm_fwd(const void* x, int32_t x_dtype, int64_t ldx, const float* weight, int32_t M, int32_t D,
+                           float eps, void* y, int32_t y_dtype, int64_t ldy, float* rstd, void* stream);
+
+/* Backward of llattn_rmsnorm_fwd: dx (x's dtype) = rstd * (g - xh * mean_d(g xh)),
+ * g = dy * w, xh = x * rstd; dweight (fp32 [D]) = sum over rows of dy * xh,
+ * through a workspace of llattn_rmsnorm_workspace_size(M, D) bytes, added in a
+ * fixed order (deterministic, no atomics).  Replaces the autograd backward of
+ * the reference RMSNorm (reference models.py:40-47). */
+size_t llattn_rmsnorm_workspace_size(int32_t M, int32_t D);
+int32_t llattn_rmsnorm_bwd(const void* dy, int32_t dy_dtype, int64_t lddy, const void* x, int32_t x_dtype,
+                           int64_t ldx, const float* rstd, const float* weight, int32_t M, int32_t D, void* dx,
+                           int64_t lddx, float* dweight, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

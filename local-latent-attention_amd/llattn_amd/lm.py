@@ -6,8 +6,10 @@ reference LM (reference models.py:40-58 ``RMSNorm`` / ``FeedForward``,
 dicts load here and the other way round.  The attention of every block is
 :func:`~llattn_amd.config.build_attention` (the gfx950 HIP block), as the
 reference builds it when ``use_triton_kernel`` is set (reference
-models.py:465-488).  ``attention_factory`` replaces it, e.g. with another
-implementation to compare against.
+models.py:465-488), and the norms run on the gfx950 RMSNorm kernels
+(:func:`~llattn_amd.norm.rms_norm`, bf16 output under autocast).
+``attention_factory`` / ``norm_factory`` replace them, e.g. with other
+implementations to compare against.
 
 :func:`lm_loss` is the token-level loss and metrics of the reference trainer
 (reference train.py:340-370, ``compute_loss_and_metrics`` for [B, T] targets),
@@ -26,10 +28,11 @@ import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint
 
 from .config import MODEL_PRESETS, ModelConfig, build_attention
+from .norm import rms_norm
 
 
 class RMSNorm(nn.Module):
-    """reference models.py:40-47"""
+    """reference models.py:40-47 (same parameter and eps), on the gfx950 kernels."""
 
     def __init__(self, dim: int, eps: float = 1e-6) -> None:
         super().__init__()
@@ -37,7 +40,7 @@ class RMSNorm(nn.Module):
         self.eps = eps
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return F.rms_norm(x, (self.weight.shape[0],), self.weight, self.eps)
+        return rms_norm(x, self.weight, self.eps)
 
 
 class FeedForward(nn.Module):
@@ -56,10 +59,11 @@ class FeedForward(nn.Module):
 class TransformerBlock(nn.Module):
     """Pre-norm residual block (reference models.py:490-502)."""
 
-    def __init__(self, config: ModelConfig, attention_factory: Callable[[ModelConfig], nn.Module]) -> None:
+    def __init__(self, config: ModelConfig, attention_factory: Callable[[ModelConfig], nn.Module],
+                 norm_factory: Callable[[int], nn.Module] = RMSNorm) -> None:
         super().__init__()
-        self.norm1 = RMSNorm(config.d_model)
-        self.norm2 = RMSNorm(config.d_model)
+        self.norm1 = norm_factory(config.d_model)
+        self.norm2 = norm_factory(config.d_model)
         self.attn = attention_factory(config)
         self.ff = FeedForward(config)
 
@@ -72,16 +76,17 @@ class LocalLatentLM(nn.Module):
     """Token + learned position embeddings, ``n_layers`` blocks, final norm, LM head tied to the token
     embedding (reference models.py:505-580)."""
 
-    def __init__(self, config: ModelConfig,
-                 attention_factory: Optional[Callable[[ModelConfig], nn.Module]] = None) -> None:
+    def __init__(self, config: ModelConfig, attention_factory: Optional[Callable[[ModelConfig], nn.Module]] = None,
+                 norm_factory: Optional[Callable[[int], nn.Module]] = None) -> None:
         super().__init__()
         self.config = config
         self.checkpoint_blocks = config.checkpoint_blocks
         factory = attention_factory or build_attention
+        norm = norm_factory or RMSNorm
         self.embedding = nn.Embedding(config.vocab_size, config.d_model)
         self.position = nn.Embedding(config.max_seq_len, config.d_model)
-        self.blocks = nn.ModuleList([TransformerBlock(config, factory) for _ in range(config.n_layers)])
-        self.norm = RMSNorm(config.d_model)
+        self.blocks = nn.ModuleList([TransformerBlock(config, factory, norm) for _ in range(config.n_layers)])
+        self.norm = norm(config.d_model)
         self.lm_head = nn.Linear(config.d_model, config.vocab_size, bias=False)
         self.lm_head.weight = self.embedding.weight
         self._init_weights(config.n_layers)
@@ -132,12 +137,13 @@ class LocalLatentLM(nn.Module):
         return self.lm_head(self.norm(x))
 
 
-def build_model(preset: Optional[str] = None, attention_factory=None, **overrides) -> LocalLatentLM:
+def build_model(preset: Optional[str] = None, attention_factory=None, norm_factory=None,
+                **overrides) -> LocalLatentLM:
     """``LocalLatentLM`` from ``ModelConfig`` defaults, a trainer preset's architecture keys (reference
     train.py:71-102) and explicit overrides, in that order of precedence (lowest first)."""
     fields = dict(MODEL_PRESETS[preset]) if preset else {}
     fields.update(overrides)
-    return LocalLatentLM(ModelConfig(**fields), attention_factory)
+    return LocalLatentLM(ModelConfig(**fields), attention_factory, norm_factory)
 
 
 def lm_loss(logits: torch.Tensor, targets: torch.Tensor):

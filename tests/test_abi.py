@@ -24,7 +24,7 @@ def _declared_functions():
 def test_library_exports_every_declared_symbol():
     L, lib = _lib()
     names = _declared_functions()
-    assert len(names) == 13, names
+    assert len(names) == 16, names
     for n in names:
         assert hasattr(lib, n), n
         assert n in L.SIGNATURES, f"{n} has no ctypes signature"
@@ -170,6 +170,29 @@ def test_colsum_validation():
 
 
 # ---------------------------------------------------------------- host logic
+
+def test_rmsnorm_validation():
+    L, lib = _lib()
+    buf = ctypes.c_void_p(1 << 20)  # never dereferenced: every call below fails validation first
+    f32, bf = L.F32, L.BF16
+    rc = lib.llattn_rmsnorm_fwd(buf, f32, 64, buf, 4, 62, 1e-6, buf, bf, 64, buf, None)
+    assert rc == L.ERR_UNSUPPORTED and b"multiple of 4" in lib.llattn_last_error()
+    rc = lib.llattn_rmsnorm_fwd(buf, f32, 8192, buf, 4, 8192, 1e-6, buf, bf, 8192, buf, None)
+    assert rc == L.ERR_UNSUPPORTED and b"at most 4096" in lib.llattn_last_error()
+    rc = lib.llattn_rmsnorm_fwd(buf, 7, 64, buf, 4, 64, 1e-6, buf, bf, 64, buf, None)
+    assert rc == L.ERR_DTYPE
+    rc = lib.llattn_rmsnorm_fwd(buf, f32, 60, buf, 4, 64, 1e-6, buf, bf, 64, buf, None)
+    assert rc == L.ERR_LAYOUT and b"ld >= D" in lib.llattn_last_error()
+    rc = lib.llattn_rmsnorm_fwd(None, f32, 64, buf, 4, 64, 1e-6, buf, bf, 64, buf, None)
+    assert rc == L.ERR_LAYOUT
+    rc = lib.llattn_rmsnorm_fwd(buf, f32, 64, buf, 0, 64, 1e-6, buf, bf, 64, buf, None)
+    assert rc == L.ERR_SHAPE
+    need = lib.llattn_rmsnorm_workspace_size(32768, 1408)
+    assert need > 0 and need % (1408 * 4) == 0
+    rc = lib.llattn_rmsnorm_bwd(buf, bf, 1408, buf, f32, 1408, buf, buf, 32768, 1408, buf, 1408, buf, buf, need - 4,
+                                None)
+    assert rc == L.ERR_WORKSPACE and b"workspace" in lib.llattn_last_error()
+
 
 def test_resolve_layout_matches_reference_rules():
     from llattn_amd import resolve_layout

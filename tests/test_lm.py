@@ -51,10 +51,10 @@ def _oracle_attention_factory():
     return factory
 
 
-def _build(meta, factory=None):
+def _build(meta, factory=None, norm_factory=None):
     from llattn_amd.lm import build_model
     torch.manual_seed(meta["seed"])
-    return build_model(attention_factory=factory, **{k: meta[k] for k in LM_KEYS})
+    return build_model(attention_factory=factory, norm_factory=norm_factory, **{k: meta[k] for k in LM_KEYS})
 
 
 def test_lm_keys_and_init_match_reference_under_seed():
@@ -69,7 +69,8 @@ def test_lm_keys_and_init_match_reference_under_seed():
 
 def test_lm_forward_backward_matches_reference_with_oracle_attention():
     meta, z, params, grads = _lm_golden()
-    m = _build(meta, _oracle_attention_factory()).double()
+    import bench
+    m = _build(meta, _oracle_attention_factory(), bench.TorchRMSNorm).double()
     m.load_state_dict({k: torch.from_numpy(v) for k, v in params.items()}, strict=False)
     from llattn_amd.lm import lm_loss
     logits = m(torch.from_numpy(z["inputs"]))
@@ -159,7 +160,7 @@ def test_lm_bf16_training_step_against_fp32_reference_path():
         return float(loss), {n: p.grad.detach().double().cpu().numpy() for n, p in model.named_parameters()}
 
     # the reference path and its bf16 floor run on the CPU
-    ref = build_model(attention_factory=bench.TorchPathAttention, **kw)
+    ref = build_model(attention_factory=bench.TorchPathAttention, norm_factory=bench.TorchRMSNorm, **kw)
     ref.load_state_dict({k: v.cpu() for k, v in init.items()})
     loss_ref, g_ref = grads_of(ref, False)
     _, g_floor = grads_of(ref, True)
