@@ -13,7 +13,8 @@ Prints ONE JSON line.  Besides the driver's fields it carries
 ``roofline`` (the C-ABI entry point with the most time per step, priced
 against bf16 MFMA peak for the projection GEMM and against HBM peak for the
 attention kernels; durations measured with HIP events on the launch stream
-inside the timed region),
+in a second timed region of K steps, because an event record costs the GPU
+about 5 us between kernels and would inflate the step time of the first),
 ``mfma_frac_module`` (algorithmic module FLOPs / step time / bf16 dense
 peak), per-kernel event timings, and ``cpu_baseline`` (the reference
 PyTorch path restated in fp32, timed on the host cores on a bounded
@@ -445,14 +446,25 @@ def main():
 
     for _ in range(args.warmup):
         step()
+    # Timed region 1: the K steps as a user runs them -> value, ms_per_step.
     torch.cuda.synchronize()
-    llops.EVENT_LOG = []
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    # Timed region 2: the same K steps with a HIP event pair on the launch stream around every C-ABI call
+    # -> per-entry-point durations for `roofline` / `kernels`.  Each event record costs the GPU about 5 us
+    # between kernels, so these steps are not the ones `value` is measured on.
+    torch.cuda.synchronize()
+    llops.EVENT_LOG = []
+    t2 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t3 = time.perf_counter()
     events, llops.EVENT_LOG = llops.EVENT_LOG, None
+    log(f"step {(t1 - t0) * 1000.0 / args.steps:.3f} ms; with per-call events {(t3 - t2) * 1000.0 / args.steps:.3f} ms")
 
     ms = (t1 - t0) * 1000.0 / args.steps
     tokens = cfg["B"] * cfg["T"]

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define LLATTN_ABI_VERSION 1
+#define LLATTN_ABI_VERSION 2
 
 /* status codes */
 #define LLATTN_OK 0
@@ -171,6 +171,10 @@ typedef struct llattn_gemm_desc {
   int32_t accumulate;  /* 1: add into C */
   const float* bias;   /* fp32 [N] or NULL */
   int32_t split_k;     /* 0: automatic */
+  float* a_rowsum;     /* fp32 [M] or NULL: also rowsum[m] = sum_k A(m,k), i.e. the bias gradient
+                          sum_tokens dy of a weight-gradient product dy^T x, contracted against a
+                          column of ones in place of the unused column N of the last tile (needs
+                          b_trans = 1, fp32 C and N % 256 != 0); overwritten, never accumulated */
 } llattn_gemm_desc;
 
 size_t llattn_gemm_workspace_size(const llattn_gemm_desc* d);

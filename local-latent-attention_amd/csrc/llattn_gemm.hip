@@ -50,7 +50,8 @@ struct GemmArgs {
   const uint16_t* B; int64_t ldb, b_bytes;
   void* C; int64_t ldc;
   const float* bias;
-  float* part;  // split-K partials [S][M][N]
+  float* part;     // split-K partials [S][M][N], then (rowsum) [S][M]
+  float* rowsum;   // fp32 [M] or null: sum_k A(m, k), from a column of ones in place of B's column N
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -183,6 +184,17 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
   uint32_t offa[DMA_PER_TILE], offb[DMA_PER_TILE];
   tile_offsets<AK>(offa, a.lda, m0, a.M, wave, lane);
   tile_offsets<BKM, PB>(offb, a.ldb, n0, a.N, wave, lane);
+  // Row sums of A: column N of the product (never stored as C) contracts against ones.  It lies in
+  // B fragment block `jones` (wave-uniform; -1: not in this wave's columns) at lane r == rones.
+  const int nrel = a.N - n0 - wn * 128;
+  const int jones = (!PB && a.rowsum && nrel >= 0 && nrel < 128) ? (nrel >> 4) : -1;
+  const bool lane_ones = (r == (nrel & 15));
+  auto ones_fix = [&](bf16x8& f, int j) {
+    if (j == jones && lane_ones) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = (__bf16)1.0f;
+    }
+  };
   // DMA of this wave's block q (0..3: operand A, 4..7: operand B) of step kt into `stage`
   auto dma = [&](const i32x4& rsa, const i32x4& rsb, int stage, int q) {
     unsigned char* st = smem + stage * STAGE_BYTES;
@@ -218,8 +230,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
     step_rsrcs(min(kt + NST, nk - 1), rsa, rsb);
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
-      if (q < 8) na[q] = frag<AK>(Ns, wm * 128 + 16 * q, r, g);
-      else nb[q - 8] = frag<BKM, PB>(Ns + TILE_BYTES, bcol(q - 8), r, g);
+      if (q < 8) {
+        na[q] = frag<AK>(Ns, wm * 128 + 16 * q, r, g);
+      } else {
+        nb[q - 8] = frag<BKM, PB>(Ns + TILE_BYTES, bcol(q - 8), r, g);
+        if (!PB) ones_fix(nb[q - 8], q - 8);
+      }
       if (q & 1) dma(rsa, rsb, kt % NST, q >> 1);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {  // B first: lane (r, g) accumulates C[m = r][n = 4g + e]
@@ -242,7 +258,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) fa0[i] = frag<AK>(smem, wm * 128 + 16 * i, r, g);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) fb0[j] = frag<BKM, PB>(smem + TILE_BYTES, bcol(j), r, g);
+  for (int j = 0; j < 8; ++j) {
+    fb0[j] = frag<BKM, PB>(smem + TILE_BYTES, bcol(j), r, g);
+    if (!PB) ones_fix(fb0[j], j);
+  }
   for (int kt = 0; kt < nk; kt += 2) {  // nk is even; fragment buffers alternate between steps
     step(kt, fa0, fb0, fa1, fb1);
     step(kt + 1, fa1, fb1, fa0, fb0);
@@ -371,6 +390,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
             v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
           }
           *reinterpret_cast<float4*>(p) = v;
+        } else if (a.rowsum && row < a.M && col == a.N) {  // the ones column: sum_k A(row, k)
+          if (EPI == EPI_PART) a.part[(int64_t)a.n_split * a.M * a.N + (int64_t)split * a.M + row] = v.x;
+          else a.rowsum[row] = v.x;
         }
       }
     }
@@ -585,13 +607,22 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
 }
 
 // C = sum over splits of the partials (+ bias) (+ C), 4 columns per thread.
+// Threads past the M x N/4 quads add the row-sum partials [S][M] the same way, one row each.
 template <int EPI>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs a, int S) {
   const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;  // quad index over M x N/4
   const int nq = a.N / 4;
-  if (q >= (int64_t)a.M * nq) return;
-  const int row = (int)(q / nq), col = (int)(q % nq) * 4;
   const int64_t mn = (int64_t)a.M * a.N;
+  if (q >= (int64_t)a.M * nq) {
+    const int64_t row = q - (int64_t)a.M * nq;
+    if (!a.rowsum || row >= a.M) return;
+    const float* p = a.part + (int64_t)S * mn + row;
+    float s = p[0];
+    for (int i = 1; i < S; ++i) s += p[(int64_t)i * a.M];
+    a.rowsum[row] = s;
+    return;
+  }
+  const int row = (int)(q / nq), col = (int)(q % nq) * 4;
   const float* p = a.part + (int64_t)row * a.N + col;
   float4 s = *reinterpret_cast<const float4*>(p);
   int i = 1;
@@ -635,7 +666,7 @@ void launch(const GemmArgs& a, int S, int c_dtype, hipStream_t st) {
   const dim3 grid(a.tiles_m * a.tiles_n * S), block(256);
   if (S > 1) {
     hipLaunchKernelGGL((gemm_kernel<AK, BKM, EPI_PART>), grid, block, 0, st, a);
-    const int64_t quads = (int64_t)a.M * (a.N / 4);
+    const int64_t quads = (int64_t)a.M * (a.N / 4) + (a.rowsum ? a.M : 0);
     const dim3 rg((unsigned)((quads + 255) / 256));
     if (c_dtype == LLATTN_F32)
       hipLaunchKernelGGL((splitk_reduce_kernel<EPI_F32>), rg, block, 0, st, a, S);
@@ -669,7 +700,7 @@ using namespace llattn::gemm;
 extern "C" size_t llattn_gemm_workspace_size(const llattn_gemm_desc* d) {
   if (!d) return 0;
   const int S = resolve_split(d);
-  return S > 1 ? (size_t)S * d->M * d->N * sizeof(float) : 0;
+  return S > 1 ? (size_t)S * d->M * (d->N + (d->a_rowsum ? 1 : 0)) * sizeof(float) : 0;
 }
 
 extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_t workspace_bytes, void* stream) {
@@ -699,6 +730,10 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
   const int64_t b_bytes = (d->b_trans ? (int64_t)(d->K - 1) * d->ldb + d->N : (int64_t)(d->N - 1) * d->ldb + d->K) * 2;
   if (a_bytes >= (int64_t(1) << 32) || b_bytes >= (int64_t(1) << 32))
     return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: operands of 4 GiB or more are not supported");
+  if (d->a_rowsum && (!d->b_trans || d->c_dtype != LLATTN_F32 || d->N % BN == 0 || !aligned16(d->a_rowsum)))
+    return fail(LLATTN_ERR_UNSUPPORTED,
+                "llattn_gemm: row sums of A need an m/n-contiguous B, fp32 C, N not a multiple of %d (a spare "
+                "column in the last tile; N=%d) and a 16-byte aligned output", BN, d->N);
   const size_t need = llattn_gemm_workspace_size(d);
   if (need && (!workspace || workspace_bytes < need || !aligned16(workspace)))
     return fail(LLATTN_ERR_WORKSPACE, "llattn_gemm: %d K splits need %zu workspace bytes (got %zu)", S, need,
@@ -712,6 +747,7 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
   a.C = d->C; a.ldc = d->ldc;
   a.bias = d->bias;
   a.part = static_cast<float*>(workspace);
+  a.rowsum = d->a_rowsum;
   hipStream_t st = static_cast<hipStream_t>(stream);
   // bf16 x Wᵀ (+ bias) without K split or accumulation: the persistent kernel, one workgroup per CU
   const int64_t c_bytes = ((int64_t)(d->M - 1) * d->ldc + d->N) * 2;

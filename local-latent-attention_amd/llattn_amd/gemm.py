@@ -28,15 +28,18 @@ def _check2d(name: str, t: torch.Tensor) -> None:
 
 
 def _run(M: int, N: int, K: int, A: torch.Tensor, a_trans: bool, B: torch.Tensor, b_trans: bool, C: torch.Tensor,
-         bias: torch.Tensor | None, accumulate: bool, split_k: int = 0) -> None:
+         bias: torch.Tensor | None, accumulate: bool, split_k: int = 0, rowsum: torch.Tensor | None = None) -> None:
     L.require_gpu(A, B, C)
+    if rowsum is not None and (rowsum.dtype != torch.float32 or not rowsum.is_contiguous() or rowsum.numel() != M):
+        raise ValueError(f"rowsum must be a contiguous fp32 vector of {M} elements")
     if C.dim() != 2 or C.stride(1) != 1 or C.dtype not in (torch.bfloat16, torch.float32):
         raise ValueError("output must be a 2-D bf16 / fp32 view with a contiguous inner dimension")
     if bias is not None and (bias.dtype != torch.float32 or not bias.is_contiguous() or bias.numel() != N):
         raise ValueError(f"bias must be a contiguous fp32 vector of {N} elements")
     desc = L.LlattnGemmDesc(M, N, K, int(a_trans), int(b_trans), A.data_ptr(), A.stride(0), B.data_ptr(),
                             B.stride(0), C.data_ptr(), C.stride(0), L.dtype_code(C.dtype), int(accumulate),
-                            None if bias is None else bias.data_ptr(), split_k)
+                            None if bias is None else bias.data_ptr(), split_k,
+                            None if rowsum is None else rowsum.data_ptr())
     lib = L.load()
     nws = lib.llattn_gemm_workspace_size(ctypes.byref(desc))
     ws = torch.empty((max(nws, 1),), dtype=torch.uint8, device=C.device) if nws else None
@@ -75,9 +78,16 @@ def matmul_nn(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None,
     return out
 
 
+def rowsum_supported(n: int) -> bool:
+    """Whether :func:`matmul_tn` can also give the row sums of ``a^T`` for an output width ``n``: the sums are
+    contracted against a column of ones in place of the unused column ``n`` of the last 256-wide tile."""
+    return n % 256 != 0
+
+
 def matmul_tn(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None, accumulate: bool = False,
-              split_k: int = 0) -> torch.Tensor:
-    """``a [K, M]^T @ b [K, N]`` -> fp32 ``[M, N]`` (weight gradients: K = tokens)."""
+              split_k: int = 0, rowsum: torch.Tensor | None = None) -> torch.Tensor:
+    """``a [K, M]^T @ b [K, N]`` -> fp32 ``[M, N]`` (weight gradients: K = tokens).  With ``rowsum`` (fp32 ``[M]``,
+    overwritten) also ``a.sum(0)`` -- the bias gradient -- from the same pass (``rowsum_supported(N)``)."""
     _check2d("a", a)
     _check2d("b", b)
     K, M = a.shape
@@ -86,7 +96,9 @@ def matmul_tn(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None,
         raise ValueError(f"a is [{K}, {M}] but b is {tuple(b.shape)}")
     if out is None:
         out = torch.empty((M, N), dtype=torch.float32, device=a.device)
-    _run(M, N, K, a, True, b, True, out, None, accumulate, split_k)
+    if rowsum is not None and not rowsum_supported(N):
+        raise ValueError(f"row sums need an output width that is not a multiple of 256 (N={N})")
+    _run(M, N, K, a, True, b, True, out, None, accumulate, split_k, rowsum)
     return out
 
 

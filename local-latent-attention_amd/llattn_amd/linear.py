@@ -52,6 +52,9 @@ def weight_grad(dy2: torch.Tensor, x2: torch.Tensor, bias_grad: bool = False):
     K, N = dy2.shape
     D = x2.shape[1]
     if tn_supported(K, N, D) and dy2.stride(1) == 1 and x2.stride(1) == 1:
+        if bias_grad and gemm.rowsum_supported(D):  # bias gradient from the weight-gradient pass itself
+            db = torch.empty((N,), dtype=torch.float32, device=dy2.device)
+            return gemm.matmul_tn(dy2, x2, rowsum=db), db
         return gemm.matmul_tn(dy2, x2), (gemm.colsum(dy2) if bias_grad else None)
     # shapes the MFMA kernel does not tile (token counts that are not a multiple of 64): library GEMM
     return torch.mm(dy2.t(), x2).float(), (dy2.sum(0, dtype=torch.float32) if bias_grad else None)

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_empty_error():
     L, lib = _lib()
-    assert lib.llattn_abi_version() == L.ABI_VERSION == 1
+    assert lib.llattn_abi_version() == L.ABI_VERSION == 2
 
 
 def _shape(L, **kw):
@@ -155,6 +155,34 @@ def test_gemm_split_k_needs_workspace():
     # a full-chip output needs no split
     d = _gemm_desc(L, M=32768, N=4736, K=1408, lda=1408, ldb=1408, ldc=4736)
     assert lib.llattn_gemm_workspace_size(ctypes.byref(d)) == 0
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(b_trans=0, ldb=1024), b"m/n-contiguous B"),
+    (dict(c_dtype=1), b"fp32 C"),
+    (dict(N=512, ldb=512, ldc=512), b"not a multiple of 256"),
+    (dict(a_rowsum=0x5004), b"16-byte aligned"),
+])
+def test_gemm_rowsum_validation(kw, msg):
+    """Row sums of A (the fused bias gradient) need a spare column in the last tile of an m/n-contiguous B."""
+    L, lib = _lib()
+    base = dict(M=264, N=136, K=1024, a_trans=1, b_trans=1, lda=264, ldb=136, ldc=136, c_dtype=L.F32,
+                a_rowsum=0x5000)
+    base.update(kw)
+    d = _gemm_desc(L, **base)
+    rc = lib.llattn_gemm(ctypes.byref(d), None, 0, None)
+    assert rc == L.ERR_UNSUPPORTED, lib.llattn_last_error()
+    assert msg in lib.llattn_last_error()
+
+
+def test_gemm_rowsum_workspace():
+    """With row sums the split-K workspace also holds [S][M] row-sum partials."""
+    L, lib = _lib()
+    kw = dict(M=1408, N=1408, K=32768, a_trans=1, b_trans=1, lda=1408, ldb=1408, ldc=1408, c_dtype=L.F32)
+    plain = lib.llattn_gemm_workspace_size(ctypes.byref(_gemm_desc(L, **kw)))
+    fused = lib.llattn_gemm_workspace_size(ctypes.byref(_gemm_desc(L, a_rowsum=0x5000, **kw)))
+    S = plain // (1408 * 1408 * 4)
+    assert S > 1 and fused == plain + S * 1408 * 4
 
 
 def test_colsum_validation():

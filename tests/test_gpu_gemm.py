@@ -47,6 +47,26 @@ def test_matmul_nn(M, N, K):
     assert _err(gemm.matmul_nn(a, b), a.float() @ b.float()) < BF16_TOL
 
 
+@pytest.mark.parametrize("K,M,N,S", [(64, 256, 264, 1), (1024, 264, 136, 0), (2048, 40, 96, 1), (4096, 264, 136, 3),
+                                     (4096, 1000, 520, 1), (32768, 1408, 1408, 0), (32768, 4736, 1408, 0)])
+def test_matmul_tn_rowsum(K, M, N, S):
+    """Weight gradient with the bias gradient of the same pass: rowsum = a.sum(0), contracted against a column
+    of ones in the spare column N of the last tile; the product itself is unchanged by it."""
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: tn rowsum", K, M, N, S, flush=True)
+    g = torch.Generator(device=dev).manual_seed(3 * K + M + N)
+    a, b = _rand(K, M, gen=g, dev=dev), _rand(K, N, gen=g, dev=dev)
+    rs = torch.full((M,), float("nan"), device=dev)
+    got = gemm.matmul_tn(a, b, split_k=S, rowsum=rs)
+    assert _err(got, a.float().T @ b.float()) < FP32_TOL
+    assert _err(rs, a.float().sum(0)) < FP32_TOL
+    # run to run: bitwise identical (ordered split-K reduction)
+    rs2 = torch.empty_like(rs)
+    got2 = gemm.matmul_tn(a, b, split_k=S, rowsum=rs2)
+    assert torch.equal(rs, rs2) and torch.equal(got, got2)
+
+
 @pytest.mark.parametrize("K,M,N,S", [(64, 256, 256, 1), (1024, 264, 136, 0), (4096, 1408, 512, 4),
                                      (2048, 40, 96, 2), (4096, 264, 136, 3), (32768, 1408, 1408, 0),
                                      (32768, 4736, 1408, 0), (32768, 1408, 512, 0)])
