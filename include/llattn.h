@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define LLATTN_ABI_VERSION 2
+#define LLATTN_ABI_VERSION 3
 
 /* status codes */
 #define LLATTN_OK 0
@@ -136,16 +136,20 @@ int32_t llattn_local_gate_fwd(const llattn_shape* s, const llattn_tensor* q, con
 /* Backward of llattn_local_gate_fwd given dy: writes dq, dk, dv
  * ([B][T][H][Dh]), dremote per token ([B][T][H][Dh]; fold it onto latent
  * queries with llattn_pool_fwd(LLATTN_DIV_ONE) in macro-block mode) and the
- * fp32 gate gradients dgate_l / dgate_r ([H][Dh], per head; sum over heads for
- * a shared gate).  No atomics.  Replaces the local + gate part of the
- * reference backward launches (reference kernels/llattn_op.py:87-181). */
+ * fp32 gate gradients dgate_l / dgate_r ([H][Dh] with gate_per_head, else
+ * [Dh]: the gradient of the shared gate, summed over heads).  dremote_colsum
+ * (fp32 [H*Dh], or NULL) receives the fp32 sum of dremote over every token
+ * and batch: the bias gradient of r_out, whose output is remote.  No
+ * atomics; every sum runs in a fixed order.  Replaces the local + gate part
+ * of the reference backward launches (reference kernels/llattn_op.py:87-181)
+ * and r_out's bias gradient (reference models.py:84, 395). */
 int32_t llattn_local_gate_bwd(const llattn_shape* s, const llattn_tensor* q, const llattn_tensor* k,
                               const llattn_tensor* v, const llattn_tensor* remote, const float* gate_l,
                               const float* gate_r, const llattn_tensor* o_local, const float* lse,
                               const float* w, const llattn_tensor* dy, const llattn_tensor* dq,
                               const llattn_tensor* dk, const llattn_tensor* dv, const llattn_tensor* dremote,
-                              float* dgate_l, float* dgate_r, void* workspace, size_t workspace_bytes,
-                              void* stream);
+                              float* dgate_l, float* dgate_r, float* dremote_colsum, void* workspace,
+                              size_t workspace_bytes, void* stream);
 
 /* Projection GEMM on bf16 MFMA: C[m][n] = sum_k A(m,k) B(n,k) (+ bias[n])
  * (+ C[m][n] when accumulate).  A and B are bf16; each is stored

@@ -81,7 +81,7 @@ size_t llattn_workspace_size(const llattn_shape* s, int32_t kind) {
   auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
   if (kind == LLATTN_WS_LOCAL_BWD) {
     const size_t nqt = (T + 63) / 64;
-    return up(B * T * H * Dh * elem_size(s->dtype)) + up(B * H * T * 4) + up(B * H * nqt * 2 * Dh * 4);
+    return up(B * T * H * Dh * elem_size(s->dtype)) + up(B * H * T * 4) + up(B * H * nqt * 3 * Dh * 4);
   }
   if (kind == LLATTN_WS_LATENT_BWD) return latent_workspace_bytes(s);
   fail(LLATTN_ERR_SHAPE, "unknown workspace kind %d", kind);

@@ -37,7 +37,7 @@ struct LocalArgs {
   void* dr; int64_t dr_sb, dr_st, dr_sh;
   void* dO;      // workspace [B][T][H][Dh], storage type
   float* Dsum;   // workspace [B][H][T]
-  float* gpart;  // workspace [H][2][Dh][B*n_qt]
+  float* gpart;  // workspace [H][3][Dh][rows]: gate_l, gate_r and dremote column partial sums
 };
 
 // ----------------------------------------------------------------------------
@@ -192,7 +192,7 @@ __global__ __launch_bounds__(256) void local_bwd_q_kernel(const LocalArgs a) {
   __shared__ __align__(16) T S0[64 * KP];  // dy -> dO_local (kept: dO rows)            | loop: key rows
   __shared__ __align__(16) T S1[64 * KP];  // o_local -> query rows                       | loop: value rows
   __shared__ __align__(16) T S2[64 * KP];  // remote -> dremote                           | epilogue: dq
-  __shared__ float gsum[4][2][DHP];
+  __shared__ float gsum[4][3][DHP];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane & 15, g = lane >> 4;
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
@@ -253,14 +253,16 @@ __global__ __launch_bounds__(256) void local_bwd_q_kernel(const LocalArgs a) {
     }
     store4<T>(S0 + row * KP + d, dov);  // in place over the dy elements this lane read
     store4<T>(S2 + row * KP + d, drv);  // in place over the remote elements
-    // gate partial sums over the 16 queries of this wave
+    // gate and dremote column partial sums over the 16 queries of this wave (rows past the end are 0)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float pl = sum_rows16_last(delta * olv[t][i]);
       const float pr = sum_rows16_last(-delta * rv[t][i]);
+      const float pb = sum_rows16_last(drv[i]);
       if (r == 15) {
         gsum[wave][0][d + i] = pl;
         gsum[wave][1][d + i] = pr;
+        gsum[wave][2][d + i] = pb;
       }
     }
   }
@@ -273,11 +275,11 @@ __global__ __launch_bounds__(256) void local_bwd_q_kernel(const LocalArgs a) {
   store_tile<T, DHP, KP>(static_cast<T*>(a.dr) + b * a.dr_sb + h * a.dr_sh, a.dr_st, S2, q0, qend, Dh);
   {
     const int nrow = a.B * a.n_qt, prow = b * a.n_qt + qt;
-    for (int idx = tid; idx < 2 * DHP; idx += 256) {
+    for (int idx = tid; idx < 3 * DHP; idx += 256) {
       const int which = idx / DHP, d = idx % DHP;
       if (d < Dh) {
         const float sum = gsum[0][which][d] + gsum[1][which][d] + gsum[2][which][d] + gsum[3][which][d];
-        a.gpart[(((int64_t)h * 2 + which) * Dh + d) * nrow + prow] = sum;
+        a.gpart[(((int64_t)h * 3 + which) * Dh + d) * nrow + prow] = sum;
       }
     }
   }
@@ -526,8 +528,8 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
   const bool qb1 = a.q_block == 1;
   uint2 pdy[2][GV], pol[2][GV], prm[2][GV];
   float pw[2], plse[2];
-  // this thread's gate partial sums (over the segment's rows it gates)
-  float accl[GS], accr[GS];
+  // this thread's gate and dremote column partial sums (over the segment's rows it gates)
+  float accl[GS], accr[GS], accb[GS];
   auto goff = [&](int grow, int st, int j) {
     return gd0 + 4 * j < Dh ? (uint32_t)(grow * st + gd0 + 4 * j) * 2u : kOffOOB;
   };
@@ -595,17 +597,22 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int e = 4 * j + i;
-          dov[i] = round_t<T>(wq * dyv[e] + delta * glv[i]);
+          dov[i] = wq * dyv[e] + delta * glv[i];
           drv[i] = (1.f - wq) * dyv[e] - delta * grv[i];
-          Dp += dov[i] * olv[e];
         }
-        ::llattn::store4<T>(so + grow * KP + d, dov);
+        // dO_local rounded to bf16 once: the packed words go to LDS and their values feed D = dO.o_local
+        const uint2 dop = make_uint2(pack_bf16x2(dov[0], dov[1]), pack_bf16x2(dov[2], dov[3]));
+        unpack_bf16x4(dop, dov);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Dp += dov[i] * olv[4 * j + i];
+        *reinterpret_cast<uint2*>(so + grow * KP + d) = dop;
         store4(rdr, (full && qv && d < Dh) ? (uint32_t)(qi * dr_st + d) * 2u : kOffOOB, drv);
         if (full) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             accl[4 * j + i] += delta * olv[4 * j + i];
             accr[4 * j + i] -= delta * rmv[4 * j + i];
+            accb[4 * j + i] += qv ? drv[i] : 0.f;
           }
         }
       }
@@ -641,7 +648,7 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
   // ---- prologue: tile t0 staged and gated, keys of tile t0-1 staged ----
   if (qrole) {
 #pragma unroll
-    for (int e = 0; e < GS; ++e) accl[e] = accr[e] = 0.f;
+    for (int e = 0; e < GS; ++e) accl[e] = accr[e] = accb[e] = 0.f;
     load_gate(t0);
     gate(t0, slab(static_cast<T*>(a.dr) + b * a.dr_sb + h * a.dr_sh, dr_st));
     load_gate(t0 + 1);
@@ -827,25 +834,27 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
       }
     }
   }
-  // gate partials of the segment: the 32 row threads of each dim (two rows each) added in order,
-  // through LDS that no wave reads any more (the key tiles)
-  float* gacc = reinterpret_cast<float*>(SK);  // [l | r][256 threads][GS]
+  // gate and dremote partials of the segment: the 32 row threads of each dim (two rows each) added in
+  // order, through LDS that no wave reads any more (the key tiles: 3 x 256 x GS floats fit in SK)
+  static_assert(3 * 256 * GS * 4 <= 3 * TILE * 2, "partials staging exceeds the key tiles");
+  float* gacc = reinterpret_cast<float*>(SK);  // [l | r | b][256 threads][GS]
   if (qrole) {
 #pragma unroll
     for (int e = 0; e < GS; ++e) {
       gacc[rtid * GS + e] = accl[e];
       gacc[(256 + rtid) * GS + e] = accr[e];
+      gacc[(512 + rtid) * GS + e] = accb[e];
     }
   }
   lds_barrier();
   const int nrow = a.B * n_seg, prow = b * n_seg + seg;
-  for (int idx = tid; idx < 2 * DHP; idx += 512) {
+  for (int idx = tid; idx < 3 * DHP; idx += 512) {
     const int which = idx / DHP, d = idx % DHP;
     if (d < Dh) {
       const int sg = d / GS, e = d % GS;
       float s = 0.f;
       for (int rr = 0; rr < 32; ++rr) s += gacc[(which * 256 + rr * 8 + sg) * GS + e];
-      a.gpart[(((int64_t)h * 2 + which) * Dh + d) * nrow + prow] = s;
+      a.gpart[(((int64_t)h * 3 + which) * Dh + d) * nrow + prow] = s;
     }
   }
 }
@@ -858,22 +867,37 @@ int fused_seg_tiles(const LocalArgs& a) {
   return max(2, (a.n_qt + want - 1) / want);
 }
 
-// Ordered sum of the gate partials: dgate[h][d] = sum over the nrow partial rows of part[h][which][d][row].
-// One wave per output: lanes stride over the contiguous partials, then a fixed butterfly.
+// Ordered sums of the partials part[h][which][d][row] (which 0: gate_l, 1: gate_r, 2: dremote columns):
+// dgate_l / dgate_r per head ([H][Dh]) or, for a gate shared by the heads, summed over them too ([Dh]);
+// dbr[h][d] (when requested) over the rows.  One wave per output: lanes stride over the contiguous
+// partials (head by head), then a fixed butterfly.
 __global__ __launch_bounds__(256) void gate_reduce_kernel(const float* __restrict__ part, float* dgl, float* dgr,
-                                                          int H, int Dh, int nrow) {
+                                                          float* dbr, int H, int Dh, int nrow, int per_head) {
   const int lane = threadIdx.x & 63;
-  const int o = blockIdx.x * 4 + (threadIdx.x >> 6);  // over H * 2 * Dh
-  if (o >= H * 2 * Dh) return;                         // whole waves exit; no barrier follows
-  const float* p = part + (int64_t)o * nrow;
+  const int o = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int ng = per_head ? H * Dh : Dh;  // outputs per gate vector
+  if (o >= 2 * ng + (dbr ? H * Dh : 0)) return;  // whole waves exit; no barrier follows
+  int which, h0, d, od;
+  if (o < 2 * ng) {
+    which = o / ng;
+    od = o % ng;
+    h0 = per_head ? od / Dh : 0;
+    d = od % Dh;
+  } else {
+    which = 2;
+    od = o - 2 * ng;
+    h0 = od / Dh;
+    d = od % Dh;
+  }
+  const int h1 = (which < 2 && !per_head) ? H : h0 + 1;
   float s = 0.f;
-  for (int i = lane; i < nrow; i += 64) s += p[i];
+  for (int h = h0; h < h1; ++h) {
+    const float* p = part + (((int64_t)h * 3 + which) * Dh + d) * nrow;
+    for (int i = lane; i < nrow; i += 64) s += p[i];
+  }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
-  if (lane == 0) {
-    const int h = o / (2 * Dh), which = (o / Dh) % 2, d = o % Dh;
-    (which == 0 ? dgl : dgr)[h * Dh + d] = s;
-  }
+  if (lane == 0) (which == 0 ? dgl : which == 1 ? dgr : dbr)[od] = s;
 }
 
 // ----------------------------------------------------------------------------
@@ -993,7 +1017,8 @@ extern "C" int32_t llattn_local_gate_bwd(const llattn_shape* s, const llattn_ten
                                          const float* w, const llattn_tensor* dy, const llattn_tensor* dq,
                                          const llattn_tensor* dk, const llattn_tensor* dv,
                                          const llattn_tensor* dremote, float* dgate_l, float* dgate_r,
-                                         void* workspace, size_t workspace_bytes, void* stream) {
+                                         float* dremote_colsum, void* workspace, size_t workspace_bytes,
+                                         void* stream) {
   LocalArgs a;
   int32_t rc = common_args(s, q, k, v, remote, gate_l, gate_r, &a);
   if (rc) return rc;
@@ -1028,7 +1053,9 @@ extern "C" int32_t llattn_local_gate_bwd(const llattn_shape* s, const llattn_ten
   // gate partial rows: one per (batch, segment) from the fused kernel, one per (batch, query tile) otherwise
   const int seg_tiles = fused_seg_tiles(a);
   const int nrow = fused_bwd(a, s->dtype, dhp) ? s->B * ((a.n_qt + seg_tiles - 1) / seg_tiles) : s->B * a.n_qt;
-  hipLaunchKernelGGL(gate_reduce_kernel, dim3((s->H * 2 * s->Dh + 3) / 4), dim3(256), 0, st, a.gpart, dgate_l, dgate_r,
-                     s->H, s->Dh, nrow);
+  const int per_head = s->gate_per_head ? 1 : 0;
+  const int outs = 2 * (per_head ? s->H * s->Dh : s->Dh) + (dremote_colsum ? s->H * s->Dh : 0);
+  hipLaunchKernelGGL(gate_reduce_kernel, dim3((outs + 3) / 4), dim3(256), 0, st, a.gpart, dgate_l, dgate_r,
+                     dremote_colsum, s->H, s->Dh, nrow, per_head);
   return check_launch("llattn_local_gate_bwd");
 }

@@ -16,7 +16,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libllattn_gfx950.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OK, ERR_SHAPE, ERR_DTYPE, ERR_LAYOUT, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_LAUNCH = range(7)
 F32, BF16 = 0, 1
@@ -60,7 +60,8 @@ SIGNATURES = {
     "llattn_latent_fwd": (_I32, [_S, _T, _T, _T, _T, _P, _P]),
     "llattn_latent_bwd": (_I32, [_S, _T, _T, _T, _P, _T, _T, _T, _T, _P, _SZ, _P]),
     "llattn_local_gate_fwd": (_I32, [_S, _T, _T, _T, _T, _P, _P, _T, _T, _P, _P, _P]),
-    "llattn_local_gate_bwd": (_I32, [_S, _T, _T, _T, _T, _P, _P, _T, _P, _P, _T, _T, _T, _T, _T, _P, _P, _P, _SZ, _P]),
+    "llattn_local_gate_bwd": (_I32, [_S, _T, _T, _T, _T, _P, _P, _T, _P, _P, _T, _T, _T, _T, _T, _P, _P, _P, _P, _SZ,
+                                     _P]),
     "llattn_gemm_workspace_size": (_SZ, [_G]),
     "llattn_gemm": (_I32, [_G, _P, _SZ, _P]),
     "llattn_colsum_workspace_size": (_SZ, [_I32, _I32]),

@@ -179,22 +179,25 @@ def _core_forward(lay: L.Layout, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, r_b, 
 
 def _core_backward(lay: L.Layout, dy, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, has_rb, lat, lse_lat, R, ol, lse,
                    w, dq, dk, dv, drq, dgk, dgv, dt, device):
-    """Writes dq/dk/dv/drq/dgk/dgv (LlattnTensor views) and returns (dgate_l_h, dgate_r_h, dr_w, dr_b)."""
+    """Writes dq/dk/dv/drq/dgk/dgv (LlattnTensor views) and returns (dgate_l, dgate_r, dr_w, dr_b): the gate
+    gradients per head ([H, Dh]) or, for a shared gate, already summed over heads ([Dh]); r_out's bias
+    gradient comes from the local backward (the column sums of dremote)."""
     B, T, H, Dh, Lh, Ldh = lay.B, lay.T, lay.H, lay.Dh, lay.Lh, lay.Ldh
     D, Ld = H * Dh, Lh * Ldh
     per_head = gate_l.dim() == 2 and gate_l.shape[0] > 1
     shape = lay.shape(dt, per_head)
     stream = L.stream_ptr(device)
     drem = _empty((B, T, D), dt, device)
-    dgl = _empty((H, Dh), torch.float32, device)
-    dgr = _empty((H, Dh), torch.float32, device)
+    dgl = _empty((H, Dh) if per_head else (Dh,), torch.float32, device)
+    dgr = _empty((H, Dh) if per_head else (Dh,), torch.float32, device)
+    dr_b = _empty((D,), torch.float32, device) if has_rb else None
     ws = _empty((L.workspace_bytes(shape, L.WS_LOCAL_BWD),), torch.uint8, device)
     _call("llattn_local_gate_bwd",
           _byref(shape), _byref(q), _byref(k), _byref(v), _byref(L.view(R, R.stride(0), R.stride(1), Dh)),
           gate_l.data_ptr(), gate_r.data_ptr(), _byref(L.view_bnhd(ol)), lse.data_ptr(), w.data_ptr(),
           _byref(L.view(dy, dy.stride(0), dy.stride(1), Dh)), _byref(dq), _byref(dk), _byref(dv),
           _byref(L.view(drem, drem.stride(0), drem.stride(1), Dh)), dgl.data_ptr(), dgr.data_ptr(),
-          ws.data_ptr(), ws.numel(), stream)
+          None if dr_b is None else dr_b.data_ptr(), ws.data_ptr(), ws.numel(), stream)
     if lay.macro:
         dR = _empty((B, lay.n_q, D), dt, device)
         pool_fwd_into(drem, dR, lay.q_block, lay.n_q, L.DIV_ONE)
@@ -205,19 +208,17 @@ def _core_backward(lay: L.Layout, dy, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, 
         dlat = (input_grad(dR2, r_w.to(dt)) if dt == torch.bfloat16 else torch.mm(dR2, r_w.to(dt))).view(
             B, lay.n_q, Lh, Ldh)
         if dt == torch.bfloat16:
-            dr_w, dr_b = weight_grad(dR2, lat.view(B * lay.n_q, Ld), has_rb)
+            dr_w, _ = weight_grad(dR2, lat.view(B * lay.n_q, Ld), False)
         else:
             dr_w = torch.mm(dR2.t(), lat.view(B * lay.n_q, Ld))
-            dr_b = dR2.sum(dim=0, dtype=torch.float32) if has_rb else None
     ws2 = _empty((L.workspace_bytes(shape, L.WS_LATENT_BWD),), torch.uint8, device)
     _call("llattn_latent_bwd", _byref(shape), _byref(rq), _byref(gk), _byref(gv), lse_lat.data_ptr(),
           _byref(L.view_bnhd(dlat)), _byref(drq), _byref(dgk), _byref(dgv), ws2.data_ptr(), ws2.numel(), stream)
     return dgl, dgr, dr_w, dr_b
 
 
-def _gate_grad(dg_h: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
-    g = dg_h if (like.dim() == 2 and like.shape[0] > 1) else dg_h.sum(0, keepdim=True)
-    return g.reshape(like.shape).to(like.dtype)
+def _gate_grad(dg: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
+    return dg.reshape(like.shape).to(like.dtype)
 
 
 # ---------------------------------------------------------------------------

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_empty_error():
     L, lib = _lib()
-    assert lib.llattn_abi_version() == L.ABI_VERSION == 2
+    assert lib.llattn_abi_version() == L.ABI_VERSION == 3
 
 
 def _shape(L, **kw):
@@ -47,9 +47,10 @@ def test_workspace_sizes():
     L, lib = _lib()
     s = _shape(L)
     n_local = lib.llattn_workspace_size(ctypes.byref(s), L.WS_LOCAL_BWD)
-    # dO (bf16) + row sums + gate partials, each rounded up to 256 bytes
+    # dO (bf16) + row sums + partials (gate_l, gate_r, dremote columns) per (batch, query tile), each rounded
+    # up to 256 bytes
     up = lambda x: (x + 255) // 256 * 256  # noqa: E731
-    assert n_local == up(2 * 97 * 2 * 32 * 2) + up(2 * 2 * 97 * 4) + up(2 * 2 * 2 * 2 * 32 * 4)
+    assert n_local == up(2 * 97 * 2 * 32 * 2) + up(2 * 2 * 97 * 4) + up(2 * 2 * 2 * 3 * 32 * 4)
     # D per latent query + per-segment partials of 16-latent tiles (one segment of 512 queries here)
     assert lib.llattn_workspace_size(ctypes.byref(s), L.WS_LATENT_BWD) == up(2 * 2 * 97 * 4) + up(2 * 2 * 1 * 16 * 2 * 8 * 4)
     assert lib.llattn_workspace_size(ctypes.byref(s), 7) == 0
@@ -109,7 +110,7 @@ def test_workspace_too_small_is_runtime_error():
     t = L.LlattnTensor(ctypes.c_void_p(0x1000), 64, 64, 32)
     g = ctypes.c_void_p(0x2000)
     rc = lib.llattn_local_gate_bwd(ctypes.byref(s), *(ctypes.byref(t),) * 4, g, g, ctypes.byref(t), g, g,
-                                   *(ctypes.byref(t),) * 5, g, g, g, 16, None)
+                                   *(ctypes.byref(t),) * 5, g, g, None, g, 16, None)
     assert rc == L.ERR_WORKSPACE
     with pytest.raises(RuntimeError, match="workspace"):
         L.check(rc, "llattn_local_gate_bwd")
