@@ -139,7 +139,11 @@ class LocalLatentAttentionTriton(nn.Module):
             rq = None
         if prof is not None:
             prof.lap("qkv_ms")
-        gkgv = self.rkv_proj(pool(x, *latents) if pooled is None else pooled)
+        if pooled is None:
+            pooled = pool(x, *latents)
+        # the pooled latents' projection (256 rows at config 2) on the MFMA GEMM as well: split-K forward,
+        # bias gradient from the weight-gradient pass
+        gkgv = project(pooled, self.rkv_proj) if bf16 else self.rkv_proj(pooled)
         if prof is not None:
             prof.lap("pool_ms")
         rqc = None if rq is None else rq.to(qkvr.dtype)

@@ -260,9 +260,11 @@ class LLAttnCore(torch.autograd.Function):
         rqv = L.view(qkv, sb, sn, Ldh, 3 * D) if rq is None else L.view(rq, rq.stride(0), rq.stride(1), Ldh)
         gk = L.view(gkgv, gkgv.stride(0), gkgv.stride(1), Ldh)
         gv = L.view(gkgv, gkgv.stride(0), gkgv.stride(1), Ldh, Ld)
-        y, ol, lse, w, lat, lse_lat, R = _core_forward(lay, q, k, v, rqv, gk, gv, gl, gr, r_w, r_b, dt, device, prof)
-        ctx.save_for_backward(qkv, rq, gkgv, gl, gr, r_w, lat, lse_lat, R, ol, lse, w)
+        r_wd = r_w.detach().to(dt)  # cast once: the backward's input gradient reuses it
+        y, ol, lse, w, lat, lse_lat, R = _core_forward(lay, q, k, v, rqv, gk, gv, gl, gr, r_wd, r_b, dt, device, prof)
+        ctx.save_for_backward(qkv, rq, gkgv, gl, gr, r_wd, lat, lse_lat, R, ol, lse, w)
         ctx.lay, ctx.has_rb, ctx.packed = lay, r_b is not None, rq is None
+        ctx.r_w_dtype = r_w.dtype
         ctx.gate_like = (gate_l, gate_r)
         ctx.r_b_dtype = None if r_b is None else r_b.dtype
         if prof is not None:
@@ -296,7 +298,7 @@ class LLAttnCore(torch.autograd.Function):
         dgl, dgr, dr_w, dr_b = _core_backward(lay, dy, q, k, v, rqv, gk, gv, gl, gr, r_w, ctx.has_rb, lat, lse_lat,
                                               R, ol, lse, w, dq, dk, dv, drq, dgk, dgv, dt, device)
         gate_l, gate_r = ctx.gate_like
-        return (dqkv, drq_t, dgkgv, _gate_grad(dgl, gate_l), _gate_grad(dgr, gate_r), dr_w.to(r_w.dtype),
+        return (dqkv, drq_t, dgkgv, _gate_grad(dgl, gate_l), _gate_grad(dgr, gate_r), dr_w.to(ctx.r_w_dtype),
                 None if dr_b is None else dr_b.to(ctx.r_b_dtype), None, None)
 
 
