@@ -512,6 +512,27 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
     __builtin_amdgcn_raw_buffer_store_b64(x, rs, off, 0, 0);
   };
 
+  // An accumulator tile row (lane (r, g) holds columns 16t + 4g .. 16t + 4g + 3 of block t, t < NT) times
+  // `scale`, as bf16 16-byte pieces: for each block pair (2p, 2p+1) lanes g and g ^ 1 (16 lanes apart)
+  // swap halves with v_permlane16_swap, so an even g holds columns 32p + 4g .. +7 and an odd g columns
+  // 32p + 16 + 4(g-1) .. +7, and one store writes 64 contiguous bytes of each of 16 rows.  Every lane
+  // takes part in the swaps; rows or columns out of range store past the buffer extent (dropped).
+  auto store_acc16 = [&](__amdgpu_buffer_rsrc_t rs, bool ok, int grow, int st, const f32x4 (&v)[NT], float sc) {
+    typedef int i32x4_t __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int p = 0; p < NT / 2; ++p) {
+      const f32x4 u = v[2 * p], w = v[2 * p + 1];
+      const auto s0 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(u[0] * sc, u[1] * sc),
+                                                        pack_bf16x2(w[0] * sc, w[1] * sc), false, false);
+      const auto s1 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(u[2] * sc, u[3] * sc),
+                                                        pack_bf16x2(w[2] * sc, w[3] * sc), false, false);
+      const int d = 32 * p + ((g & 1) ? 16 + 4 * (g - 1) : 4 * g);
+      const i32x4_t x = {(int)s0[0], (int)s1[0], (int)s0[1], (int)s1[1]};
+      __builtin_amdgcn_raw_buffer_store_b128(x, rs, (ok && d < Dh) ? (uint32_t)(grow * st + d) * 2u : kOffOOB, 0, 0);
+    }
+  };
+  static_assert(NT % 2 == 0, "block pairs");
+
   for (int d = tid; d < DHP; d += 512) {
     gls[d] = d < Dh ? a.gl[h * a.gate_hs + d] : 0.f;
     grs[d] = d < Dh ? a.gr[h * a.gate_hs + d] : 0.f;
@@ -718,14 +739,7 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
         }
       }
       // lane holds dQ[query qi][16t + 4g + i]
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const int d = 16 * t + 4 * g;
-        float v4[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v4[i] = dq[t][i] * a.scale;
-        store4(rdq, (full && qv && d < Dh) ? (uint32_t)(qi * dq_st + d) * 2u : kOffOOB, v4);
-      }
+      store_acc16(rdq, full && qv, qi, dq_st, dq, a.scale);
       lds_barrier();  // tile qt+1 is staged and gated; every wave is done with tile qt-1's buffers
     }
   } else {
@@ -795,18 +809,8 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
         }
         if (half == 0) {  // key tile qt-1 is complete: lane holds dK / dV[key kj][16t + 4g + i]
           const bool st_ok = own_prev && kv;
-#pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            const int d = 16 * t + 4 * g;
-            float k4[4], v4[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              k4[i] = dk[t][i] * a.scale;
-              v4[i] = dv[t][i];
-            }
-            store4(rdk, (st_ok && d < Dh) ? (uint32_t)(kj * dk_st + d) * 2u : kOffOOB, k4);
-            store4(rdv, (st_ok && d < Dh) ? (uint32_t)(kj * dv_st + d) * 2u : kOffOOB, v4);
-          }
+          store_acc16(rdk, st_ok, kj, dk_st, dk, a.scale);
+          store_acc16(rdv, st_ok, kj, dv_st, dv, 1.f);
         } else {
 #pragma unroll
           for (int t = 0; t < NT; ++t) {
@@ -820,18 +824,8 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
     // a segment that ends the sequence: its last key tile gets no more queries
     if (t1 == a.n_qt) {
       const int kj = (t1 - 1) * 64 + row;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const int d = 16 * t + 4 * g;
-        float k4[4], v4[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          k4[i] = pk[t][i] * a.scale;
-          v4[i] = pv[t][i];
-        }
-        store4(rdk, (kj < T_ && d < Dh) ? (uint32_t)(kj * dk_st + d) * 2u : kOffOOB, k4);
-        store4(rdv, (kj < T_ && d < Dh) ? (uint32_t)(kj * dv_st + d) * 2u : kOffOOB, v4);
-      }
+      store_acc16(rdk, kj < T_, kj, dk_st, pk, a.scale);
+      store_acc16(rdv, kj < T_, kj, dv_st, pv, 1.f);
     }
   }
   // gate and dremote partials of the segment: the 32 row threads of each dim (two rows each) added in
