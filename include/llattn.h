@@ -193,6 +193,17 @@ size_t llattn_colsum_workspace_size(int32_t M, int32_t N);
 int32_t llattn_colsum(const void* x, int64_t ld, int32_t M, int32_t N, float* out, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/* fp32 arrays copied in one launch, each to bf16 (round to nearest even) or
+ * fp32 per dst_dtype[i] (LLATTN_BF16 / LLATTN_F32): dst[i][0..n[i]) =
+ * src[i][0..n[i]) for i < nseg <= LLATTN_CAST_MAX_SEGS; arrays aligned to
+ * their element size (16-byte aligned ones move with vector loads/stores).  The per-forward fp32 -> bf16 weight casts that bf16 autocast makes
+ * for every nn.Linear of the block (reference train.py:722, 982 around
+ * models.py:80-84), and the concatenated biases of projections that share one
+ * GEMM (qkv_proj + rq_proj), as one launch instead of one per array. */
+#define LLATTN_CAST_MAX_SEGS 8
+int32_t llattn_cast(int32_t nseg, const float* const* src, void* const* dst, const int64_t* n,
+                    const int32_t* dst_dtype, void* stream);
+
 /* RMSNorm of the residual stream around the block (reference models.py:40-47,
  * F.rms_norm(x, (D,), w, eps), the LM's norm1 / norm2 / norm of reference
  * models.py:493-494, 513):

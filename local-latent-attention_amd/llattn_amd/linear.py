@@ -18,6 +18,40 @@ import torch.nn.functional as F
 from . import gemm
 
 BF16 = torch.bfloat16
+MAX_SEGS = 8  # LLATTN_CAST_MAX_SEGS
+
+
+def pack_params(groups):
+    """``groups``: ``[(tensors, dtype), ...]`` of fp32 parameters.  Returns one new contiguous tensor per group,
+    ``torch.cat(tensors)`` converted to ``dtype`` (bf16: round to nearest even, as ``.to(torch.bfloat16)``), all
+    written by one ``llattn_cast`` launch (per 8 arrays): the weight casts bf16 autocast makes once per forward."""
+    import ctypes
+
+    from . import _lib as L
+    from .ops import _call
+    outs, segs = [], []
+    for tensors, dtype in groups:
+        ts = [t.detach() for t in tensors]
+        lead = sum(t.shape[0] for t in ts)
+        out = torch.empty((lead, *ts[0].shape[1:]), dtype=dtype, device=ts[0].device)
+        o = 0
+        for t in ts:
+            if t.dtype != torch.float32 or not t.is_contiguous():
+                t = t.float().contiguous()
+            n = t.shape[0]
+            segs.append((t, out[o:o + n], t.numel(), L.dtype_code(dtype)))
+            o += n
+        outs.append(out)
+    L.require_gpu(*[sg[0] for sg in segs])
+    for i in range(0, len(segs), MAX_SEGS):
+        chunk = segs[i:i + MAX_SEGS]
+        k = len(chunk)
+        src = (ctypes.c_void_p * k)(*[sg[0].data_ptr() for sg in chunk])
+        dst = (ctypes.c_void_p * k)(*[sg[1].data_ptr() for sg in chunk])
+        n = (ctypes.c_int64 * k)(*[sg[2] for sg in chunk])
+        dt = (ctypes.c_int32 * k)(*[sg[3] for sg in chunk])
+        _call("llattn_cast", k, src, dst, n, dt, L.stream_ptr(chunk[0][0].device))
+    return outs
 
 
 def tn_supported(k: int, m: int, n: int) -> bool:
@@ -62,8 +96,9 @@ def weight_grad(dy2: torch.Tensor, x2: torch.Tensor, bias_grad: bool = False):
 
 class _Project(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, library, pools, *params):
-        # library: (forward on hipBLASLt, input gradient on hipBLASLt)
+    def forward(ctx, x, library, pools, packed, *params):
+        # library: (forward on hipBLASLt, input gradient on hipBLASLt); packed: (bf16 weights, fp32 biases) already
+        # concatenated by pack_params, or None
         ctx.set_materialize_grads(False)
         ws, bs = params[0::2], params[1::2]
         has_bias = bs[0] is not None
@@ -73,14 +108,16 @@ class _Project(torch.autograd.Function):
             x2 = x.reshape(-1, K).to(BF16)
             if not x2.is_contiguous():
                 x2 = x2.contiguous()
-            wcat = torch.empty((sum(rows), K), dtype=BF16, device=x.device)
-            bcat = torch.empty((sum(rows),), dtype=torch.float32, device=x.device) if has_bias else None
-            o = 0
-            for w, b, n in zip(ws, bs, rows):
-                wcat[o:o + n].copy_(w)
-                if has_bias:
-                    bcat[o:o + n].copy_(b)
-                o += n
+            if packed is not None:
+                wcat, bcat = packed
+            elif len(ws) == 1:
+                wcat = ws[0].detach().to(BF16)
+                b = bs[0]
+                bcat = None if b is None else (b.detach() if b.dtype == torch.float32 and b.is_contiguous()
+                                               and b.data_ptr() % 16 == 0 else b.detach().float().contiguous().clone())
+            else:
+                packs = pack_params([(ws, BF16)] + ([(bs, torch.float32)] if has_bias else []))
+                wcat, bcat = packs[0], (packs[1] if has_bias else None)
             y = linear_fwd(x2, wcat, bcat, library[0])
             pooled = []
             if pools:
@@ -127,11 +164,11 @@ class _Project(torch.autograd.Function):
             grads.append(None if dw is None else dw[o:o + n].to(wd))
             grads.append(None if db is None else db[o:o + n].to(bd))
             o += n
-        return (dx, None, None, *grads)
+        return (dx, None, None, None, *grads)
 
 
 def project(x: torch.Tensor, *linears: torch.nn.Linear, library_fwd: bool = False, library_dx: bool = False,
-            pools=()):
+            pools=(), packed=None):
     """bf16 ``x @ [W_1; W_2; ...]^T + [b_1; b_2; ...]`` (all layers share the input width); backward gives
     fp32 weight and bias gradients in the parameters' dtypes.  ``library_fwd`` / ``library_dx`` put the
     forward / input-gradient product on hipBLASLt instead of the MFMA kernel (the weight gradient always
@@ -140,9 +177,10 @@ def project(x: torch.Tensor, *linears: torch.nn.Linear, library_fwd: bool = Fals
     ``pools``: ``(seg, n_seg, divisor)`` segment poolings of the same ``x [B, T, K]`` (as
     :func:`llattn_amd.ops.pool`) returned after the projection, ``(y, pooled_1, ...)``; their backward adds
     into the projection's input gradient in place, so the block's input gradient is formed once.  Without
-    ``pools`` the projection alone is returned."""
+    ``pools`` the projection alone is returned.  ``packed``: ``(bf16 [sum N_i, K] weights, fp32 biases or None)``
+    already cast and concatenated (:func:`pack_params`), so a caller casts all its weights in one launch."""
     params = []
     for lin in linears:
         params += [lin.weight, lin.bias]
-    out = _Project.apply(x, (library_fwd, library_dx), tuple(pools), *params)
+    out = _Project.apply(x, (library_fwd, library_dx), tuple(pools), packed, *params)
     return out if pools else out[0]

@@ -27,7 +27,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _lib as L
-from .linear import project
+from .linear import pack_params, project
 from .ops import LLAttnCore, _Prof, pool
 
 # Which bf16 projection products run on hipBLASLt rather than the MFMA kernel (measured at config 2,
@@ -121,16 +121,18 @@ class LocalLatentAttentionTriton(nn.Module):
         bf16 = torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
         latents = (lay.chunk, lay.n_chunks, L.DIV_COUNT)
         pooled = None
+        packed = self._packed_weights(macro) if bf16 else {}
         if macro and bf16:
             # both poolings of x ride on the projection, whose backward adds their gradients in place
             qkvr, pq, pooled = project(x, self.qkv_proj, library_fwd=QKV_FWD_LIBRARY,
-                                       pools=[(lay.q_block, lay.n_q, L.DIV_SEG), latents])
-            rq = project(pq, self.rq_proj)
+                                       pools=[(lay.q_block, lay.n_q, L.DIV_SEG), latents], packed=packed["qkv"])
+            rq = project(pq, self.rq_proj, packed=packed["rq"])
         elif macro:
             qkvr = self.qkv_proj(x)
             rq = self.rq_proj(pool(x, lay.q_block, lay.n_q, L.DIV_SEG))
         elif bf16:
-            qkvr, pooled = project(x, self.qkv_proj, self.rq_proj, library_fwd=QKV_FWD_LIBRARY, pools=[latents])
+            qkvr, pooled = project(x, self.qkv_proj, self.rq_proj, library_fwd=QKV_FWD_LIBRARY, pools=[latents],
+                                   packed=packed["qkv"])
             rq = None
         else:
             w = torch.cat([self.qkv_proj.weight, self.rq_proj.weight], dim=0)
@@ -143,17 +145,36 @@ class LocalLatentAttentionTriton(nn.Module):
             pooled = pool(x, *latents)
         # the pooled latents' projection (256 rows at config 2) on the MFMA GEMM as well: split-K forward,
         # bias gradient from the weight-gradient pass
-        gkgv = project(pooled, self.rkv_proj) if bf16 else self.rkv_proj(pooled)
+        gkgv = project(pooled, self.rkv_proj, packed=packed["rkv"]) if bf16 else self.rkv_proj(pooled)
         if prof is not None:
             prof.lap("pool_ms")
         rqc = None if rq is None else rq.to(qkvr.dtype)
         y = LLAttnCore.apply(qkvr, rqc, gkgv.to(qkvr.dtype), self.gate_local.weight, self.gate_remote.weight,
-                             self.r_out.weight, self.r_out.bias, lay, prof)
+                             self.r_out.weight, self.r_out.bias, lay, prof, packed.get("r_out"))
         if prof is not None:
             # the gate mix runs in the local kernel's epilogue: its time is in local_attention_ms
             prof.t["gate_mix_ms"] = 0.0
             self._record_profile(prof, lay)
-        return project(y, self.out, library_fwd=OUT_FWD_LIBRARY) if bf16 else self.out(y)
+        return project(y, self.out, library_fwd=OUT_FWD_LIBRARY, packed=packed["out"]) if bf16 else self.out(y)
+
+    def _packed_weights(self, macro: bool) -> dict:
+        """The bf16 copies of every projection weight that this forward multiplies with (what bf16 autocast casts
+        per forward), and the concatenated fp32 biases of qkv_proj + rq_proj, written by one llattn_cast launch.
+        Single projections take their fp32 bias as it is."""
+        qkv = [self.qkv_proj] if macro else [self.qkv_proj, self.rq_proj]
+        has_b = self.qkv_proj.bias is not None
+        groups = [([m.weight for m in qkv], torch.bfloat16)]
+        if has_b:
+            groups.append(([m.bias for m in qkv], torch.float32))
+        singles = (["rq"] if macro else []) + ["rkv", "out", "r_out"]
+        mods = {"rq": self.rq_proj, "rkv": self.rkv_proj, "out": self.out, "r_out": self.r_out}
+        groups += [([mods[k].weight], torch.bfloat16) for k in singles]
+        outs = pack_params(groups)
+        packed = {"qkv": (outs[0], outs[1] if has_b else None)}
+        for i, k in enumerate(singles):
+            b = mods[k].bias
+            packed[k] = outs[(2 if has_b else 1) + i] if k == "r_out" else (outs[(2 if has_b else 1) + i], b)
+        return packed
 
     def _record_profile(self, prof, lay: L.Layout) -> None:
         t = prof.t

@@ -238,7 +238,7 @@ class LLAttnCore(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, qkv, rq, gkgv, gate_l, gate_r, r_w, r_b, lay: L.Layout, prof=None):
+    def forward(ctx, qkv, rq, gkgv, gate_l, gate_r, r_w, r_b, lay: L.Layout, prof=None, r_w_cast=None):
         L.require_gpu(qkv, rq, gkgv)
         dt, device = qkv.dtype, qkv.device
         H, Dh, Lh, Ldh = lay.H, lay.Dh, lay.Lh, lay.Ldh
@@ -260,7 +260,8 @@ class LLAttnCore(torch.autograd.Function):
         rqv = L.view(qkv, sb, sn, Ldh, 3 * D) if rq is None else L.view(rq, rq.stride(0), rq.stride(1), Ldh)
         gk = L.view(gkgv, gkgv.stride(0), gkgv.stride(1), Ldh)
         gv = L.view(gkgv, gkgv.stride(0), gkgv.stride(1), Ldh, Ld)
-        r_wd = r_w.detach().to(dt)  # cast once: the backward's input gradient reuses it
+        # cast once (or given cast): the backward's input gradient reuses it
+        r_wd = r_w_cast if r_w_cast is not None and r_w_cast.dtype == dt else r_w.detach().to(dt)
         y, ol, lse, w, lat, lse_lat, R = _core_forward(lay, q, k, v, rqv, gk, gv, gl, gr, r_wd, r_b, dt, device, prof)
         ctx.save_for_backward(qkv, rq, gkgv, gl, gr, r_wd, lat, lse_lat, R, ol, lse, w)
         ctx.lay, ctx.has_rb, ctx.packed = lay, r_b is not None, rq is None
@@ -299,7 +300,7 @@ class LLAttnCore(torch.autograd.Function):
                                               R, ol, lse, w, dq, dk, dv, drq, dgk, dgv, dt, device)
         gate_l, gate_r = ctx.gate_like
         return (dqkv, drq_t, dgkgv, _gate_grad(dgl, gate_l), _gate_grad(dgr, gate_r), dr_w.to(ctx.r_w_dtype),
-                None if dr_b is None else dr_b.to(ctx.r_b_dtype), None, None)
+                None if dr_b is None else dr_b.to(ctx.r_b_dtype), None, None, None)
 
 
 # ---------------------------------------------------------------------------

@@ -24,7 +24,7 @@ def _declared_functions():
 def test_library_exports_every_declared_symbol():
     L, lib = _lib()
     names = _declared_functions()
-    assert len(names) == 16, names
+    assert len(names) == 17, names
     for n in names:
         assert hasattr(lib, n), n
         assert n in L.SIGNATURES, f"{n} has no ctypes signature"
@@ -184,6 +184,26 @@ def test_gemm_rowsum_workspace():
     fused = lib.llattn_gemm_workspace_size(ctypes.byref(_gemm_desc(L, a_rowsum=0x5000, **kw)))
     S = plain // (1408 * 1408 * 4)
     assert S > 1 and fused == plain + S * 1408 * 4
+
+
+def test_cast_validation():
+    """llattn_cast checks its segment count, output dtypes and alignment before launching anything."""
+    L, lib = _lib()
+    P, I64, I32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
+    src, dst = (P * 2)(0x1000, 0x2000), (P * 2)(0x3000, 0x4000)
+    n, dt = (I64 * 2)(64, 8), (I32 * 2)(L.BF16, L.F32)
+    rc = lib.llattn_cast(0, src, dst, n, dt, None)
+    assert rc == L.ERR_SHAPE and b"segments" in lib.llattn_last_error()
+    rc = lib.llattn_cast(9, src, dst, n, dt, None)
+    assert rc == L.ERR_SHAPE
+    rc = lib.llattn_cast(2, src, dst, n, (I32 * 2)(L.BF16, 7), None)
+    assert rc == L.ERR_DTYPE and b"output dtype" in lib.llattn_last_error()
+    rc = lib.llattn_cast(2, (P * 2)(0x1002, 0x2000), dst, n, dt, None)
+    assert rc == L.ERR_LAYOUT and b"element-aligned" in lib.llattn_last_error()
+    rc = lib.llattn_cast(2, src, dst, (I64 * 2)(64, -1), dt, None)
+    assert rc == L.ERR_SHAPE and b"negative" in lib.llattn_last_error()
+    rc = lib.llattn_cast(1, src, dst, (I64 * 1)(0), dt, None)  # nothing to copy: no launch, success
+    assert rc == L.OK
 
 
 def test_colsum_validation():

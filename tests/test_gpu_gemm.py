@@ -181,3 +181,22 @@ def test_project_with_pools_matches_fp32():
     assert _err(y, yr) < BF16_TOL
     assert _err(p1, r1) < BF16_TOL and _err(p2, r2) < BF16_TOL
     assert _err(x.grad, xr.grad) < BF16_TOL
+
+
+@pytest.mark.parametrize("sizes", [[(4224, 1408), (512, 1408)], [(5,), (13,), (1029,)], [(7,)] * 11])
+def test_pack_params_matches_torch_casts(sizes):
+    """llattn_cast through pack_params: bf16 groups equal torch.cat(...).to(bfloat16) bit for bit (round to
+    nearest even), fp32 groups equal the concatenation; lengths that are not multiples of 8 and more than 8
+    arrays (two launches) included."""
+    from llattn_amd.linear import pack_params
+    dev = require_cuda()
+    print("case: pack", sizes, flush=True)
+    g = torch.Generator(device=dev).manual_seed(len(sizes))
+    ts = [torch.randn(*s, device=dev, generator=g) * 3.0 for s in sizes]
+    ts[0].view(-1)[:4] = torch.tensor([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -2.5e-39, float("inf")], device=dev)
+    half = len(ts) // 2 or 1
+    groups = [(ts[:half], torch.bfloat16)] + ([(ts[half:], torch.float32)] if ts[half:] else [])
+    outs = pack_params(groups)
+    assert torch.equal(outs[0].view(torch.int16), torch.cat(ts[:half]).to(torch.bfloat16).view(torch.int16))
+    if ts[half:]:
+        assert torch.equal(outs[1], torch.cat(ts[half:]))
