@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define LLATTN_ABI_VERSION 3
+#define LLATTN_ABI_VERSION 4
 
 /* status codes */
 #define LLATTN_OK 0
@@ -162,6 +162,16 @@ int32_t llattn_local_gate_bwd(const llattn_shape* s, const llattn_tensor* q, con
  * partials to the workspace (llattn_gemm_workspace_size bytes) and sums them
  * in a fixed order.  Replaces the block's nn.Linear products and their
  * autograd backward (reference models.py:80-84, 315, 333-353, 395, 462). */
+/* A bf16 matrix of rows broadcast onto token rows of C: C[m][n] += ptr[(m / rows_per_seq) * n_seg + t / seg][n]
+ * / divisor with t = m % rows_per_seq (divisor as llattn_pool_bwd: LLATTN_DIV_COUNT, _SEG or _ONE).  The
+ * backward of a pooling of the GEMM's input (reference models.py:159-230) added into its input gradient
+ * before the bf16 rounding, without a separate pass over it.  ptr NULL: none. */
+typedef struct llattn_gemm_rowadd {
+  const void* ptr;  /* bf16 rows, 8-byte aligned */
+  int64_t ld;       /* elements between rows, >= N, a multiple of 4 */
+  int32_t rows_per_seq, seg, n_seg, divisor;
+} llattn_gemm_rowadd;
+
 typedef struct llattn_gemm_desc {
   int32_t M, N, K;
   int32_t a_trans, b_trans;
@@ -179,6 +189,7 @@ typedef struct llattn_gemm_desc {
                           sum_tokens dy of a weight-gradient product dy^T x, contracted against a
                           column of ones in place of the unused column N of the last tile (needs
                           b_trans = 1, fp32 C and N % 256 != 0); overwritten, never accumulated */
+  llattn_gemm_rowadd rowadd[2]; /* bf16 C, a_trans = 0, b_trans = 1 (input gradients) */
 } llattn_gemm_desc;
 
 size_t llattn_gemm_workspace_size(const llattn_gemm_desc* d);

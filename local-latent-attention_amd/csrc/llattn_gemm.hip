@@ -52,7 +52,30 @@ struct GemmArgs {
   const float* bias;
   float* part;     // split-K partials [S][M][N], then (rowsum) [S][M]
   float* rowsum;   // fp32 [M] or null: sum_k A(m, k), from a column of ones in place of B's column N
+  // bf16 C only: C[m][n] += ra[(m / T) * n_seg + (m % T) / seg][n] / divisor for each of up to two addends
+  const uint16_t* ra_ptr[2];
+  int64_t ra_ld[2];
+  int ra_T[2], ra_seg[2], ra_nseg[2], ra_div[2];
 };
+
+// Row of addend q (0, 1) that C row m reads, and its scale (the pooled gradient broadcast to its tokens).
+__device__ __forceinline__ const uint16_t* rowadd_row(const GemmArgs& a, int q, int m, float& sc) {
+  const int T = a.ra_T[q], t = m % T, s = t / a.ra_seg[q];
+  sc = a.ra_div[q] == LLATTN_DIV_COUNT ? 1.f / (float)(min((s + 1) * a.ra_seg[q], T) - s * a.ra_seg[q])
+     : a.ra_div[q] == LLATTN_DIV_SEG ? 1.f / (float)a.ra_seg[q] : 1.f;
+  return a.ra_ptr[q] + ((int64_t)(m / T) * a.ra_nseg[q] + s) * a.ra_ld[q];
+}
+__device__ __forceinline__ void add_bf16x4(uint2 u, float sc, float (&v)[4]) {
+  v[0] += sc * __uint_as_float(u.x << 16);
+  v[1] += sc * __uint_as_float(u.x & 0xffff0000u);
+  v[2] += sc * __uint_as_float(u.y << 16);
+  v[3] += sc * __uint_as_float(u.y & 0xffff0000u);
+}
+__device__ __forceinline__ void rowadd4(const GemmArgs& a, int q, int m, int c, float (&v)[4]) {
+  float sc;
+  const uint16_t* p = rowadd_row(a, q, m, sc);
+  add_bf16x4(*reinterpret_cast<const uint2*>(p + c), sc, v);
+}
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) const void gbl_void;
@@ -323,13 +346,30 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
   }
   if constexpr (EPI == EPI_BF16) {
     // bf16 rows of 256 B; 8-byte unit u of row rl stored at u ^ (rl & 15)
+    const bool ra0 = a.ra_ptr[0] != nullptr, ra1 = a.ra_ptr[1] != nullptr;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int rl = 16 * i + r;
+      // broadcast addends of this row: all eight 4-column pieces loaded before the first is used
+      uint2 rv[2][8];
+      float rsc[2] = {0.f, 0.f};
+      if (ra0 || ra1) {
+        const int mrow = min(row0 + rl, a.M - 1);  // rows past M are never stored
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          if (q == 0 ? !ra0 : !ra1) continue;
+          const uint16_t* p = rowadd_row(a, q, mrow, rsc[q]);
+#pragma unroll
+          for (int j = 0; j < 8; ++j)  // columns past N are never stored
+            rv[q][j] = *reinterpret_cast<const uint2*>(p + min(col0 + 16 * j + 4 * g, a.N - 4));
+        }
+      }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float v[4] = {acc[i][j][0] + bias4[j].x, acc[i][j][1] + bias4[j].y, acc[i][j][2] + bias4[j].z,
-                            acc[i][j][3] + bias4[j].w};
+        float v[4] = {acc[i][j][0] + bias4[j].x, acc[i][j][1] + bias4[j].y, acc[i][j][2] + bias4[j].z,
+                      acc[i][j][3] + bias4[j].w};
+        if (ra0) add_bf16x4(rv[0][j], rsc[0], v);
+        if (ra1) add_bf16x4(rv[1][j], rsc[1], v);
         uint2 x;
         x.x = static_cast<uint32_t>(f2bf(v[0])) | (static_cast<uint32_t>(f2bf(v[1])) << 16);
         x.y = static_cast<uint32_t>(f2bf(v[2])) | (static_cast<uint32_t>(f2bf(v[3])) << 16);
@@ -657,6 +697,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs a, in
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] += o[e];
     }
+    if (a.ra_ptr[0]) rowadd4(a, 0, row, col, v);
+    if (a.ra_ptr[1]) rowadd4(a, 1, row, col, v);
     store4<uint16_t>(c, v);
   }
 }
@@ -734,6 +776,20 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
     return fail(LLATTN_ERR_UNSUPPORTED,
                 "llattn_gemm: row sums of A need an m/n-contiguous B, fp32 C, N not a multiple of %d (a spare "
                 "column in the last tile; N=%d) and a 16-byte aligned output", BN, d->N);
+  for (int q = 0; q < 2; ++q) {
+    const llattn_gemm_rowadd& ra = d->rowadd[q];
+    if (!ra.ptr) continue;
+    if (d->c_dtype != LLATTN_BF16 || !d->b_trans || d->a_trans)
+      return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: row addends need bf16 C and the input-gradient layout "
+                  "(a_trans = 0, b_trans = 1)");
+    if (ra.rows_per_seq <= 0 || d->M % ra.rows_per_seq || ra.seg <= 0 || ra.n_seg != (ra.rows_per_seq + ra.seg - 1) / ra.seg ||
+        (ra.divisor != LLATTN_DIV_COUNT && ra.divisor != LLATTN_DIV_SEG && ra.divisor != LLATTN_DIV_ONE))
+      return fail(LLATTN_ERR_SHAPE, "llattn_gemm: row addend %d: M=%d must be whole sequences of %d rows, n_seg=%d "
+                  "must be ceil(%d / seg=%d), divisor %d known", q, d->M, ra.rows_per_seq, ra.n_seg, ra.rows_per_seq,
+                  ra.seg, ra.divisor);
+    if ((uintptr_t)ra.ptr % 8 || ra.ld % 4 || ra.ld < d->N)
+      return fail(LLATTN_ERR_LAYOUT, "llattn_gemm: row addend %d must be 8-byte aligned with ld >= N, a multiple of 4", q);
+  }
   const size_t need = llattn_gemm_workspace_size(d);
   if (need && (!workspace || workspace_bytes < need || !aligned16(workspace)))
     return fail(LLATTN_ERR_WORKSPACE, "llattn_gemm: %d K splits need %zu workspace bytes (got %zu)", S, need,
@@ -748,6 +804,14 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
   a.bias = d->bias;
   a.part = static_cast<float*>(workspace);
   a.rowsum = d->a_rowsum;
+  for (int q = 0; q < 2; ++q) {
+    a.ra_ptr[q] = static_cast<const uint16_t*>(d->rowadd[q].ptr);
+    a.ra_ld[q] = d->rowadd[q].ld;
+    a.ra_T[q] = d->rowadd[q].rows_per_seq > 0 ? d->rowadd[q].rows_per_seq : 1;
+    a.ra_seg[q] = d->rowadd[q].seg > 0 ? d->rowadd[q].seg : 1;
+    a.ra_nseg[q] = d->rowadd[q].n_seg;
+    a.ra_div[q] = d->rowadd[q].divisor;
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   // bf16 x Wᵀ (+ bias) without K split or accumulation: the persistent kernel, one workgroup per CU
   const int64_t c_bytes = ((int64_t)(d->M - 1) * d->ldc + d->N) * 2;

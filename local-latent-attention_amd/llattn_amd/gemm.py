@@ -28,7 +28,8 @@ def _check2d(name: str, t: torch.Tensor) -> None:
 
 
 def _run(M: int, N: int, K: int, A: torch.Tensor, a_trans: bool, B: torch.Tensor, b_trans: bool, C: torch.Tensor,
-         bias: torch.Tensor | None, accumulate: bool, split_k: int = 0, rowsum: torch.Tensor | None = None) -> None:
+         bias: torch.Tensor | None, accumulate: bool, split_k: int = 0, rowsum: torch.Tensor | None = None,
+         rowadd=()) -> None:
     L.require_gpu(A, B, C)
     if rowsum is not None and (rowsum.dtype != torch.float32 or not rowsum.is_contiguous() or rowsum.numel() != M):
         raise ValueError(f"rowsum must be a contiguous fp32 vector of {M} elements")
@@ -40,6 +41,12 @@ def _run(M: int, N: int, K: int, A: torch.Tensor, a_trans: bool, B: torch.Tensor
                             B.stride(0), C.data_ptr(), C.stride(0), L.dtype_code(C.dtype), int(accumulate),
                             None if bias is None else bias.data_ptr(), split_k,
                             None if rowsum is None else rowsum.data_ptr())
+    if len(rowadd) > 2:
+        raise ValueError("at most two row addends")
+    for q, (rows, per_seq, seg, n_seg, divisor) in enumerate(rowadd):
+        if rows.dtype != torch.bfloat16 or rows.stride(-1) != 1 or rows.shape[-1] != N:
+            raise ValueError(f"row addend {q} must be bf16 rows of {N} contiguous elements")
+        desc.rowadd[q] = L.LlattnGemmRowadd(rows.data_ptr(), rows.stride(-2), per_seq, seg, n_seg, divisor)
     lib = L.load()
     nws = lib.llattn_gemm_workspace_size(ctypes.byref(desc))
     ws = torch.empty((max(nws, 1),), dtype=torch.uint8, device=C.device) if nws else None
@@ -64,8 +71,10 @@ def linear(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None, o
 
 
 def matmul_nn(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None,
-              accumulate: bool = False) -> torch.Tensor:
-    """``a [M, K] @ b [K, N]`` -> bf16 ``[M, N]`` (b read row-major, no transpose copy)."""
+              accumulate: bool = False, rowadd=()) -> torch.Tensor:
+    """``a [M, K] @ b [K, N]`` -> bf16 ``[M, N]`` (b read row-major, no transpose copy).  ``rowadd``: up to two
+    ``(rows, rows_per_seq, seg, n_seg, divisor)`` -- bf16 ``[n_seq * n_seg, N]`` rows added to every output row of
+    their segment before the rounding, as ``llattn_pool_bwd`` adds a pooling's gradient into its input gradient."""
     _check2d("a", a)
     _check2d("b", b)
     M, K = a.shape
@@ -74,7 +83,7 @@ def matmul_nn(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None,
         raise ValueError(f"a is [{M}, {K}] but b is {tuple(b.shape)}")
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
-    _run(M, N, K, a, False, b, True, out, None, accumulate)
+    _run(M, N, K, a, False, b, True, out, None, accumulate, rowadd=rowadd)
     return out
 
 

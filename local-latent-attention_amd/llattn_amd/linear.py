@@ -73,10 +73,13 @@ def linear_fwd(x2: torch.Tensor, w: torch.Tensor, b32: torch.Tensor | None, libr
     return F.linear(x2, w, None if b32 is None else b32.to(BF16))
 
 
-def input_grad(dy2: torch.Tensor, w: torch.Tensor, library: bool = False) -> torch.Tensor:
-    """bf16 ``dy2 @ w`` (w [N, K] read row-major)."""
+def input_grad(dy2: torch.Tensor, w: torch.Tensor, library: bool = False, rowadd=()) -> torch.Tensor:
+    """bf16 ``dy2 @ w`` (w [N, K] read row-major), plus the broadcast ``rowadd`` pooling gradients
+    (:func:`llattn_amd.gemm.matmul_nn`; only on the MFMA kernel)."""
     if not library and mfma_supported(dy2.shape[1], w.shape[1]):
-        return gemm.matmul_nn(dy2, w)
+        return gemm.matmul_nn(dy2, w, rowadd=rowadd)
+    if rowadd:
+        raise ValueError("row addends need the MFMA input-gradient kernel")
     return torch.mm(dy2, w)
 
 
@@ -146,7 +149,17 @@ class _Project(torch.autograd.Function):
                 if not dy2.is_contiguous():
                     dy2 = dy2.contiguous()
                 if ctx.needs_input_grad[0]:
-                    dx = input_grad(dy2, wcat, library[1]).view(*lead, K).to(xdt)
+                    # the poolings' gradients (bf16) join the input gradient in the GEMM's epilogue
+                    fuse = (xdt == BF16 and not library[1] and mfma_supported(N, K) and len(lead) == 2
+                            and all(g is None or g.dtype == BF16 for g in dpooled))
+                    rowadd = []
+                    if fuse:
+                        from .ops import _contig
+                        for g, (seg, n_seg, divisor) in zip(dpooled, pools):
+                            if g is not None:
+                                rowadd.append((_contig(g).view(-1, K), lead[1], seg, n_seg, divisor))
+                        dpooled = ()
+                    dx = input_grad(dy2, wcat, library[1], rowadd).view(*lead, K).to(xdt)
                 dw, db = weight_grad(dy2, x2, has_bias)
             if ctx.needs_input_grad[0] and any(g is not None for g in dpooled):
                 # pooling backward accumulates straight into the projection's input gradient

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_empty_error():
     L, lib = _lib()
-    assert lib.llattn_abi_version() == L.ABI_VERSION == 3
+    assert lib.llattn_abi_version() == L.ABI_VERSION == 4
 
 
 def _shape(L, **kw):
@@ -173,6 +173,25 @@ def test_gemm_rowsum_validation(kw, msg):
     d = _gemm_desc(L, **base)
     rc = lib.llattn_gemm(ctypes.byref(d), None, 0, None)
     assert rc == L.ERR_UNSUPPORTED, lib.llattn_last_error()
+    assert msg in lib.llattn_last_error()
+
+
+@pytest.mark.parametrize("ra,kw,code,msg", [
+    (dict(rows_per_seq=256, seg=64, n_seg=4, divisor=0, ld=264), dict(c_dtype=0), 4, b"row addends need bf16 C"),
+    (dict(rows_per_seq=300, seg=64, n_seg=5, divisor=0, ld=264), {}, 1, b"whole sequences"),
+    (dict(rows_per_seq=256, seg=64, n_seg=3, divisor=0, ld=264), {}, 1, b"ceil"),
+    (dict(rows_per_seq=256, seg=64, n_seg=4, divisor=5, ld=264), {}, 1, b"divisor"),
+    (dict(rows_per_seq=256, seg=64, n_seg=4, divisor=0, ld=100), {}, 3, b"ld >= N"),
+])
+def test_gemm_rowadd_validation(ra, kw, code, msg):
+    """Broadcast row addends (the pooling backward fused into an input gradient) are checked on the host."""
+    L, lib = _lib()
+    base = dict(M=512, N=264, K=128, a_trans=0, b_trans=1, lda=128, ldb=264, ldc=264, c_dtype=L.BF16)
+    base.update(kw)
+    d = _gemm_desc(L, **base)
+    d.rowadd[0] = L.LlattnGemmRowadd(0x5000, **ra)
+    rc = lib.llattn_gemm(ctypes.byref(d), None, 0, None)
+    assert rc == code, lib.llattn_last_error()
     assert msg in lib.llattn_last_error()
 
 

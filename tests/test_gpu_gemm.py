@@ -47,6 +47,36 @@ def test_matmul_nn(M, N, K):
     assert _err(gemm.matmul_nn(a, b), a.float() @ b.float()) < BF16_TOL
 
 
+@pytest.mark.parametrize("B,T,N,K,pools", [
+    (2, 300, 264, 128, [(64, 0)]),               # latent-style mean, last segment 44 tokens
+    (3, 256, 136, 192, [(64, 1), (100, 0)]),     # query-block (zero-padded) mean and a ragged chunk mean
+    (16, 2048, 1408, 4736, [(128, 0)]),          # config 2: qkv input gradient with the latent pooling
+    (2, 97, 40, 64, [(17, 2)]),                  # plain sums
+    (2, 2048, 1408, 4736, [(128, 0), (64, 1)]),  # a split-K shape: the addends join in the ordered reduction
+])
+def test_matmul_nn_rowadd(B, T, N, K, pools):
+    """Input gradient with the pooling backward in its epilogue: a @ b + sum over poolings of rows[b, t // seg] /
+    divisor (divisor 0: real tokens in the segment, 1: seg, 2: one), against fp32 torch; bf16 output."""
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: nn rowadd", B, T, N, K, pools, flush=True)
+    g = torch.Generator(device=dev).manual_seed(B * T + N)
+    a, b = _rand(B * T, K, gen=g, dev=dev), _rand(K, N, gen=g, dev=dev)
+    ref = a.float() @ b.float()
+    rowadd = []
+    t = torch.arange(T, device=dev)
+    for seg, div in pools:
+        n_seg = -(-T // seg)
+        rows = _rand(B * n_seg, N, gen=g, dev=dev) * 4
+        s_id = t // seg
+        count = torch.minimum((s_id + 1) * seg, torch.full_like(s_id, T)) - s_id * seg
+        scale = {0: 1.0 / count.float(), 1: torch.full((T,), 1.0 / seg, device=dev), 2: torch.ones(T, device=dev)}[div]
+        add = rows.float().view(B, n_seg, N)[:, s_id] * scale[None, :, None]
+        ref = ref + add.reshape(B * T, N)
+        rowadd.append((rows, T, seg, n_seg, div))
+    assert _err(gemm.matmul_nn(a, b, rowadd=rowadd), ref) < BF16_TOL
+
+
 @pytest.mark.parametrize("K,M,N,S", [(64, 256, 264, 1), (1024, 264, 136, 0), (2048, 40, 96, 1), (4096, 264, 136, 3),
                                      (4096, 1000, 520, 1), (32768, 1408, 1408, 0), (32768, 4736, 1408, 0)])
 def test_matmul_tn_rowsum(K, M, N, S):
