@@ -17,7 +17,7 @@
 namespace llattn {
 namespace {
 
-constexpr int kBwdBlocks = 256;  // workgroups of the backward (one per CU); dw partial rows
+constexpr int kBwdBlocks = 512;  // workgroups of the backward (two per CU); dw partial rows
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -109,10 +109,12 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const DYT* __restrict_
     }
   }
   const float inv_d = 1.0f / (float)D;
-  // row data of the next row is loaded before the current row is computed (two register sets)
-  auto load_row = [&](int row, float (&xv)[NCH][4], float (&dv)[NCH][4]) {
+  // row data of the next row -- x, dy and rstd -- is loaded before the current row is computed (two
+  // register sets), so no load issued while a row is computed is waited for by that row
+  auto load_row = [&](int row, float (&xv)[NCH][4], float (&dv)[NCH][4], float& rs) {
     const XT* xr = x + (int64_t)row * ldx;
     const DYT* dr = dy + (int64_t)row * lddy;
+    rs = rstd[row];
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
       const int c = lane + 64 * i;
@@ -126,8 +128,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const DYT* __restrict_
     }
   };
   // xh = x * rstd and g = dy * w are formed twice (for the row dot product, then for dx) rather than kept
-  auto do_row = [&](int row, const float (&xv)[NCH][4], const float (&dv)[NCH][4]) {
-    const float r = rstd[row];
+  auto do_row = [&](int row, const float (&xv)[NCH][4], const float (&dv)[NCH][4], const float r) {
     float dot = 0.f;
 #pragma unroll
     for (int i = 0; i < NCH; ++i)
@@ -148,21 +149,21 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const DYT* __restrict_
       if (c < nq) st4(o + 4 * c, v);
     }
   };
-  float xa[NCH][4], da[NCH][4];
+  float xa[NCH][4], da[NCH][4], ra = 0.f;
   if constexpr (NCH <= 8) {  // two register sets: the next row loads while this one is computed
-    float xb[NCH][4], db[NCH][4];
-    if (r0 < r1) load_row(r0, xa, da);
+    float xb[NCH][4], db[NCH][4], rb = 0.f;
+    if (r0 < r1) load_row(r0, xa, da, ra);
     for (int row = r0; row < r1; row += 2) {
-      if (row + 1 < r1) load_row(row + 1, xb, db);
-      do_row(row, xa, da);
+      if (row + 1 < r1) load_row(row + 1, xb, db, rb);
+      do_row(row, xa, da, ra);
       if (row + 1 >= r1) break;
-      if (row + 2 < r1) load_row(row + 2, xa, da);
-      do_row(row + 1, xb, db);
+      if (row + 2 < r1) load_row(row + 2, xa, da, ra);
+      do_row(row + 1, xb, db, rb);
     }
   } else {
     for (int row = r0; row < r1; ++row) {
-      load_row(row, xa, da);
-      do_row(row, xa, da);
+      load_row(row, xa, da, ra);
+      do_row(row, xa, da, ra);
     }
   }
   // the workgroup's four waves, added in wave order
