@@ -237,6 +237,24 @@ int32_t llattn_rmsnorm_bwd(const void* dy, int32_t dy_dtype, int64_t lddy, const
                            int64_t ldx, const float* rstd, const float* weight, int32_t M, int32_t D, void* dx,
                            int64_t lddx, float* dweight, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Cross entropy of bf16 logit rows and its gradient in one pass (the tied LM
+ * head's loss, reference train.py:354-370: F.cross_entropy over [B*T, V]
+ * logits in fp32 under autocast, ignore_index, and logits.argmax(-1) for the
+ * accuracy metric; reference models.py:516-517, 576 for the head).  For each
+ * of `rows` rows of V logits (leading dimension ld elements, 16-byte aligned
+ * rows, V a multiple of 8, at most 65536):
+ *   loss[r] = logsumexp(x_r) - x_r[t_r]   (0 where t_r == ignore_index,
+ *             NaN where t_r lies outside [0, V) otherwise),
+ *   pred[r] = first index of the row maximum (pred may be null),
+ * and, when dlogits is non-null, dlogits[r][j] = (softmax(x_r)_j - [j == t_r])
+ * * (*grad_scale) as bf16 (0 for ignored rows); dlogits may be the logits
+ * buffer itself (in place) or a disjoint one.  targets: int64 [rows].
+ * grad_scale: a device fp32 scalar (1 / valid rows for a mean).  One read and
+ * one write of the logits; fixed-order reductions (deterministic). */
+int32_t llattn_xent(const void* logits, int64_t ld, int32_t rows, int32_t V, const int64_t* targets,
+                    int64_t ignore_index, float* loss, int32_t* pred, void* dlogits, int64_t ld_d,
+                    const float* grad_scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -75,6 +75,7 @@ SIGNATURES = {
     "llattn_rmsnorm_fwd": (_I32, [_P, _I32, _I64, _P, _I32, _I32, ctypes.c_float, _P, _I32, _I64, _P, _P]),
     "llattn_rmsnorm_workspace_size": (_SZ, [_I32, _I32]),
     "llattn_rmsnorm_bwd": (_I32, [_P, _I32, _I64, _P, _I32, _I64, _P, _P, _I32, _I32, _P, _I64, _P, _P, _SZ, _P]),
+    "llattn_xent": (_I32, [_P, _I64, _I32, _I32, _P, _I64, _P, _P, _P, _I64, _P, _P]),
 }
 
 _lib = None

@@ -12,7 +12,9 @@ models.py:465-488), and the norms run on the gfx950 RMSNorm kernels
 implementations to compare against.
 
 :func:`lm_loss` is the token-level loss and metrics of the reference trainer
-(reference train.py:340-370, ``compute_loss_and_metrics`` for [B, T] targets),
+(reference train.py:340-370, ``compute_loss_and_metrics`` for [B, T] targets);
+:meth:`LocalLatentLM.loss` computes the same from the hidden states with the
+head and the cross entropy in row chunks (no full logits tensor),
 :func:`make_optimizer` its AdamW set-up (reference train.py:851-859) and
 :func:`train_step` one optimiser step as its loop runs it (reference
 train.py:960-1037, one micro-step, gradient clipping, no loss scaling in bf16).
@@ -125,7 +127,8 @@ class LocalLatentLM(nn.Module):
                 totals[k] = totals.get(k, 0.0) + v
         return {k: v / count for k, v in totals.items()} if count else {}
 
-    def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
+    def hidden(self, input_ids: torch.Tensor) -> torch.Tensor:
+        """The final-norm hidden states ``[B, T, D]`` that the tied head maps to logits."""
         _, seq_len = input_ids.shape
         pos = torch.arange(seq_len, device=input_ids.device)
         x = self.embedding(input_ids) + self.position(pos).unsqueeze(0)
@@ -134,7 +137,17 @@ class LocalLatentLM(nn.Module):
                 x = checkpoint(block, x, use_reentrant=False)
             else:
                 x = block(x)
-        return self.lm_head(self.norm(x))
+        return self.norm(x)
+
+    def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
+        return self.lm_head(self.hidden(input_ids))
+
+    def loss(self, input_ids: torch.Tensor, targets: torch.Tensor, chunk_rows: int = 8192):
+        """:func:`lm_loss` of ``self(input_ids)`` without the ``[B*T, V]`` logits: the tied head and the cross
+        entropy run in row chunks on the gfx950 kernels (:func:`~llattn_amd.xent.lm_head_loss`)."""
+        from .xent import lm_head_loss
+        loss, pred = lm_head_loss(self.hidden(input_ids), self.lm_head.weight, targets, chunk_rows=chunk_rows)
+        return loss, _metrics(loss, (pred == targets).float().mean())
 
 
 def build_model(preset: Optional[str] = None, attention_factory=None, norm_factory=None,
@@ -151,11 +164,13 @@ def lm_loss(logits: torch.Tensor, targets: torch.Tensor):
     synchronisation), as reference train.py:354-370 computes them."""
     flat = logits.reshape(-1, logits.size(-1))
     loss = F.cross_entropy(flat, targets.reshape(-1))
-    acc = (logits.argmax(dim=-1) == targets).float().mean()
+    return loss, _metrics(loss, (logits.argmax(dim=-1) == targets).float().mean())
+
+
+def _metrics(loss: torch.Tensor, acc: torch.Tensor) -> dict:
     loss_det = loss.detach()
-    return loss, {"eval_loss": loss_det, "eval_acc": acc,
-                  "eval_perplexity": torch.exp(torch.clamp(loss_det, max=20.0)),
-                  "eval_bpt": loss_det / math.log(2.0)}
+    return {"eval_loss": loss_det, "eval_acc": acc, "eval_perplexity": torch.exp(torch.clamp(loss_det, max=20.0)),
+            "eval_bpt": loss_det / math.log(2.0)}
 
 
 def make_optimizer(model: nn.Module, lr: float = 3e-4) -> torch.optim.Optimizer:
@@ -169,12 +184,16 @@ def make_optimizer(model: nn.Module, lr: float = 3e-4) -> torch.optim.Optimizer:
 
 
 def train_step(model: nn.Module, optimizer: torch.optim.Optimizer, inputs: torch.Tensor, targets: torch.Tensor,
-               grad_clip: float = 1.0) -> torch.Tensor:
+               grad_clip: float = 1.0, fused_loss: bool = True) -> torch.Tensor:
     """One bf16-autocast optimiser step: forward, loss, backward, gradient clipping, AdamW update, gradients
-    cleared (reference train.py:960-1037 with one micro-step).  Returns the detached loss (no sync)."""
+    cleared (reference train.py:960-1037 with one micro-step).  ``fused_loss``: the chunked head + cross entropy
+    (:meth:`LocalLatentLM.loss`) instead of full logits and ``F.cross_entropy``.  Returns the detached loss (no
+    sync)."""
     with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
-        logits = model(inputs)
-        loss, _ = lm_loss(logits, targets)
+        if fused_loss:
+            loss, _ = model.loss(inputs, targets)
+        else:
+            loss, _ = lm_loss(model(inputs), targets)
         loss.backward()
     if grad_clip > 0:
         torch.nn.utils.clip_grad_norm_(model.parameters(), grad_clip)

@@ -444,3 +444,25 @@ def init_params(shape: BlockShape, rng: np.random.Generator, std: float = 0.02,
             if n_layers is not None and name.split(".")[0] in ("out", "r_out"):
                 p[name] = p[name] / math.sqrt(2 * n_layers)
     return p
+
+
+def cross_entropy_rows(logits: np.ndarray, targets: np.ndarray, ignore_index: int = -100):
+    """Per-row cross entropy of the LM head (reference train.py:354-357, ``F.cross_entropy`` over
+    ``[rows, V]`` logits with its default ``ignore_index=-100`` and mean reduction; :358 ``argmax``):
+    returns float64 ``loss [rows]`` (``logsumexp(x) - x[t]``, 0 for ignored rows), ``pred [rows]``
+    (first index of the maximum, as torch's argmax) and ``grad [rows, V]`` = ``softmax(x) - onehot(t)``
+    (0 for ignored rows) -- the gradient of the summed loss; the mean's gradient divides it by the
+    number of rows that count."""
+    x = np.asarray(logits, dtype=np.float64)
+    t = np.asarray(targets).reshape(-1).astype(np.int64)
+    m = x.max(axis=1, keepdims=True)
+    e = np.exp(x - m)
+    s = e.sum(axis=1, keepdims=True)
+    lse = (m + np.log(s))[:, 0]
+    keep = t != ignore_index
+    tt = np.where(keep, t, 0)
+    loss = np.where(keep, lse - x[np.arange(x.shape[0]), tt], 0.0)
+    grad = e / s
+    grad[np.arange(x.shape[0]), tt] -= 1.0
+    grad[~keep] = 0.0
+    return loss, x.argmax(axis=1), grad

@@ -24,7 +24,7 @@ def _declared_functions():
 def test_library_exports_every_declared_symbol():
     L, lib = _lib()
     names = _declared_functions()
-    assert len(names) == 17, names
+    assert len(names) == 18, names
     for n in names:
         assert hasattr(lib, n), n
         assert n in L.SIGNATURES, f"{n} has no ctypes signature"
@@ -223,6 +223,31 @@ def test_cast_validation():
     assert rc == L.ERR_SHAPE and b"negative" in lib.llattn_last_error()
     rc = lib.llattn_cast(1, src, dst, (I64 * 1)(0), dt, None)  # nothing to copy: no launch, success
     assert rc == L.OK
+
+
+def test_xent_validation():
+    """llattn_xent checks sizes, alignment and buffer overlap before launching anything."""
+    L, lib = _lib()
+    P = ctypes.c_void_p
+    lg, tg, ls, pr, sc = P(1 << 20), P(2 << 20), P(3 << 20), P(4 << 20), P(5 << 20)  # never dereferenced
+    rc = lib.llattn_xent(lg, 64, 4, 60, tg, -100, ls, pr, None, 0, None, None)
+    assert rc == L.ERR_SHAPE and b"multiple of 8" in lib.llattn_last_error()
+    rc = lib.llattn_xent(lg, 70000, 4, 65544, tg, -100, ls, pr, None, 0, None, None)
+    assert rc == L.ERR_SHAPE
+    rc = lib.llattn_xent(lg, 64, -1, 64, tg, -100, ls, pr, None, 0, None, None)
+    assert rc == L.ERR_SHAPE
+    rc = lib.llattn_xent(lg, 64, 0, 64, None, -100, None, None, None, 0, None, None)  # no rows: nothing to do
+    assert rc == L.OK
+    rc = lib.llattn_xent(lg, 56, 4, 64, tg, -100, ls, pr, None, 0, None, None)
+    assert rc == L.ERR_LAYOUT and b"ld" in lib.llattn_last_error()
+    rc = lib.llattn_xent(P((1 << 20) + 8), 64, 4, 64, tg, -100, ls, pr, None, 0, None, None)
+    assert rc == L.ERR_LAYOUT
+    rc = lib.llattn_xent(lg, 64, 4, 64, None, -100, ls, pr, None, 0, None, None)
+    assert rc == L.ERR_LAYOUT and b"null" in lib.llattn_last_error()
+    rc = lib.llattn_xent(lg, 64, 4, 64, tg, -100, ls, pr, P(6 << 20), 64, None, None)
+    assert rc == L.ERR_LAYOUT and b"grad_scale" in lib.llattn_last_error()
+    rc = lib.llattn_xent(lg, 64, 4, 64, tg, -100, ls, pr, P((1 << 20) + 128), 64, sc, None)
+    assert rc == L.ERR_LAYOUT and b"overlaps" in lib.llattn_last_error()
 
 
 def test_colsum_validation():
