@@ -409,7 +409,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(one process drives one MI355X here; the sharding design is described in DESIGN.md)",
+              "(the library drives one GPU per process and has no multi-GPU path)",
               file=sys.stderr)
         sys.exit(2)
 
