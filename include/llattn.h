@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define LLATTN_ABI_VERSION 4
+#define LLATTN_ABI_VERSION 5
 
 /* status codes */
 #define LLATTN_OK 0
@@ -223,19 +223,28 @@ int32_t llattn_cast(int32_t nseg, const float* const* src, void* const* dst, con
  * 16-byte (fp32) or 8-byte (bf16) aligned), each LLATTN_F32 or LLATTN_BF16 --
  * y in bf16 feeds the block's bf16 projections without a cast.  weight fp32
  * [D] (16-byte aligned); rstd fp32 [M] is written for the backward.
- * D must be a multiple of 4 and at most 4096. */
+ * D must be a multiple of 4 and at most 4096.
+ * With res non-null (fp32 x only): the residual add in front of the norm is
+ * fused, as the LM block writes it (reference models.py:499-502,
+ * x = x + attn(norm1(x)); x = x + ffn(norm2(x)) followed by the next norm):
+ * xsum = x + res (fp32; res fp32 or bf16 per res_dtype, rows aligned as x's)
+ * is written (xsum may be x itself) and y normalises xsum. */
 int32_t llattn_rmsnorm_fwd(const void* x, int32_t x_dtype, int64_t ldx, const float* weight, int32_t M, int32_t D,
-                           float eps, void* y, int32_t y_dtype, int64_t ldy, float* rstd, void* stream);
+                           float eps, void* y, int32_t y_dtype, int64_t ldy, float* rstd, const void* res,
+                           int32_t res_dtype, int64_t ldres, float* xsum, int64_t ldxsum, void* stream);
 
 /* Backward of llattn_rmsnorm_fwd: dx (x's dtype) = rstd * (g - xh * mean_d(g xh)),
  * g = dy * w, xh = x * rstd; dweight (fp32 [D]) = sum over rows of dy * xh,
  * through a workspace of llattn_rmsnorm_workspace_size(M, D) bytes, added in a
  * fixed order (deterministic, no atomics).  Replaces the autograd backward of
- * the reference RMSNorm (reference models.py:40-47). */
+ * the reference RMSNorm (reference models.py:40-47).  dres (x's dtype, may be
+ * null; dx may be dres itself): the gradient reaching the norm's input through
+ * the residual path, added to dx -- the backward of the fused residual add. */
 size_t llattn_rmsnorm_workspace_size(int32_t M, int32_t D);
 int32_t llattn_rmsnorm_bwd(const void* dy, int32_t dy_dtype, int64_t lddy, const void* x, int32_t x_dtype,
                            int64_t ldx, const float* rstd, const float* weight, int32_t M, int32_t D, void* dx,
-                           int64_t lddx, float* dweight, void* workspace, size_t workspace_bytes, void* stream);
+                           int64_t lddx, float* dweight, const void* dres, int64_t lddres, void* workspace,
+                           size_t workspace_bytes, void* stream);
 
 /* Cross entropy of bf16 logit rows and its gradient in one pass (the tied LM
  * head's loss, reference train.py:354-370: F.cross_entropy over [B*T, V]

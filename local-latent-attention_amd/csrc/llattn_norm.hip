@@ -46,9 +46,11 @@ __device__ __forceinline__ void st4(T* p, const float v[4]) {
 
 // NCH: 4-element chunks per lane (D <= 256 NCH)
 template <typename XT, typename YT, int NCH>
-__global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const XT* __restrict__ x, int64_t ldx,
+__global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const XT* x, int64_t ldx,
                                                           const float* __restrict__ w, int M, int D, float eps,
-                                                          YT* __restrict__ y, int64_t ldy, float* __restrict__ rstd) {
+                                                          YT* __restrict__ y, int64_t ldy, float* __restrict__ rstd,
+                                                          const void* res, int r_bf16, int64_t ldr, float* xo,
+                                                          int64_t ldxo) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= M) return;  // wave-uniform
@@ -61,6 +63,14 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const XT* __restrict__
     const int c = lane + 64 * i;
     if (c < nq) {
       ld4(xr + 4 * c, v[i]);
+      if (res) {  // residual add first (fp32, as x + res promotes): the normalised rows are those of the sum
+        float rv[4];
+        if (r_bf16) ld4(static_cast<const uint16_t*>(res) + (int64_t)row * ldr + 4 * c, rv);
+        else ld4(static_cast<const float*>(res) + (int64_t)row * ldr + 4 * c, rv);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[i][e] += rv[e];
+        st4(xo + (int64_t)row * ldxo + 4 * c, v[i]);
+      }
     } else {
       v[i][0] = v[i][1] = v[i][2] = v[i][3] = 0.f;
     }
@@ -88,7 +98,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const DYT* __restrict_
                                                           const float* __restrict__ rstd,
                                                           const float* __restrict__ w, int M, int D,
                                                           XT* __restrict__ dx, int64_t lddx,
-                                                          float* __restrict__ part) {
+                                                          float* __restrict__ part, const XT* dres, int64_t lddres) {
   extern __shared__ float red[];  // [4][D]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nq = D >> 2;
@@ -127,6 +137,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const DYT* __restrict_
       }
     }
   };
+  const int64_t ldo = lddx, ldr = lddres;
   // xh = x * rstd and g = dy * w are formed twice (for the row dot product, then for dx) rather than kept
   auto do_row = [&](int row, const float (&xv)[NCH][4], const float (&dv)[NCH][4], const float r) {
     float dot = 0.f;
@@ -135,7 +146,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const DYT* __restrict_
 #pragma unroll
       for (int e = 0; e < 4; ++e) dot += (dv[i][e] * wv[i][e]) * (xv[i][e] * r);
     const float mdot = wave_sum(dot) * inv_d;
-    XT* o = dx + (int64_t)row * lddx;
+    XT* o = dx + (int64_t)row * ldo;
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
       const int c = lane + 64 * i;
@@ -146,7 +157,15 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const DYT* __restrict_
         v[e] = r * (dv[i][e] * wv[i][e] - xh * mdot);
         dw[i][e] += dv[i][e] * xh;
       }
-      if (c < nq) st4(o + 4 * c, v);
+      if (c < nq) {
+        if (dres) {  // the gradient that reaches the normalised rows' input through the residual path
+          float g[4];
+          ld4(dres + (int64_t)row * ldr + 4 * c, g);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] += g[e];
+        }
+        st4(o + 4 * c, v);
+      }
     }
   };
   float xa[NCH][4], da[NCH][4], ra = 0.f;
@@ -211,35 +230,36 @@ int chunks_for(int D) {  // 4-element chunks per lane, rounded up to a compiled 
 
 template <typename XT, typename YT>
 void launch_fwd(int nch, const void* x, int64_t ldx, const float* w, int M, int D, float eps, void* y, int64_t ldy,
-                float* rstd, hipStream_t st) {
+                float* rstd, const void* r, int r_bf16, int64_t ldr, float* xo, int64_t ldxo, hipStream_t st) {
   const dim3 grid((M + 3) / 4), block(256);
   const XT* xp = static_cast<const XT*>(x);
   YT* yp = static_cast<YT*>(y);
   switch (nch) {
-    case 2: hipLaunchKernelGGL((rmsnorm_fwd_kernel<XT, YT, 2>), grid, block, 0, st, xp, ldx, w, M, D, eps, yp, ldy, rstd); break;
-    case 4: hipLaunchKernelGGL((rmsnorm_fwd_kernel<XT, YT, 4>), grid, block, 0, st, xp, ldx, w, M, D, eps, yp, ldy, rstd); break;
-    case 6: hipLaunchKernelGGL((rmsnorm_fwd_kernel<XT, YT, 6>), grid, block, 0, st, xp, ldx, w, M, D, eps, yp, ldy, rstd); break;
-    case 8: hipLaunchKernelGGL((rmsnorm_fwd_kernel<XT, YT, 8>), grid, block, 0, st, xp, ldx, w, M, D, eps, yp, ldy, rstd); break;
-    case 12: hipLaunchKernelGGL((rmsnorm_fwd_kernel<XT, YT, 12>), grid, block, 0, st, xp, ldx, w, M, D, eps, yp, ldy, rstd); break;
-    default: hipLaunchKernelGGL((rmsnorm_fwd_kernel<XT, YT, 16>), grid, block, 0, st, xp, ldx, w, M, D, eps, yp, ldy, rstd); break;
+    case 2: hipLaunchKernelGGL((rmsnorm_fwd_kernel<XT, YT, 2>), grid, block, 0, st, xp, ldx, w, M, D, eps, yp, ldy, rstd, r, r_bf16, ldr, xo, ldxo); break;
+    case 4: hipLaunchKernelGGL((rmsnorm_fwd_kernel<XT, YT, 4>), grid, block, 0, st, xp, ldx, w, M, D, eps, yp, ldy, rstd, r, r_bf16, ldr, xo, ldxo); break;
+    case 6: hipLaunchKernelGGL((rmsnorm_fwd_kernel<XT, YT, 6>), grid, block, 0, st, xp, ldx, w, M, D, eps, yp, ldy, rstd, r, r_bf16, ldr, xo, ldxo); break;
+    case 8: hipLaunchKernelGGL((rmsnorm_fwd_kernel<XT, YT, 8>), grid, block, 0, st, xp, ldx, w, M, D, eps, yp, ldy, rstd, r, r_bf16, ldr, xo, ldxo); break;
+    case 12: hipLaunchKernelGGL((rmsnorm_fwd_kernel<XT, YT, 12>), grid, block, 0, st, xp, ldx, w, M, D, eps, yp, ldy, rstd, r, r_bf16, ldr, xo, ldxo); break;
+    default: hipLaunchKernelGGL((rmsnorm_fwd_kernel<XT, YT, 16>), grid, block, 0, st, xp, ldx, w, M, D, eps, yp, ldy, rstd, r, r_bf16, ldr, xo, ldxo); break;
   }
 }
 
 template <typename XT, typename DYT>
 void launch_bwd(int nch, int nblk, const void* dy, int64_t lddy, const void* x, int64_t ldx, const float* rstd,
-                const float* w, int M, int D, void* dx, int64_t lddx, float* part, hipStream_t st) {
+                const float* w, int M, int D, void* dx, int64_t lddx, float* part, const void* dres, int64_t lddres,
+                hipStream_t st) {
   const dim3 grid(nblk), block(256);
   const size_t lds = (size_t)4 * D * sizeof(float);
   const DYT* dyp = static_cast<const DYT*>(dy);
   const XT* xp = static_cast<const XT*>(x);
   XT* dxp = static_cast<XT*>(dx);
   switch (nch) {
-    case 2: hipLaunchKernelGGL((rmsnorm_bwd_kernel<XT, DYT, 2>), grid, block, lds, st, dyp, lddy, xp, ldx, rstd, w, M, D, dxp, lddx, part); break;
-    case 4: hipLaunchKernelGGL((rmsnorm_bwd_kernel<XT, DYT, 4>), grid, block, lds, st, dyp, lddy, xp, ldx, rstd, w, M, D, dxp, lddx, part); break;
-    case 6: hipLaunchKernelGGL((rmsnorm_bwd_kernel<XT, DYT, 6>), grid, block, lds, st, dyp, lddy, xp, ldx, rstd, w, M, D, dxp, lddx, part); break;
-    case 8: hipLaunchKernelGGL((rmsnorm_bwd_kernel<XT, DYT, 8>), grid, block, lds, st, dyp, lddy, xp, ldx, rstd, w, M, D, dxp, lddx, part); break;
-    case 12: hipLaunchKernelGGL((rmsnorm_bwd_kernel<XT, DYT, 12>), grid, block, lds, st, dyp, lddy, xp, ldx, rstd, w, M, D, dxp, lddx, part); break;
-    default: hipLaunchKernelGGL((rmsnorm_bwd_kernel<XT, DYT, 16>), grid, block, lds, st, dyp, lddy, xp, ldx, rstd, w, M, D, dxp, lddx, part); break;
+    case 2: hipLaunchKernelGGL((rmsnorm_bwd_kernel<XT, DYT, 2>), grid, block, lds, st, dyp, lddy, xp, ldx, rstd, w, M, D, dxp, lddx, part, static_cast<const XT*>(dres), lddres); break;
+    case 4: hipLaunchKernelGGL((rmsnorm_bwd_kernel<XT, DYT, 4>), grid, block, lds, st, dyp, lddy, xp, ldx, rstd, w, M, D, dxp, lddx, part, static_cast<const XT*>(dres), lddres); break;
+    case 6: hipLaunchKernelGGL((rmsnorm_bwd_kernel<XT, DYT, 6>), grid, block, lds, st, dyp, lddy, xp, ldx, rstd, w, M, D, dxp, lddx, part, static_cast<const XT*>(dres), lddres); break;
+    case 8: hipLaunchKernelGGL((rmsnorm_bwd_kernel<XT, DYT, 8>), grid, block, lds, st, dyp, lddy, xp, ldx, rstd, w, M, D, dxp, lddx, part, static_cast<const XT*>(dres), lddres); break;
+    case 12: hipLaunchKernelGGL((rmsnorm_bwd_kernel<XT, DYT, 12>), grid, block, lds, st, dyp, lddy, xp, ldx, rstd, w, M, D, dxp, lddx, part, static_cast<const XT*>(dres), lddres); break;
+    default: hipLaunchKernelGGL((rmsnorm_bwd_kernel<XT, DYT, 16>), grid, block, lds, st, dyp, lddy, xp, ldx, rstd, w, M, D, dxp, lddx, part, static_cast<const XT*>(dres), lddres); break;
   }
 }
 
@@ -267,20 +287,29 @@ using namespace llattn;
 
 extern "C" int32_t llattn_rmsnorm_fwd(const void* x, int32_t x_dtype, int64_t ldx, const float* weight, int32_t M,
                                       int32_t D, float eps, void* y, int32_t y_dtype, int64_t ldy, float* rstd,
+                                      const void* res, int32_t res_dtype, int64_t ldres, float* xsum, int64_t ldxsum,
                                       void* stream) {
   const char* what = "llattn_rmsnorm_fwd";
   int32_t rc;
   if ((rc = check_dims(what, M, D)) || (rc = check_rows(what, "x", x, ldx, x_dtype, D)) ||
       (rc = check_rows(what, "y", y, ldy, y_dtype, D)))
     return rc;
+  if (res) {
+    if (x_dtype != LLATTN_F32)
+      return fail(LLATTN_ERR_DTYPE, "%s: a residual addend needs fp32 x (the sum is kept in fp32)", what);
+    if ((rc = check_rows(what, "res", res, ldres, res_dtype, D)) ||
+        (rc = check_rows(what, "xsum", xsum, ldxsum, LLATTN_F32, D)))
+      return rc;
+  }
   if (!weight || !aligned16(weight) || !rstd)
     return fail(LLATTN_ERR_LAYOUT, "%s: weight (16-byte aligned fp32 [D]) and rstd (fp32 [M]) are required", what);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int nch = chunks_for(D);
-  if (x_dtype == LLATTN_F32 && y_dtype == LLATTN_F32) launch_fwd<float, float>(nch, x, ldx, weight, M, D, eps, y, ldy, rstd, st);
-  else if (x_dtype == LLATTN_F32) launch_fwd<float, uint16_t>(nch, x, ldx, weight, M, D, eps, y, ldy, rstd, st);
-  else if (y_dtype == LLATTN_F32) launch_fwd<uint16_t, float>(nch, x, ldx, weight, M, D, eps, y, ldy, rstd, st);
-  else launch_fwd<uint16_t, uint16_t>(nch, x, ldx, weight, M, D, eps, y, ldy, rstd, st);
+  const int rb = res && res_dtype == LLATTN_BF16;
+  if (x_dtype == LLATTN_F32 && y_dtype == LLATTN_F32) launch_fwd<float, float>(nch, x, ldx, weight, M, D, eps, y, ldy, rstd, res, rb, ldres, xsum, ldxsum, st);
+  else if (x_dtype == LLATTN_F32) launch_fwd<float, uint16_t>(nch, x, ldx, weight, M, D, eps, y, ldy, rstd, res, rb, ldres, xsum, ldxsum, st);
+  else if (y_dtype == LLATTN_F32) launch_fwd<uint16_t, float>(nch, x, ldx, weight, M, D, eps, y, ldy, rstd, nullptr, 0, 0, nullptr, 0, st);
+  else launch_fwd<uint16_t, uint16_t>(nch, x, ldx, weight, M, D, eps, y, ldy, rstd, nullptr, 0, 0, nullptr, 0, st);
   return check_launch(what);
 }
 
@@ -291,13 +320,14 @@ extern "C" size_t llattn_rmsnorm_workspace_size(int32_t M, int32_t D) {
 
 extern "C" int32_t llattn_rmsnorm_bwd(const void* dy, int32_t dy_dtype, int64_t lddy, const void* x, int32_t x_dtype,
                                       int64_t ldx, const float* rstd, const float* weight, int32_t M, int32_t D,
-                                      void* dx, int64_t lddx, float* dweight, void* workspace, size_t workspace_bytes,
-                                      void* stream) {
+                                      void* dx, int64_t lddx, float* dweight, const void* dres, int64_t lddres,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
   const char* what = "llattn_rmsnorm_bwd";
   int32_t rc;
   if ((rc = check_dims(what, M, D)) || (rc = check_rows(what, "dy", dy, lddy, dy_dtype, D)) ||
       (rc = check_rows(what, "x", x, ldx, x_dtype, D)) || (rc = check_rows(what, "dx", dx, lddx, x_dtype, D)))
     return rc;
+  if (dres && (rc = check_rows(what, "dres", dres, lddres, x_dtype, D))) return rc;
   if (!weight || !aligned16(weight) || !rstd || !dweight)
     return fail(LLATTN_ERR_LAYOUT, "%s: weight (16-byte aligned fp32 [D]), rstd and dweight are required", what);
   const size_t need = llattn_rmsnorm_workspace_size(M, D);
@@ -306,10 +336,10 @@ extern "C" int32_t llattn_rmsnorm_bwd(const void* dy, int32_t dy_dtype, int64_t 
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int nch = chunks_for(D);
   float* part = static_cast<float*>(workspace);
-  if (x_dtype == LLATTN_F32 && dy_dtype == LLATTN_F32) launch_bwd<float, float>(nch, kBwdBlocks, dy, lddy, x, ldx, rstd, weight, M, D, dx, lddx, part, st);
-  else if (x_dtype == LLATTN_F32) launch_bwd<float, uint16_t>(nch, kBwdBlocks, dy, lddy, x, ldx, rstd, weight, M, D, dx, lddx, part, st);
-  else if (dy_dtype == LLATTN_F32) launch_bwd<uint16_t, float>(nch, kBwdBlocks, dy, lddy, x, ldx, rstd, weight, M, D, dx, lddx, part, st);
-  else launch_bwd<uint16_t, uint16_t>(nch, kBwdBlocks, dy, lddy, x, ldx, rstd, weight, M, D, dx, lddx, part, st);
+  if (x_dtype == LLATTN_F32 && dy_dtype == LLATTN_F32) launch_bwd<float, float>(nch, kBwdBlocks, dy, lddy, x, ldx, rstd, weight, M, D, dx, lddx, part, dres, lddres, st);
+  else if (x_dtype == LLATTN_F32) launch_bwd<float, uint16_t>(nch, kBwdBlocks, dy, lddy, x, ldx, rstd, weight, M, D, dx, lddx, part, dres, lddres, st);
+  else if (dy_dtype == LLATTN_F32) launch_bwd<uint16_t, float>(nch, kBwdBlocks, dy, lddy, x, ldx, rstd, weight, M, D, dx, lddx, part, dres, lddres, st);
+  else launch_bwd<uint16_t, uint16_t>(nch, kBwdBlocks, dy, lddy, x, ldx, rstd, weight, M, D, dx, lddx, part, dres, lddres, st);
   hipLaunchKernelGGL(rmsnorm_dw_kernel, dim3((D + 63) / 64), dim3(256), 0, st, part, kBwdBlocks, D, dweight);
   return check_launch(what);
 }

@@ -16,7 +16,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libllattn_gfx950.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 OK, ERR_SHAPE, ERR_DTYPE, ERR_LAYOUT, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_LAUNCH = range(7)
 F32, BF16 = 0, 1
@@ -72,9 +72,11 @@ SIGNATURES = {
     "llattn_colsum_workspace_size": (_SZ, [_I32, _I32]),
     "llattn_colsum": (_I32, [_P, _I64, _I32, _I32, _P, _P, _SZ, _P]),
     "llattn_cast": (_I32, [_I32, _P, _P, _P, _P, _P]),
-    "llattn_rmsnorm_fwd": (_I32, [_P, _I32, _I64, _P, _I32, _I32, ctypes.c_float, _P, _I32, _I64, _P, _P]),
+    "llattn_rmsnorm_fwd": (_I32, [_P, _I32, _I64, _P, _I32, _I32, ctypes.c_float, _P, _I32, _I64, _P, _P, _I32, _I64,
+                                  _P, _I64, _P]),
     "llattn_rmsnorm_workspace_size": (_SZ, [_I32, _I32]),
-    "llattn_rmsnorm_bwd": (_I32, [_P, _I32, _I64, _P, _I32, _I64, _P, _P, _I32, _I32, _P, _I64, _P, _P, _SZ, _P]),
+    "llattn_rmsnorm_bwd": (_I32, [_P, _I32, _I64, _P, _I32, _I64, _P, _P, _I32, _I32, _P, _I64, _P, _P, _I64, _P, _SZ,
+                                  _P]),
     "llattn_xent": (_I32, [_P, _I64, _I32, _I32, _P, _I64, _P, _P, _P, _I64, _P, _P]),
 }
 

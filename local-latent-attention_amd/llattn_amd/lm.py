@@ -30,7 +30,7 @@ import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint
 
 from .config import MODEL_PRESETS, ModelConfig, build_attention
-from .norm import rms_norm
+from .norm import add_rms_norm, rms_norm
 
 
 class RMSNorm(nn.Module):
@@ -83,6 +83,7 @@ class LocalLatentLM(nn.Module):
         super().__init__()
         self.config = config
         self.checkpoint_blocks = config.checkpoint_blocks
+        self.fuse_residual_norms = True  # residual adds inside the next norm (same values, fewer passes)
         factory = attention_factory or build_attention
         norm = norm_factory or RMSNorm
         self.embedding = nn.Embedding(config.vocab_size, config.d_model)
@@ -132,6 +133,8 @@ class LocalLatentLM(nn.Module):
         _, seq_len = input_ids.shape
         pos = torch.arange(seq_len, device=input_ids.device)
         x = self.embedding(input_ids) + self.position(pos).unsqueeze(0)
+        if self._fused_norms(x):
+            return self._hidden_fused(x)
         for block in self.blocks:
             if self.checkpoint_blocks and self.training:
                 x = checkpoint(block, x, use_reentrant=False)
@@ -141,6 +144,25 @@ class LocalLatentLM(nn.Module):
 
     def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
         return self.lm_head(self.hidden(input_ids))
+
+    def _fused_norms(self, x: torch.Tensor) -> bool:
+        """Whether each residual add runs inside the following norm (:func:`~llattn_amd.norm.add_rms_norm`): all
+        norms are this module's GPU RMSNorm, the stream is fp32 and blocks are not checkpointed one by one."""
+        if not self.fuse_residual_norms or not len(self.blocks) or (self.checkpoint_blocks and self.training):
+            return False
+        norms = [self.norm] + [m for b in self.blocks for m in (b.norm1, b.norm2)]
+        return x.is_cuda and x.dtype == torch.float32 and all(type(n) is RMSNorm for n in norms)
+
+    def _hidden_fused(self, x: torch.Tensor) -> torch.Tensor:
+        # x_{i+1} = x_i + attn(norm1(x_i)) + ff(norm2(...)) as in TransformerBlock.forward, with each sum formed by
+        # the norm that reads it: norm2 of the same block, then norm1 of the next block (the final norm last)
+        blocks = list(self.blocks)
+        h = blocks[0].norm1(x)
+        for i, blk in enumerate(blocks):
+            x, h2 = add_rms_norm(x, blk.attn(h), blk.norm2.weight, blk.norm2.eps)
+            nxt = blocks[i + 1].norm1 if i + 1 < len(blocks) else self.norm
+            x, h = add_rms_norm(x, blk.ff(h2), nxt.weight, nxt.eps)
+        return h
 
     def loss(self, input_ids: torch.Tensor, targets: torch.Tensor, chunk_rows: int = 8192):
         """:func:`lm_loss` of ``self(input_ids)`` without the ``[B*T, V]`` logits: the tied head and the cross

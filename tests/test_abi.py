@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_empty_error():
     L, lib = _lib()
-    assert lib.llattn_abi_version() == L.ABI_VERSION == 4
+    assert lib.llattn_abi_version() == L.ABI_VERSION == 5
 
 
 def _shape(L, **kw):
@@ -268,23 +268,31 @@ def test_rmsnorm_validation():
     L, lib = _lib()
     buf = ctypes.c_void_p(1 << 20)  # never dereferenced: every call below fails validation first
     f32, bf = L.F32, L.BF16
-    rc = lib.llattn_rmsnorm_fwd(buf, f32, 64, buf, 4, 62, 1e-6, buf, bf, 64, buf, None)
+    rc = lib.llattn_rmsnorm_fwd(buf, f32, 64, buf, 4, 62, 1e-6, buf, bf, 64, buf, None, 0, 0, None, 0, None)
     assert rc == L.ERR_UNSUPPORTED and b"multiple of 4" in lib.llattn_last_error()
-    rc = lib.llattn_rmsnorm_fwd(buf, f32, 8192, buf, 4, 8192, 1e-6, buf, bf, 8192, buf, None)
+    rc = lib.llattn_rmsnorm_fwd(buf, f32, 8192, buf, 4, 8192, 1e-6, buf, bf, 8192, buf, None, 0, 0, None, 0, None)
     assert rc == L.ERR_UNSUPPORTED and b"at most 4096" in lib.llattn_last_error()
-    rc = lib.llattn_rmsnorm_fwd(buf, 7, 64, buf, 4, 64, 1e-6, buf, bf, 64, buf, None)
+    rc = lib.llattn_rmsnorm_fwd(buf, 7, 64, buf, 4, 64, 1e-6, buf, bf, 64, buf, None, 0, 0, None, 0, None)
     assert rc == L.ERR_DTYPE
-    rc = lib.llattn_rmsnorm_fwd(buf, f32, 60, buf, 4, 64, 1e-6, buf, bf, 64, buf, None)
+    rc = lib.llattn_rmsnorm_fwd(buf, f32, 60, buf, 4, 64, 1e-6, buf, bf, 64, buf, None, 0, 0, None, 0, None)
     assert rc == L.ERR_LAYOUT and b"ld >= D" in lib.llattn_last_error()
-    rc = lib.llattn_rmsnorm_fwd(None, f32, 64, buf, 4, 64, 1e-6, buf, bf, 64, buf, None)
+    rc = lib.llattn_rmsnorm_fwd(None, f32, 64, buf, 4, 64, 1e-6, buf, bf, 64, buf, None, 0, 0, None, 0, None)
     assert rc == L.ERR_LAYOUT
-    rc = lib.llattn_rmsnorm_fwd(buf, f32, 64, buf, 0, 64, 1e-6, buf, bf, 64, buf, None)
+    rc = lib.llattn_rmsnorm_fwd(buf, f32, 64, buf, 0, 64, 1e-6, buf, bf, 64, buf, None, 0, 0, None, 0, None)
     assert rc == L.ERR_SHAPE
     need = lib.llattn_rmsnorm_workspace_size(32768, 1408)
     assert need > 0 and need % (1408 * 4) == 0
-    rc = lib.llattn_rmsnorm_bwd(buf, bf, 1408, buf, f32, 1408, buf, buf, 32768, 1408, buf, 1408, buf, buf, need - 4,
-                                None)
+    rc = lib.llattn_rmsnorm_bwd(buf, bf, 1408, buf, f32, 1408, buf, buf, 32768, 1408, buf, 1408, buf, None, 0, buf,
+                                need - 4, None)
     assert rc == L.ERR_WORKSPACE and b"workspace" in lib.llattn_last_error()
+    rc = lib.llattn_rmsnorm_bwd(buf, bf, 1408, buf, f32, 1408, buf, buf, 32768, 1408, buf, 1408, buf,
+                                ctypes.c_void_p((1 << 20) + 4), 1408, buf, need, None)
+    assert rc == L.ERR_LAYOUT and b"dres" in lib.llattn_last_error()
+    # the fused residual add needs an fp32 stream and an aligned fp32 sum
+    rc = lib.llattn_rmsnorm_fwd(buf, bf, 64, buf, 4, 64, 1e-6, buf, bf, 64, buf, buf, bf, 64, buf, 64, None)
+    assert rc == L.ERR_DTYPE and b"residual" in lib.llattn_last_error()
+    rc = lib.llattn_rmsnorm_fwd(buf, f32, 64, buf, 4, 64, 1e-6, buf, bf, 64, buf, buf, bf, 64, None, 64, None)
+    assert rc == L.ERR_LAYOUT and b"xsum" in lib.llattn_last_error()
 
 
 def test_resolve_layout_matches_reference_rules():

@@ -76,3 +76,61 @@ def test_rms_norm_autocast_output_dtype():
     with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
         y = rms_norm(x, w, 1e-6)
     assert y.dtype == torch.bfloat16 and y.shape == x.shape
+
+
+@pytest.mark.parametrize("M,D", [(7, 64), (513, 1000), (2048, 1408)])
+@pytest.mark.parametrize("rdt", [torch.float32, torch.bfloat16])
+def test_add_rms_norm_matches_torch(M, D, rdt):
+    """Fused residual add + norm: s = x + res and y = rms_norm(s) forward; the backward with gradients arriving at
+    both s (the residual stream) and y, against float64 autograd of the unfused ops."""
+    print(f"add_rms_norm M={M} D={D} res={rdt}", flush=True)
+    from llattn_amd.norm import add_rms_norm
+    dev = require_cuda()
+    g = torch.Generator(device="cpu").manual_seed(M + D)
+    x = torch.randn(M, D, generator=g).to(dev)
+    r = torch.randn(M, D, generator=g).to(dev).to(rdt)
+    w = (1 + 0.1 * torch.randn(D, generator=g)).to(dev)
+    ds, dy = torch.randn(M, D, generator=g).to(dev), torch.randn(M, D, generator=g).to(dev)
+    xg, rg, wg = x.clone().requires_grad_(True), r.clone().requires_grad_(True), w.clone().requires_grad_(True)
+    s, y = add_rms_norm(xg, rg, wg, 1e-6)
+    (s * ds).sum().backward(retain_graph=True)
+    (y * dy).sum().backward()
+    xd, rd, wd = (t.detach().double().requires_grad_(True) for t in (x, r.float(), w))
+    sd = xd + rd
+    yd = F.rms_norm(sd, (D,), wd, 1e-6)
+    ((sd * ds.double()).sum() + (yd * dy.double()).sum()).backward()
+    assert s.dtype == torch.float32 and y.dtype == torch.float32
+    c = lambda t: t.detach().float().cpu()  # noqa: E731
+    assert_fp32_close(c(s), c(sd))
+    assert_fp32_close(c(y), c(yd))
+    assert_fp32_close(c(xg.grad), c(xd.grad))
+    if rdt == torch.float32:
+        assert_fp32_close(c(rg.grad), c(rd.grad))
+    else:
+        assert rg.grad.dtype == torch.bfloat16
+        assert_bf16_close(c(rg.grad), c(rd.grad))
+    assert_fp32_close(c(wg.grad), c(wd.grad))
+
+
+def test_lm_fused_residual_norms_match_unfused():
+    """The LM with every residual add inside the following norm gives the same loss and gradients as the
+    unfused block order (same kernels, same fp32 sums): bitwise, forward and backward."""
+    from llattn_amd.lm import build_model
+    dev = require_cuda()
+    torch.manual_seed(0)
+    kw = dict(vocab_size=512, max_seq_len=256, d_model=192, n_heads=2, n_layers=2, d_ff=384, local_window=32,
+              local_block_size=64, latent_tokens=8, latent_d_model=64, latent_heads=2)
+    model = build_model(**kw).to(dev)
+    inputs = torch.randint(0, 512, (2, 256), device=dev)
+    targets = torch.randint(0, 512, (2, 256), device=dev)
+    runs = []
+    for fused in (True, False):
+        model.fuse_residual_norms = fused
+        model.zero_grad(set_to_none=True)
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+            loss, _ = model.loss(inputs, targets)
+            loss.backward()
+        runs.append((loss.detach(), {n: p.grad.clone() for n, p in model.named_parameters()}))
+    assert torch.equal(runs[0][0], runs[1][0])
+    for n, g in runs[0][1].items():
+        assert torch.equal(g, runs[1][1][n]), n
