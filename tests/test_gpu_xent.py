@@ -138,3 +138,31 @@ def test_model_loss_matches_logits_path():
     for n, p in model.named_parameters():
         err = (g1[n] - p.grad).abs().max() / p.grad.abs().max().clamp(min=1e-30)
         assert err < 5e-2, (n, float(err))
+
+
+def test_xent_smallest_vocab_and_single_row():
+    xent = _xent()
+    x = torch.tensor([[0.5, -1.0, 2.0, 2.0, 0.0, -3.0, 1.5, 2.0]], device=DEV).to(torch.bfloat16)
+    t = torch.tensor([6], device=DEV)
+    scale = torch.tensor(1.0, device=DEV)
+    d = torch.empty_like(x)
+    loss, pred = xent.xent_rows(x, t, grad_scale=scale, dlogits=d)
+    lo, po, go = cross_entropy_rows(x.float().cpu().numpy(), t.cpu().numpy())
+    assert int(pred[0]) == 2 == int(po[0])  # three-way tie at 2.0: the first index
+    assert float(loss[0]) == pytest.approx(float(lo[0]), rel=1e-6)
+    np.testing.assert_allclose(d.float().cpu().numpy(), go, rtol=8e-3, atol=1e-3)
+
+
+def test_lm_head_loss_all_rows_ignored_and_chunk_rounding():
+    """Every target ignored: NaN loss (as torch's mean over no rows) and zero gradients; a chunk size that is
+    not a multiple of 64 is rounded down to one."""
+    xent = _xent()
+    h = torch.randn(130, 64, device=DEV).to(torch.bfloat16).requires_grad_(True)
+    w = (torch.randn(128, 64, device=DEV) * 0.05).requires_grad_(True)
+    t = torch.full((130,), -100, device=DEV)
+    loss, _ = xent.lm_head_loss(h, w, t, chunk_rows=100)
+    loss.backward()
+    assert torch.isnan(loss)
+    assert not h.grad.any() and not w.grad.any()
+    ref = torch.nn.functional.cross_entropy(torch.randn(130, 128), t.cpu())
+    assert torch.isnan(ref)
