@@ -38,7 +38,7 @@ struct LatentArgs {
   float* part;  // workspace [B][Lh][n_seg][n_lt*16][2][Ldh]
 };
 
-constexpr int kSeg = 512;  // queries per segment of the latent-stationary pass
+constexpr int kSeg = 256;  // queries per segment of the latent-stationary pass
 
 // number of latents visible to latent query s
 __device__ __forceinline__ int visible(int s, const LatentArgs& a) {
