@@ -151,6 +151,26 @@ int32_t llattn_local_gate_bwd(const llattn_shape* s, const llattn_tensor* q, con
                               float* dgate_l, float* dgate_r, float* dremote_colsum, void* workspace,
                               size_t workspace_bytes, void* stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): llattn_local_gate_bwd with the same arguments and
+ * results, minus the workspace.  Its scratch is a library-owned device array
+ * of LLATTN_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends): the
+ * gate partial sums, H*3*Dh*rows fp32 (rows = B * query segments for the
+ * fused bf16 backward, W <= 64; B * ceil(T/64) otherwise), plus dO_local and
+ * D (B*T*H*Dh elements, B*H*T fp32) for the two-kernel backward.  A shape
+ * that needs more returns LLATTN_ERR_WORKSPACE.  Calls share their GPU's
+ * array, so two calls that overlap on one GPU (different streams, threads or
+ * processes) race; calls on one stream are ordered.  Allocates nothing. */
+#define LLATTN_NOALLOC_SCRATCH_BYTES (8u << 20)
+int32_t llattn_local_gate_bwd_noalloc(const llattn_shape* s, const llattn_tensor* q, const llattn_tensor* k,
+                                      const llattn_tensor* v, const llattn_tensor* remote, const float* gate_l,
+                                      const float* gate_r, const llattn_tensor* o_local, const float* lse,
+                                      const float* w, const llattn_tensor* dy, const llattn_tensor* dq,
+                                      const llattn_tensor* dk, const llattn_tensor* dv,
+                                      const llattn_tensor* dremote, float* dgate_l, float* dgate_r,
+                                      float* dremote_colsum, void* stream);
+
 /* Projection GEMM on bf16 MFMA: C[m][n] = sum_k A(m,k) B(n,k) (+ bias[n])
  * (+ C[m][n] when accumulate).  A and B are bf16; each is stored
  * k-contiguous (A[M][K] / B[N][K], trans = 0) or m/n-contiguous

@@ -14,6 +14,7 @@
 #include "llattn_device.h"
 
 #include <climits>
+#include <mutex>
 
 namespace llattn {
 
@@ -1005,6 +1006,88 @@ extern "C" int32_t llattn_local_gate_fwd(const llattn_shape* s, const llattn_ten
   return check_launch("llattn_local_gate_fwd");
 }
 
+namespace llattn {
+namespace {
+
+// Scratch of llattn_local_gate_bwd_noalloc: one copy per GPU, held from module load until the
+// process ends.  Host code never passes the array's name to a kernel (on the host it is only a
+// stand-in for the symbol); it passes the device address that hipGetSymbolAddress returns for the
+// current device.
+static __device__ __align__(256) unsigned char scratch[LLATTN_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per device.
+int32_t scratch_on_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(LLATTN_ERR_LAUNCH, "llattn_local_gate_bwd_noalloc: no current HIP device (or more than %d)",
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(LLATTN_ERR_LAUNCH, "llattn_local_gate_bwd_noalloc: hipGetSymbolAddress(scratch) on device %d: %s",
+                  dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return LLATTN_OK;
+}
+
+// Argument checks and views of the backward; the scratch pointers are filled in by the caller.
+int32_t bwd_args(const llattn_shape* s, const llattn_tensor* q, const llattn_tensor* k, const llattn_tensor* v,
+                 const llattn_tensor* remote, const float* gate_l, const float* gate_r, const llattn_tensor* o_local,
+                 const float* lse, const float* w, const llattn_tensor* dy, const llattn_tensor* dq,
+                 const llattn_tensor* dk, const llattn_tensor* dv, const llattn_tensor* dremote, float* dgate_l,
+                 float* dgate_r, LocalArgs* a) {
+  int32_t rc = common_args(s, q, k, v, remote, gate_l, gate_r, a);
+  if (rc) return rc;
+  if ((rc = check_view("o_local", o_local, s->dtype, true)) || (rc = check_view("dy", dy, s->dtype, true)) ||
+      (rc = check_view("dq", dq, s->dtype, true)) || (rc = check_view("dk", dk, s->dtype, true)) ||
+      (rc = check_view("dv", dv, s->dtype, true)) || (rc = check_view("dremote", dremote, s->dtype, true)))
+    return rc;
+  if (!lse || !w || !dgate_l || !dgate_r) return fail(LLATTN_ERR_LAYOUT, "lse / w / dgate pointers must be non-null");
+  set_view(o_local, &a->ol, &a->o_sb, &a->o_st, &a->o_sh);
+  set_view(dy, &a->dy, &a->dy_sb, &a->dy_st, &a->dy_sh);
+  set_view(dq, &a->dq, &a->dq_sb, &a->dq_st, &a->dq_sh);
+  set_view(dk, &a->dk, &a->dk_sb, &a->dk_st, &a->dk_sh);
+  set_view(dv, &a->dv, &a->dv_sb, &a->dv_st, &a->dv_sh);
+  set_view(dremote, &a->dr, &a->dr_sb, &a->dr_st, &a->dr_sh);
+  a->lse = const_cast<float*>(lse);
+  a->w = const_cast<float*>(w);
+  return LLATTN_OK;
+}
+
+size_t up256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Gate partial rows: one per (batch, segment) from the fused kernel, one per (batch, query tile) otherwise.
+int gate_rows(const LocalArgs& a, int dtype) {
+  const int seg_tiles = fused_seg_tiles(a);
+  return fused_bwd(a, dtype, padded_head_dim(a.Dh)) ? a.B * ((a.n_qt + seg_tiles - 1) / seg_tiles) : a.B * a.n_qt;
+}
+
+// Launches the backward kernels and the ordered gate reduction; a.dO / a.Dsum / a.gpart are set.
+int32_t launch_bwd_all(const llattn_shape* s, const LocalArgs& a, float* dgate_l, float* dgate_r,
+                       float* dremote_colsum, hipStream_t st) {
+  const int dhp = padded_head_dim(s->Dh);
+  const bool ok =
+      s->dtype == LLATTN_F32 ? dispatch<float>(dhp, false, a, st) : dispatch<uint16_t>(dhp, false, a, st);
+  if (!ok) return fail(LLATTN_ERR_UNSUPPORTED, "head_dim %d unsupported", s->Dh);
+  const int nrow = gate_rows(a, s->dtype);
+  const int per_head = s->gate_per_head ? 1 : 0;
+  const int outs = 2 * (per_head ? s->H * s->Dh : s->Dh) + (dremote_colsum ? s->H * s->Dh : 0);
+  hipLaunchKernelGGL(gate_reduce_kernel, dim3((outs + 3) / 4), dim3(256), 0, st, a.gpart, dgate_l, dgate_r,
+                     dremote_colsum, s->H, s->Dh, nrow, per_head);
+  return LLATTN_OK;
+}
+
+}  // namespace
+}  // namespace llattn
+
 extern "C" int32_t llattn_local_gate_bwd(const llattn_shape* s, const llattn_tensor* q, const llattn_tensor* k,
                                          const llattn_tensor* v, const llattn_tensor* remote, const float* gate_l,
                                          const float* gate_r, const llattn_tensor* o_local, const float* lse,
@@ -1014,42 +1097,52 @@ extern "C" int32_t llattn_local_gate_bwd(const llattn_shape* s, const llattn_ten
                                          float* dremote_colsum, void* workspace, size_t workspace_bytes,
                                          void* stream) {
   LocalArgs a;
-  int32_t rc = common_args(s, q, k, v, remote, gate_l, gate_r, &a);
+  int32_t rc = bwd_args(s, q, k, v, remote, gate_l, gate_r, o_local, lse, w, dy, dq, dk, dv, dremote, dgate_l,
+                        dgate_r, &a);
   if (rc) return rc;
-  if ((rc = check_view("o_local", o_local, s->dtype, true)) || (rc = check_view("dy", dy, s->dtype, true)) ||
-      (rc = check_view("dq", dq, s->dtype, true)) || (rc = check_view("dk", dk, s->dtype, true)) ||
-      (rc = check_view("dv", dv, s->dtype, true)) || (rc = check_view("dremote", dremote, s->dtype, true)))
-    return rc;
-  if (!lse || !w || !dgate_l || !dgate_r) return fail(LLATTN_ERR_LAYOUT, "lse / w / dgate pointers must be non-null");
   const size_t need = llattn_workspace_size(s, LLATTN_WS_LOCAL_BWD);
   if (!workspace || workspace_bytes < need || !aligned16(workspace))
     return fail(LLATTN_ERR_WORKSPACE, "local backward needs %zu workspace bytes (got %zu)", need, workspace_bytes);
-  set_view(o_local, &a.ol, &a.o_sb, &a.o_st, &a.o_sh);
-  set_view(dy, &a.dy, &a.dy_sb, &a.dy_st, &a.dy_sh);
-  set_view(dq, &a.dq, &a.dq_sb, &a.dq_st, &a.dq_sh);
-  set_view(dk, &a.dk, &a.dk_sb, &a.dk_st, &a.dk_sh);
-  set_view(dv, &a.dv, &a.dv_sb, &a.dv_st, &a.dv_sh);
-  set_view(dremote, &a.dr, &a.dr_sb, &a.dr_st, &a.dr_sh);
-  a.lse = const_cast<float*>(lse);
-  a.w = const_cast<float*>(w);
-  auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
   char* ws = static_cast<char*>(workspace);
-  const size_t n_do = up((size_t)s->B * s->T * s->H * s->Dh * elem_size(s->dtype));
-  const size_t n_d = up((size_t)s->B * s->H * s->T * 4);
+  const size_t n_do = up256((size_t)s->B * s->T * s->H * s->Dh * elem_size(s->dtype));
+  const size_t n_d = up256((size_t)s->B * s->H * s->T * 4);
   a.dO = ws;
   a.Dsum = reinterpret_cast<float*>(ws + n_do);
   a.gpart = reinterpret_cast<float*>(ws + n_do + n_d);
-  const int dhp = padded_head_dim(s->Dh);
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool ok =
-      s->dtype == LLATTN_F32 ? dispatch<float>(dhp, false, a, st) : dispatch<uint16_t>(dhp, false, a, st);
-  if (!ok) return fail(LLATTN_ERR_UNSUPPORTED, "head_dim %d unsupported", s->Dh);
-  // gate partial rows: one per (batch, segment) from the fused kernel, one per (batch, query tile) otherwise
-  const int seg_tiles = fused_seg_tiles(a);
-  const int nrow = fused_bwd(a, s->dtype, dhp) ? s->B * ((a.n_qt + seg_tiles - 1) / seg_tiles) : s->B * a.n_qt;
-  const int per_head = s->gate_per_head ? 1 : 0;
-  const int outs = 2 * (per_head ? s->H * s->Dh : s->Dh) + (dremote_colsum ? s->H * s->Dh : 0);
-  hipLaunchKernelGGL(gate_reduce_kernel, dim3((outs + 3) / 4), dim3(256), 0, st, a.gpart, dgate_l, dgate_r,
-                     dremote_colsum, s->H, s->Dh, nrow, per_head);
+  if ((rc = launch_bwd_all(s, a, dgate_l, dgate_r, dremote_colsum, static_cast<hipStream_t>(stream)))) return rc;
   return check_launch("llattn_local_gate_bwd");
+}
+
+// The scratch holds only what the chosen kernels read and write: the gate partials for the fused
+// one-pass backward; dO_local and the row sums D as well for the two-kernel backward.  Every byte
+// the kernels read is written earlier in the same call, so nothing is cleared between calls.
+extern "C" int32_t llattn_local_gate_bwd_noalloc(const llattn_shape* s, const llattn_tensor* q,
+                                                 const llattn_tensor* k, const llattn_tensor* v,
+                                                 const llattn_tensor* remote, const float* gate_l,
+                                                 const float* gate_r, const llattn_tensor* o_local, const float* lse,
+                                                 const float* w, const llattn_tensor* dy, const llattn_tensor* dq,
+                                                 const llattn_tensor* dk, const llattn_tensor* dv,
+                                                 const llattn_tensor* dremote, float* dgate_l, float* dgate_r,
+                                                 float* dremote_colsum, void* stream) {
+  LocalArgs a;
+  int32_t rc = bwd_args(s, q, k, v, remote, gate_l, gate_r, o_local, lse, w, dy, dq, dk, dv, dremote, dgate_l,
+                        dgate_r, &a);
+  if (rc) return rc;
+  const bool fused = fused_bwd(a, s->dtype, padded_head_dim(s->Dh));
+  const size_t n_do = fused ? 0 : up256((size_t)s->B * s->T * s->H * s->Dh * elem_size(s->dtype));
+  const size_t n_d = fused ? 0 : up256((size_t)s->B * s->H * s->T * 4);
+  const size_t n_g = up256((size_t)s->H * 3 * s->Dh * gate_rows(a, s->dtype) * 4);
+  if (n_do + n_d + n_g > LLATTN_NOALLOC_SCRATCH_BYTES)
+    return fail(LLATTN_ERR_WORKSPACE,
+                "llattn_local_gate_bwd_noalloc: this shape needs %zu scratch bytes, more than the library's "
+                "%zu; call llattn_local_gate_bwd with a workspace instead",
+                n_do + n_d + n_g, (size_t)LLATTN_NOALLOC_SCRATCH_BYTES);
+  void* base = nullptr;
+  if ((rc = scratch_on_current_device(&base))) return rc;
+  char* ws = static_cast<char*>(base);
+  a.dO = fused ? nullptr : ws;
+  a.Dsum = fused ? nullptr : reinterpret_cast<float*>(ws + n_do);
+  a.gpart = reinterpret_cast<float*>(ws + n_do + n_d);
+  if ((rc = launch_bwd_all(s, a, dgate_l, dgate_r, dremote_colsum, static_cast<hipStream_t>(stream)))) return rc;
+  return check_launch("llattn_local_gate_bwd_noalloc");
 }

@@ -22,6 +22,7 @@ OK, ERR_SHAPE, ERR_DTYPE, ERR_LAYOUT, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_LAUNCH
 F32, BF16 = 0, 1
 DIV_COUNT, DIV_SEG, DIV_ONE = 0, 1, 2
 WS_LOCAL_BWD, WS_LATENT_BWD = 0, 1
+NOALLOC_SCRATCH_BYTES = 8 << 20  # LLATTN_NOALLOC_SCRATCH_BYTES
 
 _DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16}
 
@@ -67,6 +68,8 @@ SIGNATURES = {
     "llattn_local_gate_fwd": (_I32, [_S, _T, _T, _T, _T, _P, _P, _T, _T, _P, _P, _P]),
     "llattn_local_gate_bwd": (_I32, [_S, _T, _T, _T, _T, _P, _P, _T, _P, _P, _T, _T, _T, _T, _T, _P, _P, _P, _P, _SZ,
                                      _P]),
+    "llattn_local_gate_bwd_noalloc": (_I32, [_S, _T, _T, _T, _T, _P, _P, _T, _P, _P, _T, _T, _T, _T, _T, _P, _P, _P,
+                                             _P]),
     "llattn_gemm_workspace_size": (_SZ, [_G]),
     "llattn_gemm": (_I32, [_G, _P, _SZ, _P]),
     "llattn_colsum_workspace_size": (_SZ, [_I32, _I32]),

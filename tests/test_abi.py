@@ -24,7 +24,7 @@ def _declared_functions():
 def test_library_exports_every_declared_symbol():
     L, lib = _lib()
     names = _declared_functions()
-    assert len(names) == 18, names
+    assert len(names) == 19, names
     for n in names:
         assert hasattr(lib, n), n
         assert n in L.SIGNATURES, f"{n} has no ctypes signature"
@@ -114,6 +114,20 @@ def test_workspace_too_small_is_runtime_error():
     assert rc == L.ERR_WORKSPACE
     with pytest.raises(RuntimeError, match="workspace"):
         L.check(rc, "llattn_local_gate_bwd")
+
+
+def test_noalloc_backward_refuses_shapes_beyond_its_scratch():
+    """The two-kernel backward (window > 64) keeps dO_local in scratch: 1 x 8192 x 16 x 64 bf16 = 16 MiB is more
+    than the library's array, so the call fails before it touches a device."""
+    L, lib = _lib()
+    s = _shape(L, B=1, T=8192, H=16, Dh=64, window=512, block=512, chunk=64, n_chunks=128, n_q=8192)
+    t = L.LlattnTensor(ctypes.c_void_p(0x1000), 8192 * 3072, 3072, 64)
+    g = ctypes.c_void_p(0x2000)
+    rc = lib.llattn_local_gate_bwd_noalloc(ctypes.byref(s), *(ctypes.byref(t),) * 4, g, g, ctypes.byref(t), g, g,
+                                           *(ctypes.byref(t),) * 5, g, g, None, None)
+    assert rc == L.ERR_WORKSPACE
+    msg = lib.llattn_last_error()
+    assert b"scratch bytes" in msg and str(L.NOALLOC_SCRATCH_BYTES).encode() in msg
 
 
 def _gemm_desc(L, **kw):
