@@ -28,6 +28,11 @@
 // Split-K (for the weight gradients, whose M x N is small and K = tokens is
 // large): split s covers the 64-wide k steps [s*P/S, (s+1)*P/S) of P and writes fp32 partials; an
 // ordered reduction adds them (deterministic, no atomics).
+//
+// K need not be a multiple of the step: the last steps read zero past K.  Rows of an m/n-contiguous
+// operand past K lie beyond its buffer extent and read zero by themselves; a k-contiguous operand
+// (K a multiple of 8) masks the lanes whose 8 k values start at or past K with an out-of-range
+// offset (kmask), so no lane reads the next row's elements.
 #include <type_traits>
 
 #include "llattn_abi.h"
@@ -45,7 +50,7 @@ constexpr int DMA_PER_STEP = 2 * DMA_PER_TILE;       // per wave
 enum Epi { EPI_BF16 = 0, EPI_F32 = 1, EPI_PART = 2 };
 
 struct GemmArgs {
-  int M, N, K, k_pairs, n_split, tiles_m, tiles_n, accumulate;  // k_pairs: 64-wide k steps
+  int M, N, K, k_pairs, n_split, tiles_m, tiles_n, accumulate;  // k_pairs: 64-wide k steps, ceil(K / 64)
   const uint16_t* A; int64_t lda, a_bytes;
   const uint16_t* B; int64_t ldb, b_bytes;
   void* C; int64_t ldc;
@@ -121,6 +126,15 @@ __device__ __forceinline__ int kswz(int row) {
   return PERM ? (((row >> 1) & 1) | (((row >> 3) & 1) << 1)) : ((row >> 1) & 3);
 }
 
+// An offset past every operand extent (operands are below 4 GiB - 16 bytes): the lane reads zero.
+constexpr uint32_t kOffPastK = 0xFFFFFFF0u;
+// First k (0, 8, 16 or 24) of the 16-byte chunk that lane `lane` moves in every DMA block of a
+// k-contiguous tile: the swizzle depends on the row only through bits that equal those of lane / 4.
+template <bool PERM>
+__device__ __forceinline__ int lane_k0(int lane) { return 8 * ((lane & 3) ^ kswz<PERM>(lane >> 2)); }
+// A k-contiguous lane's offset for a step whose K tail starts `klim` elements in (klim >= BK: no tail).
+__device__ __forceinline__ uint32_t kmask(uint32_t off, int kc, int klim) { return kc < klim ? off : kOffPastK; }
+
 template <bool KMAJ, bool PERM = false>
 __device__ __forceinline__ void tile_offsets(uint32_t (&off)[DMA_PER_TILE], int64_t ld, int o0, int omax, int wave,
                                              int lane) {
@@ -146,7 +160,9 @@ template <bool KMAJ>
 __device__ __forceinline__ i32x4 step_rsrc(const uint16_t* base, int64_t ld, int64_t bytes, int k0) {
   const int64_t skip = (KMAJ ? (int64_t)k0 : (int64_t)k0 * ld) * 2;
   const uint64_t addr = reinterpret_cast<uint64_t>(base) + (uint64_t)skip;
-  return i32x4{(int)(uint32_t)addr, (int)((addr >> 32) & 0xffff), (int)(uint32_t)(bytes - skip), kRsrcWord3};
+  // a step wholly past K can start beyond a small operand's end: extent 0, every lane reads zero
+  const int64_t ext = bytes > skip ? bytes - skip : 0;
+  return i32x4{(int)(uint32_t)addr, (int)((addr >> 32) & 0xffff), (int)(uint32_t)ext, kRsrcWord3};
 }
 
 // 8 k values (8g .. 8g+7 of the step) of tile row/column o16 + r for lane (r, g).  PERM (k-contiguous
@@ -218,11 +234,18 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
       for (int e = 0; e < 8; ++e) f[e] = (__bf16)1.0f;
     }
   };
-  // DMA of this wave's block q (0..3: operand A, 4..7: operand B) of step kt into `stage`
-  auto dma = [&](const i32x4& rsa, const i32x4& rsb, int stage, int q) {
+  // DMA of this wave's block q (0..3: operand A, 4..7: operand B) of a step into `stage`; klim = K - k0 of
+  // the step (wave-uniform): below BK, k-contiguous lanes from klim on read zero
+  const int kca = lane_k0<false>(lane), kcb = lane_k0<PB>(lane);
+  auto dma = [&](const i32x4& rsa, const i32x4& rsb, int stage, int q, int klim) {
     unsigned char* st = smem + stage * STAGE_BYTES;
-    if (q < DMA_PER_TILE) dma_block(rsa, offa[q], st + (wave * DMA_PER_TILE + q) * 1024);
-    else dma_block(rsb, offb[q - DMA_PER_TILE], st + TILE_BYTES + (wave * DMA_PER_TILE + q - DMA_PER_TILE) * 1024);
+    if (q < DMA_PER_TILE) {
+      const uint32_t o = (AK && klim < BK) ? kmask(offa[q], kca, klim) : offa[q];
+      dma_block(rsa, o, st + (wave * DMA_PER_TILE + q) * 1024);
+    } else {
+      const uint32_t o = (BKM && klim < BK) ? kmask(offb[q - DMA_PER_TILE], kcb, klim) : offb[q - DMA_PER_TILE];
+      dma_block(rsb, o, st + TILE_BYTES + (wave * DMA_PER_TILE + q - DMA_PER_TILE) * 1024);
+    }
   };
   auto step_rsrcs = [&](int kt, i32x4& rsa, i32x4& rsb) {
     const int k0 = kbeg + kt * BK;
@@ -250,7 +273,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     const unsigned char* Ns = smem + ((kt + 1) % NST) * STAGE_BYTES;  // past the last step: unused data
     i32x4 rsa, rsb;
-    step_rsrcs(min(kt + NST, nk - 1), rsa, rsb);
+    const int kd = min(kt + NST, nk - 1), klim = a.K - (kbeg + kd * BK);
+    step_rsrcs(kd, rsa, rsb);
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
       if (q < 8) {
@@ -259,7 +283,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
         nb[q - 8] = frag<BKM, PB>(Ns + TILE_BYTES, bcol(q - 8), r, g);
         if (!PB) ones_fix(nb[q - 8], q - 8);
       }
-      if (q & 1) dma(rsa, rsb, kt % NST, q >> 1);
+      if (q & 1) dma(rsa, rsb, kt % NST, q >> 1, klim);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {  // B first: lane (r, g) accumulates C[m = r][n = 4g + e]
         const int n = 4 * q + u, i = n >> 3, j = n & 7;
@@ -272,9 +296,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
 #pragma unroll
   for (int s = 0; s < NST; ++s) {
     i32x4 rsa, rsb;
-    step_rsrcs(min(s, nk - 1), rsa, rsb);
+    const int kd = min(s, nk - 1), klim = a.K - (kbeg + kd * BK);
+    step_rsrcs(kd, rsa, rsb);
 #pragma unroll
-    for (int q = 0; q < DMA_PER_STEP; ++q) dma(rsa, rsb, s, q);
+    for (int q = 0; q < DMA_PER_STEP; ++q) dma(rsa, rsb, s, q, klim);
   }
   __builtin_amdgcn_s_waitcnt(wait_vm((NST - 1) * DMA_PER_STEP));
   __builtin_amdgcn_s_barrier();
@@ -470,7 +495,8 @@ __device__ __forceinline__ void tile_rel_offsets(uint32_t (&off)[DMA_PER_TILE], 
 __device__ __forceinline__ i32x4 tile_rsrc(const uint16_t* base, int64_t ld, int64_t bytes, int o0, int k0) {
   const int64_t skip = ((int64_t)o0 * ld + k0) * 2;
   const uint64_t addr = reinterpret_cast<uint64_t>(base) + (uint64_t)skip;
-  return i32x4{(int)(uint32_t)addr, (int)((addr >> 32) & 0xffff), (int)(uint32_t)(bytes - skip), kRsrcWord3};
+  const int64_t ext = bytes > skip ? bytes - skip : 0;
+  return i32x4{(int)(uint32_t)addr, (int)((addr >> 32) & 0xffff), (int)(uint32_t)ext, kRsrcWord3};
 }
 
 // tile v -> origin: contiguous tile ranges per XCD, then groups of 8 tile rows
@@ -489,7 +515,7 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
   const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const int total = a.tiles_m * a.tiles_n, nk = a.K / BK;  // nk >= 4 and even (launcher)
+  const int total = a.tiles_m * a.tiles_n, nk = 2 * a.k_pairs;  // nk >= 4 (launcher)
 
   auto bcol = [&](int j) { return wn * 128 + 32 * (j >> 1) + 4 * (j & 1); };
   auto opaque_lane = [&]() {
@@ -501,15 +527,19 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
   // than kept live across the tile loop: with 256 accumulators and two fragment buffers the
   // register file is full, and a spilled offset would be reloaded with a vmcnt wait that drains
   // the previous tile's stores.
-  auto dma = [&](const i32x4& rsa, const i32x4& rsb, int stage, int q, int ln) {
+  // klim: K - k0 of the step (K tail: lanes from klim on read zero, see kmask)
+  auto dma = [&](const i32x4& rsa, const i32x4& rsb, int stage, int q, int ln, int klim) {
     unsigned char* st = smem + stage * STAGE_BYTES;
     uint32_t off[DMA_PER_TILE];
     if (q < DMA_PER_TILE) {
       tile_rel_offsets<false>(off, a.lda, wave, ln);
-      dma_block(rsa, off[q], st + (wave * DMA_PER_TILE + q) * 1024);
+      const uint32_t o = klim < BK ? kmask(off[q], lane_k0<false>(ln), klim) : off[q];
+      dma_block(rsa, o, st + (wave * DMA_PER_TILE + q) * 1024);
     } else {
       tile_rel_offsets<true>(off, a.ldb, wave, ln);
-      dma_block(rsb, off[q - DMA_PER_TILE], st + TILE_BYTES + (wave * DMA_PER_TILE + q - DMA_PER_TILE) * 1024);
+      const int qb = q - DMA_PER_TILE;
+      const uint32_t o = klim < BK ? kmask(off[qb], lane_k0<true>(ln), klim) : off[qb];
+      dma_block(rsb, o, st + TILE_BYTES + (wave * DMA_PER_TILE + qb) * 1024);
     }
   };
 
@@ -542,7 +572,7 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
   for (int s = 0; s < NST; ++s) {
     const i32x4 rsa = tile_rsrc(a.A, a.lda, a.a_bytes, m0, s * BK), rsb = tile_rsrc(a.B, a.ldb, a.b_bytes, n0, s * BK);
 #pragma unroll
-    for (int q = 0; q < DMA_PER_STEP; ++q) dma(rsa, rsb, s, q, lane);
+    for (int q = 0; q < DMA_PER_STEP; ++q) dma(rsa, rsb, s, q, lane, a.K - s * BK);
   }
   bias_dma(n0, 0);
 #pragma unroll
@@ -571,15 +601,19 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
     const unsigned char* Ns = smem + ((gs + kt + 1) % NST) * STAGE_BYTES;
     const int ka = kt + NST;
     i32x4 rsa, rsb;
+    int klim;
     if (ka < nk) {
       rsa = tile_rsrc(a.A, a.lda, a.a_bytes, m0, ka * BK);
       rsb = tile_rsrc(a.B, a.ldb, a.b_bytes, n0, ka * BK);
+      klim = a.K - ka * BK;
     } else if (vn < total) {
       rsa = tile_rsrc(a.A, a.lda, a.a_bytes, m0n, (ka - nk) * BK);
       rsb = tile_rsrc(a.B, a.ldb, a.b_bytes, n0n, (ka - nk) * BK);
+      klim = a.K - (ka - nk) * BK;
     } else {
       rsa = tile_rsrc(a.A, a.lda, a.a_bytes, m0, (nk - 1) * BK);
       rsb = tile_rsrc(a.B, a.ldb, a.b_bytes, n0, (nk - 1) * BK);
+      klim = a.K - (nk - 1) * BK;
     }
     const int dstage = (gs + kt) % NST;
     const int ln = tln, rr = ln & 15, gg = ln >> 4;
@@ -587,7 +621,7 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
     for (int q = 0; q < 16; ++q) {
       if (q < 8) na[q] = frag<true>(Ns, wm * 128 + 16 * q, rr, gg);
       else nb[q - 8] = frag<true, true>(Ns + TILE_BYTES, bcol(q - 8), rr, gg);
-      if (q & 1) dma(rsa, rsb, dstage, q >> 1, ln);
+      if (q & 1) dma(rsa, rsb, dstage, q >> 1, ln, klim);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int n = 4 * q + u, i = n >> 3, j = n & 7;
@@ -728,8 +762,8 @@ void launch(const GemmArgs& a, int S, int c_dtype, hipStream_t st) {
 int resolve_split(const llattn_gemm_desc* d) {
   if (d->split_k > 0) return d->split_k;
   const int64_t tiles = (int64_t)((d->M + BM - 1) / BM) * ((d->N + BN - 1) / BN);
-  if (tiles >= 224 || d->K % (2 * BK)) return 1;
-  const int64_t s = std::min<int64_t>(256 / tiles, d->K / (2 * BK) / 4);
+  if (tiles >= 224) return 1;
+  const int64_t s = std::min<int64_t>(256 / tiles, (d->K + 2 * BK - 1) / (2 * BK) / 4);
   return s < 1 ? 1 : (int)s;
 }
 
@@ -752,9 +786,11 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
   if (d->c_dtype != LLATTN_BF16 && d->c_dtype != LLATTN_F32)
     return fail(LLATTN_ERR_DTYPE, "llattn_gemm: unknown output dtype %d", d->c_dtype);
   const int S = resolve_split(d);
-  if (d->K % (2 * BK) != 0)
-    return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: K=%d must be a multiple of %d", d->K, 2 * BK);
-  if (S < 1 || S > d->K / (2 * BK))
+  const int k_pairs = (d->K + 2 * BK - 1) / (2 * BK);
+  if ((!d->a_trans || !d->b_trans) && d->K % 8 != 0)
+    return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: K=%d must be a multiple of 8 when an operand is k-contiguous",
+                d->K);
+  if (S < 1 || S > k_pairs)
     return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: %d K splits for K=%d: at most one per %d-wide k step", S, d->K,
                 2 * BK);
   if (d->N % 8 != 0 || (d->a_trans && d->M % 8 != 0))
@@ -770,7 +806,7 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
   // storage extents of the operands (the last row ends at its used width)
   const int64_t a_bytes = (d->a_trans ? (int64_t)(d->K - 1) * d->lda + d->M : (int64_t)(d->M - 1) * d->lda + d->K) * 2;
   const int64_t b_bytes = (d->b_trans ? (int64_t)(d->K - 1) * d->ldb + d->N : (int64_t)(d->N - 1) * d->ldb + d->K) * 2;
-  if (a_bytes >= (int64_t(1) << 32) || b_bytes >= (int64_t(1) << 32))
+  if (a_bytes > (int64_t)kOffPastK || b_bytes > (int64_t)kOffPastK)
     return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: operands of 4 GiB or more are not supported");
   if (d->a_rowsum && (!d->b_trans || d->c_dtype != LLATTN_F32 || d->N % BN == 0 || !aligned16(d->a_rowsum)))
     return fail(LLATTN_ERR_UNSUPPORTED,
@@ -795,7 +831,7 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
     return fail(LLATTN_ERR_WORKSPACE, "llattn_gemm: %d K splits need %zu workspace bytes (got %zu)", S, need,
                 workspace_bytes);
   GemmArgs a{};
-  a.M = d->M; a.N = d->N; a.K = d->K; a.k_pairs = d->K / (2 * BK); a.n_split = S;
+  a.M = d->M; a.N = d->N; a.K = d->K; a.k_pairs = k_pairs; a.n_split = S;
   a.tiles_m = (d->M + BM - 1) / BM; a.tiles_n = (d->N + BN - 1) / BN;
   a.accumulate = d->accumulate;
   a.A = static_cast<const uint16_t*>(d->A); a.lda = d->lda; a.a_bytes = a_bytes;
@@ -815,7 +851,7 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
   hipStream_t st = static_cast<hipStream_t>(stream);
   // bf16 x Wᵀ (+ bias) without K split or accumulation: the persistent kernel, one workgroup per CU
   const int64_t c_bytes = ((int64_t)(d->M - 1) * d->ldc + d->N) * 2;
-  if (!d->a_trans && !d->b_trans && S == 1 && d->c_dtype == LLATTN_BF16 && !d->accumulate && d->K >= 4 * BK &&
+  if (!d->a_trans && !d->b_trans && S == 1 && d->c_dtype == LLATTN_BF16 && !d->accumulate && k_pairs >= 2 &&
       c_bytes < (int64_t(1) << 31)) {
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)

@@ -13,7 +13,6 @@ rounded to bf16 first.
 from __future__ import annotations
 
 import torch
-import torch.nn.functional as F
 
 from . import gemm
 
@@ -54,54 +53,33 @@ def pack_params(groups):
     return outs
 
 
-def tn_supported(k: int, m: int, n: int) -> bool:
-    """Shapes the weight-gradient kernel takes: the token count is split into whole 64-wide steps and the
-    output widths are multiples of 8."""
-    return k % 64 == 0 and m % 8 == 0 and n % 8 == 0
+def linear_fwd(x2: torch.Tensor, w: torch.Tensor, b32: torch.Tensor | None) -> torch.Tensor:
+    """bf16 ``x2 @ w^T + b`` (fp32 bias added before the bf16 rounding of the output) on the MFMA GEMM."""
+    return gemm.linear(x2, w, b32)
 
 
-def mfma_supported(k: int, n: int) -> bool:
-    """Shapes the forward / input-gradient kernel takes: the contraction in whole 64-wide steps and an
-    output width that is a multiple of 8."""
-    return k % 64 == 0 and n % 8 == 0
-
-
-def linear_fwd(x2: torch.Tensor, w: torch.Tensor, b32: torch.Tensor | None, library: bool = False) -> torch.Tensor:
-    """bf16 ``x2 @ w^T + b`` (fp32 bias added before the bf16 rounding of the output)."""
-    if not library and mfma_supported(x2.shape[1], w.shape[0]):
-        return gemm.linear(x2, w, b32)
-    return F.linear(x2, w, None if b32 is None else b32.to(BF16))
-
-
-def input_grad(dy2: torch.Tensor, w: torch.Tensor, library: bool = False, rowadd=()) -> torch.Tensor:
+def input_grad(dy2: torch.Tensor, w: torch.Tensor, rowadd=()) -> torch.Tensor:
     """bf16 ``dy2 @ w`` (w [N, K] read row-major), plus the broadcast ``rowadd`` pooling gradients
-    (:func:`llattn_amd.gemm.matmul_nn`; only on the MFMA kernel)."""
-    if not library and mfma_supported(dy2.shape[1], w.shape[1]):
-        return gemm.matmul_nn(dy2, w, rowadd=rowadd)
-    if rowadd:
-        raise ValueError("row addends need the MFMA input-gradient kernel")
-    return torch.mm(dy2, w)
+    (:func:`llattn_amd.gemm.matmul_nn`)."""
+    return gemm.matmul_nn(dy2, w, rowadd=rowadd)
 
 
 def weight_grad(dy2: torch.Tensor, x2: torch.Tensor, bias_grad: bool = False):
-    """fp32 ``dy2^T @ x2`` for bf16 ``dy2 [K, N]``, ``x2 [K, D]`` (K = tokens), and with ``bias_grad`` also the
-    fp32 column sums of ``dy2`` (the bias gradient): returns ``(dW, db)``."""
-    K, N = dy2.shape
-    D = x2.shape[1]
-    if tn_supported(K, N, D) and dy2.stride(1) == 1 and x2.stride(1) == 1:
-        if bias_grad and gemm.rowsum_supported(D):  # bias gradient from the weight-gradient pass itself
-            db = torch.empty((N,), dtype=torch.float32, device=dy2.device)
-            return gemm.matmul_tn(dy2, x2, rowsum=db), db
-        return gemm.matmul_tn(dy2, x2), (gemm.colsum(dy2) if bias_grad else None)
-    # shapes the MFMA kernel does not tile (token counts that are not a multiple of 64): library GEMM
-    return torch.mm(dy2.t(), x2).float(), (dy2.sum(0, dtype=torch.float32) if bias_grad else None)
+    """fp32 ``dy2^T @ x2`` for bf16 ``dy2 [K, N]``, ``x2 [K, D]`` (K = tokens, any count), and with ``bias_grad``
+    also the fp32 column sums of ``dy2`` (the bias gradient): returns ``(dW, db)``.  The bias gradient comes
+    from the weight-gradient pass itself (a column of ones) when D is not a multiple of 256, else from
+    the column-sum kernel."""
+    N, D = dy2.shape[1], x2.shape[1]
+    if bias_grad and gemm.rowsum_supported(D):
+        db = torch.empty((N,), dtype=torch.float32, device=dy2.device)
+        return gemm.matmul_tn(dy2, x2, rowsum=db), db
+    return gemm.matmul_tn(dy2, x2), (gemm.colsum(dy2) if bias_grad else None)
 
 
 class _Project(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, library, pools, packed, *params):
-        # library: (forward on hipBLASLt, input gradient on hipBLASLt); packed: (bf16 weights, fp32 biases) already
-        # concatenated by pack_params, or None
+    def forward(ctx, x, pools, packed, *params):
+        # packed: (bf16 weights, fp32 biases) already concatenated by pack_params, or None
         ctx.set_materialize_grads(False)
         ws, bs = params[0::2], params[1::2]
         has_bias = bs[0] is not None
@@ -121,7 +99,7 @@ class _Project(torch.autograd.Function):
             else:
                 packs = pack_params([(ws, BF16)] + ([(bs, torch.float32)] if has_bias else []))
                 wcat, bcat = packs[0], (packs[1] if has_bias else None)
-            y = linear_fwd(x2, wcat, bcat, library[0])
+            y = linear_fwd(x2, wcat, bcat)
             pooled = []
             if pools:
                 from .ops import _contig, pool_fwd_into
@@ -132,14 +110,13 @@ class _Project(torch.autograd.Function):
                     pooled.append(p)
         ctx.save_for_backward(x2, wcat)
         ctx.meta = (tuple(x.shape[:-1]), rows, has_bias, [w.dtype for w in ws], [None if b is None else b.dtype
-                                                                                 for b in bs], x.dtype, library,
-                    tuple(pools))
+                                                                                 for b in bs], x.dtype, tuple(pools))
         return (y.view(*x.shape[:-1], sum(rows)), *pooled)
 
     @staticmethod
     def backward(ctx, dy, *dpooled):
         x2, wcat = ctx.saved_tensors
-        lead, rows, has_bias, wdt, bdt, xdt, library, pools = ctx.meta
+        lead, rows, has_bias, wdt, bdt, xdt, pools = ctx.meta
         N = sum(rows)
         K = x2.shape[1]
         dx = dw = db = None
@@ -150,8 +127,7 @@ class _Project(torch.autograd.Function):
                     dy2 = dy2.contiguous()
                 if ctx.needs_input_grad[0]:
                     # the poolings' gradients (bf16) join the input gradient in the GEMM's epilogue
-                    fuse = (xdt == BF16 and not library[1] and mfma_supported(N, K) and len(lead) == 2
-                            and all(g is None or g.dtype == BF16 for g in dpooled))
+                    fuse = xdt == BF16 and len(lead) == 2 and all(g is None or g.dtype == BF16 for g in dpooled)
                     rowadd = []
                     if fuse:
                         from .ops import _contig
@@ -159,7 +135,7 @@ class _Project(torch.autograd.Function):
                             if g is not None:
                                 rowadd.append((_contig(g).view(-1, K), lead[1], seg, n_seg, divisor))
                         dpooled = ()
-                    dx = input_grad(dy2, wcat, library[1], rowadd).view(*lead, K).to(xdt)
+                    dx = input_grad(dy2, wcat, rowadd).view(*lead, K).to(xdt)
                 dw, db = weight_grad(dy2, x2, has_bias)
             if ctx.needs_input_grad[0] and any(g is not None for g in dpooled):
                 # pooling backward accumulates straight into the projection's input gradient
@@ -177,15 +153,13 @@ class _Project(torch.autograd.Function):
             grads.append(None if dw is None else dw[o:o + n].to(wd))
             grads.append(None if db is None else db[o:o + n].to(bd))
             o += n
-        return (dx, None, None, None, *grads)
+        return (dx, None, None, *grads)
 
 
-def project(x: torch.Tensor, *linears: torch.nn.Linear, library_fwd: bool = False, library_dx: bool = False,
-            pools=(), packed=None):
+def project(x: torch.Tensor, *linears: torch.nn.Linear, pools=(), packed=None):
     """bf16 ``x @ [W_1; W_2; ...]^T + [b_1; b_2; ...]`` (all layers share the input width); backward gives
-    fp32 weight and bias gradients in the parameters' dtypes.  ``library_fwd`` / ``library_dx`` put the
-    forward / input-gradient product on hipBLASLt instead of the MFMA kernel (the weight gradient always
-    runs on the MFMA kernel when its shape allows); the block picks per projection whichever is faster.
+    fp32 weight and bias gradients in the parameters' dtypes.  Every product (forward, input and weight
+    gradient) runs on the gfx950 MFMA GEMM; shapes it does not take raise.
 
     ``pools``: ``(seg, n_seg, divisor)`` segment poolings of the same ``x [B, T, K]`` (as
     :func:`llattn_amd.ops.pool`) returned after the projection, ``(y, pooled_1, ...)``; their backward adds
@@ -195,5 +169,5 @@ def project(x: torch.Tensor, *linears: torch.nn.Linear, library_fwd: bool = Fals
     params = []
     for lin in linears:
         params += [lin.weight, lin.bias]
-    out = _Project.apply(x, (library_fwd, library_dx), tuple(pools), packed, *params)
+    out = _Project.apply(x, tuple(pools), packed, *params)
     return out if pools else out[0]

@@ -30,12 +30,6 @@ from . import _lib as L
 from .linear import pack_params, project
 from .ops import LLAttnCore, _Prof, pool
 
-# Which bf16 projection products run on hipBLASLt rather than the MFMA kernel (measured at config 2,
-# whole step): none -- with the persistent forward kernel every projection product of the block is
-# faster on the MFMA kernel (the two K = 1408 forwards by about 1% of the step).
-QKV_FWD_LIBRARY = False
-OUT_FWD_LIBRARY = False
-
 
 class LocalLatentAttentionTriton(nn.Module):
     """``LocalLatentAttentionTriton(d_model, n_heads, latent_heads, latent_dim, n_latents, window,
@@ -124,15 +118,14 @@ class LocalLatentAttentionTriton(nn.Module):
         packed = self._packed_weights(macro) if bf16 else {}
         if macro and bf16:
             # both poolings of x ride on the projection, whose backward adds their gradients in place
-            qkvr, pq, pooled = project(x, self.qkv_proj, library_fwd=QKV_FWD_LIBRARY,
-                                       pools=[(lay.q_block, lay.n_q, L.DIV_SEG), latents], packed=packed["qkv"])
+            qkvr, pq, pooled = project(x, self.qkv_proj, pools=[(lay.q_block, lay.n_q, L.DIV_SEG), latents],
+                                       packed=packed["qkv"])
             rq = project(pq, self.rq_proj, packed=packed["rq"])
         elif macro:
             qkvr = self.qkv_proj(x)
             rq = self.rq_proj(pool(x, lay.q_block, lay.n_q, L.DIV_SEG))
         elif bf16:
-            qkvr, pooled = project(x, self.qkv_proj, self.rq_proj, library_fwd=QKV_FWD_LIBRARY, pools=[latents],
-                                   packed=packed["qkv"])
+            qkvr, pooled = project(x, self.qkv_proj, self.rq_proj, pools=[latents], packed=packed["qkv"])
             rq = None
         else:
             w = torch.cat([self.qkv_proj.weight, self.rq_proj.weight], dim=0)
@@ -155,7 +148,7 @@ class LocalLatentAttentionTriton(nn.Module):
             # the gate mix runs in the local kernel's epilogue: its time is in local_attention_ms
             prof.t["gate_mix_ms"] = 0.0
             self._record_profile(prof, lay)
-        return project(y, self.out, library_fwd=OUT_FWD_LIBRARY, packed=packed["out"]) if bf16 else self.out(y)
+        return project(y, self.out, packed=packed["out"]) if bf16 else self.out(y)
 
     def _packed_weights(self, macro: bool) -> dict:
         """The bf16 copies of every projection weight that this forward multiplies with (what bf16 autocast casts

@@ -11,9 +11,10 @@
   r_out_w, window, chunk_size, ...)``, reference kernels/llattn_op.py:184-238)
   with the semantics of the reference PyTorch path (models.py:61-462).
 
-All device work is HIP kernels from ``libllattn_gfx950.so`` plus plain torch
-GEMMs (hipBLASLt) for ``r_out``.  Nothing here runs on the CPU: CPU tensors
-raise.
+All device work is HIP kernels from ``libllattn_gfx950.so``; under bf16 autocast
+``r_out`` runs on its MFMA GEMM as well.  Without autocast (the fp32 module, kept
+for the fp32 parity gate) ``r_out`` is a torch fp32 product, like the block's other
+fp32 projections.  Nothing here runs on the CPU: CPU tensors raise.
 """
 from __future__ import annotations
 

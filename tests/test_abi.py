@@ -140,7 +140,7 @@ def _gemm_desc(L, **kw):
 @pytest.mark.parametrize("kw,code,msg", [
     (dict(M=0), 1, b"sizes must be positive"),
     (dict(c_dtype=7), 2, b"unknown output dtype"),
-    (dict(K=96), 4, b"must be a multiple of 64"),
+    (dict(K=100), 4, b"must be a multiple of 8"),
     (dict(N=250, ldc=256), 4, b"multiples of 8"),
     (dict(a_trans=1, M=100, lda=104), 4, b"multiples of 8"),
     (dict(A=0x1004), 3, b"16-byte aligned"),

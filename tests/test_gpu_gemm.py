@@ -37,6 +37,50 @@ def test_linear_with_bias(M, N, K):
     assert _err(gemm.linear(x, w, b), ref) < BF16_TOL
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 8, 8), (1, 40, 72), (97, 40, 200), (33, 264, 1000), (4096, 512, 200),
+                                   (2000, 136, 8), (194, 208, 88)])
+def test_linear_k_tail(M, N, K):
+    """Contractions that are not a multiple of the 64-wide k step: the k-contiguous lanes past K read zero
+    (a single row included, whose buffer ends inside the last step)."""
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: linear k tail", M, N, K, flush=True)
+    g = torch.Generator(device=dev).manual_seed(M * 7 + N + K)
+    # operands cut out of wider rows, so the elements past K are real data that must not leak in
+    xb, wb = _rand(M, K + 24, gen=g, dev=dev) * 50, _rand(N, K + 24, gen=g, dev=dev) * 50
+    x, w = xb[:, :K], wb[:, :K]
+    b = torch.randn(N, device=dev, generator=g)
+    assert _err(gemm.linear(x, w, b), x.float() @ w.float().T + b) < BF16_TOL
+
+
+@pytest.mark.parametrize("M,N,K", [(97, 40, 208), (300, 264, 1000), (3, 512, 72)])
+def test_matmul_nn_k_tail(M, N, K):
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: nn k tail", M, N, K, flush=True)
+    g = torch.Generator(device=dev).manual_seed(5 * M + N + K)
+    ab = _rand(M, K + 40, gen=g, dev=dev) * 50
+    a, b = ab[:, :K], _rand(K, N, gen=g, dev=dev)
+    assert _err(gemm.matmul_nn(a, b), a.float() @ b.float()) < BF16_TOL
+
+
+@pytest.mark.parametrize("K,M,N,S", [(194, 264, 136, 0), (33, 40, 96, 1), (1001, 1408, 512, 0), (5000, 264, 136, 3),
+                                     (122, 16, 8, 2)])
+def test_matmul_tn_token_tail(K, M, N, S):
+    """Weight gradients over token counts that are not a multiple of 64 (nor of 8): rows past K lie beyond
+    the operands' extent and read zero; with split-K the last split is the short one."""
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: tn token tail", K, M, N, S, flush=True)
+    g = torch.Generator(device=dev).manual_seed(K + 3 * M + N)
+    a, b = _rand(K, M, gen=g, dev=dev), _rand(K, N, gen=g, dev=dev)
+    rs = torch.full((M,), float("nan"), device=dev) if N % 256 else None
+    got = gemm.matmul_tn(a, b, split_k=S, rowsum=rs)
+    assert _err(got, a.float().T @ b.float()) < FP32_TOL
+    if rs is not None:
+        assert _err(rs, a.float().sum(0)) < FP32_TOL
+
+
 @pytest.mark.parametrize("M,N,K", [(256, 256, 64), (300, 264, 128), (1000, 1408, 512)])
 def test_matmul_nn(M, N, K):
     from llattn_amd import gemm

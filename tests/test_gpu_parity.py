@@ -42,15 +42,34 @@ def test_module_fp32_matches_reference_golden(name):
         assert_fp32_close(grads[n], grads_ref[n], n)
 
 
+def _library_gemm(*args, **kwargs):
+    raise AssertionError("a library GEMM ran inside the bf16 block")
+
+
 @pytest.mark.parametrize("name", E2E_CASES)
-def test_module_bf16_autocast_matches_reference_golden(name):
+def test_module_bf16_autocast_matches_reference_golden(name, monkeypatch):
+    """The golden cases under bf16 autocast, with every projection product on llattn_gemm: torch's GEMM entry
+    points raise while the block runs, and the event log counts three products (forward, input gradient,
+    weight gradient) per projection: qkv|rq, rkv, r_out and out, plus rq_proj in macro-block mode."""
+    from llattn_amd import ops
     dev = require_cuda()
     _print_case("golden bf16", name)
     meta, x, dout, params, out_ref, dx_ref, grads_ref = load_case(name)
     shape = shape_from_meta(meta)
     m = build_module(shape, params, dev)
     xb = torch.tensor(x, dtype=torch.bfloat16, device=dev)
-    out, dx, grads = run_module(m, xb, torch.tensor(dout, dtype=torch.float32, device=dev), autocast_bf16=True)
+    ops.EVENT_LOG = []
+    try:
+        with monkeypatch.context() as mp:
+            for mod, attr in ((torch.nn.functional, "linear"), (torch, "mm"), (torch, "matmul"), (torch, "addmm")):
+                mp.setattr(mod, attr, _library_gemm)
+            out, dx, grads = run_module(m, xb, torch.tensor(dout, dtype=torch.float32, device=dev),
+                                        autocast_bf16=True)
+        calls = [e[0] for e in ops.EVENT_LOG]
+    finally:
+        ops.EVENT_LOG = None
+    macro = meta["latent_query_block_size"] > 1
+    assert calls.count("llattn_gemm") == (15 if macro else 12), calls
     floor = bf16_floor(params, xb.float().cpu().numpy(), dout, shape, grads_ref)
     for n in grads_ref:
         print(f"  {n}: got {err_stats(grads[n], grads_ref[n])} floor {floor[n]}")
