@@ -167,7 +167,10 @@ class LocalLatentLM(nn.Module):
     def loss(self, input_ids: torch.Tensor, targets: torch.Tensor, chunk_rows: int = 8192):
         """:func:`lm_loss` of ``self(input_ids)`` without the ``[B*T, V]`` logits: the tied head and the cross
         entropy run in row chunks on the gfx950 kernels (:func:`~llattn_amd.xent.lm_head_loss`)."""
-        from .xent import lm_head_loss
+        from .xent import head_supported, lm_head_loss
+        V, D = self.lm_head.weight.shape
+        if not head_supported(V, D):  # vocabularies the chunked kernels do not take: full logits, as the reference
+            return lm_loss(self.lm_head(self.hidden(input_ids)), targets)
         loss, pred = lm_head_loss(self.hidden(input_ids), self.lm_head.weight, targets, chunk_rows=chunk_rows)
         return loss, _metrics(loss, (pred == targets).float().mean())
 

@@ -19,7 +19,6 @@ Data flow of one forward (B, T, D = batch, tokens, d_model):
 """
 from __future__ import annotations
 
-import math
 from typing import Optional
 
 import torch
@@ -180,7 +179,7 @@ class LocalLatentAttentionTriton(nn.Module):
         tot["seq_len"] = tot.get("seq_len", 0.0) + lay.T
         tot["local_block_size"] = tot.get("local_block_size", 0.0) + lay.block
         tot["latent_count"] = tot.get("latent_count", 0.0) + lay.n_chunks
-        tot["latent_chunk_size"] = tot.get("latent_chunk_size", 0.0) + math.ceil(lay.T / lay.n_chunks)
+        tot["latent_chunk_size"] = tot.get("latent_chunk_size", 0.0) + lay.chunk
         tot["latent_query_block_size"] = tot.get("latent_query_block_size", 0.0) + lay.q_block
         self.profile_steps += 1
 

@@ -56,7 +56,7 @@ def xent_rows(logits: torch.Tensor, targets: torch.Tensor, ignore_index: int = I
 
 class _HeadLoss(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, h, weight, targets, ignore_index, chunk_rows):
+    def forward(ctx, h, weight, targets, ignore_index, chunk_rows, grad_enabled):
         L.require_gpu(h, weight, targets)
         D = h.shape[-1]
         V = weight.shape[0]
@@ -69,15 +69,15 @@ class _HeadLoss(torch.autograd.Function):
         dev = h.device
         valid = (t != ignore_index).sum()
         scale = 1.0 / valid.to(torch.float32)  # mean over the rows that count (NaN loss when none do)
-        want_h, want_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        # under no_grad needs_input_grad still reports the leaves' requires_grad: the caller's grad mode decides
+        want_h, want_w = grad_enabled and ctx.needs_input_grad[0], grad_enabled and ctx.needs_input_grad[1]
         grad = want_h or want_w
         loss_rows = torch.empty((N,), dtype=torch.float32, device=dev)
         pred = torch.empty((N,), dtype=torch.int32, device=dev)
         dh = torch.empty_like(hb) if want_h else None
         dw = torch.empty((V, D), dtype=torch.float32, device=dev) if want_w else None
         step = max(64, chunk_rows // 64 * 64)
-        # chunk rows padded to 64 for the weight-gradient GEMM (its K); pad rows carry zero gradient
-        logits = torch.empty((min(step, (N + 63) // 64 * 64), V), dtype=torch.bfloat16, device=dev)
+        logits = torch.empty((min(step, N), V), dtype=torch.bfloat16, device=dev)
         from .ops import _call
         for r0 in range(0, N, step):
             r1 = min(N, r0 + step)
@@ -90,14 +90,7 @@ class _HeadLoss(torch.autograd.Function):
             if want_h:
                 gemm.matmul_nn(lc, wb, out=dh[r0:r1])
             if want_w:
-                npad = (n + 63) // 64 * 64
-                if npad == n:
-                    gemm.matmul_tn(lc, hb[r0:r1], out=dw, accumulate=r0 > 0)
-                else:
-                    logits[n:npad].zero_()
-                    hp = torch.zeros((npad, D), dtype=torch.bfloat16, device=dev)
-                    hp[:n] = hb[r0:r1]
-                    gemm.matmul_tn(logits[:npad], hp, out=dw, accumulate=r0 > 0)
+                gemm.matmul_tn(lc, hb[r0:r1], out=dw, accumulate=r0 > 0)
         loss = loss_rows.sum() * scale
         ctx.save_for_backward(dh, dw)
         ctx.shape = h.shape
@@ -109,7 +102,13 @@ class _HeadLoss(torch.autograd.Function):
         dh, dw = ctx.saved_tensors
         gh = (dh * gl.to(dh.dtype)).view(ctx.shape) if dh is not None else None
         gw = dw * gl if dw is not None else None
-        return gh, gw, None, None, None
+        return gh, gw, None, None, None, None
+
+
+def head_supported(V: int, D: int) -> bool:
+    """Vocabulary and hidden sizes the chunked head loss takes: multiples of 8 (16-byte rows for the GEMMs and
+    the cross-entropy kernel), V at most 65536."""
+    return V % 8 == 0 and D % 8 == 0 and 0 < V <= 65536
 
 
 def lm_head_loss(h: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor, ignore_index: int = IGNORE_INDEX,
@@ -117,11 +116,11 @@ def lm_head_loss(h: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor, i
     """Mean cross entropy of ``h [..., D] @ weight [V, D]^T`` against ``targets [...]`` (``ignore_index`` rows
     excluded) and the first argmax of every logit row, without materialising the ``[rows, V]`` logits: chunks
     of ``chunk_rows`` rows (a multiple of 64).  Returns ``(loss, pred)``; ``pred`` has ``targets``' shape.
-    V and D must be multiples of 64 (the GEMMs' contraction lengths) and V at most 65536.  GPU only."""
+    V and D must be multiples of 8 and V at most 65536 (:func:`head_supported`).  GPU only."""
     D = h.shape[-1]
     V = weight.shape[0]
     if weight.dim() != 2 or weight.shape[1] != D:
         raise ValueError(f"lm_head_loss: weight {tuple(weight.shape)} does not match hidden size {D}")
-    if V % 64 or D % 64 or V > 65536:
-        raise ValueError(f"lm_head_loss: V={V} (multiple of 64, at most 65536) and D={D} (multiple of 64) unsupported")
-    return _HeadLoss.apply(h, weight, targets, int(ignore_index), int(chunk_rows))
+    if not head_supported(V, D):
+        raise ValueError(f"lm_head_loss: V={V} (multiple of 8, at most 65536) and D={D} (multiple of 8) unsupported")
+    return _HeadLoss.apply(h, weight, targets, int(ignore_index), int(chunk_rows), torch.is_grad_enabled())

@@ -21,6 +21,18 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) and the built HIP library")
 
 
+def pytest_sessionfinish(session, exitstatus):
+    """With LLATTN_PARITY_LOG set, write every GPU parity comparison (raw and scaled errors, the bar used) as
+    JSON lines to that file."""
+    import os
+    path = os.environ.get("LLATTN_PARITY_LOG")
+    if not path or "gpu_helpers" not in sys.modules:
+        return
+    with open(path, "w") as f:
+        for row in sys.modules["gpu_helpers"].RECORD:
+            f.write(json.dumps(row) + "\n")
+
+
 E2E_CASES = ("tiny_tok", "tiny_macro", "w1_chunk1", "dh88_single_block", "qbs1_is_tokenwise", "macro_ragged")
 
 

@@ -11,6 +11,27 @@ BF16_MAX_TOL = 2e-2        # max-abs, bf16 kernels vs the fp32 reference
 BF16_MEANREL_TOL = 1e-2    # mean(|a-b|) / mean(|b|)
 
 
+# Every comparison made through assert_fp32_close / assert_bf16_close, as
+# (case, tensor, dtype bar, raw max|a-ref|, max|ref|, scaled max-abs, mean-rel, max-abs bar, mean-rel bar);
+# conftest writes it out when LLATTN_PARITY_LOG names a file.
+RECORD: list = []
+CASE = [""]
+
+
+def set_case(name: str) -> None:
+    CASE[0] = name
+
+
+def _record(what, a, ref, bar, tmx, tmr):
+    a = np.asarray(a, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    mx, mr = err_stats(a, ref)
+    RECORD.append({"case": CASE[0], "tensor": what, "bar": bar, "raw_max_abs": float(np.abs(a - ref).max()),
+                   "max_ref": float(np.abs(ref).max()), "scaled_max_abs": mx, "mean_rel": mr,
+                   "max_abs_bar": tmx, "mean_rel_bar": tmr})
+    return mx, mr
+
+
 def require_cuda():
     assert torch.cuda.is_available(), "GPU test run without a visible GPU"
     return torch.device("cuda:0")
@@ -52,7 +73,7 @@ def err_stats(a, ref):
 
 
 def assert_fp32_close(a, ref, what=""):
-    mx, _ = err_stats(a, ref)
+    mx, _ = _record(what, a, ref, "fp32", FP32_TOL, None)
     assert mx <= FP32_TOL, f"{what}: scaled max-abs {mx:.3e} > {FP32_TOL}"
 
 
@@ -60,10 +81,10 @@ def assert_bf16_close(a, ref, what="", floor=None):
     """bf16 bar: scaled max-abs <= 2e-2 and mean-rel <= 1e-2.  With ``floor`` = the (max, mean-rel) error
     that the reference math itself reaches when run under bf16 autocast on the same inputs, the bar is
     raised to twice that floor where the floor alone already exceeds it."""
-    mx, mr = err_stats(a, ref)
     tmx, tmr = BF16_MAX_TOL, BF16_MEANREL_TOL
     if floor is not None:
         tmx, tmr = max(tmx, 2.0 * floor[0]), max(tmr, 2.0 * floor[1])
+    mx, mr = _record(what, a, ref, "bf16" if floor is None else "bf16 floor", tmx, tmr)
     assert mx <= tmx, f"{what}: scaled max-abs {mx:.3e} > {tmx:.3e}"
     assert mr <= tmr, f"{what}: mean-rel {mr:.3e} > {tmr:.3e}"
 

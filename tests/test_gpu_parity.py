@@ -22,6 +22,8 @@ pytestmark = pytest.mark.gpu
 
 
 def _print_case(*args):
+    from gpu_helpers import set_case
+    set_case(" ".join(str(a) for a in args))
     print("case:", *args, flush=True)
 
 
@@ -329,12 +331,21 @@ def _config_row_check(cfg_name, rows):
     _print_case(cfg_name, "full batch")
     out, dx, grads = run_module(m, x, dout, autocast_bf16=True)
     params = {n: p.detach().float().cpu() for n, p in m.named_parameters()}
+    del grads
     for b in rows:
         _print_case(cfg_name, "reference row", b)
         o_ref, dx_ref, g_ref = torch_ref.block_forward_backward(params, x[b:b + 1].float().cpu(),
                                                                 dout[b:b + 1].float().cpu(), shape)
         assert_bf16_close(out[b:b + 1], o_ref.numpy(), f"out[{b}]")
         assert_bf16_close(dx[b:b + 1], dx_ref.numpy(), f"dx[{b}]")
+        # every parameter gradient of that sequence alone (full T: the window > 64 two-pass local backward,
+        # its gate partial rows, r_out's bias from dremote, the column-sum bias gradients of the D = 1024
+        # projections, the macro-block scatter in config 4)
+        _print_case(cfg_name, "parameter gradients of row", b)
+        _, _, g_row = run_module(m, x[b:b + 1], dout[b:b + 1], autocast_bf16=True)
+        assert set(g_row) == set(g_ref)
+        for n in g_ref:
+            assert_bf16_close(g_row[n], g_ref[n].numpy(), f"{n}[{b}]")
     return m, x, dout, params, shape
 
 
@@ -344,3 +355,46 @@ def test_c3_long_context_rows_match_fp32_reference():
 
 def test_c4_macro_block_rows_match_fp32_reference():
     _config_row_check("c4", rows=(0, 3))
+
+
+# ---------------------------------------------------------------- profiling API (reference models.py:131-157)
+
+PROFILE_KEYS = ("profile_local_latent_total_ms", "profile_qkv_ms", "profile_pool_ms", "profile_local_attention_ms",
+                "profile_latent_attention_ms", "profile_gate_mix_ms", "profile_gate_mean", "profile_seq_len",
+                "profile_local_block_size", "profile_latent_count", "profile_latent_chunk_size",
+                "profile_latent_query_block_size")
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_profile_stats_on_config1(c1_golden, bf16):
+    """set_profile(True) at the config-1 shape: the reference's twelve profile_* keys, averaged over forwards;
+    positive stage times whose sum is the total (the gate mix runs inside the local kernel: 0 ms); the
+    resolved sizes; gate_mean equal to the mean local gate weight w of the oracle's forward."""
+    dev = require_cuda()
+    _print_case("profile config 1", "bf16" if bf16 else "fp32")
+    meta, params, x, dout, *_ = c1_golden
+    shape = orc.BlockShape(d_model=256, n_heads=4, window=128, local_block_size=256, latent_tokens=8,
+                           latent_d_model=32, latent_heads=2)
+    m = build_module(shape, {k: v.numpy() for k, v in params.items()}, dev)
+    assert m.get_profile_stats() == {}
+    m.set_profile(True)
+    xd = x.to(dev)
+    for _ in range(3):
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16, enabled=bf16):
+            m(xd)
+    st = m.get_profile_stats()
+    assert tuple(sorted(st)) == tuple(sorted(PROFILE_KEYS))
+    for k in ("profile_qkv_ms", "profile_pool_ms", "profile_local_attention_ms", "profile_latent_attention_ms"):
+        assert st[k] > 0.0, k
+    assert st["profile_gate_mix_ms"] == 0.0
+    parts = sum(st[k] for k in ("profile_qkv_ms", "profile_pool_ms", "profile_local_attention_ms",
+                                "profile_latent_attention_ms", "profile_gate_mix_ms"))
+    assert abs(st["profile_local_latent_total_ms"] - parts) < 1e-9
+    assert st["profile_seq_len"] == 512 and st["profile_local_block_size"] == 256
+    assert st["profile_latent_count"] == 8 and st["profile_latent_chunk_size"] == 64
+    assert st["profile_latent_query_block_size"] == 1
+    _, cache = orc.module_forward({k: v.double().numpy() for k, v in params.items()}, x.double().numpy(), shape,
+                                  keep=True)
+    assert abs(st["profile_gate_mean"] - float(np.mean(cache["w"]))) < (2e-3 if bf16 else 1e-5)
+    m.set_profile(False)
+    assert m.get_profile_stats() == {}

@@ -166,3 +166,42 @@ def test_lm_head_loss_all_rows_ignored_and_chunk_rounding():
     assert not h.grad.any() and not w.grad.any()
     ref = torch.nn.functional.cross_entropy(torch.randn(130, 128), t.cpu())
     assert torch.isnan(ref)
+
+
+def test_lm_head_loss_vocab_and_width_not_multiples_of_64():
+    """V = 1000 and D = 200 (multiples of 8 only) and a row count that is not a multiple of 64: the GEMMs' K
+    tails (D in the logits, V in the hidden-state gradient, the rows in the weight gradient) are masked."""
+    xent = _xent()
+    g = torch.Generator().manual_seed(8)
+    N, D, V = 197, 200, 1000
+    hq = torch.randn(N, D, generator=g).to(DEV).to(torch.bfloat16).requires_grad_(True)
+    w = (torch.randn(V, D, generator=g) * 0.05).to(DEV).requires_grad_(True)
+    t = torch.randint(0, V, (N,), generator=g).to(DEV)
+    loss, _ = xent.lm_head_loss(hq, w, t, chunk_rows=128)
+    loss.backward()
+    ref_loss, _, ref_dh, ref_dw = _reference_head_loss(hq, w, t)
+    assert float(loss) == pytest.approx(float(ref_loss), rel=1e-4)
+    for got, want in ((hq.grad.float(), ref_dh), (w.grad, ref_dw)):
+        assert float((got - want).abs().max() / want.abs().max()) < 2e-2
+
+
+def test_lm_head_loss_under_no_grad_runs_only_the_forward_products():
+    """Under torch.no_grad the head computes no gradients (one logits GEMM per chunk, no input- or weight-
+    gradient GEMM, no gradient written by the cross-entropy kernel), though its leaves require grad."""
+    from llattn_amd import ops
+    xent = _xent()
+    h = torch.randn(300, 128, device=DEV).to(torch.bfloat16).requires_grad_(True)
+    w = (torch.randn(512, 128, device=DEV) * 0.05).requires_grad_(True)
+    t = torch.randint(0, 512, (300,), device=DEV)
+    with torch.no_grad():
+        ref, _ = xent.lm_head_loss(h, w, t, chunk_rows=128)
+    ops.EVENT_LOG = []
+    try:
+        with torch.no_grad():
+            loss, _ = xent.lm_head_loss(h, w, t, chunk_rows=128)
+        calls = [(e[0], e[3]) for e in ops.EVENT_LOG]
+    finally:
+        ops.EVENT_LOG = None
+    assert [c[0] for c in calls].count("llattn_gemm") == 3, calls  # 3 chunks of <= 128 rows, forward only
+    assert all(wk == n * 512 * 2 for (name, wk), n in zip([c for c in calls if c[0] == "llattn_xent"], (128, 128, 44)))
+    assert float(loss) == float(ref) and not loss.requires_grad

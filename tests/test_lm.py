@@ -171,3 +171,64 @@ def test_lm_bf16_training_step_against_fp32_reference_path():
     opt = make_optimizer(hip, lr=1e-3)
     losses = [float(train_step(hip, opt, inputs, targets)) for _ in range(4)]
     assert all(np.isfinite(losses)) and losses[-1] < losses[0], losses
+
+
+@pytest.mark.gpu
+def test_c5_full_size_step_against_reference_path_loss():
+    """BASELINE config 5 at full size: the 0.55b LocalLatentLM (22 layers, the HIP block in each) at B16 T2048,
+    vocab 32000, one bf16 AdamW training step; its loss and every updated parameter are finite.  The forward
+    loss of sequence 0 under bf16 autocast lies within 2e-2 of the same weights on the reference path (the
+    PyTorch attention block of reference models.py:307-462 and torch RMSNorm), run in fp32 on the CPU."""
+    import bench
+    from gpu_helpers import require_cuda
+    from llattn_amd.lm import build_model, make_optimizer, train_step
+    dev = require_cuda()
+    V, B, T = 32000, 16, 2048
+    print("case: c5 full size build", flush=True)
+    torch.manual_seed(0)
+    model = build_model("0.55b", vocab_size=V, max_seq_len=T).to(dev)
+    init = {k: v.detach().cpu().clone() for k, v in model.state_dict().items()}
+    g = torch.Generator(device=dev).manual_seed(5)
+    tokens = torch.randint(0, V, (B, T + 1), device=dev, generator=g)
+    inputs, targets = tokens[:, :-1], tokens[:, 1:]
+    print("case: c5 sequence-0 loss on the GPU", flush=True)
+    with torch.no_grad(), torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        loss0, _ = model.loss(inputs[:1], targets[:1])
+    loss0 = float(loss0)
+    print("case: c5 training step", flush=True)
+    opt = make_optimizer(model)
+    loss = float(train_step(model, opt, inputs, targets))
+    assert np.isfinite(loss) and abs(loss - np.log(V)) < 1.0, loss
+    for n, p in model.named_parameters():
+        assert torch.isfinite(p).all(), n
+        assert p.grad is None or torch.isfinite(p.grad).all(), n
+    del model, opt
+    torch.cuda.empty_cache()
+    print("case: c5 sequence-0 loss on the CPU reference path", flush=True)
+    torch.set_num_threads(max(1, torch.get_num_threads()))
+    ref = build_model("0.55b", attention_factory=bench.TorchPathAttention, norm_factory=bench.TorchRMSNorm,
+                      vocab_size=V, max_seq_len=T)
+    ref.load_state_dict(init)
+    with torch.no_grad():
+        logits = ref(inputs[:1].cpu())
+        loss_ref = float(torch.nn.functional.cross_entropy(logits.reshape(-1, V).float(), targets[:1].cpu().reshape(-1)))
+    print(f"c5 sequence-0 loss: HIP bf16 {loss0:.5f}, reference fp32 {loss_ref:.5f}", flush=True)
+    assert abs(loss0 - loss_ref) < 2e-2
+
+
+def test_odd_vocabulary_takes_the_full_logits_loss(monkeypatch):
+    """A vocabulary the chunked head kernels do not take (50257, GPT-2's: not a multiple of 8) makes
+    LocalLatentLM.loss fall back to full logits + lm_loss, as the reference computes it, instead of raising."""
+    from llattn_amd import lm, xent
+    assert xent.head_supported(32000, 1408) and not xent.head_supported(50257, 1408)
+    assert not xent.head_supported(70000, 1408) and not xent.head_supported(32000, 100)
+    model = lm.build_model(vocab_size=50257, max_seq_len=16, d_model=64, n_heads=2, n_layers=1, d_ff=128,
+                           local_window=8, local_block_size=8, latent_tokens=2, latent_d_model=16, latent_heads=2)
+    seen = []
+    monkeypatch.setattr(lm.LocalLatentLM, "hidden", lambda self, ids: torch.zeros(*ids.shape, 64))
+    monkeypatch.setattr(xent, "lm_head_loss", lambda *a, **k: seen.append("chunked"))
+    real = lm.lm_loss
+    monkeypatch.setattr(lm, "lm_loss", lambda logits, t: (seen.append("full"), real(logits, t))[1])
+    ids = torch.randint(0, 50257, (1, 16))
+    loss, _ = model.loss(ids, ids)
+    assert seen == ["full"] and abs(float(loss) - float(np.log(50257))) < 1e-3
