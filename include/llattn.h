@@ -104,8 +104,9 @@ int32_t llattn_pool_bwd(const void* dpooled, int64_t dp_sb, int64_t dp_sn, void*
  * latent head lh attends latents n < chunk_of(s) with scale 1/sqrt(Ldh);
  * queries with no latent output 0.  rq: [B][n_q][Lh][Ldh], gk/gv:
  * [B][n_chunks][Lh][Ldh], out: [B][n_q][Lh][Ldh]; lse: fp32 [B][Lh][n_q]
- * contiguous (-inf for empty rows).  Replaces the latent half of the
- * reference fused forward launch (reference kernels/llattn_op.py:34-84). */
+ * contiguous (-inf for empty rows), or NULL when no backward follows
+ * (inference).  Replaces the latent half of the reference fused forward
+ * launch (reference kernels/llattn_op.py:34-84). */
 int32_t llattn_latent_fwd(const llattn_shape* s, const llattn_tensor* rq, const llattn_tensor* gk,
                           const llattn_tensor* gv, const llattn_tensor* out, float* lse, void* stream);
 
@@ -126,8 +127,11 @@ int32_t llattn_latent_bwd(const llattn_shape* s, const llattn_tensor* rq, const 
  * i / q_block.  gate_l / gate_r: fp32 [Dh] (shared) or [H][Dh].  Writes
  * y = w*O + (1-w)*remote with w = sigmoid(gate_l.O - gate_r.remote),
  * o_local = O (pre-gate), lse [B][H][T] and w [B][H][T] (fp32, contiguous).
- * q/k/v/y/o_local: [B][T][H][Dh].  Replaces the local + gate half of the
- * reference fused forward launch (reference kernels/llattn_op.py:34-84). */
+ * q/k/v/y/o_local: [B][T][H][Dh].  o_local, lse and w only feed the
+ * backward: a forward-only call (inference, reference generate.py:188-190)
+ * passes NULL for all three (o_local NULL or with a NULL ptr) and the kernel
+ * writes y alone.  Replaces the local + gate half of the reference fused
+ * forward launch (reference kernels/llattn_op.py:34-84). */
 int32_t llattn_local_gate_fwd(const llattn_shape* s, const llattn_tensor* q, const llattn_tensor* k,
                               const llattn_tensor* v, const llattn_tensor* remote, const float* gate_l,
                               const float* gate_r, const llattn_tensor* y, const llattn_tensor* o_local,

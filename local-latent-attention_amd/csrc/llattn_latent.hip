@@ -101,7 +101,7 @@ __global__ __launch_bounds__(256) void latent_fwd_kernel(const LatentArgs a) {
         store4<T>(op + d, v4);
       }
     }
-    if (g == 0) a.lse[((int64_t)b * a.Lh + lh) * a.n_q + qi] = l > 0.f ? (m_run + __log2f(l)) * kLn2 : kNegInf;
+    if (g == 0 && a.lse) a.lse[((int64_t)b * a.Lh + lh) * a.n_q + qi] = l > 0.f ? (m_run + __log2f(l)) * kLn2 : kNegInf;
   }
 }
 
@@ -390,7 +390,6 @@ extern "C" int32_t llattn_latent_fwd(const llattn_shape* s, const llattn_tensor*
   int32_t rc = common(s, rq, gk, gv, &a);
   if (rc) return rc;
   if ((rc = check_view("latent_out", out, s->dtype, true))) return rc;
-  if (!lse) return fail(LLATTN_ERR_LAYOUT, "lse output must be non-null");
   a.out = out->ptr; a.o_sb = out->sb; a.o_sn = out->sn; a.o_sh = out->sh;
   a.lse = lse;
   const int dhp = padded_head_dim(s->Ldh);

@@ -173,14 +173,15 @@ __global__ __launch_bounds__(256) void local_fwd_kernel(const LocalArgs a) {
     store4<T>(S0 + row * KP + d, yv);
     store4<T>(S1 + row * KP + d, o[t]);
   }
+  // o_local, lse and w feed only the backward: a forward-only call passes null for them
   if (qv && g == 0) {
     const int64_t idx = ((int64_t)b * a.H + h) * T_ + qi;
-    a.lse[idx] = l > 0.f ? (m_run + __log2f(l)) * kLn2 : kNegInf;
-    a.w[idx] = wl;
+    if (a.lse) a.lse[idx] = l > 0.f ? (m_run + __log2f(l)) * kLn2 : kNegInf;
+    if (a.w) a.w[idx] = wl;
   }
   lds_barrier();
   store_tile<T, DHP, KP>(static_cast<T*>(a.y) + b * a.y_sb + h * a.y_sh, a.y_st, S0, q0, qend, Dh);
-  store_tile<T, DHP, KP>(static_cast<T*>(a.ol) + b * a.o_sb + h * a.o_sh, a.o_st, S1, q0, qend, Dh);
+  if (a.ol) store_tile<T, DHP, KP>(static_cast<T*>(a.ol) + b * a.o_sb + h * a.o_sh, a.o_st, S1, q0, qend, Dh);
 }
 
 // ----------------------------------------------------------------------------
@@ -993,10 +994,15 @@ extern "C" int32_t llattn_local_gate_fwd(const llattn_shape* s, const llattn_ten
   LocalArgs a;
   int32_t rc = common_args(s, q, k, v, remote, gate_l, gate_r, &a);
   if (rc) return rc;
-  if ((rc = check_view("y", y, s->dtype, true)) || (rc = check_view("o_local", o_local, s->dtype, true))) return rc;
-  if (!lse || !w) return fail(LLATTN_ERR_LAYOUT, "lse / w outputs must be non-null");
+  if ((rc = check_view("y", y, s->dtype, true))) return rc;
+  // forward only: o_local (null view or null pointer), lse and w may all be omitted together
+  const bool infer = (!o_local || !o_local->ptr) && !lse && !w;
+  if (!infer) {
+    if ((rc = check_view("o_local", o_local, s->dtype, true))) return rc;
+    if (!lse || !w) return fail(LLATTN_ERR_LAYOUT, "lse / w outputs must be non-null (or all of o_local, lse, w null)");
+    set_view(o_local, &a.ol, &a.o_sb, &a.o_st, &a.o_sh);
+  }
   set_view(y, &a.y, &a.y_sb, &a.y_st, &a.y_sh);
-  set_view(o_local, &a.ol, &a.o_sb, &a.o_st, &a.o_sh);
   a.lse = lse;
   a.w = w;
   const int dhp = padded_head_dim(s->Dh);

@@ -145,6 +145,40 @@ class LocalLatentLM(nn.Module):
     def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
         return self.lm_head(self.hidden(input_ids))
 
+    @torch.no_grad()
+    def next_token_logits(self, context: torch.Tensor) -> torch.Tensor:
+        """Logits ``[B, V]`` of the last position of each context row: the full forward over the context, which
+        reference generate.py:188-190 re-runs for every new token (the latent chunk and the local block depend
+        on the context length, so no earlier state can be reused), with the tied head applied to the last
+        position only and nothing kept for a backward."""
+        return self.lm_head(self.hidden(context)[:, -1])
+
+    @torch.no_grad()
+    def generate(self, prompt_ids: torch.Tensor, max_new_tokens: int, temperature: float = 0.0, top_k: int = 0,
+                 eos_token_id: Optional[int] = None, generator: Optional[torch.Generator] = None) -> torch.Tensor:
+        """Continue ``prompt_ids [1, P]`` by up to ``max_new_tokens`` tokens, one full re-forward of the last
+        ``max_seq_len`` tokens per new token (reference generate.py:169-204).  ``temperature`` 0 takes the
+        argmax, otherwise the token is drawn from softmax(logits / temperature), restricted to the ``top_k``
+        largest logits when ``top_k`` > 0.  Stops after ``eos_token_id``.  The reference sampler's repetition
+        penalty and n-gram bans (generation UX) are not part of this.  Returns ``[1, P + n]``."""
+        if prompt_ids.dim() != 2 or prompt_ids.shape[0] != 1 or prompt_ids.shape[1] == 0:
+            raise ValueError("prompt_ids must be a non-empty [1, P] tensor")
+        ids = prompt_ids
+        for _ in range(max_new_tokens):
+            logits = self.next_token_logits(ids[:, -self.config.max_seq_len:]).float()
+            if temperature <= 0.0:
+                nxt = logits.argmax(-1, keepdim=True)
+            else:
+                logits = logits / temperature
+                if top_k > 0:
+                    kth = torch.topk(logits, min(top_k, logits.shape[-1]), dim=-1).values[:, -1:]
+                    logits = logits.masked_fill(logits < kth, float("-inf"))
+                nxt = torch.multinomial(torch.softmax(logits, -1), 1, generator=generator)
+            ids = torch.cat([ids, nxt.to(ids.dtype)], dim=1)
+            if eos_token_id is not None and int(nxt) == eos_token_id:
+                break
+        return ids
+
     def _fused_norms(self, x: torch.Tensor) -> bool:
         """Whether each residual add runs inside the following norm (:func:`~llattn_amd.norm.add_rms_norm`): all
         norms are this module's GPU RMSNorm, the stream is fp32 and blocks are not checkpointed one by one."""

@@ -141,8 +141,10 @@ class LocalLatentAttentionTriton(nn.Module):
         if prof is not None:
             prof.lap("pool_ms")
         rqc = None if rq is None else rq.to(qkvr.dtype)
+        # forward only (no_grad, e.g. generation): the kernels skip what only the backward reads
+        saved = torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))
         y = LLAttnCore.apply(qkvr, rqc, gkgv.to(qkvr.dtype), self.gate_local.weight, self.gate_remote.weight,
-                             self.r_out.weight, self.r_out.bias, lay, prof, packed.get("r_out"))
+                             self.r_out.weight, self.r_out.bias, lay, prof, packed.get("r_out"), saved)
         if prof is not None:
             # the gate mix runs in the local kernel's epilogue: its time is in local_attention_ms
             prof.t["gate_mix_ms"] = 0.0

@@ -143,9 +143,12 @@ class _Prof:
             self._last = now
 
 
-def _core_forward(lay: L.Layout, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, r_b, dt, device, prof=None):
+def _core_forward(lay: L.Layout, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, r_b, dt, device, prof=None,
+                  saved: bool = True):
     """Latent attention -> r_out -> local attention + gate.  q/k/v/rq/gk/gv are
-    LlattnTensor views; returns (y, o_local, lse, w, lat, lse_lat, R)."""
+    LlattnTensor views; returns (y, o_local, lse, w, lat, lse_lat, R).  ``saved=False`` (no backward
+    follows): the kernels skip o_local, lse, w and the latent lse, returned as None (w is kept when
+    profiling, for the gate mean)."""
     B, T, H, Dh, Lh, Ldh = lay.B, lay.T, lay.H, lay.Dh, lay.Lh, lay.Ldh
     D, Ld = H * Dh, Lh * Ldh
     per_head = gate_l.dim() == 2 and gate_l.shape[0] > 1
@@ -154,9 +157,9 @@ def _core_forward(lay: L.Layout, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, r_b, 
     if prof is not None:
         prof.start()
     lat = _empty((B, lay.n_q, Lh, Ldh), dt, device)
-    lse_lat = _empty((B, Lh, lay.n_q), torch.float32, device)
+    lse_lat = _empty((B, Lh, lay.n_q), torch.float32, device) if saved else None
     _call("llattn_latent_fwd", _byref(shape), _byref(rq), _byref(gk), _byref(gv), _byref(L.view_bnhd(lat)),
-          lse_lat.data_ptr(), stream)
+          None if lse_lat is None else lse_lat.data_ptr(), stream)
     with torch.autocast(device_type="cuda", enabled=False):
         if dt == torch.bfloat16:
             R = linear_fwd(lat.view(B * lay.n_q, Ld), r_w.to(dt), None if r_b is None else r_b.float()).view(
@@ -166,13 +169,14 @@ def _core_forward(lay: L.Layout, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, r_b, 
     if prof is not None:
         prof.lap("latent_attention_ms")
     y = _empty((B, T, H, Dh), dt, device)
-    ol = _empty((B, T, H, Dh), dt, device)
-    lse = _empty((B, H, T), torch.float32, device)
-    w = _empty((B, H, T), torch.float32, device)
+    keep = saved or prof is not None
+    ol = _empty((B, T, H, Dh), dt, device) if keep else None
+    lse = _empty((B, H, T), torch.float32, device) if keep else None
+    w = _empty((B, H, T), torch.float32, device) if keep else None
     _call("llattn_local_gate_fwd", _byref(shape), _byref(q), _byref(k), _byref(v),
           _byref(L.view(R, R.stride(0), R.stride(1), Dh)), gate_l.data_ptr(),
-          gate_r.data_ptr(), _byref(L.view_bnhd(y)), _byref(L.view_bnhd(ol)),
-          lse.data_ptr(), w.data_ptr(), stream)
+          gate_r.data_ptr(), _byref(L.view_bnhd(y)), None if ol is None else _byref(L.view_bnhd(ol)),
+          None if lse is None else lse.data_ptr(), None if w is None else w.data_ptr(), stream)
     if prof is not None:
         prof.lap("local_attention_ms")
     return y, ol, lse, w, lat, lse_lat, R
@@ -239,7 +243,8 @@ class LLAttnCore(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, qkv, rq, gkgv, gate_l, gate_r, r_w, r_b, lay: L.Layout, prof=None, r_w_cast=None):
+    def forward(ctx, qkv, rq, gkgv, gate_l, gate_r, r_w, r_b, lay: L.Layout, prof=None, r_w_cast=None,
+                saved: bool = True):
         L.require_gpu(qkv, rq, gkgv)
         dt, device = qkv.dtype, qkv.device
         H, Dh, Lh, Ldh = lay.H, lay.Dh, lay.Lh, lay.Ldh
@@ -263,8 +268,10 @@ class LLAttnCore(torch.autograd.Function):
         gv = L.view(gkgv, gkgv.stride(0), gkgv.stride(1), Ldh, Ld)
         # cast once (or given cast): the backward's input gradient reuses it
         r_wd = r_w_cast if r_w_cast is not None and r_w_cast.dtype == dt else r_w.detach().to(dt)
-        y, ol, lse, w, lat, lse_lat, R = _core_forward(lay, q, k, v, rqv, gk, gv, gl, gr, r_wd, r_b, dt, device, prof)
-        ctx.save_for_backward(qkv, rq, gkgv, gl, gr, r_wd, lat, lse_lat, R, ol, lse, w)
+        y, ol, lse, w, lat, lse_lat, R = _core_forward(lay, q, k, v, rqv, gk, gv, gl, gr, r_wd, r_b, dt, device, prof,
+                                                       saved=saved)
+        if saved:
+            ctx.save_for_backward(qkv, rq, gkgv, gl, gr, r_wd, lat, lse_lat, R, ol, lse, w)
         ctx.lay, ctx.has_rb, ctx.packed = lay, r_b is not None, rq is None
         ctx.r_w_dtype = r_w.dtype
         ctx.gate_like = (gate_l, gate_r)
@@ -301,7 +308,7 @@ class LLAttnCore(torch.autograd.Function):
                                               R, ol, lse, w, dq, dk, dv, drq, dgk, dgv, dt, device)
         gate_l, gate_r = ctx.gate_like
         return (dqkv, drq_t, dgkgv, _gate_grad(dgl, gate_l), _gate_grad(dgr, gate_r), dr_w.to(ctx.r_w_dtype),
-                None if dr_b is None else dr_b.to(ctx.r_b_dtype), None, None, None)
+                None if dr_b is None else dr_b.to(ctx.r_b_dtype), None, None, None, None)
 
 
 # ---------------------------------------------------------------------------

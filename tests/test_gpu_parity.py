@@ -189,6 +189,10 @@ OP_CASES = [
     (1, 140, 2, 32, 1, 128, 20, 32, 2, 0),      # latent head dim 128, 70 latents (two latent tiles)
     (1, 1100, 1, 32, 1, 16, 16, 64, 8, 0),      # 3 query segments x 9 latent tiles in the latent backward
     (2, 700, 2, 64, 2, 32, 48, 128, 7, 9),      # macro-block queries over several query tiles
+    # fused bf16 backward (W <= 64) with local blocks >= 64 that are not multiples of 64: 64-row query
+    # tiles that straddle a block boundary (the qr0 + row >= block branch of its key bounds)
+    (1, 400, 2, 64, 2, 32, 48, 100, 10, 0),
+    (2, 333, 2, 88, 2, 16, 64, 96, 7, 0),
 ]
 
 

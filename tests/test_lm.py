@@ -232,3 +232,68 @@ def test_odd_vocabulary_takes_the_full_logits_loss(monkeypatch):
     ids = torch.randint(0, 50257, (1, 16))
     loss, _ = model.loss(ids, ids)
     assert seen == ["full"] and abs(float(loss) - float(np.log(50257))) < 1e-3
+
+
+def _oracle_lm(meta, params):
+    import bench
+    m = _build(meta, _oracle_attention_factory(), bench.TorchRMSNorm).double()
+    m.load_state_dict({k: torch.from_numpy(v) for k, v in params.items()}, strict=False)
+    return m.eval()
+
+
+def test_generate_loop_matches_manual_reforward_on_cpu():
+    """LocalLatentLM.generate against a literal replay of reference generate.py:188-190 (context = the last
+    max_seq_len tokens, full forward, argmax of the last position) on the oracle LM in float64; the prompt
+    of 60 tokens grows past max_seq_len = 64, so the context is cropped in the last steps."""
+    meta, z, params, _ = _lm_golden()
+    m = _oracle_lm(meta, params)
+    prompt = torch.from_numpy(z["inputs"][:1, :60])
+    got = m.generate(prompt, max_new_tokens=8)
+    ids = prompt
+    with torch.no_grad():
+        for _ in range(8):
+            logits = m(ids[:, -meta["max_seq_len"]:])
+            ids = torch.cat([ids, logits[:, -1].argmax(-1, keepdim=True)], dim=1)
+    assert got.shape == (1, 68) and torch.equal(got, ids)
+    # the tied head on the last position alone equals the last row of the full logits
+    with torch.no_grad():
+        np.testing.assert_allclose(m.next_token_logits(prompt).numpy(), m(prompt)[:, -1].numpy(), rtol=0, atol=1e-12)
+
+
+@pytest.mark.gpu
+def test_generation_replay_on_hip_lm_matches_reference():
+    """Reference generate.py:188-190 (a full re-forward of the context per new token) on the lm_tiny LM with
+    the HIP block in fp32: teacher-forced over prefixes of golden sequence 0, every step's last-position logits
+    match the oracle LM on the same prefix (1e-4), the full-length step matches the reference's golden logits,
+    and greedy decoding from a 58-token prompt (cropped at max_seq_len = 64) picks the oracle's tokens.  The
+    forward-only path runs: the local kernel gets no o_local / lse / w to write."""
+    from gpu_helpers import assert_fp32_close, require_cuda
+    from llattn_amd import ops
+    dev = require_cuda()
+    meta, z, params, _ = _lm_golden()
+    ref = _oracle_lm(meta, params)
+    hip = _build(meta).to(dev).eval()
+    hip.load_state_dict({k: torch.tensor(v, dtype=torch.float32) for k, v in params.items()}, strict=False)
+    seq = torch.from_numpy(z["inputs"][:1])
+    seen = []
+    real_call = ops._call
+
+    def spy(name, *args, **kw):
+        if name == "llattn_local_gate_fwd":
+            seen.append(args[8:11])  # o_local, lse, w
+        return real_call(name, *args, **kw)
+    ops._call = spy
+    try:
+        for t in range(40, seq.shape[1] + 1, 3):
+            ctx = seq[:, :t]
+            got = hip.next_token_logits(ctx.to(dev)).double().cpu().numpy()
+            with torch.no_grad():
+                want = ref.next_token_logits(ctx).numpy()
+            assert_fp32_close(got, want, f"prefix {t}")
+        got = hip.next_token_logits(seq.to(dev)).double().cpu().numpy()
+        assert_fp32_close(got, z["logits"][:1, -1], "full sequence vs golden logits")
+        gen = hip.generate(seq[:, :58].to(dev), max_new_tokens=10).cpu()
+    finally:
+        ops._call = real_call
+    assert seen and all(s == (None, None, None) for s in seen)
+    assert torch.equal(gen, ref.generate(seq[:, :58], max_new_tokens=10))
