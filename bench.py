@@ -134,9 +134,21 @@ def make_module(cfg, dev):
     return m.to(dev)
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(cfg, budget_s: float):
-    """The reference PyTorch path (fp32 torch restatement, autograd backward) on the host cores, on one
-    sequence of the workload, repeated until ``budget_s`` of CPU time."""
+    """The reference PyTorch path (fp32 torch restatement of reference models.py:307-462, autograd backward)
+    on the host cores, over the whole workload batch: one warm-up pass, then the median of three timed
+    fwd+bwd passes (one when the warm-up alone took more than ``budget_s`` seconds)."""
     from oracle import torch_ref
     from oracle.llattn_oracle import BlockShape
     torch.set_num_threads(os.cpu_count() or 1)
@@ -151,20 +163,23 @@ def cpu_baseline(cfg, budget_s: float):
               "r_out.weight": (D, Ld), "r_out.bias": (D,), "out.weight": (D, D), "out.bias": (D,),
               "gate_local.weight": (1, Dh), "gate_remote.weight": (1, Dh)}
     params = {n: torch.randn(s, generator=g) * 0.02 for n, s in shapes.items()}
-    x = torch.randn(1, cfg["T"], D, generator=g)
-    dout = torch.randn(1, cfg["T"], D, generator=g)
-    torch_ref.block_forward_backward(params, x, dout, shape)  # warm-up
-    n, t0 = 0, time.perf_counter()
-    while True:
+    B, T = cfg["B"], cfg["T"]
+    x = torch.randn(B, T, D, generator=g)
+    dout = torch.randn(B, T, D, generator=g)
+
+    def one():
+        t0 = time.perf_counter()
         torch_ref.block_forward_backward(params, x, dout, shape)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or n >= 200:
-            break
-    return {"value": round(n * cfg["T"] / el, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"{n} fwd+bwd passes of one {cfg['T']}-token sequence (batch row of the workload), fp32, "
-                      f"torch CPU restatement of the reference PyTorch path, {el:.1f} s"}
+        return time.perf_counter() - t0
+
+    warm = one()
+    runs = sorted(one() for _ in range(3 if warm <= budget_s else 1))
+    med = runs[len(runs) // 2]
+    return {"value": round(B * T / med, 1), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "cpu_count": os.cpu_count(), "cpu_model": cpu_model(),
+            "sample": f"the full workload batch ({B} x {T} tokens), fp32 fwd+bwd of the torch CPU restatement of "
+                      f"the reference PyTorch path; 1 warm-up ({warm:.1f} s), median of {len(runs)} timed passes "
+                      f"({', '.join(f'{r:.2f}' for r in runs)} s)"}
 
 
 class TorchPathAttention(nn.Module):
@@ -376,6 +391,11 @@ def bench_lm(args):
             "value": round(ntok / (ms_ref * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms_ref, 3),
             "what": "same model and weights with the reference PyTorch attention block (SDPA + eager latent), "
                     "torch RMSNorm and full logits + F.cross_entropy, same GPU, same run"}
+        result["sdpa_baseline"]["deviations"] = (
+            "SDPA is pinned to its memory-efficient backend for bf16 GPU inputs and the latent attention products "
+            "run in fp32: bf16 batched products with a transposed right operand (which SDPA's math path, its "
+            "backward and the reference's latent matmuls issue) are documented to fault MI355X boxes under this "
+            "software stack, so the reference's own calls are not run as written")
         result["speedup_vs_sdpa"] = round(ms_ref / ms, 3)
         result["first_step_loss"] = {"hip": round(first, 5), "sdpa": round(first_ref, 5)}
     return result
@@ -402,7 +422,8 @@ def main():
                     help="c2 (default), c3, c4: one attention layer; c5: a full training step of the 0.55b LM")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sdpa-baseline", action="store_true", help="c5: time the HIP model only")
-    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
+    ap.add_argument("--cpu-budget", type=float, default=15.0,
+                    help="CPU baseline: three timed passes after the warm-up when it took at most this many seconds")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 3 plain device copies of MIB MiB each (scale factor for rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE counters) and exit")
