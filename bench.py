@@ -362,6 +362,8 @@ def bench_lm(args):
         torch.cuda.empty_cache()
         torch.cuda.reset_peak_memory_stats()
         ref = build_model("0.55b", attention_factory=TorchPathAttention, norm_factory=TorchRMSNorm, **kw).to(dev)
+        for blk in ref.blocks:  # the reference FeedForward: torch GEMMs and a separate GELU
+            blk.ff.fused = False
         ref.load_state_dict(init)
         del init
         ms_ref, first_ref = run(ref, "PyTorch SDPA + eager latent block", False)

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define LLATTN_ABI_VERSION 5
+#define LLATTN_ABI_VERSION 6
 
 /* status codes */
 #define LLATTN_OK 0
@@ -196,6 +196,18 @@ typedef struct llattn_gemm_rowadd {
   int32_t rows_per_seq, seg, n_seg, divisor;
 } llattn_gemm_rowadd;
 
+/* Activation epilogues of llattn_gemm (bf16 C, a_trans = 0, no accumulation, no row addends), for the
+ * FeedForward around the block (reference models.py:50-58: w2(gelu(w1 x)), F.gelu exact):
+ *   LLATTN_ACT_GELU     with u = bf16(A B^T + bias) (the pre-activation):  C = bf16(gelu(u)), the
+ *                       input of w2, and aux = bf16(gelu'(u)), what its backward multiplies by;
+ *   LLATTN_ACT_MUL_AUX  C = bf16(bf16(A B...) * aux): the input gradient of w2 taken through the GELU
+ *                       with the aux that LLATTN_ACT_GELU wrote.
+ * gelu(u) = u Phi(u), gelu'(u) = Phi(u) + u phi(u) in fp32 on the bf16-rounded u (as bf16 autocast
+ * evaluates F.gelu); gelu'(u) is then rounded to bf16 once more than autocast's backward does. */
+#define LLATTN_ACT_NONE 0
+#define LLATTN_ACT_GELU 1
+#define LLATTN_ACT_MUL_AUX 2
+
 typedef struct llattn_gemm_desc {
   int32_t M, N, K;
   int32_t a_trans, b_trans;
@@ -214,6 +226,9 @@ typedef struct llattn_gemm_desc {
                           column of ones in place of the unused column N of the last tile (needs
                           b_trans = 1, fp32 C and N % 256 != 0); overwritten, never accumulated */
   llattn_gemm_rowadd rowadd[2]; /* bf16 C, a_trans = 0, b_trans = 1 (input gradients) */
+  int32_t act;                  /* LLATTN_ACT_* */
+  void* aux;                    /* bf16 [M][ld_aux]: gelu' written (LLATTN_ACT_GELU) or read (_MUL_AUX) */
+  int64_t ld_aux;
 } llattn_gemm_desc;
 
 size_t llattn_gemm_workspace_size(const llattn_gemm_desc* d);

@@ -61,7 +61,63 @@ struct GemmArgs {
   const uint16_t* ra_ptr[2];
   int64_t ra_ld[2];
   int ra_T[2], ra_seg[2], ra_nseg[2], ra_div[2];
+  // bf16 C only: LLATTN_ACT_GELU writes C = gelu(pre), aux = gelu'(pre); LLATTN_ACT_MUL_AUX scales C by aux
+  int act;
+  uint16_t* aux;
+  int64_t ld_aux;
 };
+
+// Exact GELU u * Phi(u) of the reference FeedForward (reference models.py:57, F.gelu) and its derivative
+// Phi(u) + u phi(u), in fp32.  erf comes from Abramowitz & Stegun 7.1.26 (Handbook of Mathematical
+// Functions): erf(z) = 1 - t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-z^2), t = 1 / (1 + p z), z >= 0,
+// absolute error below 1.5e-7 (far under the bf16 rounding of the outputs).  With z = |u| / sqrt(2),
+// exp(-z^2) = exp(-u^2 / 2) is also the Gaussian density's exponential, so Phi and phi share one exp:
+//   q = t P(t) exp(-u^2/2) / 2,  Phi(u) = 1 - q (u >= 0) or q (u < 0),  phi(u) = exp(-u^2/2) / sqrt(2 pi).
+struct NormalCdf {
+  float cdf, pdf;
+};
+__device__ __forceinline__ NormalCdf normal_cdf_pdf(float u) {
+  constexpr float p = 0.3275911f, a1 = 0.254829592f, a2 = -0.284496736f, a3 = 1.421413741f,
+                  a4 = -1.453152027f, a5 = 1.061405429f;
+  const float z = fabsf(u) * 0.70710678118654752f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(p, z, 1.f));
+  const float poly = t * fmaf(t, fmaf(t, fmaf(t, fmaf(t, a5, a4), a3), a2), a1);
+  const float e = __builtin_amdgcn_exp2f(-0.5f * 1.4426950408889634f * u * u);  // exp(-u^2 / 2)
+  const float q = 0.5f * poly * e;
+  return NormalCdf{u >= 0.f ? 1.f - q : q, e * 0.39894228040143268f};
+}
+// gelu(u) and gelu'(u) of one value
+__device__ __forceinline__ void gelu_pair(float u, float& g, float& gp) {
+  const NormalCdf n = normal_cdf_pdf(u);
+  g = u * n.cdf;
+  gp = fmaf(u, n.pdf, n.cdf);
+}
+// Eight bf16 pre-activations (packed pairs; the activation acts on the bf16-rounded value, as bf16
+// autocast does) -> gelu and gelu' as bf16.
+__device__ __forceinline__ void gelu_bf16x8(uint4 x, uint4& g, uint4& gp) {
+  const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+  uint32_t o[4], d[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float g0, g1, p0, p1;
+    gelu_pair(__uint_as_float(xs[e] << 16), g0, p0);
+    gelu_pair(__uint_as_float(xs[e] & 0xffff0000u), g1, p1);
+    o[e] = pack_bf16x2(g0, g1);
+    d[e] = pack_bf16x2(p0, p1);
+  }
+  g = make_uint4(o[0], o[1], o[2], o[3]);
+  gp = make_uint4(d[0], d[1], d[2], d[3]);
+}
+// bf16 x * s elementwise (eight packed values each)
+__device__ __forceinline__ uint4 mul_bf16x8(uint4 x, uint4 s) {
+  const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, ss[4] = {s.x, s.y, s.z, s.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    o[e] = pack_bf16x2(__uint_as_float(xs[e] << 16) * __uint_as_float(ss[e] << 16),
+                       __uint_as_float(xs[e] & 0xffff0000u) * __uint_as_float(ss[e] & 0xffff0000u));
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
 
 // Row of addend q (0, 1) that C row m reads, and its scale (the pooled gradient broadcast to its tokens).
 __device__ __forceinline__ const uint16_t* rowadd_row(const GemmArgs& a, int q, int m, float& sc) {
@@ -348,8 +404,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
             v[2 * e + 1] += __uint_as_float(os[e] & 0xffff0000u);
           }
         }
-        st16(pc, make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
-                            pack_bf16x2(v[6], v[7])));
+        const uint4 xo = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                                    pack_bf16x2(v[6], v[7]));
+        if (a.act == LLATTN_ACT_GELU) {
+          uint4 g, gp;
+          gelu_bf16x8(xo, g, gp);
+          st16(pc, g);
+          st16(a.aux + (int64_t)row * a.ld_aux + col, gp);
+        } else {
+          st16(pc, xo);
+        }
       }
     }
   } else {
@@ -423,7 +487,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
           }
           x = make_uint4(rs[0], rs[1], rs[2], rs[3]);
         }
-        st16(p, x);
+        uint16_t* pa = a.aux + (int64_t)row * a.ld_aux + col;
+        if (a.act == LLATTN_ACT_MUL_AUX) x = mul_bf16x8(x, ld16(pa));
+        if (a.act == LLATTN_ACT_GELU) {
+          uint4 g, gp;
+          gelu_bf16x8(x, g, gp);
+          st16(p, g);
+          st16(pa, gp);
+        } else {
+          st16(p, x);
+        }
       }
     }
   } else {
@@ -473,10 +546,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
 // instead of in a burst that every CU pays at the same moment.
 //
 // Memory operations per tile boundary are fixed (one DMA of the next tile's bias slice into LDS,
-// 32 stores; masked lanes use out-of-range buffer offsets, and the first tile issues the same 33
-// with nothing to store), so the vmcnt immediates below are exact: the first three k steps after
-// a boundary wait with 49 younger operations in flight, the others with 16.
-constexpr int EPI_OPS = 1 + 32;  // bias DMA + stores per tile boundary
+// 32 stores, 32 more for the GELU output; masked lanes use out-of-range buffer offsets, and the first
+// tile issues the same ones with nothing to store), so the vmcnt immediates below are exact: the
+// first three k steps after a boundary wait with 16 + EPI_OPS younger operations in flight (at most
+// 63, the counter's range: with the GELU output the oldest stores are waited for too), the others
+// with 16.
+template <int ACT>
+constexpr int epi_ops() { return 1 + 32 * (ACT == LLATTN_ACT_GELU ? 2 : 1); }  // bias DMA + stores per boundary
 
 // Byte offsets relative to the tile origin (row/column 0 of the tile, k = 0) of this lane's
 // 16-byte chunk in each of the wave's blocks of a k-contiguous operand tile.
@@ -509,7 +585,9 @@ __device__ __forceinline__ void tile_origin(const GemmArgs& a, int v, int total,
   n0 = ((t % (GM * a.tiles_n)) / gm) * BN;
 }
 
+template <int ACT>
 __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) {
+  constexpr int EPI_OPS = epi_ops<ACT>();
   __shared__ __align__(1024) unsigned char smem[NST * STAGE_BYTES];
   __shared__ __align__(16) float sbias[2][BN];  // bias of the tile being finished / fetched, by tile parity
   const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
@@ -545,6 +623,8 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
 
   // C through a range-checked buffer (a masked lane's offset is past the extent)
   const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.C, ((int64_t)(a.M - 1) * a.ldc + a.N) * 2);
+  const __amdgpu_buffer_rsrc_t raux = make_rsrc(ACT == LLATTN_ACT_GELU ? a.aux : a.C,
+                                                ((int64_t)(a.M - 1) * (ACT == LLATTN_ACT_GELU ? a.ld_aux : a.ldc) + a.N) * 2);
   // this wave's 64-column slice of a tile's bias into sbias[slot] (lanes 0..15, 16 bytes each;
   // columns past N, or no bias: zero)
   auto bias_dma = [&](int n0t, int slot) {
@@ -576,8 +656,8 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
   }
   bias_dma(n0, 0);
 #pragma unroll
-  for (int u = 0; u < 32; ++u) __builtin_amdgcn_raw_buffer_store_b128(i32x4{0, 0, 0, 0}, rc, kOffOOB, 0, 0);
-  __builtin_amdgcn_s_waitcnt(wait_vm((NST - 1) * DMA_PER_STEP + EPI_OPS));
+  for (int u = 0; u < EPI_OPS - 1; ++u) __builtin_amdgcn_raw_buffer_store_b128(i32x4{0, 0, 0, 0}, rc, kOffOOB, 0, 0);
+  __builtin_amdgcn_s_waitcnt(wait_vm(std::min(63, (NST - 1) * DMA_PER_STEP + EPI_OPS)));
   __builtin_amdgcn_s_barrier();
   bf16x8 fa0[8], fb0[8], fa1[8], fb1[8];
 #pragma unroll
@@ -630,7 +710,7 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  using W56 = std::integral_constant<int, 2 * DMA_PER_STEP + EPI_OPS>;
+  using W56 = std::integral_constant<int, std::min(63, 2 * DMA_PER_STEP + EPI_OPS)>;
   using W16 = std::integral_constant<int, 2 * DMA_PER_STEP>;
 
   while (true) {
@@ -661,7 +741,15 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
         const uint4 x = make_uint4(pack_bf16x2(u[0] + b0.x, u[1] + b0.y), pack_bf16x2(u[2] + b0.z, u[3] + b0.w),
                                    pack_bf16x2(w[0] + b1.x, w[1] + b1.y), pack_bf16x2(w[2] + b1.z, w[3] + b1.w));
         const uint32_t oc = (row < a.M && col < a.N) ? (uint32_t)((int64_t)row * a.ldc + col) * 2u : kOffOOB;
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, x), rc, oc, 0, 0);
+        if constexpr (ACT == LLATTN_ACT_GELU) {
+          uint4 g, gp;
+          gelu_bf16x8(x, g, gp);
+          const uint32_t oa = (row < a.M && col < a.N) ? (uint32_t)((int64_t)row * a.ld_aux + col) * 2u : kOffOOB;
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, g), rc, oc, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, gp), raux, oa, 0, 0);
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, x), rc, oc, 0, 0);
+        }
       }
     }
     if (vn >= total) break;
@@ -733,6 +821,18 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs a, in
     }
     if (a.ra_ptr[0]) rowadd4(a, 0, row, col, v);
     if (a.ra_ptr[1]) rowadd4(a, 1, row, col, v);
+    if (a.act) {  // the activation acts on the bf16-rounded value
+      uint16_t* pa = a.aux + (int64_t)row * a.ld_aux + col;
+      float h[4];
+      if (a.act == LLATTN_ACT_MUL_AUX) load4<uint16_t>(pa, h);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float xb = round_t<uint16_t>(v[e]);
+        if (a.act == LLATTN_ACT_GELU) gelu_pair(xb, v[e], h[e]);
+        else v[e] = xb * h[e];
+      }
+      if (a.act == LLATTN_ACT_GELU) store4<uint16_t>(pa, h);
+    }
     store4<uint16_t>(c, v);
   }
 }
@@ -755,16 +855,30 @@ void launch(const GemmArgs& a, int S, int c_dtype, hipStream_t st) {
   }
 }
 
-// Number of K splits: 1 when the output tiles alone fill most of the chip,
-// otherwise as many as keep every workgroup in ONE round on the 256 CUs (one
-// 128 KB workgroup per CU) with at least four 64-wide k steps per split.  A
-// second, mostly idle round of workgroups costs more than the partials.
+// Number of K splits: 1 when the output tiles alone fill most of the chip; otherwise the split count S
+// that minimises a time model of the product: the busiest CU runs ceil(tiles S / 256) workgroups of
+// 1/S of a tile's k range each (one 128 KB workgroup per CU), plus the fp32 partials that the ordered
+// reduction reads and writes (S M N 4 bytes at ~5 TB/s, against a tile rate of ~4.4 TFLOP/s per CU).
+// Each split keeps at least four 64-wide k steps.  E.g. 96 tiles (a 4096 x 1408 weight gradient): 8
+// splits fill three rounds exactly, where 2 would leave a quarter of the CUs idle.
 int resolve_split(const llattn_gemm_desc* d) {
   if (d->split_k > 0) return d->split_k;
   const int64_t tiles = (int64_t)((d->M + BM - 1) / BM) * ((d->N + BN - 1) / BN);
   if (tiles >= 224) return 1;
-  const int64_t s = std::min<int64_t>(256 / tiles, (d->K + 2 * BK - 1) / (2 * BK) / 4);
-  return s < 1 ? 1 : (int)s;
+  const int64_t pairs = (d->K + 2 * BK - 1) / (2 * BK);
+  const int64_t smax = std::max<int64_t>(1, pairs / 4);
+  const double t_tile = 2.0 * BM * BN * (double)pairs * (2 * BK) / 4.4e12;  // seconds per whole tile
+  int best = 1;
+  double best_t = 1e30;
+  for (int64_t S = 1; S <= std::min<int64_t>(smax, 64); ++S) {
+    const double rounds = (double)((tiles * S + 255) / 256);
+    const double t = rounds / (double)S * t_tile + (S > 1 ? 2.0 * S * d->M * (double)d->N * 4.0 / 5e12 : 0.0);
+    if (t < best_t * 0.999) {
+      best_t = t;
+      best = (int)S;
+    }
+  }
+  return best;
 }
 
 }  // namespace gemm
@@ -826,6 +940,18 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
     if ((uintptr_t)ra.ptr % 8 || ra.ld % 4 || ra.ld < d->N)
       return fail(LLATTN_ERR_LAYOUT, "llattn_gemm: row addend %d must be 8-byte aligned with ld >= N, a multiple of 4", q);
   }
+  if (d->act != LLATTN_ACT_NONE) {
+    if (d->act != LLATTN_ACT_GELU && d->act != LLATTN_ACT_MUL_AUX)
+      return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: unknown activation %d", d->act);
+    if (d->c_dtype != LLATTN_BF16 || d->accumulate || d->a_trans || d->rowadd[0].ptr || d->rowadd[1].ptr)
+      return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: an activation needs bf16 C, a k-contiguous A, no "
+                  "accumulation and no row addends");
+    if (!d->aux || !aligned16(d->aux) || d->ld_aux % 8 || d->ld_aux < d->N)
+      return fail(LLATTN_ERR_LAYOUT, "llattn_gemm: the activation's aux matrix must be 16-byte aligned with "
+                  "ld_aux >= N, a multiple of 8");
+    if (((int64_t)(d->M - 1) * d->ld_aux + d->N) * 2 >= (int64_t(1) << 31))
+      return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: the activation's aux matrix must be below 2 GiB");
+  }
   const size_t need = llattn_gemm_workspace_size(d);
   if (need && (!workspace || workspace_bytes < need || !aligned16(workspace)))
     return fail(LLATTN_ERR_WORKSPACE, "llattn_gemm: %d K splits need %zu workspace bytes (got %zu)", S, need,
@@ -848,6 +974,9 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
     a.ra_nseg[q] = d->rowadd[q].n_seg;
     a.ra_div[q] = d->rowadd[q].divisor;
   }
+  a.act = d->act;
+  a.aux = static_cast<uint16_t*>(d->aux);
+  a.ld_aux = d->ld_aux;
   hipStream_t st = static_cast<hipStream_t>(stream);
   // bf16 x Wᵀ (+ bias) without K split or accumulation: the persistent kernel, one workgroup per CU
   const int64_t c_bytes = ((int64_t)(d->M - 1) * d->ldc + d->N) * 2;
@@ -857,7 +986,10 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
       cus = 256;
     const int tiles = a.tiles_m * a.tiles_n;
-    hipLaunchKernelGGL(gemm_persistent_kernel, dim3(std::min(tiles, cus)), dim3(256), 0, st, a);
+    if (a.act == LLATTN_ACT_GELU)
+      hipLaunchKernelGGL(gemm_persistent_kernel<LLATTN_ACT_GELU>, dim3(std::min(tiles, cus)), dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL(gemm_persistent_kernel<LLATTN_ACT_NONE>, dim3(std::min(tiles, cus)), dim3(256), 0, st, a);
   } else if (!d->a_trans && !d->b_trans) launch<true, true>(a, S, d->c_dtype, st);
   else if (!d->a_trans && d->b_trans) launch<true, false>(a, S, d->c_dtype, st);
   else if (d->a_trans && d->b_trans) launch<false, false>(a, S, d->c_dtype, st);

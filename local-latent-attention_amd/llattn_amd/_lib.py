@@ -16,11 +16,12 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libllattn_gfx950.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 OK, ERR_SHAPE, ERR_DTYPE, ERR_LAYOUT, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_LAUNCH = range(7)
 F32, BF16 = 0, 1
 DIV_COUNT, DIV_SEG, DIV_ONE = 0, 1, 2
+ACT_NONE, ACT_GELU, ACT_MUL_AUX = 0, 1, 2
 WS_LOCAL_BWD, WS_LATENT_BWD = 0, 1
 NOALLOC_SCRATCH_BYTES = 8 << 20  # LLATTN_NOALLOC_SCRATCH_BYTES
 
@@ -47,7 +48,8 @@ class LlattnGemmDesc(ctypes.Structure):
                 ("b_trans", ctypes.c_int32), ("A", ctypes.c_void_p), ("lda", ctypes.c_int64), ("B", ctypes.c_void_p),
                 ("ldb", ctypes.c_int64), ("C", ctypes.c_void_p), ("ldc", ctypes.c_int64), ("c_dtype", ctypes.c_int32),
                 ("accumulate", ctypes.c_int32), ("bias", ctypes.c_void_p), ("split_k", ctypes.c_int32),
-                ("a_rowsum", ctypes.c_void_p), ("rowadd", LlattnGemmRowadd * 2)]
+                ("a_rowsum", ctypes.c_void_p), ("rowadd", LlattnGemmRowadd * 2), ("act", ctypes.c_int32),
+                ("aux", ctypes.c_void_p), ("ld_aux", ctypes.c_int64)]
 
 
 _P = ctypes.c_void_p

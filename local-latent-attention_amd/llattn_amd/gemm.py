@@ -29,7 +29,7 @@ def _check2d(name: str, t: torch.Tensor) -> None:
 
 def _run(M: int, N: int, K: int, A: torch.Tensor, a_trans: bool, B: torch.Tensor, b_trans: bool, C: torch.Tensor,
          bias: torch.Tensor | None, accumulate: bool, split_k: int = 0, rowsum: torch.Tensor | None = None,
-         rowadd=()) -> None:
+         rowadd=(), act: int = 0, aux: torch.Tensor | None = None) -> None:
     L.require_gpu(A, B, C)
     if rowsum is not None and (rowsum.dtype != torch.float32 or not rowsum.is_contiguous() or rowsum.numel() != M):
         raise ValueError(f"rowsum must be a contiguous fp32 vector of {M} elements")
@@ -43,6 +43,12 @@ def _run(M: int, N: int, K: int, A: torch.Tensor, a_trans: bool, B: torch.Tensor
                             None if rowsum is None else rowsum.data_ptr())
     if len(rowadd) > 2:
         raise ValueError("at most two row addends")
+    if act:
+        if aux is None or aux.dtype != torch.bfloat16 or aux.dim() != 2 or aux.stride(1) != 1 \
+                or tuple(aux.shape) != (M, N):
+            raise ValueError(f"the activation's aux must be a bf16 [{M}, {N}] view with a contiguous inner dimension")
+        L.require_gpu(aux)
+        desc.act, desc.aux, desc.ld_aux = act, aux.data_ptr(), aux.stride(0)
     for q, (rows, per_seq, seg, n_seg, divisor) in enumerate(rowadd):
         if rows.dtype != torch.bfloat16 or rows.stride(-1) != 1 or rows.shape[-1] != N:
             raise ValueError(f"row addend {q} must be bf16 rows of {N} contiguous elements")
@@ -67,6 +73,35 @@ def linear(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None, o
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
     _run(M, N, K, x, False, w, False, out, bias, accumulate)
+    return out
+
+
+def linear_gelu(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None):
+    """With ``h = x [M, K] @ w [N, K]^T (+ bias)`` rounded to bf16: ``(gelu(h), gelu'(h))`` (exact GELU and its
+    derivative) from one GEMM, both bf16 ``[M, N]``."""
+    _check2d("x", x)
+    _check2d("w", w)
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError(f"x is [{M}, {K}] but w is {tuple(w.shape)}")
+    g = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    gp = torch.empty_like(g)
+    _run(M, N, K, x, False, w, False, g, bias, False, act=L.ACT_GELU, aux=gp)
+    return g, gp
+
+
+def matmul_nn_scaled(a: torch.Tensor, b: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    """``bf16(a [M, K] @ b [K, N]) * s`` elementwise in bf16 (``s`` bf16 ``[M, N]``): with ``s = gelu'(h)`` from
+    :func:`linear_gelu`, the input gradient of a projection whose input was ``gelu(h)``, through the GELU."""
+    _check2d("a", a)
+    _check2d("b", b)
+    M, K = a.shape
+    N = b.shape[1]
+    if b.shape[0] != K:
+        raise ValueError(f"a is [{M}, {K}] but b is {tuple(b.shape)}")
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    _run(M, N, K, a, False, b, True, out, None, False, act=L.ACT_MUL_AUX, aux=s)
     return out
 
 

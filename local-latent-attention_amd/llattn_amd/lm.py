@@ -46,15 +46,22 @@ class RMSNorm(nn.Module):
 
 
 class FeedForward(nn.Module):
-    """reference models.py:50-58 (``w2(gelu(w1 x))``; dropout 0 is the identity)."""
+    """reference models.py:50-58 (``w2(gelu(w1 x))``; dropout 0 is the identity).  Under bf16 autocast on the
+    GPU it runs as :func:`llattn_amd.ffn.feed_forward` (the GELU in the GEMM epilogues)."""
 
     def __init__(self, config: ModelConfig) -> None:
         super().__init__()
         self.w1 = nn.Linear(config.d_model, config.d_ff)
         self.w2 = nn.Linear(config.d_ff, config.d_model)
         self.dropout = nn.Dropout(config.dropout)
+        self.fused = True  # False: the reference's separate torch ops (a comparison model sets it)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        # bf16 autocast on the GPU without active dropout: both products on the MFMA GEMM, GELU in their epilogues
+        if (self.fused and x.is_cuda and torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
+                and (self.dropout.p == 0.0 or not self.training)):
+            from .ffn import feed_forward
+            return feed_forward(x, self.w1, self.w2)
         return self.dropout(self.w2(F.gelu(self.w1(x))))
 
 

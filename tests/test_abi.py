@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_empty_error():
     L, lib = _lib()
-    assert lib.llattn_abi_version() == L.ABI_VERSION == 5
+    assert lib.llattn_abi_version() == L.ABI_VERSION == 6
 
 
 def _shape(L, **kw):
@@ -148,6 +148,11 @@ def _gemm_desc(L, **kw):
     (dict(lda=64), 3, b"leading dimensions"),
     (dict(ldc=128), 3, b"leading dimensions"),
     (dict(split_k=4, K=128), 4, b"at most one per 64-wide k step"),
+    (dict(act=5), 4, b"unknown activation"),
+    (dict(act=1, c_dtype=0), 4, b"an activation needs bf16 C"),
+    (dict(act=2, c_dtype=0), 4, b"an activation needs bf16 C"),
+    (dict(act=1), 3, b"aux matrix must be 16-byte aligned"),
+    (dict(act=1, aux=0x4000, ld_aux=100), 3, b"aux matrix must be 16-byte aligned"),
 ])
 def test_gemm_validation_codes(kw, code, msg):
     L, lib = _lib()

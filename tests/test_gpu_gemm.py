@@ -274,3 +274,70 @@ def test_pack_params_matches_torch_casts(sizes):
     assert torch.equal(outs[0].view(torch.int16), torch.cat(ts[:half]).to(torch.bfloat16).view(torch.int16))
     if ts[half:]:
         assert torch.equal(outs[1], torch.cat(ts[half:]))
+
+
+def _gelu_and_grad(u):
+    uu = u.float().requires_grad_(True)
+    g = torch.nn.functional.gelu(uu)
+    g.backward(torch.ones_like(g))
+    return g.detach(), uu.grad
+
+
+@pytest.mark.parametrize("M,N,K", [(32768, 4096, 1408), (300, 264, 200), (97, 40, 64)])
+def test_linear_gelu_epilogue(M, N, K):
+    """LLATTN_ACT_GELU: gelu and gelu' of the bf16-rounded pre-activation from one GEMM, against torch's F.gelu
+    and its backward on the bf16-rounded fp32 product (small M takes the split-K reduction)."""
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: linear gelu", M, N, K, flush=True)
+    g = torch.Generator(device=dev).manual_seed(M + 2 * N + K)
+    x, w = _rand(M, K, gen=g, dev=dev), _rand(N, K, gen=g, dev=dev) * 0.1
+    b = torch.randn(N, device=dev, generator=g) * 0.5
+    got_g, got_gp = gemm.linear_gelu(x, w, b)
+    ref_g, ref_gp = _gelu_and_grad((x.float() @ w.float().T + b).to(torch.bfloat16))
+    for got, ref in ((got_g, ref_g), (got_gp, ref_gp)):
+        assert got.dtype == torch.bfloat16
+        assert _err(got, ref) < BF16_TOL
+        # one bf16 rounding of the result, plus the rare pre-activation that rounds to the neighbouring bf16
+        assert float((got.float() - ref).abs().mean()) < 2 ** -8 * float(ref.abs().mean())
+
+
+@pytest.mark.parametrize("M,N,K", [(32768, 4096, 1408), (300, 264, 200), (97, 40, 64)])
+def test_matmul_nn_scaled_epilogue(M, N, K):
+    """LLATTN_ACT_MUL_AUX: bf16(dy W) * s elementwise, against torch on the bf16-rounded product."""
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: nn scaled", M, N, K, flush=True)
+    g = torch.Generator(device=dev).manual_seed(3 * M + N + K)
+    a, b = _rand(M, K, gen=g, dev=dev), _rand(K, N, gen=g, dev=dev) * 0.1
+    sc = _rand(M, N, gen=g, dev=dev)
+    got = gemm.matmul_nn_scaled(a, b, sc)
+    ref = (a.float() @ b.float()).to(torch.bfloat16).float() * sc.float()
+    assert _err(got, ref) < BF16_TOL
+
+
+def test_feed_forward_matches_fp32_reference():
+    """The LM's FeedForward under bf16 autocast (GELU in the GEMM epilogues) against fp32 w2(gelu(w1 x)) on the
+    same bf16-rounded input and weights: output, input gradient, weight and bias gradients."""
+    from llattn_amd.ffn import feed_forward
+    dev = require_cuda()
+    print("case: feed forward", flush=True)
+    torch.manual_seed(2)
+    w1, w2 = torch.nn.Linear(256, 1024).to(dev), torch.nn.Linear(1024, 256).to(dev)
+    x = torch.randn(2, 300, 256, device=dev).to(torch.bfloat16).requires_grad_(True)
+    dy = torch.randn(2, 300, 256, device=dev)
+    with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        y = feed_forward(x, w1, w2)
+    y.backward(dy.to(y.dtype))
+    xr = x.detach().float().requires_grad_(True)
+    p = {n: t.detach().to(torch.bfloat16).float().requires_grad_(True)
+         for n, t in (("w1", w1.weight), ("b1", w1.bias), ("w2", w2.weight), ("b2", w2.bias))}
+    yr = torch.nn.functional.linear(torch.nn.functional.gelu(torch.nn.functional.linear(xr, p["w1"], p["b1"])),
+                                    p["w2"], p["b2"])
+    yr.backward(dy.to(torch.bfloat16).float())
+    assert y.dtype == torch.bfloat16
+    assert _err(y, yr) < BF16_TOL
+    assert _err(x.grad, xr.grad) < BF16_TOL
+    for got, name in ((w1.weight.grad, "w1"), (w1.bias.grad, "b1"), (w2.weight.grad, "w2"), (w2.bias.grad, "b2")):
+        assert got.dtype == torch.float32
+        assert _err(got, p[name].grad) < 2e-2, name
