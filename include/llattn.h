@@ -254,6 +254,13 @@ int32_t llattn_colsum(const void* x, int64_t ld, int32_t M, int32_t N, float* ou
 int32_t llattn_cast(int32_t nseg, const float* const* src, void* const* dst, const int64_t* n,
                     const int32_t* dst_dtype, void* stream);
 
+/* dst[c][r] = src[r][c] for a bf16 matrix of rows x cols (both multiples of 8; 16-byte aligned, leading
+ * dimensions in elements, multiples of 8).  The input gradient dy W of a projection runs as
+ * dy (W^T)^T on the persistent GEMM (both operands k-contiguous) with this transposed copy of the bf16
+ * weight (reference models.py:80-84, the nn.Linear backward under autocast). */
+int32_t llattn_transpose(const void* src, int64_t ld_src, int32_t rows, int32_t cols, void* dst, int64_t ld_dst,
+                         void* stream);
+
 /* RMSNorm of the residual stream around the block (reference models.py:40-47,
  * F.rms_norm(x, (D,), w, eps), the LM's norm1 / norm2 / norm of reference
  * models.py:493-494, 513):

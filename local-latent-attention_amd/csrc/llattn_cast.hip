@@ -50,10 +50,51 @@ __global__ __launch_bounds__(256) void cast_kernel(const CastArgs a) {
   }
 }
 
+// dst[c][r] = src[r][c] for a bf16 matrix, in 64 x 64 tiles through LDS: 16-byte row reads of src and 16-byte
+// row writes of dst (rows and columns multiples of 8).  The padded LDS rows (72 elements) spread the
+// transposing element writes over the banks.
+__global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __restrict__ src, int64_t lds, int rows,
+                                                             int cols, uint16_t* __restrict__ dst, int64_t ldd) {
+  __shared__ uint16_t t[64][72];
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64, tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int q = tid + 256 * i, rl = q >> 3, cl = 8 * (q & 7);
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (r0 + rl < rows && c0 + cl < cols) v = *reinterpret_cast<const uint4*>(src + (int64_t)(r0 + rl) * lds + c0 + cl);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      t[cl + 2 * e][rl] = (uint16_t)(w[e] & 0xffffu);
+      t[cl + 2 * e + 1][rl] = (uint16_t)(w[e] >> 16);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int q = tid + 256 * i, cl = q >> 3, rl = 8 * (q & 7);
+    if (c0 + cl < cols && r0 + rl < rows)
+      *reinterpret_cast<uint4*>(dst + (int64_t)(c0 + cl) * ldd + r0 + rl) = *reinterpret_cast<const uint4*>(&t[cl][rl]);
+  }
+}
+
 }  // namespace
 }  // namespace llattn
 
 using namespace llattn;
+
+extern "C" int32_t llattn_transpose(const void* src, int64_t ld_src, int32_t rows, int32_t cols, void* dst,
+                                    int64_t ld_dst, void* stream) {
+  if (rows <= 0 || cols <= 0 || rows % 8 || cols % 8)
+    return fail(LLATTN_ERR_SHAPE, "llattn_transpose: rows %d and cols %d must be positive multiples of 8", rows, cols);
+  if (!src || !dst || !aligned16(src) || !aligned16(dst) || ld_src % 8 || ld_dst % 8 || ld_src < cols || ld_dst < rows)
+    return fail(LLATTN_ERR_LAYOUT, "llattn_transpose: 16-byte aligned matrices with leading dimensions >= their rows, "
+                "multiples of 8, needed");
+  const dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
+  hipLaunchKernelGGL(transpose_bf16_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(src), ld_src, rows, cols, static_cast<uint16_t*>(dst), ld_dst);
+  return check_launch("llattn_transpose");
+}
 
 extern "C" int32_t llattn_cast(int32_t nseg, const float* const* src, void* const* dst, const int64_t* n,
                                const int32_t* dst_dtype, void* stream) {

@@ -55,7 +55,7 @@ class _FeedForward(torch.autograd.Function):
                 dy2 = dy2.contiguous()
             dh = gemm.matmul_nn_scaled(dy2, w2b, gp)         # (dy W2) * gelu'(h), bf16
             dw2, db2 = weight_grad(dy2, g, has_b2)           # fp32
-            dx = gemm.matmul_nn(dh, w1b) if ctx.needs_input_grad[0] else None
+            dx = gemm.input_grad(dh, w1b) if ctx.needs_input_grad[0] else None
             dw1, db1 = weight_grad(dh, x2, has_b1)
         return (None if dx is None else dx.view(*lead, x2.shape[1]).to(xdt), dw1.to(w1dt),
                 None if db1 is None else db1.to(w1dt), dw2.to(w2dt), None if db2 is None else db2.to(w2dt))

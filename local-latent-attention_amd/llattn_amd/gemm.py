@@ -122,6 +122,30 @@ def matmul_nn(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None,
     return out
 
 
+def transpose(w: torch.Tensor) -> torch.Tensor:
+    """bf16 ``w [R, C]`` -> a new contiguous ``[C, R]`` (``llattn_transpose``)."""
+    _check2d("w", w)
+    L.require_gpu(w)
+    R, C = w.shape
+    out = torch.empty((C, R), dtype=torch.bfloat16, device=w.device)
+    from .ops import _call
+    _call("llattn_transpose", w.data_ptr(), w.stride(0), R, C, out.data_ptr(), out.stride(0), L.stream_ptr(w.device),
+          work=4 * R * C)
+    return out
+
+
+def input_grad(dy: torch.Tensor, w: torch.Tensor, rowadd=()) -> torch.Tensor:
+    """``dy [M, N] @ w [N, K]`` (+ the ``rowadd`` addends of :func:`matmul_nn`) -> bf16 ``[M, K]``, the input
+    gradient of ``y = x w^T``.  Without addends and for large M as ``dy (w^T)^T`` on the persistent kernel
+    with a transposed copy of ``w`` (both operands k-contiguous: plain LDS fragment reads, the epilogue
+    overlapped with the next tile); otherwise :func:`matmul_nn` (transposing fragment reads of ``w``)."""
+    M, N = dy.shape
+    K = w.shape[1]
+    if not rowadd and M >= 4096 and K % 8 == 0 and N % 8 == 0 and N > 64:
+        return linear(dy, transpose(w))
+    return matmul_nn(dy, w, rowadd=rowadd)
+
+
 def rowsum_supported(n: int) -> bool:
     """Whether :func:`matmul_tn` can also give the row sums of ``a^T`` for an output width ``n``: the sums are
     contracted against a column of ones in place of the unused column ``n`` of the last 256-wide tile."""

@@ -60,8 +60,8 @@ def linear_fwd(x2: torch.Tensor, w: torch.Tensor, b32: torch.Tensor | None) -> t
 
 def input_grad(dy2: torch.Tensor, w: torch.Tensor, rowadd=()) -> torch.Tensor:
     """bf16 ``dy2 @ w`` (w [N, K] read row-major), plus the broadcast ``rowadd`` pooling gradients
-    (:func:`llattn_amd.gemm.matmul_nn`)."""
-    return gemm.matmul_nn(dy2, w, rowadd=rowadd)
+    added in the GEMM's epilogue (:func:`llattn_amd.gemm.input_grad`)."""
+    return gemm.input_grad(dy2, w, rowadd=rowadd)
 
 
 def weight_grad(dy2: torch.Tensor, x2: torch.Tensor, bias_grad: bool = False):

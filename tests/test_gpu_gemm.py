@@ -341,3 +341,25 @@ def test_feed_forward_matches_fp32_reference():
     for got, name in ((w1.weight.grad, "w1"), (w1.bias.grad, "b1"), (w2.weight.grad, "w2"), (w2.bias.grad, "b2")):
         assert got.dtype == torch.float32
         assert _err(got, p[name].grad) < 2e-2, name
+
+
+@pytest.mark.parametrize("R,C", [(1408, 1408), (4736, 1408), (8, 16), (200, 72)])
+def test_transpose_bf16(R, C):
+    """llattn_transpose is an exact copy: bitwise equal to torch's transpose (ragged 64-tiles included)."""
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: transpose", R, C, flush=True)
+    g = torch.Generator(device=dev).manual_seed(R + C)
+    w = _rand(R, C, gen=g, dev=dev)
+    assert torch.equal(gemm.transpose(w), w.t().contiguous())
+
+
+@pytest.mark.parametrize("M,N,K", [(32768, 1408, 1408), (32768, 512, 1408), (4096, 1408, 4096), (300, 264, 128)])
+def test_input_grad_through_transposed_weight(M, N, K):
+    """dy @ w through the persistent kernel and a transposed weight (large M) or the tiled kernel (small M)."""
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: input grad", M, N, K, flush=True)
+    g = torch.Generator(device=dev).manual_seed(M + 3 * N + K)
+    dy, w = _rand(M, K, gen=g, dev=dev), _rand(K, N, gen=g, dev=dev)
+    assert _err(gemm.input_grad(dy, w), dy.float() @ w.float()) < BF16_TOL
