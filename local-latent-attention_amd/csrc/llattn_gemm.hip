@@ -855,6 +855,178 @@ void launch(const GemmArgs& a, int S, int c_dtype, hipStream_t st) {
   }
 }
 
+
+// ---------------------------------------------------------------------------------------------------------
+// Small products: the pooled-latent projection rkv_proj (reference models.py:333-342) and its backward have
+// a few hundred rows or a contraction of a few hundred (config 2: 256 x 1024 x 1408 and its transposes).
+// On the 256 x 256 tiles they run as ~20 workgroups whose pipelines never fill.  Here: 64 x 64 output tiles,
+// one 256-thread workgroup each (4 waves of 32 x 32), the whole contraction per workgroup in 64-wide k
+// chunks staged through two LDS panel buffers (the next chunk's loads in flight during the current chunk's
+// MFMAs).  Either operand may be k- or m/n-contiguous: k-contiguous rows are copied as 16-byte pieces,
+// m/n-contiguous ones are transposed on their way into LDS, so fragments are always k-contiguous.  LDS rows
+// of 64 k (128 bytes) with 16-byte chunk c of row r at c ^ ((r >> 1) & 7): conflict-free ds_read_b128.
+// ---------------------------------------------------------------------------------------------------------
+constexpr int SBT = 64, SBK = 64;
+
+__device__ __forceinline__ int sswz(int row) { return (row >> 1) & 7; }
+
+// This thread's two 16-byte pieces of a 64 x 64 operand panel (rows o0 .., k from k0) -> registers.
+template <bool KMAJ>
+__device__ __forceinline__ void small_load(uint4 (&v)[2], const uint16_t* base, int64_t ld, int o0, int omax, int k0,
+                                           int K, int tid) {
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int q = tid + 256 * u;
+    if constexpr (KMAJ) {  // piece: row q / 8, k 8 (q % 8) .. +7
+      const int row = o0 + (q >> 3), k = k0 + 8 * (q & 7);
+      v[u] = (row < omax && k < K) ? *reinterpret_cast<const uint4*>(base + (int64_t)row * ld + k)
+                                   : make_uint4(0u, 0u, 0u, 0u);
+    } else {  // piece: k-row q / 8, rows 8 (q % 8) .. +7 of the panel
+      const int k = k0 + (q >> 3), row = o0 + 8 * (q & 7);
+      v[u] = (k < K && row < omax) ? *reinterpret_cast<const uint4*>(base + (int64_t)k * ld + row)
+                                   : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+}
+template <bool KMAJ>
+__device__ __forceinline__ void small_store(const uint4 (&v)[2], unsigned char* panel, int tid) {
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int q = tid + 256 * u;
+    if constexpr (KMAJ) {
+      const int row = q >> 3, c = q & 7;
+      *reinterpret_cast<uint4*>(panel + row * 128 + ((c ^ sswz(row)) << 4)) = v[u];
+    } else {  // eight rows of one k: one element each
+      const int k = q >> 3, r0 = 8 * (q & 7);
+      const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int row = r0 + e;
+        *reinterpret_cast<uint16_t*>(panel + row * 128 + (((k >> 3) ^ sswz(row)) << 4) + 2 * (k & 7)) =
+            (uint16_t)((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu));
+      }
+    }
+  }
+}
+
+template <bool AK, bool BKM, int EPI>
+__global__ __launch_bounds__(256) void gemm_small_kernel(const GemmArgs a) {
+  __shared__ __align__(16) unsigned char As[2][SBT * 128], Bs[2][SBT * 128];
+  __shared__ float rsum[SBT];
+  const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
+  const int wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
+  const int tn_count = (a.N + SBT - 1) / SBT;
+  const int tm = blockIdx.x / tn_count, tn = blockIdx.x % tn_count;
+  const int m0 = tm * SBT, n0 = tn * SBT;
+  const bool want_rowsum = a.rowsum && tn == 0;
+  const int nchunks = (a.K + SBK - 1) / SBK;
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float rs = 0.f;  // threads 0..63: the row sum of A row m0 + tid
+  // chunk c's loads land in register set c % 4: four chunks in flight ahead of the MFMAs
+  uint4 va[4][2], vb[4][2];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    small_load<AK>(va[d], a.A, a.lda, m0, a.M, d * SBK, a.K, tid);
+    small_load<BKM>(vb[d], a.B, a.ldb, n0, a.N, d * SBK, a.K, tid);
+  }
+  auto chunk = [&](int c, uint4 (&ra)[2], uint4 (&rb)[2]) {
+    unsigned char* pa = As[c & 1];
+    unsigned char* pb = Bs[c & 1];
+    small_store<AK>(ra, pa, tid);
+    small_store<BKM>(rb, pb, tid);
+    __syncthreads();  // the panels of chunk c are complete; the other buffer (chunk c-1) is no longer read
+    if (c + 4 < nchunks) {  // this register set is free again: chunk c + 4
+      small_load<AK>(ra, a.A, a.lda, m0, a.M, (c + 4) * SBK, a.K, tid);
+      small_load<BKM>(rb, a.B, a.ldb, n0, a.N, (c + 4) * SBK, a.K, tid);
+    }
+    if (want_rowsum && tid < SBT) {
+#pragma unroll
+      for (int cc = 0; cc < 8; ++cc) {
+        const uint4 x = *reinterpret_cast<const uint4*>(pa + tid * 128 + ((cc ^ sswz(tid)) << 4));
+        const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rs += __uint_as_float(w[e] << 16) + __uint_as_float(w[e] & 0xffff0000u);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {  // two 32-wide k steps per chunk
+      bf16x8 fa[2], fb[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int row = wm * 32 + 16 * i + r, cc = 4 * h + g;
+        fa[i] = *reinterpret_cast<const bf16x8*>(pa + row * 128 + ((cc ^ sswz(row)) << 4));
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int row = wn * 32 + 16 * j + r, cc = 4 * h + g;
+        fb[j] = *reinterpret_cast<const bf16x8*>(pb + row * 128 + ((cc ^ sswz(row)) << 4));
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();  // every wave is done with buffer c & 1 before chunk c + 2 overwrites it
+  };
+  for (int c = 0; c < nchunks; c += 4) {
+    chunk(c, va[0], vb[0]);
+    if (c + 1 < nchunks) chunk(c + 1, va[1], vb[1]);
+    if (c + 2 < nchunks) chunk(c + 2, va[2], vb[2]);
+    if (c + 3 < nchunks) chunk(c + 3, va[3], vb[3]);
+  }
+  if (want_rowsum && tid < SBT && m0 + tid < a.M) a.rowsum[m0 + tid] = rs;
+  // lane (r, g) holds C[m0 + wm*32 + 16i + r][n0 + wn*32 + 16j + 4g + e]
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int col = n0 + wn * 32 + 16 * j + 4 * g;
+    if (col >= a.N) continue;
+    const float4 b4 = (EPI == EPI_BF16 && a.bias) ? *reinterpret_cast<const float4*>(a.bias + col)
+                                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = m0 + wm * 32 + 16 * i + r;
+      if (row >= a.M) continue;
+      float v[4] = {acc[i][j][0] + b4.x, acc[i][j][1] + b4.y, acc[i][j][2] + b4.z, acc[i][j][3] + b4.w};
+      if constexpr (EPI == EPI_BF16) {
+        uint16_t* p = static_cast<uint16_t*>(a.C) + (int64_t)row * a.ldc + col;
+        if (a.accumulate) {
+          float o[4];
+          load4<uint16_t>(p, o);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] += o[e];
+        }
+        store4<uint16_t>(p, v);
+      } else {
+        float* p = static_cast<float*>(a.C) + (int64_t)row * a.ldc + col;
+        if (a.accumulate) {
+          const float4 o = *reinterpret_cast<const float4*>(p);
+          v[0] += o.x; v[1] += o.y; v[2] += o.z; v[3] += o.w;
+        }
+        *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+      }
+    }
+  }
+}
+
+template <bool AK, bool BKM>
+void launch_small(const GemmArgs& a, int c_dtype, hipStream_t st) {
+  const dim3 grid(((a.M + SBT - 1) / SBT) * ((a.N + SBT - 1) / SBT)), block(256);
+  if (c_dtype == LLATTN_F32) hipLaunchKernelGGL((gemm_small_kernel<AK, BKM, EPI_F32>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((gemm_small_kernel<AK, BKM, EPI_BF16>), grid, block, 0, st, a);
+}
+
+// The small-tile path: no K split requested, no activation or row addends, an output of at most 32 tiles of
+// 256 x 256 with one side at most 1024, and a contraction of at most 4096.
+bool use_small(const llattn_gemm_desc* d) {
+  const int64_t tiles = (int64_t)((d->M + BM - 1) / BM) * ((d->N + BN - 1) / BN);
+  return d->split_k == 0 && d->act == LLATTN_ACT_NONE && !d->rowadd[0].ptr && !d->rowadd[1].ptr && tiles <= 32 &&
+         std::min(d->M, d->N) <= 1024 && d->K <= 4096;
+}
+
 // Number of K splits: 1 when the output tiles alone fill most of the chip; otherwise the split count S
 // that minimises a time model of the product: the busiest CU runs ceil(tiles S / 256) workgroups of
 // 1/S of a tile's k range each (one 128 KB workgroup per CU), plus the fp32 partials that the ordered
@@ -889,6 +1061,7 @@ using namespace llattn::gemm;
 
 extern "C" size_t llattn_gemm_workspace_size(const llattn_gemm_desc* d) {
   if (!d) return 0;
+  if (use_small(d)) return 0;
   const int S = resolve_split(d);
   return S > 1 ? (size_t)S * d->M * (d->N + (d->a_rowsum ? 1 : 0)) * sizeof(float) : 0;
 }
@@ -978,6 +1151,13 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
   a.aux = static_cast<uint16_t*>(d->aux);
   a.ld_aux = d->ld_aux;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (use_small(d)) {
+    if (!d->a_trans && !d->b_trans) launch_small<true, true>(a, d->c_dtype, st);
+    else if (!d->a_trans && d->b_trans) launch_small<true, false>(a, d->c_dtype, st);
+    else if (d->a_trans && d->b_trans) launch_small<false, false>(a, d->c_dtype, st);
+    else launch_small<false, true>(a, d->c_dtype, st);
+    return check_launch("llattn_gemm");
+  }
   // bf16 x Wᵀ (+ bias) without K split or accumulation: the persistent kernel, one workgroup per CU
   const int64_t c_bytes = ((int64_t)(d->M - 1) * d->ldc + d->N) * 2;
   if (!d->a_trans && !d->b_trans && S == 1 && d->c_dtype == LLATTN_BF16 && !d->accumulate && k_pairs >= 2 &&
