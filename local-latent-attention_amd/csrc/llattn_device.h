@@ -528,10 +528,12 @@ __device__ __forceinline__ void online_softmax_pv(const f32x4& s, const bool ok[
 
 // Workgroups are dispatched round-robin over the 8 XCDs; remap so that each
 // XCD receives a contiguous range of logical tiles (neighbouring query tiles
-// of one head share K/V rows, which then stay in that XCD's L2).
+// of one head share K/V rows, which then stay in that XCD's L2).  XCD x holds
+// the ids x, x+8, ... < nblocks: nblocks/8 of them, one more when x < nblocks%8,
+// so its range starts after the x ranges before it.
 __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
-  if (nblocks % 8 != 0) return bid;
-  return (bid % 8) * (nblocks / 8) + bid / 8;
+  const int x = bid & 7, q = nblocks >> 3, r = nblocks & 7;
+  return x * q + min(x, r) + (bid >> 3);
 }
 
 // First key of query i (inclusive); the last is i-1.  The reference runs SDPA
