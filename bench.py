@@ -403,6 +403,121 @@ def bench_lm(args):
     return result
 
 
+def _board_sample():
+    """(socket power W, mean GFX clock MHz) from one ``amd-smi metric --power --clock`` reading, or None."""
+    import re
+    import subprocess
+    try:
+        out = subprocess.run(["amd-smi", "metric", "--power", "--clock"], capture_output=True, text=True,
+                             timeout=10).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    p = re.search(r"SOCKET_POWER:\s*([0-9.]+)\s*W", out)
+    gfx = out.split("GFX_0:", 1)[1] if "GFX_0:" in out else ""
+    # the current clock lines of the GFX_<i> sections (not their MIN_CLK / MAX_CLK lines)
+    clk = [float(v) for v in re.findall(r"^\s*CLK:\s*([0-9.]+)\s*MHz", gfx.split("MEM_0:", 1)[0], re.M)]
+    if not p or not clk:
+        return None
+    return float(p.group(1)), sum(clk) / len(clk)
+
+
+def bench_gemm_products(args):
+    """The config-2 step's nine large GEMM products, each timed alone (HIP events, 20 calls after 3 warm-up
+    calls) on this library's kernel and on torch's library GEMM (hipBLASLt) with the same bf16 operands;
+    then board power and GFX clock sampled by ``amd-smi`` during 4-second loops of the largest product on
+    each.  Output: one JSON line."""
+    import threading
+
+    from llattn_amd import gemm
+    from llattn_amd.linear import weight_grad
+
+    dev = torch.device("cuda:0")
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(3)
+    M, D, QK, R = 32768, 1408, 4736, 512   # tokens, d_model, 3 D + latent d_model, latent width (r_out)
+
+    def rnd(*s):
+        return (torch.randn(*s, device=dev, generator=g) * 0.5).to(bf)
+
+    prods = []
+    for name, N, K in (("qkv|rq", QK, D), ("out", D, D), ("r_out", D, R)):
+        x, w, b, dy = rnd(M, K), rnd(N, K), torch.randn(N, device=dev, generator=g), rnd(M, N)
+        bb = b.to(bf)
+        prods += [
+            (f"{name} forward x W^T + b", M, N, K, lambda x=x, w=w, b=b: gemm.linear(x, w, b),
+             lambda x=x, w=w, bb=bb: F.linear(x, w, bb)),
+            (f"{name} input gradient dy W", M, K, N, lambda dy=dy, w=w: gemm.input_grad(dy, w),
+             lambda dy=dy, w=w: dy @ w),
+            (f"{name} weight gradient dy^T x (+ db)", N, K, M, lambda dy=dy, x=x: weight_grad(dy, x, True),
+             lambda dy=dy, x=x: (dy.t() @ x, dy.sum(0))),
+        ]
+
+    def timed(fn, n=20):
+        for _ in range(3):
+            fn()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        s.record()
+        for _ in range(n):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) * 1e3 / n
+
+    rows = []
+    for name, m, n, k, ours, lib in prods:
+        flop = 2.0 * m * n * k
+        t_o, t_l = timed(ours), timed(lib)
+        rows.append({"product": name, "M": m, "N": n, "K": k, "us": round(t_o, 1), "tflops": round(flop / t_o / 1e6, 1),
+                     "library_us": round(t_l, 1), "library_tflops": round(flop / t_l / 1e6, 1)})
+        log(f"{name:40s} ours {t_o:7.1f} us {flop / t_o / 1e6:7.1f} TF/s | library {t_l:7.1f} us "
+            f"{flop / t_l / 1e6:7.1f} TF/s")
+
+    def sustained(fn, flop, seconds=4.0):
+        samples, stop = [], threading.Event()
+
+        def sampler():
+            time.sleep(1.0)  # let the clock settle under load
+            while not stop.is_set():
+                s = _board_sample()
+                if s:
+                    samples.append(s)
+                time.sleep(0.5)
+
+        th = threading.Thread(target=sampler)
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        th.start()
+        t0, n = time.perf_counter(), 0
+        while time.perf_counter() - t0 < seconds:
+            for _ in range(10):
+                fn()
+            torch.cuda.synchronize()
+            n += 10
+        dt = time.perf_counter() - t0
+        stop.set()
+        th.join()
+        out = {"tflops": round(flop * n / dt / 1e12, 1), "samples": len(samples)}
+        if samples:
+            out["power_w"] = round(sum(p for p, _ in samples) / len(samples), 1)
+            out["gfx_mhz"] = round(sum(c for _, c in samples) / len(samples), 1)
+        return out
+
+    idle = _board_sample()
+    _, m, n, k, ours, lib = prods[0]
+    power = {"idle": None if idle is None else {"power_w": idle[0], "gfx_mhz": idle[1]},
+             "ours qkv|rq forward loop": sustained(ours, 2.0 * m * n * k),
+             "library qkv|rq forward loop": sustained(lib, 2.0 * m * n * k)}
+    log(json.dumps(power))
+    tot_o = sum(r["us"] for r in rows)
+    tot_l = sum(r["library_us"] for r in rows)
+    return {"gemm_products": rows, "total_us": round(tot_o, 1), "library_total_us": round(tot_l, 1),
+            "board": power,
+            "note": "library = torch F.linear / matmul on the same bf16 operands (hipBLASLt); its weight gradient "
+                    "has bf16 output and a separate column sum, ours fp32 output with the bias gradient in the pass"}
+
+
 def read_traffic(config: str, kernel: str):
     """HBM bytes per call of the entry point `kernel` at `config`, as measured by the rocprofv3 --pmc
     FETCH_SIZE / WRITE_SIZE runs summarised in profiles/ (scaled by a plain copy), or None."""
@@ -429,6 +544,9 @@ def main():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 3 plain device copies of MIB MiB each (scale factor for rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE counters) and exit")
+    ap.add_argument("--gemm-products", action="store_true",
+                    help="only time the config-2 step's GEMM products alone, ours against torch's library GEMM, "
+                         "with board power and clock under sustained loops, and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -448,6 +566,9 @@ def main():
         print(json.dumps({"calibrate_copy_bytes": n}), flush=True)
         return
 
+    if args.gemm_products:
+        print(json.dumps(bench_gemm_products(args)), flush=True)
+        return
     if args.config == "c5":
         print(json.dumps(bench_lm(args)), flush=True)
         return
