@@ -12,34 +12,13 @@
 // streamed through LDS in tiles of 64 and consumed in 16-row sub-tiles.
 #include "llattn_abi.h"
 #include "llattn_device.h"
+#include "llattn_local.h"
 
 #include <climits>
 #include <mutex>
 
 namespace llattn {
 
-struct LocalArgs {
-  int B, T, H, Dh, W, bs, q_block, n_qt, gate_hs;
-  float scale, scale_log2;
-  const void* q; int64_t q_sb, q_st, q_sh;
-  const void* k; int64_t k_sb, k_st, k_sh;
-  const void* v; int64_t v_sb, v_st, v_sh;
-  const void* rem; int64_t r_sb, r_sn, r_sh;
-  const float* gl;
-  const float* gr;
-  void* y; int64_t y_sb, y_st, y_sh;
-  void* ol; int64_t o_sb, o_st, o_sh;
-  float* lse;  // [B][H][T]
-  float* w;    // [B][H][T]
-  const void* dy; int64_t dy_sb, dy_st, dy_sh;
-  void* dq; int64_t dq_sb, dq_st, dq_sh;
-  void* dk; int64_t dk_sb, dk_st, dk_sh;
-  void* dv; int64_t dv_sb, dv_st, dv_sh;
-  void* dr; int64_t dr_sb, dr_st, dr_sh;
-  void* dO;      // workspace [B][T][H][Dh], storage type
-  float* Dsum;   // workspace [B][H][T]
-  float* gpart;  // workspace [H][3][Dh][rows]: gate_l, gate_r and dremote column partial sums
-};
 
 // ----------------------------------------------------------------------------
 // forward: local attention + gate mix
@@ -899,6 +878,19 @@ __global__ __launch_bounds__(256) void gate_reduce_kernel(const float* __restric
 // ----------------------------------------------------------------------------
 // host launchers
 // ----------------------------------------------------------------------------
+bool strides_fit_32bit(const LocalArgs& a) {
+  const int64_t lim = int64_t(1) << 24;
+  const bool st32 = a.q_st <= lim && a.k_st <= lim && a.v_st <= lim && a.dy_st <= lim && a.o_st <= lim &&
+                    a.r_sn <= lim && a.dq_st <= lim && a.dk_st <= lim && a.dv_st <= lim && a.dr_st <= lim;
+  // outputs (and, in the wide backward, inputs) are addressed with 32-bit byte offsets over a (batch, head)
+  // slab of T rows
+  const int64_t slab = int64_t(1) << 30;
+  return st32 && (int64_t)a.T * a.dq_st < slab && (int64_t)a.T * a.dk_st < slab && (int64_t)a.T * a.dv_st < slab &&
+         (int64_t)a.T * a.dr_st < slab && (int64_t)a.T * a.q_st < slab && (int64_t)a.T * a.k_st < slab &&
+         (int64_t)a.T * a.v_st < slab && (int64_t)a.T * a.dy_st < slab && (int64_t)a.T * a.o_st < slab &&
+         (int64_t)a.T * a.r_sn < slab && (int64_t)a.T * a.H * a.Dh < slab;
+}
+
 namespace {
 
 template <typename T, int DHP>
@@ -911,14 +903,7 @@ void launch_fwd(const LocalArgs& a, hipStream_t stream) {
 // below 2^24 elements (its buffer loads address a 64-row tile with 32-bit
 // byte offsets) and output slabs of T rows below 2^30 elements.
 bool fused_bwd(const LocalArgs& a, int dtype, int dhp) {
-  const int64_t lim = int64_t(1) << 24;
-  const bool st32 = a.q_st <= lim && a.k_st <= lim && a.v_st <= lim && a.dy_st <= lim && a.o_st <= lim &&
-                    a.r_sn <= lim && a.dq_st <= lim && a.dk_st <= lim && a.dv_st <= lim && a.dr_st <= lim;
-  // outputs are addressed with 32-bit byte offsets over a (batch, head) slab of T rows
-  const int64_t slab = int64_t(1) << 30;
-  const bool slab32 = (int64_t)a.T * a.dq_st < slab && (int64_t)a.T * a.dk_st < slab &&
-                      (int64_t)a.T * a.dv_st < slab && (int64_t)a.T * a.dr_st < slab;
-  return dtype == LLATTN_BF16 && dhp <= 96 && a.W <= 64 && a.bs >= 64 && st32 && slab32;
+  return dtype == LLATTN_BF16 && dhp <= 96 && a.W <= 64 && a.bs >= 64 && strides_fit_32bit(a);
 }
 
 template <typename T, int DHP>
@@ -928,6 +913,12 @@ void launch_bwd(const LocalArgs& a, hipStream_t stream) {
       const int seg_tiles = fused_seg_tiles(a);
       const int n_seg = (a.n_qt + seg_tiles - 1) / seg_tiles;
       hipLaunchKernelGGL((local_bwd_fused_kernel<DHP>), dim3(a.B * a.H * n_seg), dim3(512), 0, stream, a, seg_tiles);
+      return;
+    }
+  }
+  if constexpr (std::is_same_v<T, uint16_t>) {
+    if (wide_bwd(a, LLATTN_BF16, DHP)) {
+      launch_bwd_wide(a, DHP, stream);
       return;
     }
   }
@@ -1070,10 +1061,15 @@ int32_t bwd_args(const llattn_shape* s, const llattn_tensor* q, const llattn_ten
 
 size_t up256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Gate partial rows: one per (batch, segment) from the fused kernel, one per (batch, query tile) otherwise.
+// Gate partial rows: one per (batch, segment) from the fused kernel, one per (batch, 128-query group) from
+// the wide-window kernels, one per (batch, query tile) otherwise.
 int gate_rows(const LocalArgs& a, int dtype) {
-  const int seg_tiles = fused_seg_tiles(a);
-  return fused_bwd(a, dtype, padded_head_dim(a.Dh)) ? a.B * ((a.n_qt + seg_tiles - 1) / seg_tiles) : a.B * a.n_qt;
+  const int dhp = padded_head_dim(a.Dh);
+  if (fused_bwd(a, dtype, dhp)) {
+    const int seg_tiles = fused_seg_tiles(a);
+    return a.B * ((a.n_qt + seg_tiles - 1) / seg_tiles);
+  }
+  return wide_bwd(a, dtype, dhp) ? wide_gate_rows(a) : a.B * a.n_qt;
 }
 
 // Launches the backward kernels and the ordered gate reduction; a.dO / a.Dsum / a.gpart are set.

@@ -1,0 +1,524 @@
+// Local-attention backward for windows above 64 (bf16), on 32x32x16 MFMA
+// products (reference models.py:232-305, 416-438, and the autograd of both).
+//
+// With W > 64 a query's keys span up to W/64 + 1 key tiles, so the work is
+// MFMA-shaped (10 Dh flops per (query, key) pair against a few bytes per
+// row).  A one-pass backward would keep, for every key tile in flight, the
+// partial dQ of the W/64 + 1 query tiles it feeds (147 KB of fp32 at W = 512,
+// Dh = 64): more than LDS or the register file holds.  So two atomic-free
+// kernels share the pairs:
+//
+//   query side (local_bwd_wq_kernel), one workgroup per (batch, head, 128
+//   queries): the gate backward of its rows (dO_local, D = dO.o_local,
+//   dremote, gate partial sums; dO and D to the workspace), then dQ over the
+//   keys [q0 - W, q0 + 127).  Wave w owns queries [q0 + 32 w, +32) and walks
+//   the 32-key sub-steps of every 64-key chunk the workgroup stages.
+//
+//   key side (local_bwd_wkv_kernel), one workgroup per (batch, head, 128
+//   keys): dK and dV over the queries [j0 + 1, j0 + 128 + W).  Wave w owns
+//   keys [j0 + 32 w, +32) and walks the 32-query sub-steps of every chunk.
+//
+// 32 rows per wave keep a wave within 256 registers, so two waves share each
+// SIMD (this file is compiled with -amdgpu-mfma-vgpr-form: accumulators in
+// VGPRs, no AGPRs, so the whole 256-register budget of a wave is usable): at Dh = 64 the softmax arithmetic of a score (fma, exp, the dS terms,
+// the bf16 packing) costs about as many issue cycles as its products, and the
+// two waves overlap one's VALU work with the other's MFMAs.
+//
+// Operand layouts of v_mfma_f32_32x32x16_bf16 (lane l, half h = l / 32):
+// A lane l holds row l % 32, k = 8 h .. 8 h + 7; B lane l holds column l % 32,
+// k = 8 h .. 8 h + 7; the accumulator element i of lane l is row
+// 8 (i / 4) + 4 h + i % 4, column l % 32.  Scores are formed with the row
+// index (keys in the query-side kernel, queries in the key-side one) as the
+// contraction index of the following product, so P and dS leave their
+// accumulators as B operands without any data movement: the k slots of
+// product m (0, 1) are accumulator elements 8 m .. 8 m + 7, i.e. rows
+// 16 m + 4 h + e % 4 + 8 (e / 4), and the matching A operand (K^T, Q^T, dO^T
+// with that row order) comes from two transposing LDS reads.
+#include "llattn_abi.h"
+#include "llattn_device.h"
+#include "llattn_local.h"
+
+#include <climits>
+
+namespace llattn {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWideRows = 128;  // queries (query side) or keys (key side) per workgroup
+
+__device__ __forceinline__ f32x16 mma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+// A or B operand from a row-major LDS tile (pitch P): lane l takes row `row0 + l % 32`, dims d0 + 8 h .. +7.
+template <int P>
+__device__ __forceinline__ bf16x8 frag_rows(const uint16_t* tile, int row0, int d0) {
+  const int lane = threadIdx.x & 63;
+  return __builtin_bit_cast(bf16x8, ld16(tile + (row0 + (lane & 31)) * P + d0 + 8 * (lane >> 5)));
+}
+
+// A operand X^T of a product whose 16 contraction slots are the tile rows r0 + 4 h + e % 4 + 8 (e / 4)
+// (e = 0..7) and whose operand row (lane l % 32) is tile column c0 + l % 32.  In a ds_read_b64_tr_b16 the
+// 16 lanes of a group read a 4 x 16 block (lane j: row j / 4, columns 4 (j % 4) .. +3) and lane r receives
+// column r of its four rows; groups 2 g' and 2 g' + 1 (h = g') cover columns c0 .. c0 + 31.
+template <int P>
+__device__ __forceinline__ bf16x8 frag_cols(const uint16_t* tile, int r0, int c0) {
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const uint16_t* p = tile + (r0 + 4 * (g >> 1) + (r >> 2)) * P + c0 + 16 * (g & 1) + 4 * (r & 3);
+  const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)(p));
+  const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)(p + 8 * P));
+  return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// accumulator elements 8 m .. 8 m + 7 as a bf16 B operand
+__device__ __forceinline__ bf16x8 pack8(const float (&v)[16], int m) {
+  const uint4 u = make_uint4(pack_bf16x2(v[8 * m], v[8 * m + 1]), pack_bf16x2(v[8 * m + 2], v[8 * m + 3]),
+                             pack_bf16x2(v[8 * m + 4], v[8 * m + 5]), pack_bf16x2(v[8 * m + 6], v[8 * m + 7]));
+  return __builtin_bit_cast(bf16x8, u);
+}
+
+__device__ __forceinline__ void unpack8(uint4 x, float* o) {
+  unpack_bf16x4(make_uint2(x.x, x.y), o);
+  unpack_bf16x4(make_uint2(x.z, x.w), o + 4);
+}
+
+// sum over the 16 lanes l' = l (mod 4) of a wave, in every lane: rotations within each 16-lane row, then
+// across the rows
+__device__ __forceinline__ float sum_stride4(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x124, 0xf, 0xf, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false));
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+// Block class of 32 queries [qa, qa + 32) against 32 keys [ka, ka + 32): 0 no pair in the window, 1 every
+// pair inside (distance 1 .. W - 1, so the block-start rule cannot drop one), 2 per-element masks.
+__device__ __forceinline__ int block_class(int qa, int ka, int W) {
+  const int dmin = qa - (ka + 31), dmax = qa + 31 - ka;
+  if (dmax < 1 || dmin > W) return 0;
+  return (dmin >= 1 && dmax <= W - 1) ? 1 : 2;
+}
+
+// ----------------------------------------------------------------------------
+// query side: gate backward + dQ
+// ----------------------------------------------------------------------------
+template <int DHP>
+__global__ __launch_bounds__(256, 2) void local_bwd_wq_kernel(const LocalArgs a) {
+  using T = uint16_t;
+  constexpr int KP = DHP + 8, KS = DHP / 16, DB = DHP / 32, TILE = 64 * KP;
+  constexpr int CD = DHP / 4, CV = CD / 8;  // gate layout: 4 threads per row, CD dims each
+  __shared__ __align__(16) T SQ[2 * TILE];   // query rows [q0, q0 + 128) -> dQ (bf16) at the end
+  __shared__ __align__(16) T SD[2 * TILE];   // dO_local rows
+  __shared__ __align__(16) T SKV[4 * TILE];  // key rows [buf], value rows [2 + buf]; gate sums; dQ partials
+  __shared__ __align__(16) float gls[DHP], grs[DHP];
+  __shared__ __align__(16) float lse2s[kWideRows], Dss[kWideRows];
+  __shared__ __align__(16) int los[kWideRows];
+
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, c32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n_qg = (a.T + kWideRows - 1) / kWideRows;
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int qg = bid % n_qg, bh = bid / n_qg, hd = bh % a.H, b = bh / a.H;
+  const int T_ = a.T, Dh = a.Dh, W = a.W, q0 = qg * kWideRows;
+  const int64_t hrow = ((int64_t)b * a.H + hd) * T_;
+  // 32-bit strides (checked by the launcher)
+  const int q_st = (int)a.q_st, k_st = (int)a.k_st, v_st = (int)a.v_st, dy_st = (int)a.dy_st, o_st = (int)a.o_st;
+  const int r_sn = (int)a.r_sn, dr_st = (int)a.dr_st, dq_st = (int)a.dq_st, do_st = a.H * Dh;
+  auto slab = [&](const void* base, int st, int rows) { return make_rsrc(base, ((int64_t)(rows - 1) * st + Dh) * 2); };
+
+  const T* qbase = static_cast<const T*>(a.q) + b * a.q_sb + hd * a.q_sh;
+  const T* kbase = static_cast<const T*>(a.k) + b * a.k_sb + hd * a.k_sh;
+  const T* vbase = static_cast<const T*>(a.v) + b * a.v_sb + hd * a.v_sh;
+  T* dobase = static_cast<T*>(a.dO) + ((int64_t)b * T_ * a.H + hd) * Dh;
+
+  // ---- loads: gate rows, query rows, first key / value chunk ----
+  const int kbeg = max(0, q0 - W), kend = min(T_, q0 + kWideRows) - 1;  // keys [kbeg, kend)
+  const int nch = kend > kbeg ? (kend - kbeg + 63) / 64 : 0;
+  BufTile<DHP, 256> tk, tv;
+  if (nch > 0) {
+    tk.load(kbase, k_st, kbeg, kend, Dh, tid);
+    tv.load(vbase, v_st, kbeg, kend, Dh, tid);
+  }
+  {
+    BufTile<DHP, 256> tq;
+    tq.load(qbase, q_st, q0, min(T_, q0 + 64), Dh, tid);
+    tq.template store<KP>(SQ, tid);
+    tq.load(qbase, q_st, q0 + 64, min(T_, q0 + kWideRows), Dh, tid);
+    tq.template store<KP>(SQ + TILE, tid);
+  }
+  const int gr = tid >> 2, gd0 = (tid & 3) * CD;
+  const auto rdy = slab(static_cast<const T*>(a.dy) + b * a.dy_sb + hd * a.dy_sh, dy_st, T_);
+  const auto rol = slab(static_cast<const T*>(a.ol) + b * a.o_sb + hd * a.o_sh, o_st, T_);
+  const int n_rem = (T_ + a.q_block - 1) / a.q_block;
+  const auto rrm = slab(static_cast<const T*>(a.rem) + b * a.r_sb + hd * a.r_sh, r_sn, n_rem);
+  uint4 pdy[2][CV], pol[2][CV], prm[2][CV];
+  float pw[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int qi = q0 + gr + 64 * u;
+    const bool qv = qi < T_;
+    const int rrow = qv ? qi / a.q_block : 0;
+#pragma unroll
+    for (int j = 0; j < CV; ++j) {
+      const int d = gd0 + 8 * j;
+      const bool ok = qv && d < Dh;
+      pdy[u][j] = buf_ld16(rdy, ok ? (uint32_t)(qi * dy_st + d) * 2u : kOffOOB);
+      pol[u][j] = buf_ld16(rol, ok ? (uint32_t)(qi * o_st + d) * 2u : kOffOOB);
+      prm[u][j] = buf_ld16(rrm, ok ? (uint32_t)(rrow * r_sn + d) * 2u : kOffOOB);
+    }
+    pw[u] = qv ? a.w[hrow + qi] : 0.f;
+  }
+  for (int d = tid; d < DHP; d += 256) {
+    gls[d] = d < Dh ? a.gl[hd * a.gate_hs + d] : 0.f;
+    grs[d] = d < Dh ? a.gr[hd * a.gate_hs + d] : 0.f;
+  }
+  if (tid < kWideRows) {
+    const int qi = q0 + tid;
+    const bool qv = qi < T_;
+    const float l = qv ? a.lse[hrow + qi] : kNegInf;
+    lse2s[tid] = l == kNegInf ? 0.f : l * kLog2e;
+    los[tid] = qv ? key_lo(qi, W, a.bs) : INT_MAX;
+  }
+  lds_barrier();  // gate vectors
+
+  // ---- gate backward: 4 threads per row, rows gr and gr + 64 ----
+  float accl[CD], accr[CD], accb[CD];
+#pragma unroll
+  for (int e = 0; e < CD; ++e) accl[e] = accr[e] = accb[e] = 0.f;
+  const auto rdr = slab(static_cast<T*>(a.dr) + b * a.dr_sb + hd * a.dr_sh, dr_st, T_);
+  const auto rdo = make_rsrc(dobase, ((int64_t)(T_ - 1) * do_st + Dh) * 2);
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int row = gr + 64 * u, qi = q0 + row;
+    const bool qv = qi < T_;
+    float dyv[CD], olv[CD], rmv[CD];
+#pragma unroll
+    for (int j = 0; j < CV; ++j) {
+      unpack8(pdy[u][j], dyv + 8 * j);
+      unpack8(pol[u][j], olv + 8 * j);
+      unpack8(prm[u][j], rmv + 8 * j);
+    }
+    float dot1 = 0.f;
+#pragma unroll
+    for (int e = 0; e < CD; ++e) dot1 += dyv[e] * (olv[e] - rmv[e]);
+    dot1 += __shfl_xor(dot1, 1);
+    dot1 += __shfl_xor(dot1, 2);
+    const float wq = pw[u], delta = wq * (1.f - wq) * dot1;
+    float Dp = 0.f;
+#pragma unroll
+    for (int j = 0; j < CV; ++j) {
+      float dov[8], drv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int e = 8 * j + i, d = gd0 + e;
+        dov[i] = wq * dyv[e] + delta * gls[d];
+        drv[i] = (1.f - wq) * dyv[e] - delta * grs[d];
+        accl[e] += delta * olv[e];
+        accr[e] -= delta * rmv[e];
+        accb[e] += drv[i];
+      }
+      // dO_local rounded to bf16 once: the packed words go to LDS and HBM, their values feed D = dO.o_local
+      const uint4 dop = make_uint4(pack_bf16x2(dov[0], dov[1]), pack_bf16x2(dov[2], dov[3]),
+                                   pack_bf16x2(dov[4], dov[5]), pack_bf16x2(dov[6], dov[7]));
+      unpack8(dop, dov);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) Dp += dov[i] * olv[8 * j + i];
+      const int d = gd0 + 8 * j;
+      st16(SD + row * KP + d, dop);
+      const bool ok = qv && d < Dh;
+      typedef int i32x4_t __attribute__((ext_vector_type(4)));
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, dop), rdo,
+                                             ok ? (uint32_t)(qi * do_st + d) * 2u : kOffOOB, 0, 0);
+      const uint4 drp = make_uint4(pack_bf16x2(drv[0], drv[1]), pack_bf16x2(drv[2], drv[3]),
+                                   pack_bf16x2(drv[4], drv[5]), pack_bf16x2(drv[6], drv[7]));
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, drp), rdr,
+                                             ok ? (uint32_t)(qi * dr_st + d) * 2u : kOffOOB, 0, 0);
+    }
+    Dp += __shfl_xor(Dp, 1);
+    Dp += __shfl_xor(Dp, 2);
+    if ((tid & 3) == 0) {
+      Dss[row] = qv ? Dp : 0.f;
+      if (qv) a.Dsum[hrow + qi] = Dp;
+    }
+  }
+  // gate and dremote partial sums of the 128 rows: over the 16 rows of each wave (lanes of equal tid % 4),
+  // then over the four waves in order; staged in the key / value buffers, which are not in use yet
+  float* gsum = reinterpret_cast<float*>(SKV);  // [wave][3][DHP]
+  static_assert(4 * 3 * DHP * 4 <= 4 * TILE * 2, "gate sums exceed the key / value buffers");
+#pragma unroll
+  for (int e = 0; e < CD; ++e) {
+    const float l = sum_stride4(accl[e]), r = sum_stride4(accr[e]), s = sum_stride4(accb[e]);
+    if (lane < 4) {
+      gsum[(wave * 3 + 0) * DHP + gd0 + e] = l;
+      gsum[(wave * 3 + 1) * DHP + gd0 + e] = r;
+      gsum[(wave * 3 + 2) * DHP + gd0 + e] = s;
+    }
+  }
+  lds_barrier();  // dO rows, D, gate sums
+  {
+    const int nrow = a.B * n_qg, prow = b * n_qg + qg;
+    for (int idx = tid; idx < 3 * DHP; idx += 256) {
+      const int which = idx / DHP, d = idx % DHP;
+      if (d < Dh) {
+        const float s = gsum[(0 * 3 + which) * DHP + d] + gsum[(1 * 3 + which) * DHP + d] +
+                        gsum[(2 * 3 + which) * DHP + d] + gsum[(3 * 3 + which) * DHP + d];
+        a.gpart[(((int64_t)hd * 3 + which) * Dh + d) * nrow + prow] = s;
+      }
+    }
+  }
+
+  // ---- this wave's operands: Q^T and dO^T of its 32 queries (B operands), lse, D, key bounds ----
+  const int qw = 32 * wave;  // first query row of the wave within the workgroup
+  bf16x8 qf[KS], of[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    qf[ks] = frag_rows<KP>(SQ, qw, 16 * ks);
+    of[ks] = frag_rows<KP>(SD, qw, 16 * ks);
+  }
+  const int myrow = qw + c32;
+  const float lse2 = lse2s[myrow], Dq = Dss[myrow];
+  const int lo = los[myrow], hi = q0 + myrow - 1;
+  f32x16 dq[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) dq[db] = zero16();
+  lds_barrier();  // gate sums read: the key / value buffers are free
+
+  // ---- dQ = scale * sum_j dS_ij k_j over the 64-key chunks [kbeg, kend), two 32-key sub-steps each ----
+  for (int ci = 0; ci < nch; ++ci) {
+    const int c0 = kbeg + 64 * ci, buf = ci & 1;
+    T* sk = SKV + buf * TILE;
+    T* sv = SKV + (2 + buf) * TILE;
+    tk.template store<KP>(sk, tid);
+    tv.template store<KP>(sv, tid);
+    lds_barrier();  // also: every wave is done with the chunk that used this buffer two steps ago
+    if (ci + 1 < nch) {
+      tk.load(kbase, k_st, c0 + 64, kend, Dh, tid);
+      tv.load(vbase, v_st, c0 + 64, kend, Dh, tid);
+    }
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      const int ka = c0 + 32 * sb;
+      const int cls = block_class(q0 + qw, ka, W);  // uniform over the wave
+      if (cls) {
+        f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          s = mma32(frag_rows<KP>(sk, 32 * sb, 16 * ks), qf[ks], s);    // S^T[key][query]
+          dp = mma32(frag_rows<KP>(sv, 32 * sb, 16 * ks), of[ks], dp);  // dP^T[key][query]
+        }
+        float ds[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ds[i] = fast_exp2(s[i] * a.scale_log2 - lse2) * (dp[i] - Dq);
+        if (cls == 2) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int j = ka + 8 * (i >> 2) + 4 * h + (i & 3);
+            ds[i] = ((j >= lo) & (j <= hi)) ? ds[i] : 0.f;
+          }
+        }
+        const bf16x8 d0 = pack8(ds, 0), d1 = pack8(ds, 1);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {  // K^T[dim][key] with the keys in accumulator-row order
+          dq[db] = mma32(frag_cols<KP>(sk, 32 * sb, 32 * db), d0, dq[db]);
+          dq[db] = mma32(frag_cols<KP>(sk, 32 * sb + 16, 32 * db), d1, dq[db]);
+        }
+      }
+    }
+  }
+
+  // ---- dQ rows out, through the query tile (no wave reads it any more) for 16-byte row stores ----
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = 32 * db + 8 * j + 4 * h;
+      *reinterpret_cast<uint2*>(SQ + myrow * KP + d) =
+          make_uint2(pack_bf16x2(dq[db][4 * j] * a.scale, dq[db][4 * j + 1] * a.scale),
+                     pack_bf16x2(dq[db][4 * j + 2] * a.scale, dq[db][4 * j + 3] * a.scale));
+    }
+  lds_barrier();
+  T* dqbase = static_cast<T*>(a.dq) + b * a.dq_sb + hd * a.dq_sh;
+  store_tile<T, DHP, KP>(dqbase, dq_st, SQ, q0, T_, Dh);
+  store_tile<T, DHP, KP>(dqbase, dq_st, SQ + TILE, q0 + 64, T_, Dh);
+}
+
+// ----------------------------------------------------------------------------
+// key side: dK, dV
+// ----------------------------------------------------------------------------
+template <int DHP>
+__global__ __launch_bounds__(256, 2) void local_bwd_wkv_kernel(const LocalArgs a) {
+  using T = uint16_t;
+  constexpr int KP = DHP + 8, KS = DHP / 16, DB = DHP / 32, TILE = 64 * KP;
+  __shared__ __align__(16) T SQO[4 * TILE];  // query rows [buf], dO rows [2 + buf]; prologue: keys, values
+  __shared__ __align__(16) float lse2s[2][64], Dss[2][64];
+  __shared__ __align__(16) int los[2][64];
+
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, c32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n_kg = (a.T + kWideRows - 1) / kWideRows;
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int kg = bid % n_kg, bh = bid / n_kg, hd = bh % a.H, b = bh / a.H;
+  const int T_ = a.T, Dh = a.Dh, W = a.W, j0 = kg * kWideRows;
+  const int64_t hrow = ((int64_t)b * a.H + hd) * T_;
+  const int q_st = (int)a.q_st, k_st = (int)a.k_st, v_st = (int)a.v_st, do_st = a.H * Dh;
+
+  const T* qbase = static_cast<const T*>(a.q) + b * a.q_sb + hd * a.q_sh;
+  const T* dobase = static_cast<const T*>(a.dO) + ((int64_t)b * T_ * a.H + hd) * Dh;
+
+  // queries [qbeg, qend) see at least one of the keys [j0, j0 + 128)
+  const int qbeg = j0 + 1, qend = (int)min((int64_t)T_, (int64_t)j0 + kWideRows + W);
+  const int nch = qend > qbeg ? (qend - qbeg + 63) / 64 : 0;
+  BufTile<DHP, 256> tq, to;
+  float pl = 0.f, pd = 0.f;
+  int plo = INT_MAX;
+  auto load_chunk = [&](int c0) {
+    tq.load(qbase, q_st, c0, qend, Dh, tid);
+    to.load(dobase, do_st, c0, qend, Dh, tid);
+    if (tid < 64) {
+      const int qi = c0 + tid;
+      const bool qv = qi < qend;
+      const float l = qv ? a.lse[hrow + qi] : kNegInf;
+      pl = l == kNegInf ? 0.f : l * kLog2e;
+      pd = qv ? a.Dsum[hrow + qi] : 0.f;
+      plo = qv ? key_lo(qi, W, a.bs) : INT_MAX;
+    }
+  };
+  // keys and values of the workgroup through LDS into this wave's B operands
+  {
+    BufTile<DHP, 256> t;
+    const T* kbase = static_cast<const T*>(a.k) + b * a.k_sb + hd * a.k_sh;
+    const T* vbase = static_cast<const T*>(a.v) + b * a.v_sb + hd * a.v_sh;
+    t.load(kbase, k_st, j0, min(T_, j0 + 64), Dh, tid);
+    t.template store<KP>(SQO, tid);
+    t.load(kbase, k_st, j0 + 64, min(T_, j0 + kWideRows), Dh, tid);
+    t.template store<KP>(SQO + TILE, tid);
+    t.load(vbase, v_st, j0, min(T_, j0 + 64), Dh, tid);
+    t.template store<KP>(SQO + 2 * TILE, tid);
+    t.load(vbase, v_st, j0 + 64, min(T_, j0 + kWideRows), Dh, tid);
+    t.template store<KP>(SQO + 3 * TILE, tid);
+  }
+  if (nch > 0) load_chunk(qbeg);
+  lds_barrier();
+  const int kw = 32 * wave;  // first key row of the wave within the workgroup
+  bf16x8 kB[KS], vB[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    kB[ks] = frag_rows<KP>(SQO, kw, 16 * ks);
+    vB[ks] = frag_rows<KP>(SQO + 2 * TILE, kw, 16 * ks);
+  }
+  const int kj = j0 + kw + c32;  // this lane's key (accumulator column)
+  f32x16 dk[DB], dv[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) dk[db] = dv[db] = zero16();
+  lds_barrier();  // key / value rows read: the buffers take query chunks from here on
+
+  for (int ci = 0; ci < nch; ++ci) {
+    const int c0 = qbeg + 64 * ci, buf = ci & 1;
+    T* sq = SQO + buf * TILE;
+    T* so = SQO + (2 + buf) * TILE;
+    tq.template store<KP>(sq, tid);
+    to.template store<KP>(so, tid);
+    if (tid < 64) {
+      lse2s[buf][tid] = pl;
+      Dss[buf][tid] = pd;
+      los[buf][tid] = plo;
+    }
+    lds_barrier();  // also: every wave is done with the chunk that used this buffer two steps ago
+    if (ci + 1 < nch) load_chunk(c0 + 64);
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      const int cls = block_class(c0 + 32 * sb, j0 + kw, W);  // uniform over the wave
+      if (cls) {
+        f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          s = mma32(frag_rows<KP>(sq, 32 * sb, 16 * ks), kB[ks], s);   // S[query][key]
+          dp = mma32(frag_rows<KP>(so, 32 * sb, 16 * ks), vB[ks], dp);  // dP[query][key]
+        }
+        // this lane's 16 queries are accumulator rows 8 (i / 4) + 4 h + i % 4
+        float p[16], ds[16];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int r0 = 32 * sb + 8 * jj + 4 * h;
+          const float4 l4 = *reinterpret_cast<const float4*>(&lse2s[buf][r0]);
+          const float4 d4 = *reinterpret_cast<const float4*>(&Dss[buf][r0]);
+          const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, Dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const int i = 4 * jj + c;
+            p[i] = fast_exp2(s[i] * a.scale_log2 - lv[c]);
+            ds[i] = p[i] * (dp[i] - Dv[c]);
+          }
+          if (cls == 2) {
+            const int4 lo4 = *reinterpret_cast<const int4*>(&los[buf][r0]);
+            const int lov[4] = {lo4.x, lo4.y, lo4.z, lo4.w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              const bool ok = (kj >= lov[c]) & (kj <= c0 + r0 + c - 1);
+              p[4 * jj + c] = ok ? p[4 * jj + c] : 0.f;
+              ds[4 * jj + c] = ok ? ds[4 * jj + c] : 0.f;
+            }
+          }
+        }
+        const bf16x8 p0 = pack8(p, 0), p1 = pack8(p, 1), d0 = pack8(ds, 0), d1 = pack8(ds, 1);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {  // dV^T = dO^T P, dK^T = Q^T dS (queries in accumulator-row order)
+          dv[db] = mma32(frag_cols<KP>(so, 32 * sb, 32 * db), p0, dv[db]);
+          dv[db] = mma32(frag_cols<KP>(so, 32 * sb + 16, 32 * db), p1, dv[db]);
+          dk[db] = mma32(frag_cols<KP>(sq, 32 * sb, 32 * db), d0, dk[db]);
+          dk[db] = mma32(frag_cols<KP>(sq, 32 * sb + 16, 32 * db), d1, dk[db]);
+        }
+      }
+    }
+  }
+
+  // ---- rows out: lane (c32, h) holds dims 32 db + 8 j + 4 h .. +3 of key kj ----
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  const auto rdk = make_rsrc(static_cast<T*>(a.dk) + b * a.dk_sb + hd * a.dk_sh,
+                             ((int64_t)(T_ - 1) * a.dk_st + Dh) * 2);
+  const auto rdv = make_rsrc(static_cast<T*>(a.dv) + b * a.dv_sb + hd * a.dv_sh,
+                             ((int64_t)(T_ - 1) * a.dv_st + Dh) * 2);
+  const int dk_st = (int)a.dk_st, dv_st = (int)a.dv_st;
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = 32 * db + 8 * j + 4 * h;
+      const bool ok = kj < T_ && d < Dh;
+      const u32x2 kv = {pack_bf16x2(dk[db][4 * j] * a.scale, dk[db][4 * j + 1] * a.scale),
+                        pack_bf16x2(dk[db][4 * j + 2] * a.scale, dk[db][4 * j + 3] * a.scale)};
+      const u32x2 vv = {pack_bf16x2(dv[db][4 * j], dv[db][4 * j + 1]), pack_bf16x2(dv[db][4 * j + 2], dv[db][4 * j + 3])};
+      __builtin_amdgcn_raw_buffer_store_b64(kv, rdk, ok ? (uint32_t)(kj * dk_st + d) * 2u : kOffOOB, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b64(vv, rdv, ok ? (uint32_t)(kj * dv_st + d) * 2u : kOffOOB, 0, 0);
+    }
+}
+
+}  // namespace
+
+bool wide_bwd(const LocalArgs& a, int dtype, int dhp) {
+  return dtype == LLATTN_BF16 && dhp <= 64 && a.W > 64 && strides_fit_32bit(a);
+}
+
+int wide_gate_rows(const LocalArgs& a) { return a.B * ((a.T + kWideRows - 1) / kWideRows); }
+
+void launch_bwd_wide(const LocalArgs& a, int dhp, hipStream_t stream) {
+  const int n = a.B * a.H * ((a.T + kWideRows - 1) / kWideRows);
+  if (dhp == 32) {
+    hipLaunchKernelGGL(local_bwd_wq_kernel<32>, dim3(n), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(local_bwd_wkv_kernel<32>, dim3(n), dim3(256), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL(local_bwd_wq_kernel<64>, dim3(n), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(local_bwd_wkv_kernel<64>, dim3(n), dim3(256), 0, stream, a);
+  }
+}
+
+}  // namespace llattn

@@ -16,7 +16,8 @@ PKG_DIR = Path(__file__).resolve().parent
 SRC_DIR = PKG_DIR.parent / "csrc"
 INCLUDE_DIR = PKG_DIR.parents[1] / "include"
 LIB_NAME = "libllattn_gfx950.so"
-SOURCES = ("llattn_abi.cpp", "llattn_pool.hip", "llattn_latent.hip", "llattn_local.hip", "llattn_gemm.hip",
+SOURCES = ("llattn_abi.cpp", "llattn_pool.hip", "llattn_latent.hip", "llattn_local.hip", "llattn_local_wide.hip",
+           "llattn_gemm.hip",
            "llattn_colsum.hip", "llattn_cast.hip", "llattn_norm.hip",
            "llattn_xent.hip")
 ARCH = "gfx950"
@@ -27,6 +28,11 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-result", "-Wno-inline-asm",
 ]
+
+
+# Per-source additions: the wide-window backward keeps its MFMA accumulators in VGPRs (no AGPRs), so that a
+# wave's whole 256-register budget at two waves per SIMD is usable without copies between register files.
+EXTRA_FLAGS = {"llattn_local_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def hipcc() -> str:
@@ -44,7 +50,8 @@ def build(verbose: bool = False) -> Path:
         objs, procs = [], []
         for src in SOURCES:
             obj = Path(tmp) / (Path(src).stem + ".o")
-            cmd = [cc, *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", f"-I{SRC_DIR}", "-c", str(SRC_DIR / src), "-o", str(obj)]
+            cmd = [cc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), f"-I{INCLUDE_DIR}", f"-I{SRC_DIR}", "-c",
+                   str(SRC_DIR / src), "-o", str(obj)]
             if verbose:
                 print(" ".join(cmd), flush=True)
             procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
