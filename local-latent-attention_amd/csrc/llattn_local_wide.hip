@@ -358,16 +358,17 @@ template <int DHP>
 __global__ __launch_bounds__(256, 2) void local_bwd_wkv_kernel(const LocalArgs a) {
   using T = uint16_t;
   constexpr int KP = DHP + 8, KS = DHP / 16, DB = DHP / 32, TILE = 64 * KP;
-  __shared__ __align__(16) T SQO[4 * TILE];  // query rows [buf], dO rows [2 + buf]; prologue: keys, values
-  __shared__ __align__(16) float lse2s[2][64], Dss[2][64];
-  __shared__ __align__(16) int los[2][64];
+  constexpr int CH = 128, NH = CH / 64, NSB = CH / 32;  // queries per chunk, 64-row halves, 32-query sub-steps
+  // chunk buffer `buf`: query rows at [2 buf NH TILE, +NH TILE), dO rows after them; prologue: keys, values
+  __shared__ __align__(16) T SQO[4 * NH * TILE];
+  __shared__ __align__(16) float lse2s[2][CH], Dss[2][CH];
 
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, c32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n_kg = (a.T + kWideRows - 1) / kWideRows;
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
   const int kg = bid % n_kg, bh = bid / n_kg, hd = bh % a.H, b = bh / a.H;
-  const int T_ = a.T, Dh = a.Dh, W = a.W, j0 = kg * kWideRows;
+  const int T_ = a.T, Dh = a.Dh, W = a.W, bs = a.bs, j0 = kg * kWideRows;
   const int64_t hrow = ((int64_t)b * a.H + hd) * T_;
   const int q_st = (int)a.q_st, k_st = (int)a.k_st, v_st = (int)a.v_st, do_st = a.H * Dh;
 
@@ -376,20 +377,21 @@ __global__ __launch_bounds__(256, 2) void local_bwd_wkv_kernel(const LocalArgs a
 
   // queries [qbeg, qend) see at least one of the keys [j0, j0 + 128)
   const int qbeg = j0 + 1, qend = (int)min((int64_t)T_, (int64_t)j0 + kWideRows + W);
-  const int nch = qend > qbeg ? (qend - qbeg + 63) / 64 : 0;
-  BufTile<DHP, 256> tq, to;
+  const int nch = qend > qbeg ? (qend - qbeg + CH - 1) / CH : 0;
+  BufTile<DHP, 256> tq[NH], to[NH];
   float pl = 0.f, pd = 0.f;
-  int plo = INT_MAX;
   auto load_chunk = [&](int c0) {
-    tq.load(qbase, q_st, c0, qend, Dh, tid);
-    to.load(dobase, do_st, c0, qend, Dh, tid);
-    if (tid < 64) {
+#pragma unroll
+    for (int hh = 0; hh < NH; ++hh) {
+      tq[hh].load(qbase, q_st, c0 + 64 * hh, qend, Dh, tid);
+      to[hh].load(dobase, do_st, c0 + 64 * hh, qend, Dh, tid);
+    }
+    if (tid < CH) {
       const int qi = c0 + tid;
       const bool qv = qi < qend;
       const float l = qv ? a.lse[hrow + qi] : kNegInf;
       pl = l == kNegInf ? 0.f : l * kLog2e;
       pd = qv ? a.Dsum[hrow + qi] : 0.f;
-      plo = qv ? key_lo(qi, W, a.bs) : INT_MAX;
     }
   };
   // keys and values of the workgroup through LDS into this wave's B operands
@@ -422,61 +424,64 @@ __global__ __launch_bounds__(256, 2) void local_bwd_wkv_kernel(const LocalArgs a
   lds_barrier();  // key / value rows read: the buffers take query chunks from here on
 
   for (int ci = 0; ci < nch; ++ci) {
-    const int c0 = qbeg + 64 * ci, buf = ci & 1;
-    T* sq = SQO + buf * TILE;
-    T* so = SQO + (2 + buf) * TILE;
-    tq.template store<KP>(sq, tid);
-    to.template store<KP>(so, tid);
-    if (tid < 64) {
+    const int c0 = qbeg + CH * ci, buf = ci & 1;
+    T* sq = SQO + 2 * buf * NH * TILE;
+    T* so = sq + NH * TILE;
+#pragma unroll
+    for (int hh = 0; hh < NH; ++hh) {
+      tq[hh].template store<KP>(sq + hh * TILE, tid);
+      to[hh].template store<KP>(so + hh * TILE, tid);
+    }
+    if (tid < CH) {
       lse2s[buf][tid] = pl;
       Dss[buf][tid] = pd;
-      los[buf][tid] = plo;
     }
     lds_barrier();  // also: every wave is done with the chunk that used this buffer two steps ago
-    if (ci + 1 < nch) load_chunk(c0 + 64);
+    if (ci + 1 < nch) load_chunk(c0 + CH);
+    // the first query of a local block has one key fewer (reference models.py:249-292): bs >= W > 64, so a
+    // chunk of CH queries holds at most CH / 64 block starts, the first at nb0
+    const int nb0 = (c0 + bs - 1) / bs * bs, nb1 = nb0 + bs;
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
+    for (int sb = 0; sb < NSB; ++sb) {
       const int cls = block_class(c0 + 32 * sb, j0 + kw, W);  // uniform over the wave
-      if (cls) {
-        f32x16 s = zero16(), dp = zero16();
+      if (cls == 0) continue;
+      f32x16 sc = zero16(), dpc = zero16();
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          s = mma32(frag_rows<KP>(sq, 32 * sb, 16 * ks), kB[ks], s);   // S[query][key]
-          dp = mma32(frag_rows<KP>(so, 32 * sb, 16 * ks), vB[ks], dp);  // dP[query][key]
+      for (int ks = 0; ks < KS; ++ks) {
+        sc = mma32(frag_rows<KP>(sq, 32 * sb, 16 * ks), kB[ks], sc);   // S[query][key]
+        dpc = mma32(frag_rows<KP>(so, 32 * sb, 16 * ks), vB[ks], dpc);  // dP[query][key]
+      }
+      // this lane's 16 queries are accumulator rows 8 (i / 4) + 4 h + i % 4
+      float p[16], ds[16];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int r0 = 32 * sb + 8 * jj + 4 * h;
+        const float4 l4 = *reinterpret_cast<const float4*>(&lse2s[buf][r0]);
+        const float4 d4 = *reinterpret_cast<const float4*>(&Dss[buf][r0]);
+        const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, Dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int i = 4 * jj + c;
+          p[i] = fast_exp2(sc[i] * a.scale_log2 - lv[c]);
+          ds[i] = p[i] * (dpc[i] - Dv[c]);
         }
-        // this lane's 16 queries are accumulator rows 8 (i / 4) + 4 h + i % 4
-        float p[16], ds[16];
+      }
+      if (cls == 2) {
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int r0 = 32 * sb + 8 * jj + 4 * h;
-          const float4 l4 = *reinterpret_cast<const float4*>(&lse2s[buf][r0]);
-          const float4 d4 = *reinterpret_cast<const float4*>(&Dss[buf][r0]);
-          const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, Dv[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const int i = 4 * jj + c;
-            p[i] = fast_exp2(s[i] * a.scale_log2 - lv[c]);
-            ds[i] = p[i] * (dp[i] - Dv[c]);
-          }
-          if (cls == 2) {
-            const int4 lo4 = *reinterpret_cast<const int4*>(&los[buf][r0]);
-            const int lov[4] = {lo4.x, lo4.y, lo4.z, lo4.w};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              const bool ok = (kj >= lov[c]) & (kj <= c0 + r0 + c - 1);
-              p[4 * jj + c] = ok ? p[4 * jj + c] : 0.f;
-              ds[4 * jj + c] = ok ? ds[4 * jj + c] : 0.f;
-            }
-          }
+        for (int i = 0; i < 16; ++i) {
+          const int qq = c0 + 32 * sb + 8 * (i >> 2) + 4 * h + (i & 3), dd = qq - kj;
+          const bool ok = (dd >= 1) & (dd <= W - ((qq == nb0) | (qq == nb1)));
+          p[i] = ok ? p[i] : 0.f;
+          ds[i] = ok ? ds[i] : 0.f;
         }
-        const bf16x8 p0 = pack8(p, 0), p1 = pack8(p, 1), d0 = pack8(ds, 0), d1 = pack8(ds, 1);
+      }
+      const bf16x8 p0 = pack8(p, 0), p1 = pack8(p, 1), d0 = pack8(ds, 0), d1 = pack8(ds, 1);
 #pragma unroll
-        for (int db = 0; db < DB; ++db) {  // dV^T = dO^T P, dK^T = Q^T dS (queries in accumulator-row order)
-          dv[db] = mma32(frag_cols<KP>(so, 32 * sb, 32 * db), p0, dv[db]);
-          dv[db] = mma32(frag_cols<KP>(so, 32 * sb + 16, 32 * db), p1, dv[db]);
-          dk[db] = mma32(frag_cols<KP>(sq, 32 * sb, 32 * db), d0, dk[db]);
-          dk[db] = mma32(frag_cols<KP>(sq, 32 * sb + 16, 32 * db), d1, dk[db]);
-        }
+      for (int db = 0; db < DB; ++db) {  // dV^T = dO^T P, dK^T = Q^T dS (queries in accumulator-row order)
+        dv[db] = mma32(frag_cols<KP>(so, 32 * sb, 32 * db), p0, dv[db]);
+        dv[db] = mma32(frag_cols<KP>(so, 32 * sb + 16, 32 * db), p1, dv[db]);
+        dk[db] = mma32(frag_cols<KP>(sq, 32 * sb, 32 * db), d0, dk[db]);
+        dk[db] = mma32(frag_cols<KP>(sq, 32 * sb + 16, 32 * db), d1, dk[db]);
       }
     }
   }
