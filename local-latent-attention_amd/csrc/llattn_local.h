@@ -42,4 +42,9 @@ int wide_gate_rows(const LocalArgs& a);
 // Launches its two kernels (query side, then key side).
 void launch_bwd_wide(const LocalArgs& a, int dhp, hipStream_t stream);
 
+// The forward on 32x32x16 products (llattn_local_wide.hip) takes bf16 calls of
+// any window with padded head dims up to 128.
+bool fwd32(const LocalArgs& a, int dtype, int dhp);
+void launch_fwd32(const LocalArgs& a, int dhp, hipStream_t stream);
+
 }  // namespace llattn

@@ -895,6 +895,12 @@ namespace {
 
 template <typename T, int DHP>
 void launch_fwd(const LocalArgs& a, hipStream_t stream) {
+  if constexpr (std::is_same_v<T, uint16_t>) {
+    if (fwd32(a, LLATTN_BF16, DHP)) {
+      launch_fwd32(a, DHP, stream);
+      return;
+    }
+  }
   hipLaunchKernelGGL((local_fwd_kernel<T, DHP>), dim3(a.B * a.H * a.n_qt), dim3(256), 0, stream, a);
 }
 // The fused one-pass backward covers bf16 with padded head dims up to 96,

@@ -507,10 +507,209 @@ __global__ __launch_bounds__(256, 2) void local_bwd_wkv_kernel(const LocalArgs a
     }
 }
 
+// ----------------------------------------------------------------------------
+// forward: local attention + gate mix (every window, bf16, padded head dims up to 128)
+//
+// One workgroup per (batch, head, 128 queries); wave w owns queries
+// [q0 + 32 w, +32) and keeps S^T = K Q^T for each 32-key sub-step in one
+// accumulator (lane = query, so the online-softmax statistics of a query live
+// in one lane pair), then O^T += V^T P^T with P^T passed on as the B operand
+// as in the backward.  The gate epilogue reads the remote rows staged in LDS
+// and writes y and o_local through LDS for 16-byte row stores.
+// ----------------------------------------------------------------------------
+template <int DHP>
+__global__ __launch_bounds__(256, 2) void local_fwd32_kernel(const LocalArgs a) {
+  using T = uint16_t;
+  constexpr int KP = DHP + 8, KS = DHP / 16, DB = DHP / 32, TILE = 64 * KP;
+  __shared__ __align__(16) T SQ[2 * TILE];   // query rows -> remote rows (epilogue)
+  __shared__ __align__(16) T SKV[4 * TILE];  // key rows [buf], value rows [2 + buf] -> y rows, o_local rows
+  __shared__ __align__(16) float gls[DHP], grs[DHP];
+
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, c32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n_qg = (a.T + kWideRows - 1) / kWideRows;
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int qg = bid % n_qg, bh = bid / n_qg, hd = bh % a.H, b = bh / a.H;
+  const int T_ = a.T, Dh = a.Dh, W = a.W, q0 = qg * kWideRows;
+  const int k_st = (int)a.k_st, v_st = (int)a.v_st;
+  const T* kbase = static_cast<const T*>(a.k) + b * a.k_sb + hd * a.k_sh;
+  const T* vbase = static_cast<const T*>(a.v) + b * a.v_sb + hd * a.v_sh;
+
+  const int kbeg = max(0, q0 - W), kend = min(T_, q0 + kWideRows) - 1;  // keys [kbeg, kend)
+  const int nch = kend > kbeg ? (kend - kbeg + 63) / 64 : 0;
+  BufTile<DHP, 256> tk, tv;
+  if (nch > 0) {
+    tk.load(kbase, k_st, kbeg, kend, Dh, tid);
+    tv.load(vbase, v_st, kbeg, kend, Dh, tid);
+  }
+  {
+    const T* qbase = static_cast<const T*>(a.q) + b * a.q_sb + hd * a.q_sh;
+    BufTile<DHP, 256> tq;
+    tq.load(qbase, (int)a.q_st, q0, min(T_, q0 + 64), Dh, tid);
+    tq.template store<KP>(SQ, tid);
+    tq.load(qbase, (int)a.q_st, q0 + 64, min(T_, q0 + kWideRows), Dh, tid);
+    tq.template store<KP>(SQ + TILE, tid);
+  }
+  for (int d = tid; d < DHP; d += 256) {
+    gls[d] = d < Dh ? a.gl[hd * a.gate_hs + d] : 0.f;
+    grs[d] = d < Dh ? a.gr[hd * a.gate_hs + d] : 0.f;
+  }
+  lds_barrier();
+  const int qw = 32 * wave, myrow = qw + c32, qi = q0 + myrow;  // this lane's query (accumulator column)
+  bf16x8 qf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) qf[ks] = frag_rows<KP>(SQ, qw, 16 * ks);
+  const int lo = qi < T_ ? key_lo(qi, W, a.bs) : INT_MAX, hi = qi - 1;
+  float m_run = kNegInf, l_run = 0.f;  // l_run: this lane's half of the row sum
+  f32x16 o[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) o[db] = zero16();
+
+  for (int ci = 0; ci < nch; ++ci) {
+    const int c0 = kbeg + 64 * ci, buf = ci & 1;
+    T* sk = SKV + buf * TILE;
+    T* sv = SKV + (2 + buf) * TILE;
+    tk.template store<KP>(sk, tid);
+    tv.template store<KP>(sv, tid);
+    lds_barrier();  // also: every wave is done with the chunk that used this buffer two steps ago
+    if (ci + 1 < nch) {
+      tk.load(kbase, k_st, c0 + 64, kend, Dh, tid);
+      tv.load(vbase, v_st, c0 + 64, kend, Dh, tid);
+    }
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      const int ka = c0 + 32 * sb;
+      const int cls = block_class(q0 + qw, ka, W);  // uniform over the wave
+      if (cls == 0) continue;
+      f32x16 s = zero16();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) s = mma32(frag_rows<KP>(sk, 32 * sb, 16 * ks), qf[ks], s);  // S^T[key][query]
+      float x[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[i] = s[i];
+      if (cls == 2) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int j = ka + 8 * (i >> 2) + 4 * h + (i & 3);
+          x[i] = ((j >= lo) & (j <= hi)) ? x[i] : kNegInf;
+        }
+      }
+      float smax = x[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) smax = fmaxf(smax, x[i]);
+      smax = fmaxf(smax, __shfl_xor(smax, 32));  // the two halves of the wave hold the same queries
+      const float mloc = smax * a.scale_log2;    // scale_log2 > 0
+      // The softmax reference m_run moves only when a block's maximum exceeds it by more than 8 (log2
+      // units): exponents then stay <= 8, and the rescale of O and l (and its exp) is skipped in most steps.
+      // O and l share the reference, so O / l and lse are unchanged.
+      if (__builtin_amdgcn_ballot_w64(mloc > m_run + 8.f)) {  // uniform
+        const float m_new = fmaxf(m_run, mloc);
+        const float alpha = m_new == kNegInf ? 1.f : fast_exp2(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o[db] *= alpha;
+        m_run = m_new;
+      }
+      const float mu = m_run == kNegInf ? 0.f : m_run;  // every score of this lane is masked while -inf
+      float pv[16], ps = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        pv[i] = fast_exp2(x[i] * a.scale_log2 - mu);
+        ps += pv[i];
+      }
+      l_run += ps;
+      const bf16x8 p0 = pack8(pv, 0), p1 = pack8(pv, 1);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {  // O^T = V^T P^T, keys in accumulator-row order
+        o[db] = mma32(frag_cols<KP>(sv, 32 * sb, 32 * db), p0, o[db]);
+        o[db] = mma32(frag_cols<KP>(sv, 32 * sb + 16, 32 * db), p1, o[db]);
+      }
+    }
+  }
+
+  // ---- epilogue: normalise, gate, mix.  Lane (c32, h) holds dims 32 db + 8 j + 4 h .. +3 of its query ----
+  lds_barrier();  // every wave is done with the key / value buffers and the query tile
+  {
+    RowTile<T, DHP> rr;
+    const T* rbase = static_cast<const T*>(a.rem) + b * a.r_sb + hd * a.r_sh;
+    rr.load_div(rbase, a.r_sn, q0, T_, a.q_block, Dh);
+    rr.template store<KP>(SQ);
+    rr.load_div(rbase, a.r_sn, q0 + 64, T_, a.q_block, Dh);
+    rr.template store<KP>(SQ + TILE);
+  }
+  lds_barrier();
+  const float l = l_run + __shfl_xor(l_run, 32);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  float sl = 0.f, sr = 0.f;
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = 32 * db + 8 * j + 4 * h;
+      float rv[4];
+      unpack_bf16x4(*reinterpret_cast<const uint2*>(SQ + myrow * KP + d), rv);
+      const float4 g4 = *reinterpret_cast<const float4*>(gls + d);
+      const float4 r4 = *reinterpret_cast<const float4*>(grs + d);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[db][4 * j + c] = round_t<T>(o[db][4 * j + c] * inv);
+      sl += o[db][4 * j] * g4.x + o[db][4 * j + 1] * g4.y + o[db][4 * j + 2] * g4.z + o[db][4 * j + 3] * g4.w;
+      sr += rv[0] * r4.x + rv[1] * r4.y + rv[2] * r4.z + rv[3] * r4.w;
+    }
+  sl += __shfl_xor(sl, 32);
+  sr += __shfl_xor(sr, 32);
+  const float mm = fmaxf(sl, sr);
+  const float el = __expf(sl - mm), er = __expf(sr - mm);
+  const float wl = el / (el + er), wr = er / (el + er);
+  T* SY = SKV;             // y rows [0, 128)
+  T* SO = SKV + 2 * TILE;  // o_local rows [0, 128)
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = 32 * db + 8 * j + 4 * h;
+      float rv[4], yv[4];
+      unpack_bf16x4(*reinterpret_cast<const uint2*>(SQ + myrow * KP + d), rv);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) yv[c] = wl * o[db][4 * j + c] + wr * rv[c];
+      *reinterpret_cast<uint2*>(SY + myrow * KP + d) = make_uint2(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]));
+      *reinterpret_cast<uint2*>(SO + myrow * KP + d) =
+          make_uint2(pack_bf16x2(o[db][4 * j], o[db][4 * j + 1]), pack_bf16x2(o[db][4 * j + 2], o[db][4 * j + 3]));
+    }
+  // o_local, lse and w feed only the backward: a forward-only call passes null for them
+  if (qi < T_ && h == 0) {
+    const int64_t idx = ((int64_t)b * a.H + hd) * T_ + qi;
+    if (a.lse) a.lse[idx] = l > 0.f ? (m_run + __log2f(l)) * kLn2 : kNegInf;
+    if (a.w) a.w[idx] = wl;
+  }
+  lds_barrier();
+  T* ybase = static_cast<T*>(a.y) + b * a.y_sb + hd * a.y_sh;
+  store_tile<T, DHP, KP>(ybase, a.y_st, SY, q0, T_, Dh);
+  store_tile<T, DHP, KP>(ybase, a.y_st, SY + TILE, q0 + 64, T_, Dh);
+  if (a.ol) {
+    T* obase = static_cast<T*>(a.ol) + b * a.o_sb + hd * a.o_sh;
+    store_tile<T, DHP, KP>(obase, a.o_st, SO, q0, T_, Dh);
+    store_tile<T, DHP, KP>(obase, a.o_st, SO + TILE, q0 + 64, T_, Dh);
+  }
+}
+
 }  // namespace
 
 bool wide_bwd(const LocalArgs& a, int dtype, int dhp) {
   return dtype == LLATTN_BF16 && dhp <= 64 && a.W > 64 && strides_fit_32bit(a);
+}
+
+bool fwd32(const LocalArgs& a, int dtype, int dhp) {
+  return dtype == LLATTN_BF16 && dhp <= 128 && strides_fit_32bit(a);
+}
+
+void launch_fwd32(const LocalArgs& a, int dhp, hipStream_t stream) {
+  const int n = a.B * a.H * ((a.T + kWideRows - 1) / kWideRows);
+  switch (dhp) {
+    case 32: hipLaunchKernelGGL(local_fwd32_kernel<32>, dim3(n), dim3(256), 0, stream, a); break;
+    case 64: hipLaunchKernelGGL(local_fwd32_kernel<64>, dim3(n), dim3(256), 0, stream, a); break;
+    case 96: hipLaunchKernelGGL(local_fwd32_kernel<96>, dim3(n), dim3(256), 0, stream, a); break;
+    default: hipLaunchKernelGGL(local_fwd32_kernel<128>, dim3(n), dim3(256), 0, stream, a); break;
+  }
 }
 
 int wide_gate_rows(const LocalArgs& a) { return a.B * ((a.T + kWideRows - 1) / kWideRows); }
