@@ -228,6 +228,17 @@ def test_op_per_head_gate():
         assert_fp32_close(got[k], ref[k], k)
 
 
+@pytest.mark.parametrize("case", [(2, 300, 3, 64, 2, 16, 96, 128, 10, 0), (1, 260, 2, 32, 2, 8, 70, 70, 13, 20)])
+def test_op_per_head_gate_bf16(case):
+    """Per-head gate vectors on the bf16 kernels: the 32x32 forward and, with windows above 64, the wide-window
+    backward, whose gate partial sums are kept per head (fused W <= 64 path: the C2 cases)."""
+    _print_case("op per-head gate bf16", case)
+    got, ref = _op_case(*case, seed=7, dtype=torch.bfloat16, per_head_gate=True)
+    floor = ref.pop("_floor")
+    for k in ref:
+        assert_bf16_close(got[k], ref[k], k, floor=floor.get(k))
+
+
 # ---------------------------------------------------------------- pooling op vs reference golden
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
