@@ -35,7 +35,7 @@ struct LocalArgs {
 bool strides_fit_32bit(const LocalArgs& a);
 
 // The wide-window backward (llattn_local_wide.hip) takes bf16 calls with
-// windows above 64 and padded head dims up to 64.
+// windows above 64 and padded head dims up to 128.
 bool wide_bwd(const LocalArgs& a, int dtype, int dhp);
 // Its gate partial rows: one per (batch, 128-query group).
 int wide_gate_rows(const LocalArgs& a);

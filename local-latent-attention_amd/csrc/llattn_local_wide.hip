@@ -112,7 +112,7 @@ __device__ __forceinline__ int block_class(int qa, int ka, int W) {
 // query side: gate backward + dQ
 // ----------------------------------------------------------------------------
 template <int DHP>
-__global__ __launch_bounds__(256, 2) void local_bwd_wq_kernel(const LocalArgs a) {
+__global__ __launch_bounds__(256, DHP <= 64 ? 2 : 1) void local_bwd_wq_kernel(const LocalArgs a) {
   using T = uint16_t;
   constexpr int KP = DHP + 8, KS = DHP / 16, DB = DHP / 32, TILE = 64 * KP;
   constexpr int CD = DHP / 4, CV = CD / 8;  // gate layout: 4 threads per row, CD dims each
@@ -354,8 +354,10 @@ __global__ __launch_bounds__(256, 2) void local_bwd_wq_kernel(const LocalArgs a)
 // ----------------------------------------------------------------------------
 // key side: dK, dV
 // ----------------------------------------------------------------------------
+// Two workgroups per CU up to head dims of 64; wider heads hold more accumulators (dK and dV: 2 DHP / 2 per
+// lane) and run one per CU.
 template <int DHP>
-__global__ __launch_bounds__(256, 2) void local_bwd_wkv_kernel(const LocalArgs a) {
+__global__ __launch_bounds__(256, DHP <= 64 ? 2 : 1) void local_bwd_wkv_kernel(const LocalArgs a) {
   using T = uint16_t;
   constexpr int KP = DHP + 8, KS = DHP / 16, DB = DHP / 32, TILE = 64 * KP;
   constexpr int CH = 128, NH = CH / 64, NSB = CH / 32;  // queries per chunk, 64-row halves, 32-query sub-steps
@@ -695,7 +697,7 @@ __global__ __launch_bounds__(256, 2) void local_fwd32_kernel(const LocalArgs a) 
 }  // namespace
 
 bool wide_bwd(const LocalArgs& a, int dtype, int dhp) {
-  return dtype == LLATTN_BF16 && dhp <= 64 && a.W > 64 && strides_fit_32bit(a);
+  return dtype == LLATTN_BF16 && dhp <= 128 && a.W > 64 && strides_fit_32bit(a);
 }
 
 bool fwd32(const LocalArgs& a, int dtype, int dhp) {
@@ -714,14 +716,19 @@ void launch_fwd32(const LocalArgs& a, int dhp, hipStream_t stream) {
 
 int wide_gate_rows(const LocalArgs& a) { return a.B * ((a.T + kWideRows - 1) / kWideRows); }
 
+template <int DHP>
+void launch_wide(const LocalArgs& a, int n, hipStream_t stream) {
+  hipLaunchKernelGGL(local_bwd_wq_kernel<DHP>, dim3(n), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL(local_bwd_wkv_kernel<DHP>, dim3(n), dim3(256), 0, stream, a);
+}
+
 void launch_bwd_wide(const LocalArgs& a, int dhp, hipStream_t stream) {
   const int n = a.B * a.H * ((a.T + kWideRows - 1) / kWideRows);
-  if (dhp == 32) {
-    hipLaunchKernelGGL(local_bwd_wq_kernel<32>, dim3(n), dim3(256), 0, stream, a);
-    hipLaunchKernelGGL(local_bwd_wkv_kernel<32>, dim3(n), dim3(256), 0, stream, a);
-  } else {
-    hipLaunchKernelGGL(local_bwd_wq_kernel<64>, dim3(n), dim3(256), 0, stream, a);
-    hipLaunchKernelGGL(local_bwd_wkv_kernel<64>, dim3(n), dim3(256), 0, stream, a);
+  switch (dhp) {
+    case 32: launch_wide<32>(a, n, stream); break;
+    case 64: launch_wide<64>(a, n, stream); break;
+    case 96: launch_wide<96>(a, n, stream); break;
+    default: launch_wide<128>(a, n, stream); break;
   }
 }
 

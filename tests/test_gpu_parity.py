@@ -193,7 +193,7 @@ OP_CASES = [
     # tiles that straddle a block boundary (the qr0 + row >= block branch of its key bounds)
     (1, 400, 2, 64, 2, 32, 48, 100, 10, 0),
     (2, 333, 2, 88, 2, 16, 64, 96, 7, 0),
-    # wide-window bf16 backward (W > 64, head dims <= 64): several local blocks per sequence (the first
+    # wide-window bf16 backward (W > 64): several local blocks per sequence (the first
     # query of each block loses its farthest key), ragged T, macro-block queries, a last 128-key group
     # holding one key, windows that are not multiples of 32, a long window over several key groups
     (2, 333, 2, 64, 2, 32, 100, 64, 11, 0),
@@ -201,6 +201,7 @@ OP_CASES = [
     (2, 520, 2, 64, 2, 32, 130, 256, 13, 16),
     (1, 129, 1, 64, 1, 16, 65, 65, 5, 0),
     (1, 1000, 1, 64, 2, 32, 512, 256, 20, 0),
+    (2, 400, 2, 88, 2, 16, 130, 256, 10, 0),   # 0.55b head dim (padded to 96) with a window above 64
 ]
 
 
