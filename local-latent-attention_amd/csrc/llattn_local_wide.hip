@@ -1,9 +1,10 @@
-// Local-attention backward for windows above 64 (bf16), on 32x32x16 MFMA
-// products (reference models.py:232-305, 416-438, and the autograd of both).
+// Local attention on 32x32x16 bf16 MFMA products (reference models.py:232-305,
+// 416-438, and the autograd of both): the forward for every window, and the
+// backward for windows above 64.
 //
-// With W > 64 a query's keys span up to W/64 + 1 key tiles, so the work is
-// MFMA-shaped (10 Dh flops per (query, key) pair against a few bytes per
-// row).  A one-pass backward would keep, for every key tile in flight, the
+// Backward.  With W > 64 a query's keys span up to W/64 + 1 key tiles, so the
+// work is MFMA-shaped (10 Dh flops per (query, key) pair against a few bytes
+// per row).  A one-pass backward would keep, for every key tile in flight, the
 // partial dQ of the W/64 + 1 query tiles it feeds (147 KB of fp32 at W = 512,
 // Dh = 64): more than LDS or the register file holds.  So two atomic-free
 // kernels share the pairs:
@@ -15,25 +16,28 @@
 //   the 32-key sub-steps of every 64-key chunk the workgroup stages.
 //
 //   key side (local_bwd_wkv_kernel), one workgroup per (batch, head, 128
-//   keys): dK and dV over the queries [j0 + 1, j0 + 128 + W).  Wave w owns
-//   keys [j0 + 32 w, +32) and walks the 32-query sub-steps of every chunk.
+//   keys): dK and dV over the queries [j0 + 1, j0 + 128 + W) in 128-query
+//   chunks.  Wave w owns keys [j0 + 32 w, +32) and walks the 32-query
+//   sub-steps of every chunk.
 //
 // 32 rows per wave keep a wave within 256 registers, so two waves share each
-// SIMD (this file is compiled with -amdgpu-mfma-vgpr-form: accumulators in
-// VGPRs, no AGPRs, so the whole 256-register budget of a wave is usable): at Dh = 64 the softmax arithmetic of a score (fma, exp, the dS terms,
-// the bf16 packing) costs about as many issue cycles as its products, and the
-// two waves overlap one's VALU work with the other's MFMAs.
+// SIMD up to head dims of 64.  This file is compiled with
+// -amdgpu-mfma-vgpr-form: accumulators live in VGPRs and no AGPRs are used, so
+// a wave's whole 256-register budget is usable and the loops carry no copies
+// between register files.  At Dh = 64 the softmax arithmetic of a score (an
+// FMA, a quarter-rate exp, the dS terms, the bf16 packing) costs about as many
+// issue cycles as its products.
 //
 // Operand layouts of v_mfma_f32_32x32x16_bf16 (lane l, half h = l / 32):
 // A lane l holds row l % 32, k = 8 h .. 8 h + 7; B lane l holds column l % 32,
 // k = 8 h .. 8 h + 7; the accumulator element i of lane l is row
 // 8 (i / 4) + 4 h + i % 4, column l % 32.  Scores are formed with the row
-// index (keys in the query-side kernel, queries in the key-side one) as the
-// contraction index of the following product, so P and dS leave their
-// accumulators as B operands without any data movement: the k slots of
-// product m (0, 1) are accumulator elements 8 m .. 8 m + 7, i.e. rows
-// 16 m + 4 h + e % 4 + 8 (e / 4), and the matching A operand (K^T, Q^T, dO^T
-// with that row order) comes from two transposing LDS reads.
+// index (keys in the forward and the query-side kernel, queries in the
+// key-side one) as the contraction index of the following product, so P and
+// dS leave their accumulators as B operands without any data movement: the k
+// slots of product m (0, 1) are accumulator elements 8 m .. 8 m + 7, i.e. rows
+// 16 m + 4 h + e % 4 + 8 (e / 4), and the matching A operand (K^T, V^T, Q^T,
+// dO^T with that row order) comes from two transposing LDS reads.
 #include "llattn_abi.h"
 #include "llattn_device.h"
 #include "llattn_local.h"
