@@ -534,8 +534,10 @@ __global__ __launch_bounds__(256, 2) void local_fwd32_kernel(const LocalArgs a) 
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, c32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n_qg = (a.T + kWideRows - 1) / kWideRows;
+  // heads vary fastest: the workgroups that run together (one contiguous range per XCD) read whole token
+  // rows of the packed q|k|v projection rather than one head's 2 Dh-byte slice of each row
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
-  const int qg = bid % n_qg, bh = bid / n_qg, hd = bh % a.H, b = bh / a.H;
+  const int hd = bid % a.H, rq = bid / a.H, qg = rq % n_qg, b = rq / n_qg;
   const int T_ = a.T, Dh = a.Dh, W = a.W, q0 = qg * kWideRows;
   const int k_st = (int)a.k_st, v_st = (int)a.v_st;
   const T* kbase = static_cast<const T*>(a.k) + b * a.k_sb + hd * a.k_sh;
