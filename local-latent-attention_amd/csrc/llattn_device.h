@@ -343,11 +343,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64
   const int n = bytes <= 0 ? 0 : (bytes >= (int64_t)kOffOOB ? (int)(kOffOOB - 16) : (int)bytes);
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, n, 0x00020000);
 }
+// kStream: the non-temporal cache policy (nt) for rows a kernel reads once with whole-row 16-byte loads.
+// Such rows then do not push out of L2 the lines that stores are still filling (an output row of one
+// head shares its first and last 128-byte lines with the neighbouring heads' rows, written by other
+// workgroups).  Not for rows that several load instructions or workgroups read in turn: the line is
+// then fetched again.
+constexpr int kCached = 0, kStream = 2;
+template <int POLICY = kCached>
 __device__ __forceinline__ uint4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POLICY));
 }
+template <int POLICY = kCached>
 __device__ __forceinline__ uint2 buf_ld8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, POLICY));
 }
 
 // BufTile: a bf16 RowTile read with buffer loads.  Each thread's byte offset
@@ -359,13 +367,14 @@ template <int DHP, int NTHR>
 struct BufTile {
   static constexpr int CPR = DHP / 8, TASKS = 64 * CPR, IT = (TASKS + NTHR - 1) / NTHR;
   uint4 x[IT];
-  // rows [r0, r_end) of the view at base (row stride st elements)
+  // rows [r0, r_end) of the view at base (row stride st elements), with cache policy POLICY
+  template <int POLICY = kCached>
   __device__ __forceinline__ void load(const uint16_t* base, int st, int r0, int r_end, int Dh, int tid) {
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(base + (int64_t)r0 * st, ((int64_t)(r_end - r0 - 1) * st + Dh) * 2);
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
       const int task = tid + NTHR * it, row = task / CPR, col = (task % CPR) * 8;
-      x[it] = buf_ld16(rs, (task < TASKS && col < Dh) ? (uint32_t)(row * st + col) * 2u : kOffOOB);
+      x[it] = buf_ld16<POLICY>(rs, (task < TASKS && col < Dh) ? (uint32_t)(row * st + col) * 2u : kOffOOB);
     }
   }
   // tid: the thread's index among the NTHR threads that share the tile

@@ -547,15 +547,15 @@ __global__ __launch_bounds__(256, 2) void local_fwd32_kernel(const LocalArgs a) 
   const int nch = kend > kbeg ? (kend - kbeg + 63) / 64 : 0;
   BufTile<DHP, 256> tk, tv;
   if (nch > 0) {
-    tk.load(kbase, k_st, kbeg, kend, Dh, tid);
-    tv.load(vbase, v_st, kbeg, kend, Dh, tid);
+    tk.template load<kStream>(kbase, k_st, kbeg, kend, Dh, tid);
+    tv.template load<kStream>(vbase, v_st, kbeg, kend, Dh, tid);
   }
   {
     const T* qbase = static_cast<const T*>(a.q) + b * a.q_sb + hd * a.q_sh;
     BufTile<DHP, 256> tq;
-    tq.load(qbase, (int)a.q_st, q0, min(T_, q0 + 64), Dh, tid);
+    tq.template load<kStream>(qbase, (int)a.q_st, q0, min(T_, q0 + 64), Dh, tid);
     tq.template store<KP>(SQ, tid);
-    tq.load(qbase, (int)a.q_st, q0 + 64, min(T_, q0 + kWideRows), Dh, tid);
+    tq.template load<kStream>(qbase, (int)a.q_st, q0 + 64, min(T_, q0 + kWideRows), Dh, tid);
     tq.template store<KP>(SQ + TILE, tid);
   }
   for (int d = tid; d < DHP; d += 256) {
@@ -581,8 +581,8 @@ __global__ __launch_bounds__(256, 2) void local_fwd32_kernel(const LocalArgs a) 
     tv.template store<KP>(sv, tid);
     lds_barrier();  // also: every wave is done with the chunk that used this buffer two steps ago
     if (ci + 1 < nch) {
-      tk.load(kbase, k_st, c0 + 64, kend, Dh, tid);
-      tv.load(vbase, v_st, c0 + 64, kend, Dh, tid);
+      tk.template load<kStream>(kbase, k_st, c0 + 64, kend, Dh, tid);
+      tv.template load<kStream>(vbase, v_st, c0 + 64, kend, Dh, tid);
     }
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {

@@ -170,12 +170,13 @@ def _core_forward(lay: L.Layout, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, r_b, 
         prof.lap("latent_attention_ms")
     y = _empty((B, T, H, Dh), dt, device)
     keep = saved or prof is not None
-    ol = _empty((B, T, H, Dh), dt, device) if keep else None
+    # o_local is the op's own: head-major [B, H, T, Dh], so that a head's rows are one contiguous run
+    ol = _empty((B, H, T, Dh), dt, device) if keep else None
     lse = _empty((B, H, T), torch.float32, device) if keep else None
     w = _empty((B, H, T), torch.float32, device) if keep else None
     _call("llattn_local_gate_fwd", _byref(shape), _byref(q), _byref(k), _byref(v),
           _byref(L.view(R, R.stride(0), R.stride(1), Dh)), gate_l.data_ptr(),
-          gate_r.data_ptr(), _byref(L.view_bnhd(y)), None if ol is None else _byref(L.view_bnhd(ol)),
+          gate_r.data_ptr(), _byref(L.view_bnhd(y)), None if ol is None else _byref(L.view_bhnd(ol)),
           None if lse is None else lse.data_ptr(), None if w is None else w.data_ptr(), stream)
     if prof is not None:
         prof.lap("local_attention_ms")
@@ -199,7 +200,7 @@ def _core_backward(lay: L.Layout, dy, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, 
     ws = _empty((L.workspace_bytes(shape, L.WS_LOCAL_BWD),), torch.uint8, device)
     _call("llattn_local_gate_bwd",
           _byref(shape), _byref(q), _byref(k), _byref(v), _byref(L.view(R, R.stride(0), R.stride(1), Dh)),
-          gate_l.data_ptr(), gate_r.data_ptr(), _byref(L.view_bnhd(ol)), lse.data_ptr(), w.data_ptr(),
+          gate_l.data_ptr(), gate_r.data_ptr(), _byref(L.view_bhnd(ol)), lse.data_ptr(), w.data_ptr(),
           _byref(L.view(dy, dy.stride(0), dy.stride(1), Dh)), _byref(dq), _byref(dk), _byref(dv),
           _byref(L.view(drem, drem.stride(0), drem.stride(1), Dh)), dgl.data_ptr(), dgr.data_ptr(),
           None if dr_b is None else dr_b.data_ptr(), ws.data_ptr(), ws.numel(), stream)
