@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define LLATTN_ABI_VERSION 6
+#define LLATTN_ABI_VERSION 7
 
 /* status codes */
 #define LLATTN_OK 0
@@ -208,6 +208,21 @@ typedef struct llattn_gemm_rowadd {
 #define LLATTN_ACT_GELU 1
 #define LLATTN_ACT_MUL_AUX 2
 
+/* Split-head storage of a bf16 matrix of token rows: a [rows][ld] matrix (rows = batch x T) keeps its first
+ * n * dh columns as n head slabs per sequence, [batch][n][T][dh], followed by its other ld - n * dh
+ * columns as one packed [rows][ld - n * dh] block.  Element (r, c), r = b T + t, sits at
+ *   ((b n + c / dh) T + t) dh + c % dh            for c < n dh,
+ *   rows n dh + r (ld - n dh) + c - n dh          otherwise.
+ * The forward of the block's q|k|v (| token-wise latent query) projection writes it this way (n = 3 H
+ * heads of dh = Dh), so that each head of a sequence is one contiguous run for the local-attention
+ * kernels, which read q, k and v by strides, in place of the packed [tokens][3 D (+ Ld)] matrix
+ * (reference models.py:315-316, view(B, T, 3, H, Dh)).  T = 0: plain row-major storage. */
+typedef struct llattn_heads_layout {
+  int32_t T;   /* rows per sequence; 0: none */
+  int32_t dh;  /* columns per head, a multiple of 8 */
+  int32_t n;   /* head slabs per sequence */
+} llattn_heads_layout;
+
 typedef struct llattn_gemm_desc {
   int32_t M, N, K;
   int32_t a_trans, b_trans;
@@ -229,6 +244,9 @@ typedef struct llattn_gemm_desc {
   int32_t act;                  /* LLATTN_ACT_* */
   void* aux;                    /* bf16 [M][ld_aux]: gelu' written (LLATTN_ACT_GELU) or read (_MUL_AUX) */
   int64_t ld_aux;
+  /* bf16 C [M][ldc] stored split-head (the forward of a projection: a_trans = b_trans = 0, no K split,
+     accumulation or activation, K > 64). */
+  llattn_heads_layout c_heads;
 } llattn_gemm_desc;
 
 size_t llattn_gemm_workspace_size(const llattn_gemm_desc* d);

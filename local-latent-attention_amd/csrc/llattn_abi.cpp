@@ -61,6 +61,38 @@ int32_t check_shape(const llattn_shape* s) {
   return LLATTN_OK;
 }
 
+void magic_div(uint32_t d, uint32_t* m, uint32_t* s) {
+  uint32_t sh = 0;
+  while ((uint64_t(1) << sh) < d) ++sh;
+  *s = sh;
+  *m = (uint32_t)((((uint64_t(1) << sh) - d) << 32) / d + 1);
+}
+
+int32_t heads_map(const char* who, const llattn_heads_layout* l, int64_t rows, int64_t ld, int64_t width,
+                  HeadsMap* out) {
+  *out = HeadsMap{};
+  if (l == nullptr || l->T == 0) return LLATTN_OK;
+  if (l->T < 0 || l->dh <= 0 || l->n <= 0 || l->dh % 8 || rows % l->T)
+    return fail(LLATTN_ERR_LAYOUT, "%s: split-head layout T=%d dh=%d n=%d: needs T, n > 0, dh a positive multiple of "
+                "8 and whole sequences of T rows (rows=%lld)", who, l->T, l->dh, l->n, (long long)rows);
+  const int64_t cols = (int64_t)l->n * l->dh;
+  if (cols > width || width > ld || ld % 8)
+    return fail(LLATTN_ERR_LAYOUT, "%s: split-head layout of %lld head columns in a matrix of width %lld, ld %lld",
+                who, (long long)cols, (long long)width, (long long)ld);
+  if (rows * ld * 2 >= (int64_t(1) << 31))
+    return fail(LLATTN_ERR_UNSUPPORTED, "%s: a split-head matrix must be below 2 GiB (%lld x %lld)", who,
+                (long long)rows, (long long)ld);
+  out->T = l->T;
+  out->dh = l->dh;
+  out->n = l->n;
+  out->cols = (int)cols;
+  magic_div((uint32_t)l->T, &out->mt, &out->st);
+  magic_div((uint32_t)l->dh, &out->md, &out->sd);
+  out->tail = (uint32_t)(rows * cols);
+  out->tail_ld = (int)(ld - cols);
+  return LLATTN_OK;
+}
+
 }  // namespace llattn
 
 using namespace llattn;

@@ -34,4 +34,21 @@ int32_t check_shape(const llattn_shape* s);
 // workspace bytes of llattn_latent_bwd for a checked shape
 size_t latent_workspace_bytes(const llattn_shape* s);
 
+// Split-head storage (llattn_heads_layout) as the kernels address it: divisions by T and dh become
+// multiply-high reciprocals (x / d = (umulhi(x, m) + x) >> s, exact for x < 2^31; Granlund and Montgomery,
+// "Division by invariant integers using multiplication", PLDI 1994, the 32-bit round-up variant).
+struct HeadsMap {
+  int T, dh, n, cols;       // cols = n dh; T = 0: plain row-major storage
+  uint32_t mt, st, md, sd;  // reciprocals of T and dh
+  uint32_t tail;            // element offset of the packed block: rows * cols
+  int tail_ld;              // its row length: ld - cols
+};
+// The reciprocal (m, s) of a divisor 1 <= d < 2^31.
+void magic_div(uint32_t d, uint32_t* m, uint32_t* s);
+// Checks a split-head layout of a stored matrix of `rows` token rows, `ld` elements apart, whose first
+// `width` columns are used, and fills `out` (l NULL or l->T == 0: plain storage, out->T = 0).  `who` names the
+// entry point in the error message.
+int32_t heads_map(const char* who, const llattn_heads_layout* l, int64_t rows, int64_t ld, int64_t width,
+                  HeadsMap* out);
+
 }  // namespace llattn

@@ -29,6 +29,9 @@
 // large): split s covers the 64-wide k steps [s*P/S, (s+1)*P/S) of P and writes fp32 partials; an
 // ordered reduction adds them (deterministic, no atomics).
 //
+// Split-head C (llattn_heads_layout, the q|k|v projection output stored as per-sequence head slabs): the
+// persistent kernel's stores take each 8-column piece to its slab; the arithmetic is the same.
+//
 // K need not be a multiple of the step: the last steps read zero past K.  Rows of an m/n-contiguous
 // operand past K lie beyond its buffer extent and read zero by themselves; a k-contiguous operand
 // (K a multiple of 8) masks the lanes whose 8 k values start at or past K with an out-of-range
@@ -37,6 +40,7 @@
 
 #include "llattn_abi.h"
 #include "llattn_device.h"
+#include "llattn_heads.h"
 
 namespace llattn {
 namespace gemm {
@@ -65,6 +69,7 @@ struct GemmArgs {
   int act;
   uint16_t* aux;
   int64_t ld_aux;
+  HeadsMap ch;  // bf16 C stored split-head (ch.T > 0; persistent kernel)
 };
 
 // Exact GELU u * Phi(u) of the reference FeedForward (reference models.py:57, F.gelu) and its derivative
@@ -585,7 +590,7 @@ __device__ __forceinline__ void tile_origin(const GemmArgs& a, int v, int total,
   n0 = ((t % (GM * a.tiles_n)) / gm) * BN;
 }
 
-template <int ACT>
+template <int ACT, bool CH = false>
 __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) {
   constexpr int EPI_OPS = epi_ops<ACT>();
   __shared__ __align__(1024) unsigned char smem[NST * STAGE_BYTES];
@@ -621,8 +626,8 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
     }
   };
 
-  // C through a range-checked buffer (a masked lane's offset is past the extent)
-  const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.C, ((int64_t)(a.M - 1) * a.ldc + a.N) * 2);
+  // C through a range-checked buffer (a masked lane's offset is past the extent; split-head C: the whole matrix)
+  const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.C, (CH ? (int64_t)a.M * a.ldc : (int64_t)(a.M - 1) * a.ldc + a.N) * 2);
   const __amdgpu_buffer_rsrc_t raux = make_rsrc(ACT == LLATTN_ACT_GELU ? a.aux : a.C,
                                                 ((int64_t)(a.M - 1) * (ACT == LLATTN_ACT_GELU ? a.ld_aux : a.ldc) + a.N) * 2);
   // this wave's 64-column slice of a tile's bias into sbias[slot] (lanes 0..15, 16 bytes each;
@@ -740,7 +745,9 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
         const f32x4 u = acc[i][2 * p], w = acc[i][2 * p + 1];
         const uint4 x = make_uint4(pack_bf16x2(u[0] + b0.x, u[1] + b0.y), pack_bf16x2(u[2] + b0.z, u[3] + b0.w),
                                    pack_bf16x2(w[0] + b1.x, w[1] + b1.y), pack_bf16x2(w[2] + b1.z, w[3] + b1.w));
-        const uint32_t oc = (row < a.M && col < a.N) ? (uint32_t)((int64_t)row * a.ldc + col) * 2u : kOffOOB;
+        const uint32_t oc = (row < a.M && col < a.N)
+                                ? (CH ? heads_off(a.ch, (uint32_t)row, (uint32_t)col) : (uint32_t)((int64_t)row * a.ldc + col)) * 2u
+                                : kOffOOB;
         if constexpr (ACT == LLATTN_ACT_GELU) {
           uint4 g, gp;
           gelu_bf16x8(x, g, gp);
@@ -912,7 +919,6 @@ __device__ __forceinline__ void small_store(const uint4 (&v)[2], unsigned char* 
 template <bool AK, bool BKM, int EPI>
 __global__ __launch_bounds__(256) void gemm_small_kernel(const GemmArgs a) {
   __shared__ __align__(16) unsigned char As[2][SBT * 128], Bs[2][SBT * 128];
-  __shared__ float rsum[SBT];
   const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
   const int wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
   const int tn_count = (a.N + SBT - 1) / SBT;
@@ -1023,7 +1029,8 @@ void launch_small(const GemmArgs& a, int c_dtype, hipStream_t st) {
 // 256 x 256 with one side at most 1024, and a contraction of at most 4096.
 bool use_small(const llattn_gemm_desc* d) {
   const int64_t tiles = (int64_t)((d->M + BM - 1) / BM) * ((d->N + BN - 1) / BN);
-  return d->split_k == 0 && d->act == LLATTN_ACT_NONE && !d->rowadd[0].ptr && !d->rowadd[1].ptr && tiles <= 32 &&
+  return d->split_k == 0 && d->act == LLATTN_ACT_NONE && !d->rowadd[0].ptr && !d->rowadd[1].ptr &&
+         d->c_heads.T == 0 && tiles <= 32 &&
          std::min(d->M, d->N) <= 1024 && d->K <= 4096;
 }
 
@@ -1035,6 +1042,7 @@ bool use_small(const llattn_gemm_desc* d) {
 // splits fill three rounds exactly, where 2 would leave a quarter of the CUs idle.
 int resolve_split(const llattn_gemm_desc* d) {
   if (d->split_k > 0) return d->split_k;
+  if (d->c_heads.T != 0) return 1;  // a split-head C comes from the persistent kernel
   const int64_t tiles = (int64_t)((d->M + BM - 1) / BM) * ((d->N + BN - 1) / BN);
   if (tiles >= 224) return 1;
   const int64_t pairs = (d->K + 2 * BK - 1) / (2 * BK);
@@ -1125,6 +1133,12 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
     if (((int64_t)(d->M - 1) * d->ld_aux + d->N) * 2 >= (int64_t(1) << 31))
       return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: the activation's aux matrix must be below 2 GiB");
   }
+  HeadsMap ch;
+  if (const int32_t rc = heads_map("llattn_gemm (C)", &d->c_heads, d->M, d->ldc, d->N, &ch)) return rc;
+  if (ch.T && (d->a_trans || d->b_trans || d->c_dtype != LLATTN_BF16 || d->accumulate || d->act != LLATTN_ACT_NONE ||
+               d->rowadd[0].ptr || d->rowadd[1].ptr || S != 1 || k_pairs < 2))
+    return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: a split-head C needs a_trans = b_trans = 0, bf16 C, no "
+                "accumulation, activation, row addends or K split, and K > %d", 2 * BK);
   const size_t need = llattn_gemm_workspace_size(d);
   if (need && (!workspace || workspace_bytes < need || !aligned16(workspace)))
     return fail(LLATTN_ERR_WORKSPACE, "llattn_gemm: %d K splits need %zu workspace bytes (got %zu)", S, need,
@@ -1136,6 +1150,7 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
   a.A = static_cast<const uint16_t*>(d->A); a.lda = d->lda; a.a_bytes = a_bytes;
   a.B = static_cast<const uint16_t*>(d->B); a.ldb = d->ldb; a.b_bytes = b_bytes;
   a.C = d->C; a.ldc = d->ldc;
+  a.ch = ch;
   a.bias = d->bias;
   a.part = static_cast<float*>(workspace);
   a.rowsum = d->a_rowsum;
@@ -1168,8 +1183,13 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
     const int tiles = a.tiles_m * a.tiles_n;
     if (a.act == LLATTN_ACT_GELU)
       hipLaunchKernelGGL(gemm_persistent_kernel<LLATTN_ACT_GELU>, dim3(std::min(tiles, cus)), dim3(256), 0, st, a);
+    else if (ch.T)
+      hipLaunchKernelGGL((gemm_persistent_kernel<LLATTN_ACT_NONE, true>), dim3(std::min(tiles, cus)), dim3(256), 0, st, a);
     else
       hipLaunchKernelGGL(gemm_persistent_kernel<LLATTN_ACT_NONE>, dim3(std::min(tiles, cus)), dim3(256), 0, st, a);
+  } else if (ch.T) {
+    return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: a split-head C of %lld bytes: the persistent kernel takes outputs "
+                "below 2 GiB", (long long)c_bytes);
   } else if (!d->a_trans && !d->b_trans) launch<true, true>(a, S, d->c_dtype, st);
   else if (!d->a_trans && d->b_trans) launch<true, false>(a, S, d->c_dtype, st);
   else if (d->a_trans && d->b_trans) launch<false, false>(a, S, d->c_dtype, st);

@@ -16,7 +16,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libllattn_gfx950.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 OK, ERR_SHAPE, ERR_DTYPE, ERR_LAYOUT, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_LAUNCH = range(7)
 F32, BF16 = 0, 1
@@ -43,13 +43,18 @@ class LlattnGemmRowadd(ctypes.Structure):
                 ("seg", ctypes.c_int32), ("n_seg", ctypes.c_int32), ("divisor", ctypes.c_int32)]
 
 
+class LlattnHeadsLayout(ctypes.Structure):
+    """Split-head storage of a token-row matrix (include/llattn.h llattn_heads_layout); T = 0: row-major."""
+    _fields_ = [("T", ctypes.c_int32), ("dh", ctypes.c_int32), ("n", ctypes.c_int32)]
+
+
 class LlattnGemmDesc(ctypes.Structure):
     _fields_ = [("M", ctypes.c_int32), ("N", ctypes.c_int32), ("K", ctypes.c_int32), ("a_trans", ctypes.c_int32),
                 ("b_trans", ctypes.c_int32), ("A", ctypes.c_void_p), ("lda", ctypes.c_int64), ("B", ctypes.c_void_p),
                 ("ldb", ctypes.c_int64), ("C", ctypes.c_void_p), ("ldc", ctypes.c_int64), ("c_dtype", ctypes.c_int32),
                 ("accumulate", ctypes.c_int32), ("bias", ctypes.c_void_p), ("split_k", ctypes.c_int32),
                 ("a_rowsum", ctypes.c_void_p), ("rowadd", LlattnGemmRowadd * 2), ("act", ctypes.c_int32),
-                ("aux", ctypes.c_void_p), ("ld_aux", ctypes.c_int64)]
+                ("aux", ctypes.c_void_p), ("ld_aux", ctypes.c_int64), ("c_heads", LlattnHeadsLayout)]
 
 
 _P = ctypes.c_void_p

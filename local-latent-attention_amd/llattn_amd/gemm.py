@@ -9,6 +9,11 @@ transpose copy (all operands bf16, fp32 accumulation):
 
 Each takes 2-D views whose innermost dimension is contiguous; outputs may be
 passed in (``out=``) and accumulated into (``accumulate=True``).
+
+Split-head output: ``linear(..., heads=(T, dh, n))`` stores the ``[tokens, width]`` product with its first
+``n * dh`` columns as per-sequence head slabs ``[batch][n][T][dh]`` followed by the other columns packed
+(``llattn_heads_layout`` of the C ABI).  The tensor returned is the ``[tokens, width]`` view of that storage;
+it is read by strides (the local-attention kernels), not as a row-major matrix.
 """
 from __future__ import annotations
 
@@ -27,9 +32,13 @@ def _check2d(name: str, t: torch.Tensor) -> None:
         raise ValueError(f"{name} must be bfloat16 (got {t.dtype})")
 
 
+def _heads(h) -> L.LlattnHeadsLayout:
+    return L.LlattnHeadsLayout(0, 0, 0) if h is None else L.LlattnHeadsLayout(*h)
+
+
 def _run(M: int, N: int, K: int, A: torch.Tensor, a_trans: bool, B: torch.Tensor, b_trans: bool, C: torch.Tensor,
          bias: torch.Tensor | None, accumulate: bool, split_k: int = 0, rowsum: torch.Tensor | None = None,
-         rowadd=(), act: int = 0, aux: torch.Tensor | None = None) -> None:
+         rowadd=(), act: int = 0, aux: torch.Tensor | None = None, c_heads=None) -> None:
     L.require_gpu(A, B, C)
     if rowsum is not None and (rowsum.dtype != torch.float32 or not rowsum.is_contiguous() or rowsum.numel() != M):
         raise ValueError(f"rowsum must be a contiguous fp32 vector of {M} elements")
@@ -49,6 +58,7 @@ def _run(M: int, N: int, K: int, A: torch.Tensor, a_trans: bool, B: torch.Tensor
             raise ValueError(f"the activation's aux must be a bf16 [{M}, {N}] view with a contiguous inner dimension")
         L.require_gpu(aux)
         desc.act, desc.aux, desc.ld_aux = act, aux.data_ptr(), aux.stride(0)
+    desc.c_heads = _heads(c_heads)
     for q, (rows, per_seq, seg, n_seg, divisor) in enumerate(rowadd):
         if rows.dtype != torch.bfloat16 or rows.stride(-1) != 1 or rows.shape[-1] != N:
             raise ValueError(f"row addend {q} must be bf16 rows of {N} contiguous elements")
@@ -62,8 +72,8 @@ def _run(M: int, N: int, K: int, A: torch.Tensor, a_trans: bool, B: torch.Tensor
 
 
 def linear(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None, out: torch.Tensor | None = None,
-           accumulate: bool = False) -> torch.Tensor:
-    """``x [M, K] @ w [N, K]^T (+ bias fp32 [N])`` -> bf16 ``[M, N]``."""
+           accumulate: bool = False, heads=None) -> torch.Tensor:
+    """``x [M, K] @ w [N, K]^T (+ bias fp32 [N])`` -> bf16 ``[M, N]`` (``heads``: stored split-head)."""
     _check2d("x", x)
     _check2d("w", w)
     M, K = x.shape
@@ -72,7 +82,7 @@ def linear(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None, o
         raise ValueError(f"x is [{M}, {K}] but w is {tuple(w.shape)}")
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
-    _run(M, N, K, x, False, w, False, out, bias, accumulate)
+    _run(M, N, K, x, False, w, False, out, bias, accumulate, c_heads=heads)
     return out
 
 

@@ -53,9 +53,10 @@ def pack_params(groups):
     return outs
 
 
-def linear_fwd(x2: torch.Tensor, w: torch.Tensor, b32: torch.Tensor | None) -> torch.Tensor:
-    """bf16 ``x2 @ w^T + b`` (fp32 bias added before the bf16 rounding of the output) on the MFMA GEMM."""
-    return gemm.linear(x2, w, b32)
+def linear_fwd(x2: torch.Tensor, w: torch.Tensor, b32: torch.Tensor | None, heads=None) -> torch.Tensor:
+    """bf16 ``x2 @ w^T + b`` (fp32 bias added before the bf16 rounding of the output) on the MFMA GEMM
+    (``heads``: the output stored split-head, see :mod:`llattn_amd.gemm`)."""
+    return gemm.linear(x2, w, b32, heads=heads)
 
 
 def input_grad(dy2: torch.Tensor, w: torch.Tensor, rowadd=()) -> torch.Tensor:
@@ -78,7 +79,7 @@ def weight_grad(dy2: torch.Tensor, x2: torch.Tensor, bias_grad: bool = False):
 
 class _Project(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, pools, packed, *params):
+    def forward(ctx, x, pools, packed, heads, *params):
         # packed: (bf16 weights, fp32 biases) already concatenated by pack_params, or None
         ctx.set_materialize_grads(False)
         ws, bs = params[0::2], params[1::2]
@@ -99,7 +100,7 @@ class _Project(torch.autograd.Function):
             else:
                 packs = pack_params([(ws, BF16)] + ([(bs, torch.float32)] if has_bias else []))
                 wcat, bcat = packs[0], (packs[1] if has_bias else None)
-            y = linear_fwd(x2, wcat, bcat)
+            y = linear_fwd(x2, wcat, bcat, heads)
             pooled = []
             if pools:
                 from .ops import _contig, pool_fwd_into
@@ -153,10 +154,10 @@ class _Project(torch.autograd.Function):
             grads.append(None if dw is None else dw[o:o + n].to(wd))
             grads.append(None if db is None else db[o:o + n].to(bd))
             o += n
-        return (dx, None, None, *grads)
+        return (dx, None, None, None, *grads)
 
 
-def project(x: torch.Tensor, *linears: torch.nn.Linear, pools=(), packed=None):
+def project(x: torch.Tensor, *linears: torch.nn.Linear, pools=(), packed=None, heads=None):
     """bf16 ``x @ [W_1; W_2; ...]^T + [b_1; b_2; ...]`` (all layers share the input width); backward gives
     fp32 weight and bias gradients in the parameters' dtypes.  Every product (forward, input and weight
     gradient) runs on the gfx950 MFMA GEMM; shapes it does not take raise.
@@ -165,9 +166,12 @@ def project(x: torch.Tensor, *linears: torch.nn.Linear, pools=(), packed=None):
     :func:`llattn_amd.ops.pool`) returned after the projection, ``(y, pooled_1, ...)``; their backward adds
     into the projection's input gradient in place, so the block's input gradient is formed once.  Without
     ``pools`` the projection alone is returned.  ``packed``: ``(bf16 [sum N_i, K] weights, fp32 biases or None)``
-    already cast and concatenated (:func:`pack_params`), so a caller casts all its weights in one launch."""
+    already cast and concatenated (:func:`pack_params`), so a caller casts all its weights in one launch.
+    ``heads``: ``(T, dh, n)`` -- the output ``[B, T, N]`` is stored split-head (its first ``n * dh`` columns as
+    ``[B][n][T][dh]`` slabs, the rest packed after them; :mod:`llattn_amd.gemm`), for a consumer that reads it
+    by strides (:class:`llattn_amd.ops.LLAttnCore`); its gradient comes back as a plain row-major tensor."""
     params = []
     for lin in linears:
         params += [lin.weight, lin.bias]
-    out = _Project.apply(x, tuple(pools), packed, *params)
+    out = _Project.apply(x, tuple(pools), packed, heads, *params)
     return out if pools else out[0]

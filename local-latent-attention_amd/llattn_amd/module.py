@@ -11,7 +11,9 @@ Data flow of one forward (B, T, D = batch, tokens, d_model):
 1. ``qkvr = x @ [W_qkv; W_rq]^T + b`` -- one GEMM for q|k|v and the token-wise
    latent queries (macro-block mode: ``qkv`` GEMM, HIP query-block pooling,
    ``rq_proj`` GEMM); under bf16 autocast through :func:`~llattn_amd.linear.project`,
-   whose weight gradients come from the gfx950 MFMA kernel in fp32;
+   whose weight gradients come from the gfx950 MFMA kernel in fp32, with q|k|v stored
+   split-head (``[B][3H][T][Dh]`` slabs, the latent queries packed after them) so that
+   the local-attention kernels stream each head as one contiguous run;
 2. ``pooled = chunk means of x`` (HIP) and ``gkgv = rkv_proj(pooled)`` (GEMM);
 3. :class:`~llattn_amd.ops.LLAttnCore` -- HIP latent attention, ``r_out``
    GEMM, HIP windowed attention with the gate mix fused in its epilogue;
@@ -27,7 +29,7 @@ import torch.nn.functional as F
 
 from . import _lib as L
 from .linear import pack_params, project
-from .ops import LLAttnCore, _Prof, pool
+from .ops import LLAttnCore, _Prof, heads_layout_ok, pool
 
 
 class LocalLatentAttentionTriton(nn.Module):
@@ -115,16 +117,20 @@ class LocalLatentAttentionTriton(nn.Module):
         latents = (lay.chunk, lay.n_chunks, L.DIV_COUNT)
         pooled = None
         packed = self._packed_weights(macro) if bf16 else {}
+        # bf16: q|k|v stored split-head -- each head of a sequence one contiguous run for the local-attention
+        # kernels, written and read in that order by the projection's GEMMs
+        heads = bf16 and heads_layout_ok(lay, D, not macro)
+        hl = (T, lay.Dh, 3 * self.n_heads) if heads else None
         if macro and bf16:
             # both poolings of x ride on the projection, whose backward adds their gradients in place
             qkvr, pq, pooled = project(x, self.qkv_proj, pools=[(lay.q_block, lay.n_q, L.DIV_SEG), latents],
-                                       packed=packed["qkv"])
+                                       packed=packed["qkv"], heads=hl)
             rq = project(pq, self.rq_proj, packed=packed["rq"])
         elif macro:
             qkvr = self.qkv_proj(x)
             rq = self.rq_proj(pool(x, lay.q_block, lay.n_q, L.DIV_SEG))
         elif bf16:
-            qkvr, pooled = project(x, self.qkv_proj, self.rq_proj, pools=[latents], packed=packed["qkv"])
+            qkvr, pooled = project(x, self.qkv_proj, self.rq_proj, pools=[latents], packed=packed["qkv"], heads=hl)
             rq = None
         else:
             w = torch.cat([self.qkv_proj.weight, self.rq_proj.weight], dim=0)
@@ -144,7 +150,7 @@ class LocalLatentAttentionTriton(nn.Module):
         # forward only (no_grad, e.g. generation): the kernels skip what only the backward reads
         saved = torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))
         y = LLAttnCore.apply(qkvr, rqc, gkgv.to(qkvr.dtype), self.gate_local.weight, self.gate_remote.weight,
-                             self.r_out.weight, self.r_out.bias, lay, prof, packed.get("r_out"), saved)
+                             self.r_out.weight, self.r_out.bias, lay, prof, packed.get("r_out"), saved, heads)
         if prof is not None:
             # the gate mix runs in the local kernel's epilogue: its time is in local_attention_ms
             prof.t["gate_mix_ms"] = 0.0

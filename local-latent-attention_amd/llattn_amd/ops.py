@@ -231,6 +231,28 @@ def _gate_grad(dg: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
 # packed core used by the module
 # ---------------------------------------------------------------------------
 
+def _qkv_views(lay: L.Layout, qkv: torch.Tensor, token_rq: bool, heads: bool):
+    """q, k, v (and, for token-wise latent queries, rq) views of the projection output ``qkv`` [B, T, 3D (+Ld)]:
+    packed rows (``view(B, T, 3, H, Dh)``, reference models.py:315-316) or, with ``heads``, split-head storage
+    -- the 3H heads as ``[B][3H][T][Dh]`` slabs, then the latent queries packed as ``[B T][Ld]``."""
+    B, T, H, Dh, Ldh = lay.B, lay.T, lay.H, lay.Dh, lay.Ldh
+    D, Ld = H * Dh, lay.Lh * Ldh
+    if not heads:
+        sb, sn = qkv.stride(0), qkv.stride(1)
+        q, k, v = (L.view(qkv, sb, sn, Dh, i * D) for i in range(3))
+        return q, k, v, (L.view(qkv, sb, sn, Ldh, 3 * D) if token_rq else None)
+    q, k, v = (L.view(qkv, 3 * H * T * Dh, Dh, T * Dh, i * H * T * Dh) for i in range(3))
+    return q, k, v, (L.view(qkv, T * Ld, Ld, Ldh, B * T * 3 * D) if token_rq else None)
+
+
+def heads_layout_ok(lay: L.Layout, d_model: int, token_rq: bool) -> bool:
+    """Whether the block's q|k|v projection can be stored split-head (``heads`` of :class:`LLAttnCore`): the
+    GEMM writes it from its persistent kernel (d_model > 64), all of it below 2 GiB."""
+    D = lay.H * lay.Dh
+    width = 3 * D + (lay.Lh * lay.Ldh if token_rq else 0)
+    return d_model > 64 and lay.Dh % 8 == 0 and width % 8 == 0 and lay.B * lay.T * width * 2 < (1 << 31)
+
+
 class LLAttnCore(torch.autograd.Function):
     """Fused core of ``LocalLatentAttention`` over packed projections.
 
@@ -241,11 +263,13 @@ class LLAttnCore(torch.autograd.Function):
     (reference models.py:333-342); the shared gate weights [1, Dh] (or per-head
     [H, Dh]); ``r_out`` weight [D, Ld] and bias [D].  Returns the gate-mixed
     heads [B, T, D] ready for the output projection (reference models.py:438).
+    ``heads``: ``qkv`` is stored split-head (``project(..., heads=(T, Dh, 3H))``); the gradient returned for
+    it is a plain row-major [B, T, 3D (+Ld)] tensor either way.
     """
 
     @staticmethod
     def forward(ctx, qkv, rq, gkgv, gate_l, gate_r, r_w, r_b, lay: L.Layout, prof=None, r_w_cast=None,
-                saved: bool = True):
+                saved: bool = True, heads: bool = False):
         L.require_gpu(qkv, rq, gkgv)
         dt, device = qkv.dtype, qkv.device
         H, Dh, Lh, Ldh = lay.H, lay.Dh, lay.Lh, lay.Ldh
@@ -262,9 +286,9 @@ class LLAttnCore(torch.autograd.Function):
         if tuple(gkgv.shape) != (lay.B, lay.n_chunks, 2 * Ld):
             raise ValueError(f"gkgv must be [B, {lay.n_chunks}, {2 * Ld}], got {tuple(gkgv.shape)}")
         gl, gr = _aligned_f32(gate_l), _aligned_f32(gate_r)
-        sb, sn = qkv.stride(0), qkv.stride(1)
-        q, k, v = (L.view(qkv, sb, sn, Dh, i * D) for i in range(3))
-        rqv = L.view(qkv, sb, sn, Ldh, 3 * D) if rq is None else L.view(rq, rq.stride(0), rq.stride(1), Ldh)
+        q, k, v, rqv = _qkv_views(lay, qkv, rq is None, heads)
+        if rq is not None:
+            rqv = L.view(rq, rq.stride(0), rq.stride(1), Ldh)
         gk = L.view(gkgv, gkgv.stride(0), gkgv.stride(1), Ldh)
         gv = L.view(gkgv, gkgv.stride(0), gkgv.stride(1), Ldh, Ld)
         # cast once (or given cast): the backward's input gradient reuses it
@@ -273,7 +297,7 @@ class LLAttnCore(torch.autograd.Function):
                                                        saved=saved)
         if saved:
             ctx.save_for_backward(qkv, rq, gkgv, gl, gr, r_wd, lat, lse_lat, R, ol, lse, w)
-        ctx.lay, ctx.has_rb, ctx.packed = lay, r_b is not None, rq is None
+        ctx.lay, ctx.has_rb, ctx.packed, ctx.heads = lay, r_b is not None, rq is None, heads
         ctx.r_w_dtype = r_w.dtype
         ctx.gate_like = (gate_l, gate_r)
         ctx.r_b_dtype = None if r_b is None else r_b.dtype
@@ -289,16 +313,17 @@ class LLAttnCore(torch.autograd.Function):
         H, Dh, Lh, Ldh = lay.H, lay.Dh, lay.Lh, lay.Ldh
         D, Ld = H * Dh, Lh * Ldh
         dy = _contig(dy.to(dt))
-        sb, sn = qkv.stride(0), qkv.stride(1)
-        q, k, v = (L.view(qkv, sb, sn, Dh, i * D) for i in range(3))
-        rqv = L.view(qkv, sb, sn, Ldh, 3 * D) if rq is None else L.view(rq, rq.stride(0), rq.stride(1), Ldh)
+        q, k, v, rqv = _qkv_views(lay, qkv, rq is None, ctx.heads)
+        if rq is not None:
+            rqv = L.view(rq, rq.stride(0), rq.stride(1), Ldh)
         gk = L.view(gkgv, gkgv.stride(0), gkgv.stride(1), Ldh)
         gv = L.view(gkgv, gkgv.stride(0), gkgv.stride(1), Ldh, Ld)
+        # the gradient in plain rows whatever the storage of qkv: the projection's backward GEMMs read it as
+        # their row-major operand
         dqkv = torch.empty_like(qkv)
-        db, dn = dqkv.stride(0), dqkv.stride(1)
-        dq, dk, dv = (L.view(dqkv, db, dn, Dh, i * D) for i in range(3))
+        dq, dk, dv, drq = _qkv_views(lay, dqkv, rq is None, False)
         if rq is None:
-            drq_t, drq = None, L.view(dqkv, db, dn, Ldh, 3 * D)
+            drq_t = None
         else:
             drq_t = torch.empty_like(rq)
             drq = L.view(drq_t, drq_t.stride(0), drq_t.stride(1), Ldh)
@@ -309,7 +334,7 @@ class LLAttnCore(torch.autograd.Function):
                                               R, ol, lse, w, dq, dk, dv, drq, dgk, dgv, dt, device)
         gate_l, gate_r = ctx.gate_like
         return (dqkv, drq_t, dgkgv, _gate_grad(dgl, gate_l), _gate_grad(dgr, gate_r), dr_w.to(ctx.r_w_dtype),
-                None if dr_b is None else dr_b.to(ctx.r_b_dtype), None, None, None, None)
+                None if dr_b is None else dr_b.to(ctx.r_b_dtype), None, None, None, None, None)
 
 
 # ---------------------------------------------------------------------------

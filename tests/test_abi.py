@@ -33,7 +33,59 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_empty_error():
     L, lib = _lib()
-    assert lib.llattn_abi_version() == L.ABI_VERSION == 6
+    assert lib.llattn_abi_version() == L.ABI_VERSION == 7
+
+
+def test_struct_layouts_match_header(tmp_path):
+    """The ctypes mirrors of the C structs have the header's size and field offsets (gcc on include/llattn.h)."""
+    import shutil
+    import subprocess
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    L, _ = _lib()
+    structs = {"llattn_tensor": L.LlattnTensor, "llattn_shape": L.LlattnShape,
+               "llattn_gemm_rowadd": L.LlattnGemmRowadd, "llattn_heads_layout": L.LlattnHeadsLayout,
+               "llattn_gemm_desc": L.LlattnGemmDesc}
+    lines = ["#include <stddef.h>", "#include <stdio.h>", '#include "llattn.h"', "int main(void) {"]
+    for cname, cls in structs.items():
+        lines.append(f'  printf("{cname} sizeof %zu\\n", sizeof({cname}));')
+        for fname, _ in cls._fields_:
+            lines.append(f'  printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{REPO / 'include'}", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = {(a, b): int(c) for a, b, c in (ln.split() for ln in out if ln)}
+    for cname, cls in structs.items():
+        assert got[(cname, "sizeof")] == ctypes.sizeof(cls), cname
+        for fname, _ in cls._fields_:
+            assert got[(cname, fname)] == getattr(cls, fname).offset, (cname, fname)
+
+
+def test_multiply_high_division_is_exact():
+    """x / d = (umulhi(x, m) + x) >> s with the reciprocal of magic_div (llattn_abi.cpp): exact for x < 2^31, the
+    divisions by T and the head dim in split-head addressing.  Checked on the edges (multiples of d and their
+    neighbours, the top of the range) and on random numerators, for divisors up to 2^20 and a few large ones."""
+    import numpy as np
+
+    def magic(d):
+        s = 0
+        while (1 << s) < d:
+            s += 1
+        return ((((1 << s) - d) << 32) // d + 1) & 0xFFFFFFFF, s
+
+    rng = np.random.default_rng(0)
+    divisors = list(range(1, 300)) + [2048, 8192, 16384, 4095, 88 * 3, 1 << 20, (1 << 20) + 1, 2**31 - 1, 2**30 + 7]
+    for d in divisors:
+        m, s = magic(d)
+        x = np.concatenate([rng.integers(0, 2**31, 4000, dtype=np.uint64),
+                            np.array([0, 1, d - 1, d, d + 1, 2**31 - 1, 2**31 - 2], dtype=np.uint64),
+                            (np.arange(1, 200, dtype=np.uint64) * d) % (2**31),
+                            (np.arange(1, 200, dtype=np.uint64) * d - 1) % (2**31)])
+        q = (((x * np.uint64(m)) >> np.uint64(32)) + x) >> np.uint64(s)
+        np.testing.assert_array_equal(q, x // np.uint64(d), err_msg=f"d={d}")
 
 
 def _shape(L, **kw):
@@ -192,6 +244,28 @@ def test_gemm_rowsum_validation(kw, msg):
     d = _gemm_desc(L, **base)
     rc = lib.llattn_gemm(ctypes.byref(d), None, 0, None)
     assert rc == L.ERR_UNSUPPORTED, lib.llattn_last_error()
+    assert msg in lib.llattn_last_error()
+
+
+@pytest.mark.parametrize("hl,kw,code,msg", [
+    ((2048, 88, 48), dict(accumulate=1), 4, b"split-head C needs"),
+    ((2048, 88, 48), dict(K=64, lda=64, ldb=64), 4, b"split-head C needs"),
+    ((2048, 88, 48), dict(c_dtype=0), 4, b"split-head C needs"),
+    ((2048, 88, 48), dict(split_k=2), 4, b"split-head C needs"),
+    ((2048, 84, 48), {}, 3, b"multiple of 8"),
+    ((3000, 88, 48), {}, 3, b"whole sequences"),
+    ((2048, 88, 60), {}, 3, b"head columns"),
+])
+def test_gemm_split_head_c_validation(hl, kw, code, msg):
+    """A split-head C (the q|k|v projection output stored as head slabs) only comes from the persistent
+    kernel's path, with whole sequences and 8-aligned heads that fit the output width."""
+    L, lib = _lib()
+    base = dict(M=32768, N=4736, K=1408, a_trans=0, b_trans=0, lda=1408, ldb=1408, ldc=4736, c_dtype=L.BF16)
+    base.update(kw)
+    d = _gemm_desc(L, **base)
+    d.c_heads = L.LlattnHeadsLayout(*hl)
+    rc = lib.llattn_gemm(ctypes.byref(d), None, 0, None)
+    assert rc == code, lib.llattn_last_error()
     assert msg in lib.llattn_last_error()
 
 

@@ -363,3 +363,49 @@ def test_input_grad_through_transposed_weight(M, N, K):
     g = torch.Generator(device=dev).manual_seed(M + 3 * N + K)
     dy, w = _rand(M, K, gen=g, dev=dev), _rand(K, N, gen=g, dev=dev)
     assert _err(gemm.input_grad(dy, w), dy.float() @ w.float()) < BF16_TOL
+
+
+# ---- split-head operands (llattn_heads_layout): the q|k|v projection output stored as head slabs ----
+
+def _to_heads(x: torch.Tensor, T: int, dh: int, n: int) -> torch.Tensor:
+    """Row-major [B T, W] -> the same matrix in split-head storage, as a [B T, W] tensor: the first n dh
+    columns as [B][n][T][dh] slabs, then the other columns packed [B T][W - n dh] (torch permute, independent
+    of the kernels' offset arithmetic)."""
+    R, W = x.shape
+    B, c = R // T, n * dh
+    head = x[:, :c].reshape(B, T, n, dh).permute(0, 2, 1, 3).reshape(-1)
+    return torch.cat([head, x[:, c:].reshape(-1)]).view(R, W)
+
+
+def _from_heads(s: torch.Tensor, T: int, dh: int, n: int) -> torch.Tensor:
+    R, W = s.shape
+    B, c = R // T, n * dh
+    flat = s.reshape(-1)
+    head = flat[:R * c].view(B, n, T, dh).permute(0, 2, 1, 3).reshape(R, c)
+    return torch.cat([head, flat[R * c:].view(R, W - c)], dim=1)
+
+
+HEADS_CASES = [  # (B, T, dh, n, tail, K): head columns n dh, plus `tail` packed columns; K the contraction
+    (2, 160, 32, 6, 64, 192),
+    (3, 97, 88, 12, 0, 136),      # T not a multiple of 32 or 256: slabs start inside tiles and k steps
+    (2, 300, 16, 6, 512, 256),
+    (1, 64, 64, 3, 8, 72),
+    (16, 2048, 88, 48, 512, 1408),  # config 2: q|k|v|rq of the 0.55b layer
+]
+
+
+@pytest.mark.parametrize("case", HEADS_CASES)
+def test_linear_split_head_output(case):
+    """The persistent kernel's stores in split-head order: the same product as the row-major output."""
+    from llattn_amd import gemm
+    B, T, dh, n, tail, K = case
+    dev = require_cuda()
+    print("case: linear split-head C", case, flush=True)
+    g = torch.Generator(device=dev).manual_seed(B * T + dh + n + tail)
+    M, N = B * T, n * dh + tail
+    x, w = _rand(M, K, gen=g, dev=dev), _rand(N, K, gen=g, dev=dev)
+    b = torch.randn(N, device=dev, generator=g)
+    got = gemm.linear(x, w, b, heads=(T, dh, n))
+    assert _err(_from_heads(got, T, dh, n), x.float() @ w.float().T + b) < BF16_TOL
+    if M * N >= 1 << 24:  # both on the persistent kernel: only the store order differs
+        assert torch.equal(got, _to_heads(gemm.linear(x, w, b), T, dh, n))

@@ -422,3 +422,31 @@ def test_profile_stats_on_config1(c1_golden, bf16):
     assert abs(st["profile_gate_mean"] - float(np.mean(cache["w"]))) < (2e-3 if bf16 else 1e-5)
     m.set_profile(False)
     assert m.get_profile_stats() == {}
+
+
+@pytest.mark.parametrize("cfg", ["c2_b2", "macro"])
+def test_split_head_qkv_matches_packed_layout(cfg, monkeypatch):
+    """bf16 module forward + backward with the q|k|v projection stored split-head (the default) against the
+    packed row layout: only addresses differ, so the output and every gradient agree bit for bit."""
+    import llattn_amd.module as mod
+    dev = require_cuda()
+    if cfg == "c2_b2":
+        shape, B, T = _c2_shape(), 2, 2048
+    else:
+        shape = orc.BlockShape(d_model=256, n_heads=4, window=96, local_block_size=64, latent_tokens=24,
+                               latent_d_model=128, latent_heads=2, latent_query_block_size=16)
+        B, T = 2, 520
+    _print_case("split-head vs packed", cfg)
+    torch.manual_seed(3)
+    m = build_module(shape, None, dev)
+    lay = m.layout(B, T)
+    assert mod.heads_layout_ok(lay, shape.d_model, not lay.macro)
+    x = torch.randn(B, T, shape.d_model, device=dev).to(torch.bfloat16)
+    dout = torch.randn(B, T, shape.d_model, device=dev)
+    a = run_module(m, x, dout, autocast_bf16=True)
+    monkeypatch.setattr(mod, "heads_layout_ok", lambda *args: False)
+    b = run_module(m, x, dout, autocast_bf16=True)
+    np.testing.assert_array_equal(a[0], b[0])
+    np.testing.assert_array_equal(a[1], b[1])
+    for n in a[2]:
+        np.testing.assert_array_equal(a[2][n], b[2][n], err_msg=n)
