@@ -143,6 +143,20 @@ class _Prof:
             self._last = now
 
 
+def _remote_heads(lay: L.Layout, dt) -> bool:
+    """Whether ``r_out``'s output R [B, n_q, D] is stored split-head ([B][H][n_q][Dh] slabs): in bf16, where its
+    persistent GEMM writes it so (latent width above 64, below 2 GiB).  Only the local-attention kernels read R,
+    by strides, so each head of a sequence streams as one contiguous run."""
+    return dt == torch.bfloat16 and lay.Lh * lay.Ldh > 64 and lay.Dh % 8 == 0 and \
+        lay.B * lay.n_q * lay.H * lay.Dh * 2 < (1 << 31)
+
+
+def _remote_view(lay: L.Layout, R: torch.Tensor, heads: bool) -> L.LlattnTensor:
+    if heads:
+        return L.view(R, lay.H * lay.n_q * lay.Dh, lay.Dh, lay.n_q * lay.Dh)
+    return L.view(R, R.stride(0), R.stride(1), lay.Dh)
+
+
 def _core_forward(lay: L.Layout, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, r_b, dt, device, prof=None,
                   saved: bool = True):
     """Latent attention -> r_out -> local attention + gate.  q/k/v/rq/gk/gv are
@@ -162,8 +176,9 @@ def _core_forward(lay: L.Layout, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, r_b, 
           None if lse_lat is None else lse_lat.data_ptr(), stream)
     with torch.autocast(device_type="cuda", enabled=False):
         if dt == torch.bfloat16:
-            R = linear_fwd(lat.view(B * lay.n_q, Ld), r_w.to(dt), None if r_b is None else r_b.float()).view(
-                B, lay.n_q, D)
+            rh = (lay.n_q, Dh, H) if _remote_heads(lay, dt) else None
+            R = linear_fwd(lat.view(B * lay.n_q, Ld), r_w.to(dt), None if r_b is None else r_b.float(),
+                           rh).view(B, lay.n_q, D)
         else:
             R = F.linear(lat.view(B, lay.n_q, Ld), r_w.to(dt), None if r_b is None else r_b.to(dt))
     if prof is not None:
@@ -175,7 +190,7 @@ def _core_forward(lay: L.Layout, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, r_b, 
     lse = _empty((B, H, T), torch.float32, device) if keep else None
     w = _empty((B, H, T), torch.float32, device) if keep else None
     _call("llattn_local_gate_fwd", _byref(shape), _byref(q), _byref(k), _byref(v),
-          _byref(L.view(R, R.stride(0), R.stride(1), Dh)), gate_l.data_ptr(),
+          _byref(_remote_view(lay, R, _remote_heads(lay, dt))), gate_l.data_ptr(),
           gate_r.data_ptr(), _byref(L.view_bnhd(y)), None if ol is None else _byref(L.view_bhnd(ol)),
           None if lse is None else lse.data_ptr(), None if w is None else w.data_ptr(), stream)
     if prof is not None:
@@ -199,7 +214,7 @@ def _core_backward(lay: L.Layout, dy, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, 
     dr_b = _empty((D,), torch.float32, device) if has_rb else None
     ws = _empty((L.workspace_bytes(shape, L.WS_LOCAL_BWD),), torch.uint8, device)
     _call("llattn_local_gate_bwd",
-          _byref(shape), _byref(q), _byref(k), _byref(v), _byref(L.view(R, R.stride(0), R.stride(1), Dh)),
+          _byref(shape), _byref(q), _byref(k), _byref(v), _byref(_remote_view(lay, R, _remote_heads(lay, dt))),
           gate_l.data_ptr(), gate_r.data_ptr(), _byref(L.view_bhnd(ol)), lse.data_ptr(), w.data_ptr(),
           _byref(L.view(dy, dy.stride(0), dy.stride(1), Dh)), _byref(dq), _byref(dk), _byref(dv),
           _byref(L.view(drem, drem.stride(0), drem.stride(1), Dh)), dgl.data_ptr(), dgr.data_ptr(),

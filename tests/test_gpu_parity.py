@@ -426,9 +426,10 @@ def test_profile_stats_on_config1(c1_golden, bf16):
 
 @pytest.mark.parametrize("cfg", ["c2_b2", "macro"])
 def test_split_head_qkv_matches_packed_layout(cfg, monkeypatch):
-    """bf16 module forward + backward with the q|k|v projection stored split-head (the default) against the
-    packed row layout: only addresses differ, so the output and every gradient agree bit for bit."""
+    """bf16 module forward + backward with the q|k|v projection and r_out's output stored split-head (the
+    default) against packed rows: only addresses differ, so the output and every gradient agree bit for bit."""
     import llattn_amd.module as mod
+    import llattn_amd.ops as ops
     dev = require_cuda()
     if cfg == "c2_b2":
         shape, B, T = _c2_shape(), 2, 2048
@@ -444,7 +445,9 @@ def test_split_head_qkv_matches_packed_layout(cfg, monkeypatch):
     x = torch.randn(B, T, shape.d_model, device=dev).to(torch.bfloat16)
     dout = torch.randn(B, T, shape.d_model, device=dev)
     a = run_module(m, x, dout, autocast_bf16=True)
+    assert ops._remote_heads(lay, torch.bfloat16)
     monkeypatch.setattr(mod, "heads_layout_ok", lambda *args: False)
+    monkeypatch.setattr(ops, "_remote_heads", lambda *args: False)
     b = run_module(m, x, dout, autocast_bf16=True)
     np.testing.assert_array_equal(a[0], b[0])
     np.testing.assert_array_equal(a[1], b[1])
