@@ -844,35 +844,51 @@ int fused_seg_tiles(const LocalArgs& a) {
 
 // Ordered sums of the partials part[h][which][d][row] (which 0: gate_l, 1: gate_r, 2: dremote columns):
 // dgate_l / dgate_r per head ([H][Dh]) or, for a gate shared by the heads, summed over them too ([Dh]);
-// dbr[h][d] (when requested) over the rows.  One wave per output: lanes stride over the contiguous
-// partials (head by head), then a fixed butterfly.
+// dbr[h][d] (when requested) over the rows.  Blocks [0, 2 ng) take one gate output each: the 256 threads
+// stride over its (head, row) partials, eight independent loads in flight per thread, and a fixed tree adds
+// the threads' sums (a shared gate's output sums H x rows partials; one wave per output would wait on one
+// load chain per head).  The blocks after them take four dremote columns each, one wave per column.
 __global__ __launch_bounds__(256) void gate_reduce_kernel(const float* __restrict__ part, float* dgl, float* dgr,
                                                           float* dbr, int H, int Dh, int nrow, int per_head) {
-  const int lane = threadIdx.x & 63;
-  const int o = blockIdx.x * 4 + (threadIdx.x >> 6);
+  __shared__ float red[256];
+  const int tid = threadIdx.x, lane = tid & 63;
   const int ng = per_head ? H * Dh : Dh;  // outputs per gate vector
-  if (o >= 2 * ng + (dbr ? H * Dh : 0)) return;  // whole waves exit; no barrier follows
-  int which, h0, d, od;
-  if (o < 2 * ng) {
-    which = o / ng;
-    od = o % ng;
-    h0 = per_head ? od / Dh : 0;
-    d = od % Dh;
-  } else {
-    which = 2;
-    od = o - 2 * ng;
-    h0 = od / Dh;
-    d = od % Dh;
+  if ((int)blockIdx.x < 2 * ng) {
+    const int o = blockIdx.x, which = o / ng, od = o % ng, d = od % Dh;
+    const int h0 = per_head ? od / Dh : 0, nh = per_head ? 1 : H;
+    const int n = nh * nrow;  // partials of this output: index i = (h - h0) nrow + row
+    auto at = [&](int i) {
+      const int hh = h0 + i / nrow, rr = i - (i / nrow) * nrow;
+      return part[(((int64_t)hh * 3 + which) * Dh + d) * nrow + rr];
+    };
+    float s = 0.f;
+    int i = tid;
+    for (; i + 7 * 256 < n; i += 8 * 256) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = at(i + 256 * u);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; i < n; i += 256) s += at(i);
+    red[tid] = s;
+    __syncthreads();
+#pragma unroll
+    for (int w = 128; w > 0; w >>= 1) {
+      if (tid < w) red[tid] += red[tid + w];
+      __syncthreads();
+    }
+    if (tid == 0) (which == 0 ? dgl : dgr)[od] = red[0];
+    return;
   }
-  const int h1 = (which < 2 && !per_head) ? H : h0 + 1;
+  const int od = (blockIdx.x - 2 * ng) * 4 + (tid >> 6);  // dremote column h Dh + d
+  if (!dbr || od >= H * Dh) return;  // whole waves exit; no barrier follows
+  const float* p = part + (((int64_t)(od / Dh) * 3 + 2) * Dh + od % Dh) * nrow;
   float s = 0.f;
-  for (int h = h0; h < h1; ++h) {
-    const float* p = part + (((int64_t)h * 3 + which) * Dh + d) * nrow;
-    for (int i = lane; i < nrow; i += 64) s += p[i];
-  }
+  for (int i = lane; i < nrow; i += 64) s += p[i];
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
-  if (lane == 0) (which == 0 ? dgl : which == 1 ? dgr : dbr)[od] = s;
+  if (lane == 0) dbr[od] = s;
 }
 
 // ----------------------------------------------------------------------------
@@ -1087,8 +1103,9 @@ int32_t launch_bwd_all(const llattn_shape* s, const LocalArgs& a, float* dgate_l
   if (!ok) return fail(LLATTN_ERR_UNSUPPORTED, "head_dim %d unsupported", s->Dh);
   const int nrow = gate_rows(a, s->dtype);
   const int per_head = s->gate_per_head ? 1 : 0;
-  const int outs = 2 * (per_head ? s->H * s->Dh : s->Dh) + (dremote_colsum ? s->H * s->Dh : 0);
-  hipLaunchKernelGGL(gate_reduce_kernel, dim3((outs + 3) / 4), dim3(256), 0, st, a.gpart, dgate_l, dgate_r,
+  const int ng = per_head ? s->H * s->Dh : s->Dh;
+  const int blocks = 2 * ng + (dremote_colsum ? (s->H * s->Dh + 3) / 4 : 0);
+  hipLaunchKernelGGL(gate_reduce_kernel, dim3(blocks), dim3(256), 0, st, a.gpart, dgate_l, dgate_r,
                      dremote_colsum, s->H, s->Dh, nrow, per_head);
   return LLATTN_OK;
 }
