@@ -23,7 +23,7 @@
 namespace llattn {
 
 struct LatentArgs {
-  int B, Lh, Ldh, n_q, q_block, chunk, n_chunks, n_qt, n_lt, n_seg;
+  int B, Lh, Ldh, n_q, q_block, chunk, n_chunks, n_qt, n_lt, n_seg, seg;  // seg: queries per segment
   float scale, scale_log2;
   const void* rq; int64_t rq_sb, rq_sn, rq_sh;
   const void* gk; int64_t gk_sb, gk_sn, gk_sh;
@@ -38,7 +38,15 @@ struct LatentArgs {
   float* part;  // workspace [B][Lh][n_seg][n_lt*16][2][Ldh]
 };
 
-constexpr int kSeg = 256;  // queries per segment of the latent-stationary pass
+// Queries per segment of the latent-stationary pass (a multiple of 64): about 1024 workgroups (B Lh n_lt
+// segments) fill the chip; segments stay at least 256 queries long, since each one adds fp32 partials
+// (16 n_lt x 2 Ldh per (b, lh)) that are written and then read back by the ordered reduction.
+int latent_seg(int B, int Lh, int n_chunks, int n_q) {
+  const int64_t units = (int64_t)B * Lh * ((n_chunks + 15) / 16);
+  const int64_t want = std::max<int64_t>(1, (1024 + units - 1) / units);  // segments per (b, lh, latent tile)
+  const int64_t seg = ((n_q + want - 1) / want + 63) / 64 * 64;
+  return (int)std::max<int64_t>(256, seg);
+}
 
 // number of latents visible to latent query s
 __device__ __forceinline__ int visible(int s, const LatentArgs& a) {
@@ -239,8 +247,8 @@ __global__ __launch_bounds__(256) void latent_bwd_kv_kernel(const LatentArgs a) 
   // first query that sees latent n0: s * q_block >= (n0 + 1) * chunk
   const int64_t need = (int64_t)(n0 + 1) * a.chunk;
   const int s_first = (int)((need + a.q_block - 1) / a.q_block);
-  const int qbeg = max(seg * kSeg, s_first);
-  const int qend = min((seg + 1) * kSeg, a.n_q);
+  const int qbeg = max(seg * a.seg, s_first);
+  const int qend = (int)min((int64_t)(seg + 1) * a.seg, (int64_t)a.n_q);
   for (int q0 = qbeg; q0 < qend; q0 += 64) {
     lds_barrier();
     stage_rows_t<T, DHP, KP, true>(Qs, Qt, rqb, a.rq_sn, q0, qend, a.Ldh);
@@ -363,7 +371,8 @@ int32_t common(const llattn_shape* s, const llattn_tensor* rq, const llattn_tens
   a->chunk = s->chunk; a->n_chunks = s->n_chunks;
   a->n_qt = (s->n_q + 63) / 64;
   a->n_lt = (s->n_chunks + 15) / 16;
-  a->n_seg = (s->n_q + kSeg - 1) / kSeg;
+  a->seg = latent_seg(s->B, s->Lh, s->n_chunks, s->n_q);
+  a->n_seg = (s->n_q + a->seg - 1) / a->seg;
   a->scale = 1.0f / sqrtf((float)s->Ldh);
   a->scale_log2 = a->scale * kLog2e;
   a->rq = rq->ptr; a->rq_sb = rq->sb; a->rq_sn = rq->sn; a->rq_sh = rq->sh;
@@ -376,7 +385,8 @@ int32_t common(const llattn_shape* s, const llattn_tensor* rq, const llattn_tens
 
 size_t latent_workspace_bytes(const llattn_shape* s) {
   auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
-  const size_t n_lt = (s->n_chunks + 15) / 16, n_seg = (s->n_q + kSeg - 1) / kSeg;
+  const int seg = latent_seg(s->B, s->Lh, s->n_chunks, s->n_q);
+  const size_t n_lt = (s->n_chunks + 15) / 16, n_seg = (s->n_q + seg - 1) / seg;
   return up((size_t)s->B * s->Lh * s->n_q * 4) + up((size_t)s->B * s->Lh * n_seg * n_lt * 16 * 2 * s->Ldh * 4);
 }
 
