@@ -528,12 +528,35 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
   const float* lrow = a.lse + hrow;
   const int gr0 = rtid >> 3, gd0 = (rtid & 7) * GS;
   const bool qb1 = a.q_block == 1;
-  uint2 pdy[2][GV], pol[2][GV], prm[2][GV];
+  // A thread's GS dims of a row move as a 16-byte piece A and an 8-byte piece B.  GS = 12: a lane pair (even,
+  // odd) owns dims [24p, 24p + 24); the even lane takes A = +0..7 and B = +8..11, the odd lane B = +12..15 and
+  // A = +16..23 -- two instructions per row, and the pair's B pieces are one contiguous 16 bytes.  GS = 8:
+  // A only; GS = 4: B only.
+  const bool ev = (rtid & 1) == 0;
+  const int dA = (GS == 12 && !ev) ? gd0 + 4 : gd0, dB = (GS == 12 && ev) ? gd0 + 8 : gd0;
+  struct Piece { uint4 A; uint2 B; };
+  Piece pdy[2], pol[2], prm[2];
   float pw[2], plse[2];
   // this thread's gate and dremote column partial sums (over the segment's rows it gates)
   float accl[GS], accr[GS], accb[GS];
-  auto goff = [&](int grow, int st, int j) {
-    return gd0 + 4 * j < Dh ? (uint32_t)(grow * st + gd0 + 4 * j) * 2u : kOffOOB;
+  // pieces of the row at element offset `row` (ok: the row exists)
+  auto ld_row = [&](const __amdgpu_buffer_rsrc_t& rs, int row, bool ok, Piece& p) {
+    if constexpr (GS != 4) p.A = buf_ld16(rs, (ok && dA < Dh) ? (uint32_t)(row + dA) * 2u : kOffOOB);
+    if constexpr (GS != 8) p.B = buf_ld8(rs, (ok && dB < Dh) ? (uint32_t)(row + dB) * 2u : kOffOOB);
+  };
+  auto unpack_row = [&](const Piece& p, float (&v)[GS]) {
+    float a8[8], b4[4];
+    if constexpr (GS != 4) {
+      unpack_bf16x4(make_uint2(p.A.x, p.A.y), a8);
+      unpack_bf16x4(make_uint2(p.A.z, p.A.w), a8 + 4);
+    }
+    if constexpr (GS != 8) unpack_bf16x4(p.B, b4);
+#pragma unroll
+    for (int e = 0; e < GS; ++e) {
+      if constexpr (GS == 4) v[e] = b4[e];
+      else if constexpr (GS == 8) v[e] = a8[e];
+      else v[e] = ev ? (e < 8 ? a8[e] : b4[e - 8]) : (e < 4 ? b4[e] : a8[e - 4]);
+    }
   };
   auto load_gate = [&](int qt) {  // dy / o_local / remote rows, w and lse of tile qt (zero past the end)
     const int q0 = qt * 64, qend = min(T_, q0 + 64), rows = qend - q0;
@@ -542,24 +565,16 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int grow = gr0 + 32 * u, qi = q0 + grow;
-#pragma unroll
-      for (int j = 0; j < GV; ++j) {
-        pdy[u][j] = buf_ld8(rdy, goff(grow, dy_st, j));
-        pol[u][j] = buf_ld8(rol, goff(grow, o_st, j));
-      }
+      ld_row(rdy, grow * dy_st, true, pdy[u]);
+      ld_row(rol, grow * o_st, true, pol[u]);
       if (qb1) {  // one remote row per token
         const auto rrm = make_rsrc(rbase + (int64_t)q0 * r_sn, ((int64_t)(rows - 1) * r_sn + Dh) * 2);
-#pragma unroll
-        for (int j = 0; j < GV; ++j) prm[u][j] = buf_ld8(rrm, goff(grow, r_sn, j));
+        ld_row(rrm, grow * r_sn, true, prm[u]);
       } else {  // one remote row per latent query of q_block tokens: rows counted from the tile's first one
         const int rq0 = q0 / a.q_block;
         const int rrel = (qi - rq0 * a.q_block) / a.q_block, rlast = (qend - 1) / a.q_block - rq0;
         const auto rrm = make_rsrc(rbase + (int64_t)rq0 * r_sn, ((int64_t)rlast * r_sn + Dh) * 2);
-#pragma unroll
-        for (int j = 0; j < GV; ++j) {
-          const int d = gd0 + 4 * j;
-          prm[u][j] = buf_ld8(rrm, (qi < T_ && d < Dh) ? (uint32_t)(rrel * r_sn + d) * 2u : kOffOOB);
-        }
+        ld_row(rrm, rrel * r_sn, qi < T_, prm[u]);
       }
       const int qc = min(qi, T_ - 1);  // always one load each (rows past the end are masked by the gate)
       pw[u] = wrow[qc];
@@ -577,12 +592,10 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
       const bool qv = qi < T_;
       const float wq = qv ? pw[u] : 0.f, lse_nat = qv ? plse[u] : kNegInf;
       float dyv[GS], olv[GS], rmv[GS];
-#pragma unroll
-      for (int j = 0; j < GV; ++j) {
-        unpack_bf16x4(pdy[u][j], dyv + 4 * j);
-        unpack_bf16x4(pol[u][j], olv + 4 * j);
-        unpack_bf16x4(prm[u][j], rmv + 4 * j);
-      }
+      uint2 drp[GV];  // dremote of this thread's dims, bf16 pairs
+      unpack_row(pdy[u], dyv);
+      unpack_row(pol[u], olv);
+      unpack_row(prm[u], rmv);
       float dot1 = 0.f;
 #pragma unroll
       for (int e = 0; e < GS; ++e) dot1 += dyv[e] * (olv[e] - rmv[e]);
@@ -608,7 +621,7 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
 #pragma unroll
         for (int i = 0; i < 4; ++i) Dp += dov[i] * olv[4 * j + i];
         *reinterpret_cast<uint2*>(so + grow * KP + d) = dop;
-        store4(rdr, (full && qv && d < Dh) ? (uint32_t)(qi * dr_st + d) * 2u : kOffOOB, drv);
+        drp[j] = make_uint2(pack_bf16x2(drv[0], drv[1]), pack_bf16x2(drv[2], drv[3]));
         if (full) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -616,6 +629,22 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
             accr[4 * j + i] -= delta * rmv[4 * j + i];
             accb[4 * j + i] += qv ? drv[i] : 0.f;
           }
+        }
+      }
+      // dremote in the pieces the row was read in
+      {
+        const bool ok = full && qv;
+        if constexpr (GS != 4) {
+          typedef int i32x4_t __attribute__((ext_vector_type(4)));
+          const uint2 lo = (GS == 12 && !ev) ? drp[1] : drp[0], hi = (GS == 12 && !ev) ? drp[GV - 1] : drp[1];
+          const i32x4_t x = {(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+          __builtin_amdgcn_raw_buffer_store_b128(x, rdr, (ok && dA < Dh) ? (uint32_t)(qi * dr_st + dA) * 2u : kOffOOB,
+                                                 0, 0);
+        }
+        if constexpr (GS != 8) {
+          const uint2 x = (GS == 12 && ev) ? drp[GV - 1] : drp[0];
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned int, x), rdr,
+                                                (ok && dB < Dh) ? (uint32_t)(qi * dr_st + dB) * 2u : kOffOOB, 0, 0);
         }
       }
       Dp = sum_lanes8(Dp);
