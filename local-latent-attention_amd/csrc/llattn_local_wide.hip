@@ -20,8 +20,12 @@
 //   chunks.  Wave w owns keys [j0 + 32 w, +32) and walks the 32-query
 //   sub-steps of every chunk.
 //
-// 32 rows per wave keep a wave within 256 registers, so two waves share each
-// SIMD up to head dims of 64.  This file is compiled with
+// 32 rows per wave keep a wave within 168 registers up to head dims of 64 in
+// the forward and the query-side kernel, and their query (and dO) tiles share
+// LDS with the key / value buffers (the waves hold their query operands in
+// registers before the key loop starts), so three or four workgroups share a
+// CU: the prologue's global-load round trips of one workgroup overlap the
+// products of the others.  This file is compiled with
 // -amdgpu-mfma-vgpr-form: accumulators live in VGPRs and no AGPRs are used, so
 // a wave's whole 256-register budget is usable and the loops carry no copies
 // between register files.  At Dh = 64 the softmax arithmetic of a score (an
@@ -116,13 +120,16 @@ __device__ __forceinline__ int block_class(int qa, int ka, int W) {
 // query side: gate backward + dQ
 // ----------------------------------------------------------------------------
 template <int DHP>
-__global__ __launch_bounds__(256, DHP <= 64 ? 2 : 1) void local_bwd_wq_kernel(const LocalArgs a) {
+__global__ __launch_bounds__(256, DHP <= 64 ? 3 : 1) void local_bwd_wq_kernel(const LocalArgs a) {
   using T = uint16_t;
   constexpr int KP = DHP + 8, KS = DHP / 16, DB = DHP / 32, TILE = 64 * KP;
   constexpr int CD = DHP / 4, CV = CD / 8;  // gate layout: 4 threads per row, CD dims each
-  __shared__ __align__(16) T SQ[2 * TILE];   // query rows [q0, q0 + 128) -> dQ (bf16) at the end
-  __shared__ __align__(16) T SD[2 * TILE];   // dO_local rows
-  __shared__ __align__(16) T SKV[4 * TILE];  // key rows [buf], value rows [2 + buf]; gate sums; dQ partials
+  // key rows [buf], value rows [2 + buf]; before the key loop the query rows [q0, q0 + 128) (SQ) and the
+  // dO_local rows (SD), whose operands the waves then hold in registers; dQ (bf16) in SQ at the end
+  __shared__ __align__(16) T SKV[4 * TILE];
+  T* const SQ = SKV;
+  T* const SD = SKV + 2 * TILE;
+  __shared__ __align__(16) float gsum[4 * 3 * DHP];  // gate and dremote partial sums [wave][3][DHP]
   __shared__ __align__(16) float gls[DHP], grs[DHP];
   __shared__ __align__(16) float lse2s[kWideRows], Dss[kWideRows];
   __shared__ __align__(16) int los[kWideRows];
@@ -147,18 +154,14 @@ __global__ __launch_bounds__(256, DHP <= 64 ? 2 : 1) void local_bwd_wq_kernel(co
   // ---- loads: gate rows, query rows, first key / value chunk ----
   const int kbeg = max(0, q0 - W), kend = min(T_, q0 + kWideRows) - 1;  // keys [kbeg, kend)
   const int nch = kend > kbeg ? (kend - kbeg + 63) / 64 : 0;
-  BufTile<DHP, 256> tk, tv;
+  // every load of the prologue is issued before the first LDS store waits for one: a single round trip
+  BufTile<DHP, 256> tk, tv, tq0, tq1;
   if (nch > 0) {
     tk.load(kbase, k_st, kbeg, kend, Dh, tid);
     tv.load(vbase, v_st, kbeg, kend, Dh, tid);
   }
-  {
-    BufTile<DHP, 256> tq;
-    tq.load(qbase, q_st, q0, min(T_, q0 + 64), Dh, tid);
-    tq.template store<KP>(SQ, tid);
-    tq.load(qbase, q_st, q0 + 64, min(T_, q0 + kWideRows), Dh, tid);
-    tq.template store<KP>(SQ + TILE, tid);
-  }
+  tq0.load(qbase, q_st, q0, min(T_, q0 + 64), Dh, tid);
+  tq1.load(qbase, q_st, q0 + 64, min(T_, q0 + kWideRows), Dh, tid);
   const int gr = tid >> 2, gd0 = (tid & 3) * CD;
   const auto rdy = slab(static_cast<const T*>(a.dy) + b * a.dy_sb + hd * a.dy_sh, dy_st, T_);
   const auto rol = slab(static_cast<const T*>(a.ol) + b * a.o_sb + hd * a.o_sh, o_st, T_);
@@ -181,16 +184,19 @@ __global__ __launch_bounds__(256, DHP <= 64 ? 2 : 1) void local_bwd_wq_kernel(co
     }
     pw[u] = qv ? a.w[hrow + qi] : 0.f;
   }
-  for (int d = tid; d < DHP; d += 256) {
-    gls[d] = d < Dh ? a.gl[hd * a.gate_hs + d] : 0.f;
-    grs[d] = d < Dh ? a.gr[hd * a.gate_hs + d] : 0.f;
+  const float glv = tid < Dh ? a.gl[hd * a.gate_hs + tid] : 0.f;  // DHP <= 128: one dim per thread
+  const float grv = tid < Dh ? a.gr[hd * a.gate_hs + tid] : 0.f;
+  const int qt = q0 + tid;
+  const float lv = tid < kWideRows && qt < T_ ? a.lse[hrow + qt] : kNegInf;
+  tq0.template store<KP>(SQ, tid);
+  tq1.template store<KP>(SQ + TILE, tid);
+  if (tid < DHP) {
+    gls[tid] = glv;
+    grs[tid] = grv;
   }
   if (tid < kWideRows) {
-    const int qi = q0 + tid;
-    const bool qv = qi < T_;
-    const float l = qv ? a.lse[hrow + qi] : kNegInf;
-    lse2s[tid] = l == kNegInf ? 0.f : l * kLog2e;
-    los[tid] = qv ? key_lo(qi, W, a.bs) : INT_MAX;
+    lse2s[tid] = lv == kNegInf ? 0.f : lv * kLog2e;
+    los[tid] = qt < T_ ? key_lo(qt, W, a.bs) : INT_MAX;
   }
   lds_barrier();  // gate vectors
 
@@ -255,9 +261,7 @@ __global__ __launch_bounds__(256, DHP <= 64 ? 2 : 1) void local_bwd_wq_kernel(co
     }
   }
   // gate and dremote partial sums of the 128 rows: over the 16 rows of each wave (lanes of equal tid % 4),
-  // then over the four waves in order; staged in the key / value buffers, which are not in use yet
-  float* gsum = reinterpret_cast<float*>(SKV);  // [wave][3][DHP]
-  static_assert(4 * 3 * DHP * 4 <= 4 * TILE * 2, "gate sums exceed the key / value buffers");
+  // then over the four waves in order
 #pragma unroll
   for (int e = 0; e < CD; ++e) {
     const float l = sum_stride4(accl[e]), r = sum_stride4(accr[e]), s = sum_stride4(accb[e]);
@@ -294,7 +298,7 @@ __global__ __launch_bounds__(256, DHP <= 64 ? 2 : 1) void local_bwd_wq_kernel(co
   f32x16 dq[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) dq[db] = zero16();
-  lds_barrier();  // gate sums read: the key / value buffers are free
+  lds_barrier();  // query and dO rows read: the key / value buffers are free
 
   // ---- dQ = scale * sum_j dS_ij k_j over the 64-key chunks [kbeg, kend), two 32-key sub-steps each ----
   for (int ci = 0; ci < nch; ++ci) {
@@ -339,7 +343,8 @@ __global__ __launch_bounds__(256, DHP <= 64 ? 2 : 1) void local_bwd_wq_kernel(co
     }
   }
 
-  // ---- dQ rows out, through the query tile (no wave reads it any more) for 16-byte row stores ----
+  // ---- dQ rows out, through the query tile for 16-byte row stores ----
+  lds_barrier();  // every wave is done with the key / value buffers
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -401,20 +406,18 @@ __global__ __launch_bounds__(256, DHP <= 64 ? 2 : 1) void local_bwd_wkv_kernel(c
     }
   };
   // keys and values of the workgroup through LDS into this wave's B operands
-  {
-    BufTile<DHP, 256> t;
+  {  // the four key / value halves and the first query chunk in flight before the first LDS store waits
+    BufTile<DHP, 256> t[4];
     const T* kbase = static_cast<const T*>(a.k) + b * a.k_sb + hd * a.k_sh;
     const T* vbase = static_cast<const T*>(a.v) + b * a.v_sb + hd * a.v_sh;
-    t.load(kbase, k_st, j0, min(T_, j0 + 64), Dh, tid);
-    t.template store<KP>(SQO, tid);
-    t.load(kbase, k_st, j0 + 64, min(T_, j0 + kWideRows), Dh, tid);
-    t.template store<KP>(SQO + TILE, tid);
-    t.load(vbase, v_st, j0, min(T_, j0 + 64), Dh, tid);
-    t.template store<KP>(SQO + 2 * TILE, tid);
-    t.load(vbase, v_st, j0 + 64, min(T_, j0 + kWideRows), Dh, tid);
-    t.template store<KP>(SQO + 3 * TILE, tid);
+    t[0].load(kbase, k_st, j0, min(T_, j0 + 64), Dh, tid);
+    t[1].load(kbase, k_st, j0 + 64, min(T_, j0 + kWideRows), Dh, tid);
+    t[2].load(vbase, v_st, j0, min(T_, j0 + 64), Dh, tid);
+    t[3].load(vbase, v_st, j0 + 64, min(T_, j0 + kWideRows), Dh, tid);
+    if (nch > 0) load_chunk(qbeg);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t[i].template store<KP>(SQO + i * TILE, tid);
   }
-  if (nch > 0) load_chunk(qbeg);
   lds_barrier();
   const int kw = 32 * wave;  // first key row of the wave within the workgroup
   bf16x8 kB[KS], vB[KS];
@@ -524,11 +527,14 @@ __global__ __launch_bounds__(256, DHP <= 64 ? 2 : 1) void local_bwd_wkv_kernel(c
 // and writes y and o_local through LDS for 16-byte row stores.
 // ----------------------------------------------------------------------------
 template <int DHP>
-__global__ __launch_bounds__(256, 2) void local_fwd32_kernel(const LocalArgs a) {
+__global__ __launch_bounds__(256, DHP <= 64 ? 3 : 2) void local_fwd32_kernel(const LocalArgs a) {
   using T = uint16_t;
   constexpr int KP = DHP + 8, KS = DHP / 16, DB = DHP / 32, TILE = 64 * KP;
-  __shared__ __align__(16) T SQ[2 * TILE];   // query rows -> remote rows (epilogue)
-  __shared__ __align__(16) T SKV[4 * TILE];  // key rows [buf], value rows [2 + buf] -> y rows, o_local rows
+  // key rows [buf], value rows [2 + buf]; before the key loop the query rows (SQ, tiles 0 and 1), whose
+  // operands the waves then hold in registers; in the epilogue the remote rows, replaced in place by the
+  // y rows, in SQ and the o_local rows in tiles 2 and 3
+  __shared__ __align__(16) T SKV[4 * TILE];
+  T* const SQ = SKV;
   __shared__ __align__(16) float gls[DHP], grs[DHP];
 
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, c32 = lane & 31;
@@ -550,23 +556,26 @@ __global__ __launch_bounds__(256, 2) void local_fwd32_kernel(const LocalArgs a) 
     tk.template load<kStream>(kbase, k_st, kbeg, kend, Dh, tid);
     tv.template load<kStream>(vbase, v_st, kbeg, kend, Dh, tid);
   }
-  {
+  {  // both query halves and the gate vectors in flight before the first LDS store waits for them
     const T* qbase = static_cast<const T*>(a.q) + b * a.q_sb + hd * a.q_sh;
-    BufTile<DHP, 256> tq;
-    tq.template load<kStream>(qbase, (int)a.q_st, q0, min(T_, q0 + 64), Dh, tid);
-    tq.template store<KP>(SQ, tid);
-    tq.template load<kStream>(qbase, (int)a.q_st, q0 + 64, min(T_, q0 + kWideRows), Dh, tid);
-    tq.template store<KP>(SQ + TILE, tid);
-  }
-  for (int d = tid; d < DHP; d += 256) {
-    gls[d] = d < Dh ? a.gl[hd * a.gate_hs + d] : 0.f;
-    grs[d] = d < Dh ? a.gr[hd * a.gate_hs + d] : 0.f;
+    BufTile<DHP, 256> tq0, tq1;
+    tq0.template load<kStream>(qbase, (int)a.q_st, q0, min(T_, q0 + 64), Dh, tid);
+    tq1.template load<kStream>(qbase, (int)a.q_st, q0 + 64, min(T_, q0 + kWideRows), Dh, tid);
+    const float glv = tid < Dh ? a.gl[hd * a.gate_hs + tid] : 0.f;  // DHP <= 128: one dim per thread
+    const float grv = tid < Dh ? a.gr[hd * a.gate_hs + tid] : 0.f;
+    tq0.template store<KP>(SQ, tid);
+    tq1.template store<KP>(SQ + TILE, tid);
+    if (tid < DHP) {
+      gls[tid] = glv;
+      grs[tid] = grv;
+    }
   }
   lds_barrier();
   const int qw = 32 * wave, myrow = qw + c32, qi = q0 + myrow;  // this lane's query (accumulator column)
   bf16x8 qf[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) qf[ks] = frag_rows<KP>(SQ, qw, 16 * ks);
+  lds_barrier();  // query rows read: the key / value buffers are free
   const int lo = qi < T_ ? key_lo(qi, W, a.bs) : INT_MAX, hi = qi - 1;
   float m_run = kNegInf, l_run = 0.f;  // l_run: this lane's half of the row sum
   f32x16 o[DB];
@@ -636,7 +645,7 @@ __global__ __launch_bounds__(256, 2) void local_fwd32_kernel(const LocalArgs a) 
   }
 
   // ---- epilogue: normalise, gate, mix.  Lane (c32, h) holds dims 32 db + 8 j + 4 h .. +3 of its query ----
-  lds_barrier();  // every wave is done with the key / value buffers and the query tile
+  lds_barrier();  // every wave is done with the key / value buffers
   {
     RowTile<T, DHP> rr;
     const T* rbase = static_cast<const T*>(a.rem) + b * a.r_sb + hd * a.r_sh;
@@ -668,7 +677,8 @@ __global__ __launch_bounds__(256, 2) void local_fwd32_kernel(const LocalArgs a) 
   const float mm = fmaxf(sl, sr);
   const float el = __expf(sl - mm), er = __expf(sr - mm);
   const float wl = el / (el + er), wr = er / (el + er);
-  T* SY = SKV;             // y rows [0, 128)
+  // y rows [0, 128) in place of the remote rows: lane (c32, h) is the only reader and writer of its dims
+  T* SY = SQ;
   T* SO = SKV + 2 * TILE;  // o_local rows [0, 128)
 #pragma unroll
   for (int db = 0; db < DB; ++db)
