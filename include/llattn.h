@@ -238,8 +238,9 @@ typedef struct llattn_gemm_desc {
   int32_t split_k;     /* 0: automatic */
   float* a_rowsum;     /* fp32 [M] or NULL: also rowsum[m] = sum_k A(m,k), i.e. the bias gradient
                           sum_tokens dy of a weight-gradient product dy^T x, contracted against a
-                          column of ones in place of the unused column N of the last tile (needs
-                          b_trans = 1, fp32 C and N % 256 != 0); overwritten, never accumulated */
+                          column of ones in place of the unused column N of the last tile, or, for
+                          N % 256 == 0 (needs a_trans = 1 then), in extra products of the first tile
+                          column; needs b_trans = 1 and fp32 C; overwritten, never accumulated */
   llattn_gemm_rowadd rowadd[2]; /* bf16 C, a_trans = 0, b_trans = 1 (input gradients) */
   int32_t act;                  /* LLATTN_ACT_* */
   void* aux;                    /* bf16 [M][ld_aux]: gelu' written (LLATTN_ACT_GELU) or read (_MUL_AUX) */

@@ -250,7 +250,10 @@ __device__ __forceinline__ bf16x8 frag(const unsigned char* tile, int o16, int r
   }
 }
 
-template <bool AK, bool BKM, int EPI>
+// RS: row sums of A for an N with no spare column (a multiple of 256): every lane adds the 8 k values of each of
+// its A fragments into one fp32 sum per fragment block (v_dot2 against a pair of ones, 32 per step, beside the
+// 64 products), and the waves that own the left half of the first tile column store them.
+template <bool AK, bool BKM, int EPI, bool RS = false>
 __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
   // bf16 output from a k-contiguous B: permuted B fragments, so each lane writes 16-byte rows directly
   constexpr bool PB = BKM && EPI == EPI_BF16;
@@ -295,6 +298,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
       for (int e = 0; e < 8; ++e) f[e] = (__bf16)1.0f;
     }
   };
+  const bool rs_wave = RS && tn == 0 && wn == 0;  // wave-uniform
+  float rsum[8];  // RS: lane (r, g)'s part (k = 8g .. 8g+7 of each step) of sum_k A(m0 + wm*128 + 16i + r, k)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) rsum[i] = 0.f;
   // DMA of this wave's block q (0..3: operand A, 4..7: operand B) of a step into `stage`; klim = K - k0 of
   // the step (wave-uniform): below BK, k-contiguous lanes from klim on read zero
   const int kca = lane_k0<false>(lane), kcb = lane_k0<PB>(lane);
@@ -349,6 +356,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
       for (int u = 0; u < 4; ++u) {  // B first: lane (r, g) accumulates C[m = r][n = 4g + e]
         const int n = 4 * q + u, i = n >> 3, j = n & 7;
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cb[j], ca[i], acc[i][j], 0, 0, 0);
+      }
+      if constexpr (RS) {  // fragment block q / 2, pairs 2 (q % 2) and 2 (q % 2) + 1 of its 4 bf16 pairs
+        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+        const bf16x2 one2 = {(__bf16)1.0f, (__bf16)1.0f};
+        const bf16x8 f = ca[q >> 1];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int pr = 2 * (q & 1) + e;
+          rsum[q >> 1] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{f[2 * pr], f[2 * pr + 1]}, one2, rsum[q >> 1], false);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -537,6 +554,18 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
           if (EPI == EPI_PART) a.part[(int64_t)a.n_split * a.M * a.N + (int64_t)split * a.M + row] = v.x;
           else a.rowsum[row] = v.x;
         }
+      }
+    }
+    if (rs_wave) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {  // the four lane groups g hold the row's four 8-wide k slices
+        float v = rsum[i];
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+        const int row = row0 + 16 * i + r;
+        if (g != 0 || row >= a.M) continue;
+        if (EPI == EPI_PART) a.part[(int64_t)a.n_split * a.M * a.N + (int64_t)split * a.M + row] = v;
+        else a.rowsum[row] = v;
       }
     }
   }
@@ -847,8 +876,11 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs a, in
 template <bool AK, bool BKM>
 void launch(const GemmArgs& a, int S, int c_dtype, hipStream_t st) {
   const dim3 grid(a.tiles_m * a.tiles_n * S), block(256);
+  // row sums with no spare column (N a multiple of 256): the weight-gradient layout only
+  const bool rs = !AK && !BKM && a.rowsum && a.N % BN == 0;
   if (S > 1) {
-    hipLaunchKernelGGL((gemm_kernel<AK, BKM, EPI_PART>), grid, block, 0, st, a);
+    if (rs) hipLaunchKernelGGL((gemm_kernel<AK, BKM, EPI_PART, !AK && !BKM>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((gemm_kernel<AK, BKM, EPI_PART>), grid, block, 0, st, a);
     const int64_t quads = (int64_t)a.M * (a.N / 4) + (a.rowsum ? a.M : 0);
     const dim3 rg((unsigned)((quads + 255) / 256));
     if (c_dtype == LLATTN_F32)
@@ -856,7 +888,8 @@ void launch(const GemmArgs& a, int S, int c_dtype, hipStream_t st) {
     else
       hipLaunchKernelGGL((splitk_reduce_kernel<EPI_BF16>), rg, block, 0, st, a, S);
   } else if (c_dtype == LLATTN_F32) {
-    hipLaunchKernelGGL((gemm_kernel<AK, BKM, EPI_F32>), grid, block, 0, st, a);
+    if (rs) hipLaunchKernelGGL((gemm_kernel<AK, BKM, EPI_F32, !AK && !BKM>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((gemm_kernel<AK, BKM, EPI_F32>), grid, block, 0, st, a);
   } else {
     hipLaunchKernelGGL((gemm_kernel<AK, BKM, EPI_BF16>), grid, block, 0, st, a);
   }
@@ -1103,10 +1136,11 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
   const int64_t b_bytes = (d->b_trans ? (int64_t)(d->K - 1) * d->ldb + d->N : (int64_t)(d->N - 1) * d->ldb + d->K) * 2;
   if (a_bytes > (int64_t)kOffPastK || b_bytes > (int64_t)kOffPastK)
     return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: operands of 4 GiB or more are not supported");
-  if (d->a_rowsum && (!d->b_trans || d->c_dtype != LLATTN_F32 || d->N % BN == 0 || !aligned16(d->a_rowsum)))
+  if (d->a_rowsum && (!d->b_trans || d->c_dtype != LLATTN_F32 || (d->N % BN == 0 && !d->a_trans) ||
+                      !aligned16(d->a_rowsum)))
     return fail(LLATTN_ERR_UNSUPPORTED,
-                "llattn_gemm: row sums of A need an m/n-contiguous B, fp32 C, N not a multiple of %d (a spare "
-                "column in the last tile; N=%d) and a 16-byte aligned output", BN, d->N);
+                "llattn_gemm: row sums of A need an m/n-contiguous B, fp32 C, an m-contiguous A when N is a multiple "
+                "of %d (N=%d) and a 16-byte aligned output", BN, d->N);
   for (int q = 0; q < 2; ++q) {
     const llattn_gemm_rowadd& ra = d->rowadd[q];
     if (!ra.ptr) continue;

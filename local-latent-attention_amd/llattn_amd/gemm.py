@@ -156,16 +156,12 @@ def input_grad(dy: torch.Tensor, w: torch.Tensor, rowadd=()) -> torch.Tensor:
     return matmul_nn(dy, w, rowadd=rowadd)
 
 
-def rowsum_supported(n: int) -> bool:
-    """Whether :func:`matmul_tn` can also give the row sums of ``a^T`` for an output width ``n``: the sums are
-    contracted against a column of ones in place of the unused column ``n`` of the last 256-wide tile."""
-    return n % 256 != 0
-
-
 def matmul_tn(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None, accumulate: bool = False,
               split_k: int = 0, rowsum: torch.Tensor | None = None) -> torch.Tensor:
     """``a [K, M]^T @ b [K, N]`` -> fp32 ``[M, N]`` (weight gradients: K = tokens).  With ``rowsum`` (fp32 ``[M]``,
-    overwritten) also ``a.sum(0)`` -- the bias gradient -- from the same pass (``rowsum_supported(N)``)."""
+    overwritten) also ``a.sum(0)`` -- the bias gradient -- from the same pass: contracted against a column of ones
+    in place of the unused column ``N`` of the last 256-wide tile, or, when ``N`` is a multiple of 256, by one
+    more product per A fragment block in the first tile column."""
     _check2d("a", a)
     _check2d("b", b)
     K, M = a.shape
@@ -174,8 +170,6 @@ def matmul_tn(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None,
         raise ValueError(f"a is [{K}, {M}] but b is {tuple(b.shape)}")
     if out is None:
         out = torch.empty((M, N), dtype=torch.float32, device=a.device)
-    if rowsum is not None and not rowsum_supported(N):
-        raise ValueError(f"row sums need an output width that is not a multiple of 256 (N={N})")
     _run(M, N, K, a, True, b, True, out, None, accumulate, split_k, rowsum)
     return out
 

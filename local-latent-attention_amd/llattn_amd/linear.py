@@ -68,13 +68,12 @@ def input_grad(dy2: torch.Tensor, w: torch.Tensor, rowadd=()) -> torch.Tensor:
 def weight_grad(dy2: torch.Tensor, x2: torch.Tensor, bias_grad: bool = False):
     """fp32 ``dy2^T @ x2`` for bf16 ``dy2 [K, N]``, ``x2 [K, D]`` (K = tokens, any count), and with ``bias_grad``
     also the fp32 column sums of ``dy2`` (the bias gradient): returns ``(dW, db)``.  The bias gradient comes
-    from the weight-gradient pass itself (a column of ones) when D is not a multiple of 256, else from
-    the column-sum kernel."""
-    N, D = dy2.shape[1], x2.shape[1]
-    if bias_grad and gemm.rowsum_supported(D):
+    from the weight-gradient pass itself: ``dy2`` contracted against ones (:func:`llattn_amd.gemm.matmul_tn`)."""
+    N = dy2.shape[1]
+    if bias_grad:
         db = torch.empty((N,), dtype=torch.float32, device=dy2.device)
         return gemm.matmul_tn(dy2, x2, rowsum=db), db
-    return gemm.matmul_tn(dy2, x2), (gemm.colsum(dy2) if bias_grad else None)
+    return gemm.matmul_tn(dy2, x2), None
 
 
 class _Project(torch.autograd.Function):

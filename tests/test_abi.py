@@ -232,11 +232,12 @@ def test_gemm_split_k_needs_workspace():
 @pytest.mark.parametrize("kw,msg", [
     (dict(b_trans=0, ldb=1024), b"m/n-contiguous B"),
     (dict(c_dtype=1), b"fp32 C"),
-    (dict(N=512, ldb=512, ldc=512), b"not a multiple of 256"),
+    (dict(N=512, ldb=512, ldc=512, a_trans=0, lda=1024), b"m-contiguous A when N is a multiple"),
     (dict(a_rowsum=0x5004), b"16-byte aligned"),
 ])
 def test_gemm_rowsum_validation(kw, msg):
-    """Row sums of A (the fused bias gradient) need a spare column in the last tile of an m/n-contiguous B."""
+    """Row sums of A (the fused bias gradient) need an m/n-contiguous B, fp32 C, and for an N without a spare
+    column in the last tile (a multiple of 256) the weight-gradient layout of A."""
     L, lib = _lib()
     base = dict(M=264, N=136, K=1024, a_trans=1, b_trans=1, lda=264, ldb=136, ldc=136, c_dtype=L.F32,
                 a_rowsum=0x5000)

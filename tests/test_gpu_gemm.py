@@ -74,11 +74,10 @@ def test_matmul_tn_token_tail(K, M, N, S):
     print("case: tn token tail", K, M, N, S, flush=True)
     g = torch.Generator(device=dev).manual_seed(K + 3 * M + N)
     a, b = _rand(K, M, gen=g, dev=dev), _rand(K, N, gen=g, dev=dev)
-    rs = torch.full((M,), float("nan"), device=dev) if N % 256 else None
+    rs = torch.full((M,), float("nan"), device=dev)
     got = gemm.matmul_tn(a, b, split_k=S, rowsum=rs)
     assert _err(got, a.float().T @ b.float()) < FP32_TOL
-    if rs is not None:
-        assert _err(rs, a.float().sum(0)) < FP32_TOL
+    assert _err(rs, a.float().sum(0)) < FP32_TOL
 
 
 @pytest.mark.parametrize("M,N,K", [(256, 256, 64), (300, 264, 128), (1000, 1408, 512)])
@@ -122,10 +121,15 @@ def test_matmul_nn_rowadd(B, T, N, K, pools):
 
 
 @pytest.mark.parametrize("K,M,N,S", [(64, 256, 264, 1), (1024, 264, 136, 0), (2048, 40, 96, 1), (4096, 264, 136, 3),
-                                     (4096, 1000, 520, 1), (32768, 1408, 1408, 0), (32768, 4736, 1408, 0)])
+                                     (4096, 1000, 520, 1), (32768, 1408, 1408, 0), (32768, 4736, 1408, 0),
+                                     # N a multiple of 256 (no spare column): the first tile column's extra
+                                     # products against ones; single pass, split-K, a ragged M and token tail
+                                     (4096, 1000, 512, 1), (4096, 264, 256, 3), (1001, 520, 768, 2),
+                                     (32768, 3200, 1024, 0), (32768, 1024, 1024, 0)])
 def test_matmul_tn_rowsum(K, M, N, S):
     """Weight gradient with the bias gradient of the same pass: rowsum = a.sum(0), contracted against a column
-    of ones in the spare column N of the last tile; the product itself is unchanged by it."""
+    of ones in the spare column N of the last tile, or (N a multiple of 256) against ones in extra products of
+    the first tile column; the product itself is unchanged by it."""
     from llattn_amd import gemm
     dev = require_cuda()
     print("case: tn rowsum", K, M, N, S, flush=True)
@@ -139,6 +143,7 @@ def test_matmul_tn_rowsum(K, M, N, S):
     rs2 = torch.empty_like(rs)
     got2 = gemm.matmul_tn(a, b, split_k=S, rowsum=rs2)
     assert torch.equal(rs, rs2) and torch.equal(got, got2)
+    assert torch.equal(got, gemm.matmul_tn(a, b, split_k=S))  # the same products with and without the row sums
 
 
 @pytest.mark.parametrize("K,M,N,S", [(64, 256, 256, 1), (1024, 264, 136, 0), (4096, 1408, 512, 4),
