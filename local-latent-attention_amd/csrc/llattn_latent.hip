@@ -78,9 +78,13 @@ __global__ __launch_bounds__(256) void latent_fwd_kernel(const LatentArgs a) {
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int n0 = 0; n0 < nmax; n0 += 64) {
+    RowTile<T, DHP> tk;  // both tiles' loads in flight before the first LDS store waits for them
+    TransTile<T, DHP> tv;
+    tk.load(gkb, a.gk_sn, n0, nmax, a.Ldh);
+    tv.load(gvb, a.gv_sn, n0, nmax, a.Ldh);
     lds_barrier();
-    stage_rows<T, DHP, KP>(Ks, gkb, a.gk_sn, n0, nmax, a.Ldh);
-    stage_rows_t<T, DHP, KP, false>(nullptr, Vt, gvb, a.gv_sn, n0, nmax, a.Ldh);
+    tk.template store<KP>(Ks);
+    tv.store_t(Vt);
     lds_barrier();
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
@@ -142,15 +146,20 @@ __global__ __launch_bounds__(256) void latent_bwd_q_kernel(const LatentArgs a) {
 
   // pass 1: D = sum_n P_n dP_n
   float D = 0.f;
+  // keys (rows, and transposed when one tile serves both passes) and values, loads in flight together
+  auto stage = [&](int n0, bool trans) {
+    TransTile<T, DHP> tk;
+    RowTile<T, DHP> tv;
+    tk.load(gkb, a.gk_sn, n0, nmax, a.Ldh);
+    tv.load(gvb, a.gv_sn, n0, nmax, a.Ldh);
+    lds_barrier();
+    tk.template store_rows<KP>(Ks);
+    if (trans) tk.store_t(Kt);
+    tv.template store<KP>(Vs);
+    lds_barrier();
+  };
   for (int n0 = 0; n0 < nmax; n0 += 64) {
-    lds_barrier();
-    if (single) {
-      stage_rows_t<T, DHP, KP, true>(Ks, Kt, gkb, a.gk_sn, n0, nmax, a.Ldh);
-    } else {
-      stage_rows<T, DHP, KP>(Ks, gkb, a.gk_sn, n0, nmax, a.Ldh);
-    }
-    stage_rows<T, DHP, KP>(Vs, gvb, a.gv_sn, n0, nmax, a.Ldh);
-    lds_barrier();
+    stage(n0, single);
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const int s0 = n0 + 16 * st;
@@ -173,12 +182,7 @@ __global__ __launch_bounds__(256) void latent_bwd_q_kernel(const LatentArgs a) {
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int n0 = 0; n0 < nmax; n0 += 64) {
-    if (!single) {
-      lds_barrier();
-      stage_rows_t<T, DHP, KP, true>(Ks, Kt, gkb, a.gk_sn, n0, nmax, a.Ldh);
-      stage_rows<T, DHP, KP>(Vs, gvb, a.gv_sn, n0, nmax, a.Ldh);
-      lds_barrier();
-    }
+    if (!single) stage(n0, true);
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const int s0 = n0 + 16 * st;
