@@ -202,7 +202,8 @@ def _core_backward(lay: L.Layout, dy, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, 
                    w, dq, dk, dv, drq, dgk, dgv, dt, device):
     """Writes dq/dk/dv/drq/dgk/dgv (LlattnTensor views) and returns (dgate_l, dgate_r, dr_w, dr_b): the gate
     gradients per head ([H, Dh]) or, for a shared gate, already summed over heads ([Dh]); r_out's bias
-    gradient comes from the local backward (the column sums of dremote)."""
+    gradient comes from the local backward (the column sums of dremote).  ``dy``: [B, T, H, Dh] with any
+    16-byte strides (packed rows or head slabs), Dh contiguous."""
     B, T, H, Dh, Lh, Ldh = lay.B, lay.T, lay.H, lay.Dh, lay.Lh, lay.Ldh
     D, Ld = H * Dh, Lh * Ldh
     per_head = gate_l.dim() == 2 and gate_l.shape[0] > 1
@@ -216,7 +217,7 @@ def _core_backward(lay: L.Layout, dy, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, 
     _call("llattn_local_gate_bwd",
           _byref(shape), _byref(q), _byref(k), _byref(v), _byref(_remote_view(lay, R, _remote_heads(lay, dt))),
           gate_l.data_ptr(), gate_r.data_ptr(), _byref(L.view_bhnd(ol)), lse.data_ptr(), w.data_ptr(),
-          _byref(L.view(dy, dy.stride(0), dy.stride(1), Dh)), _byref(dq), _byref(dk), _byref(dv),
+          _byref(L.view(dy, dy.stride(0), dy.stride(1), dy.stride(2))), _byref(dq), _byref(dk), _byref(dv),
           _byref(L.view(drem, drem.stride(0), drem.stride(1), Dh)), dgl.data_ptr(), dgr.data_ptr(),
           None if dr_b is None else dr_b.data_ptr(), ws.data_ptr(), ws.numel(), stream)
     if lay.macro:
@@ -327,7 +328,7 @@ class LLAttnCore(torch.autograd.Function):
         dt, device = qkv.dtype, qkv.device
         H, Dh, Lh, Ldh = lay.H, lay.Dh, lay.Lh, lay.Ldh
         D, Ld = H * Dh, Lh * Ldh
-        dy = _contig(dy.to(dt))
+        dy = _contig(dy.to(dt)).view(lay.B, lay.T, H, Dh)
         q, k, v, rqv = _qkv_views(lay, qkv, rq is None, ctx.heads)
         if rq is not None:
             rqv = L.view(rq, rq.stride(0), rq.stride(1), Ldh)
@@ -418,13 +419,13 @@ class LLAttnFunction(torch.autograd.Function):
         lay = ctx.lay
         dt, device = Q.dtype, Q.device
         B, H, S, Dh = Q.shape
-        dy = _contig(dOut.to(dt).permute(0, 2, 1, 3))  # [B, S, H, Dh]
+        dy = _contig_last(dOut.to(dt).permute(0, 2, 1, 3))  # [B, S, H, Dh], read by its strides
         dQ, dK, dV = (_empty((B, S, H, Dh), dt, device) for _ in range(3))
         dGQ = _empty((B, lay.n_q, lay.Lh, lay.Ldh), dt, device)
         dGK = _empty((B, lay.n_chunks, lay.Lh, lay.Ldh), dt, device)
         dGV = _empty((B, lay.n_chunks, lay.Lh, lay.Ldh), dt, device)
         dgl, dgr, dr_w, dr_b = _core_backward(
-            lay, dy.view(B, S, H * Dh), L.view_bhnd(Q), L.view_bhnd(K), L.view_bhnd(V), L.view_bhnd(GQ),
+            lay, dy, L.view_bhnd(Q), L.view_bhnd(K), L.view_bhnd(V), L.view_bhnd(GQ),
             L.view_bhnd(GK), L.view_bhnd(GV), gl, gr, r_w, ctx.has_rb, lat, lse_lat, R, ol, lse, w,
             L.view_bnhd(dQ), L.view_bnhd(dK), L.view_bnhd(dV), L.view_bnhd(dGQ), L.view_bnhd(dGK), L.view_bnhd(dGV),
             dt, device)
