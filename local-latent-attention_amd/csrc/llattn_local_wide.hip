@@ -372,7 +372,7 @@ __global__ __launch_bounds__(256, DHP <= 64 ? 2 : 1) void local_bwd_wkv_kernel(c
   constexpr int CH = 128, NH = CH / 64, NSB = CH / 32;  // queries per chunk, 64-row halves, 32-query sub-steps
   // chunk buffer `buf`: query rows at [2 buf NH TILE, +NH TILE), dO rows after them; prologue: keys, values
   __shared__ __align__(16) T SQO[4 * NH * TILE];
-  __shared__ __align__(16) float lse2s[2][CH], Dss[2][CH];
+  __shared__ __align__(16) float lse2s[2][CH], Dss[2][CH];  // Dss: -D, the dP accumulators' initial values
 
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, c32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -402,7 +402,7 @@ __global__ __launch_bounds__(256, DHP <= 64 ? 2 : 1) void local_bwd_wkv_kernel(c
       const bool qv = qi < qend;
       const float l = qv ? a.lse[hrow + qi] : kNegInf;
       pl = l == kNegInf ? 0.f : l * kLog2e;
-      pd = qv ? a.Dsum[hrow + qi] : 0.f;
+      pd = qv ? -a.Dsum[hrow + qi] : 0.f;
     }
   };
   // keys and values of the workgroup through LDS into this wave's B operands
@@ -454,25 +454,32 @@ __global__ __launch_bounds__(256, DHP <= 64 ? 2 : 1) void local_bwd_wkv_kernel(c
     for (int sb = 0; sb < NSB; ++sb) {
       const int cls = block_class(c0 + 32 * sb, j0 + kw, W);  // uniform over the wave
       if (cls == 0) continue;
-      f32x16 sc = zero16(), dpc = zero16();
+      // this lane's 16 queries are accumulator rows 8 (i / 4) + 4 h + i % 4; the dP accumulator starts at
+      // -D of its query, so it ends as dP - D
+      f32x16 sc = zero16(), dpc;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const float4 d4 = *reinterpret_cast<const float4*>(&Dss[buf][32 * sb + 8 * jj + 4 * h]);
+        dpc[4 * jj] = d4.x;
+        dpc[4 * jj + 1] = d4.y;
+        dpc[4 * jj + 2] = d4.z;
+        dpc[4 * jj + 3] = d4.w;
+      }
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         sc = mma32(frag_rows<KP>(sq, 32 * sb, 16 * ks), kB[ks], sc);   // S[query][key]
-        dpc = mma32(frag_rows<KP>(so, 32 * sb, 16 * ks), vB[ks], dpc);  // dP[query][key]
+        dpc = mma32(frag_rows<KP>(so, 32 * sb, 16 * ks), vB[ks], dpc);  // dP[query][key] - D[query]
       }
-      // this lane's 16 queries are accumulator rows 8 (i / 4) + 4 h + i % 4
       float p[16], ds[16];
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        const int r0 = 32 * sb + 8 * jj + 4 * h;
-        const float4 l4 = *reinterpret_cast<const float4*>(&lse2s[buf][r0]);
-        const float4 d4 = *reinterpret_cast<const float4*>(&Dss[buf][r0]);
-        const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, Dv[4] = {d4.x, d4.y, d4.z, d4.w};
+        const float4 l4 = *reinterpret_cast<const float4*>(&lse2s[buf][32 * sb + 8 * jj + 4 * h]);
+        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const int i = 4 * jj + c;
           p[i] = fast_exp2(sc[i] * a.scale_log2 - lv[c]);
-          ds[i] = p[i] * (dpc[i] - Dv[c]);
+          ds[i] = p[i] * dpc[i];
         }
       }
       if (cls == 2) {
