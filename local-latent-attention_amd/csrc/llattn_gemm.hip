@@ -1084,8 +1084,12 @@ int resolve_split(const llattn_gemm_desc* d) {
   int best = 1;
   double best_t = 1e30;
   for (int64_t S = 1; S <= std::min<int64_t>(smax, 64); ++S) {
+    // each round of workgroups also pays ~15 us of pipeline fill and partial-tile epilogue, so a split that
+    // needs a second round must save more than that (52 tiles, K = 32768: 4 splits in one round 260 us,
+    // 9 splits in two rounds ~300 us)
     const double rounds = (double)((tiles * S + 255) / 256);
-    const double t = rounds / (double)S * t_tile + (S > 1 ? 2.0 * S * d->M * (double)d->N * 4.0 / 5e12 : 0.0);
+    const double t = rounds * (t_tile / (double)S + 15e-6) +
+                     (S > 1 ? 2.0 * S * d->M * (double)d->N * 4.0 / 5e12 : 0.0);
     if (t < best_t * 0.999) {
       best_t = t;
       best = (int)S;
