@@ -397,12 +397,12 @@ __global__ __launch_bounds__(256, DHP <= 64 ? 2 : 1) void local_bwd_wkv_kernel(c
       tq[hh].load(qbase, q_st, c0 + 64 * hh, qend, Dh, tid);
       to[hh].load(dobase, do_st, c0 + 64 * hh, qend, Dh, tid);
     }
+    // raw values of a valid row (rows past qend are zeroed when staged): nothing here uses the loaded values,
+    // so the loads stay in flight with the tiles' until the chunk is staged
     if (tid < CH) {
-      const int qi = c0 + tid;
-      const bool qv = qi < qend;
-      const float l = qv ? a.lse[hrow + qi] : kNegInf;
-      pl = l == kNegInf ? 0.f : l * kLog2e;
-      pd = qv ? -a.Dsum[hrow + qi] : 0.f;
+      const int qi = min(c0 + tid, qend - 1);
+      pl = a.lse[hrow + qi];
+      pd = a.Dsum[hrow + qi];
     }
   };
   // keys and values of the workgroup through LDS into this wave's B operands
@@ -442,8 +442,9 @@ __global__ __launch_bounds__(256, DHP <= 64 ? 2 : 1) void local_bwd_wkv_kernel(c
       to[hh].template store<KP>(so + hh * TILE, tid);
     }
     if (tid < CH) {
-      lse2s[buf][tid] = pl;
-      Dss[buf][tid] = pd;
+      const bool qv = c0 + tid < qend;
+      lse2s[buf][tid] = (qv && pl != kNegInf) ? pl * kLog2e : 0.f;
+      Dss[buf][tid] = qv ? -pd : 0.f;
     }
     lds_barrier();  // also: every wave is done with the chunk that used this buffer two steps ago
     if (ci + 1 < nch) load_chunk(c0 + CH);
