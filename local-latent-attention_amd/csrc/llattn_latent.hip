@@ -140,8 +140,9 @@ __global__ __launch_bounds__(256) void latent_bwd_q_kernel(const LatentArgs a) {
   RowFrag<T, DQ> qf, dof;
   qf.load(static_cast<const T*>(a.rq) + b * a.rq_sb + lh * a.rq_sh + (int64_t)qi * a.rq_sn, g, a.Ldh, qv);
   dof.load(static_cast<const T*>(a.dout) + b * a.do_sb + lh * a.do_sh + (int64_t)qi * a.do_sn, g, a.Ldh, qv);
-  const float lse_nat = qv ? a.lse[row] : kNegInf;
-  const float lse2 = lse_nat == kNegInf ? 0.f : lse_nat * kLog2e;
+  // lse of a valid row, transformed only after the first latent tile is staged: a use right here would wait
+  // for the query rows' loads before the tile's loads are even issued
+  const float lse_raw = a.lse[((int64_t)b * a.Lh + lh) * a.n_q + min(qi, a.n_q - 1)];
   const bool single = nmax <= 64;  // one latent tile: stage it once for both passes
 
   // pass 1: D = sum_n P_n dP_n
@@ -158,8 +159,10 @@ __global__ __launch_bounds__(256) void latent_bwd_q_kernel(const LatentArgs a) {
     tv.template store<KP>(Vs);
     lds_barrier();
   };
+  if (nmax > 0) stage(0, single);
+  const float lse2 = (!qv || lse_raw == kNegInf) ? 0.f : lse_raw * kLog2e;
   for (int n0 = 0; n0 < nmax; n0 += 64) {
-    stage(n0, single);
+    if (n0 > 0) stage(n0, single);
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const int s0 = n0 + 16 * st;
