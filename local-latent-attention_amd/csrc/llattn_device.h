@@ -461,48 +461,6 @@ struct TransTile {
   }
 };
 
-// The same rows stored transposed into LDS [DHP][kTP] (row index contiguous),
-// and row-major into lds_rows as well when kRows.  Writes are whole dwords
-// with the row index varying fastest across lanes (bank-conflict free): bf16
-// threads handle a pair of rows and pack the two rows' elements of one dim.
-template <typename T, int DHP, int P, bool kRows>
-__device__ __forceinline__ void stage_rows_t(T* lds_rows, T* lds_t, const T* base, int64_t st, int r0, int r_end,
-                                             int Dh) {
-  constexpr int V = Vec16<T>::N, CPR = DHP / V;
-  if constexpr (std::is_same_v<T, float>) {
-    for (int task = threadIdx.x; task < 64 * CPR; task += 256) {
-      const int row = task % 64, col = (task / 64) * V, rr = r0 + row;
-      uint4 x = make_uint4(0, 0, 0, 0);
-      if (rr < r_end && col < Dh) x = ld16(base + (int64_t)rr * st + col);
-      if constexpr (kRows) st16(lds_rows + row * P + col, x);
-      lds_t[(col + 0) * kTP + row] = __uint_as_float(x.x);
-      lds_t[(col + 1) * kTP + row] = __uint_as_float(x.y);
-      lds_t[(col + 2) * kTP + row] = __uint_as_float(x.z);
-      lds_t[(col + 3) * kTP + row] = __uint_as_float(x.w);
-    }
-  } else {
-    for (int task = threadIdx.x; task < 32 * CPR; task += 256) {
-      const int row = 2 * (task % 32), col = (task / 32) * V, rr = r0 + row;
-      uint4 x0 = make_uint4(0, 0, 0, 0), x1 = make_uint4(0, 0, 0, 0);
-      if (col < Dh) {
-        if (rr < r_end) x0 = ld16(base + (int64_t)rr * st + col);
-        if (rr + 1 < r_end) x1 = ld16(base + (int64_t)(rr + 1) * st + col);
-      }
-      if constexpr (kRows) {
-        st16(lds_rows + row * P + col, x0);
-        st16(lds_rows + (row + 1) * P + col, x1);
-      }
-      const uint32_t a[4] = {x0.x, x0.y, x0.z, x0.w}, b[4] = {x1.x, x1.y, x1.z, x1.w};
-      uint32_t* dst = reinterpret_cast<uint32_t*>(lds_t + col * kTP + row);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        dst[(2 * j) * (kTP / 2)] = (a[j] & 0xffffu) | (b[j] << 16);
-        dst[(2 * j + 1) * (kTP / 2)] = (a[j] >> 16) | (b[j] & 0xffff0000u);
-      }
-    }
-  }
-}
-
 // ---- online softmax + PV for one 16-key sub-tile -----------------------------
 // s: S^T[key 4g+i][query r] (raw scores); ok[i]: key 4g+i visible to query r.
 // Updates the running max / partial sum of query r (max shared by the four

@@ -256,23 +256,36 @@ __global__ __launch_bounds__(256) void latent_bwd_kv_kernel(const LatentArgs a) 
   const int s_first = (int)((need + a.q_block - 1) / a.q_block);
   const int qbeg = max(seg * a.seg, s_first);
   const int qend = (int)min((int64_t)(seg + 1) * a.seg, (int64_t)a.n_q);
+  // kAhead: the next 64 query rows (lse / D raw, transformed when staged) load while the current tile is worked
+  // on; only where the extra registers leave the waves per SIMD as they are (narrow latent heads)
+  constexpr bool kAhead = DHP * sizeof(T) <= 64;
+  TransTile<T, DHP> tq, to;
+  float pl = 0.f, pd = 0.f;
+  auto load_tile = [&](int q0) {
+    tq.load(rqb, a.rq_sn, q0, qend, a.Ldh);
+    to.load(dlb, a.do_sn, q0, qend, a.Ldh);
+    if (tid < 64) {
+      const int qi = min(q0 + tid, qend - 1);
+      pl = a.lse[hrow + qi];
+      pd = a.Dsum[hrow + qi];
+    }
+  };
+  if (kAhead && qbeg < qend) load_tile(qbeg);
   for (int q0 = qbeg; q0 < qend; q0 += 64) {
+    if (!kAhead) load_tile(q0);
     lds_barrier();
-    stage_rows_t<T, DHP, KP, true>(Qs, Qt, rqb, a.rq_sn, q0, qend, a.Ldh);
-    stage_rows_t<T, DHP, KP, true>(Os, Ot, dlb, a.do_sn, q0, qend, a.Ldh);
+    tq.template store_rows<KP>(Qs);
+    tq.store_t(Qt);
+    to.template store_rows<KP>(Os);
+    to.store_t(Ot);
     if (tid < 64) {
       const int qq = q0 + tid;
-      if (qq < qend) {
-        const float ls = a.lse[hrow + qq];
-        lse2s[tid] = ls == kNegInf ? 0.f : ls * kLog2e;
-        Dss[tid] = a.Dsum[hrow + qq];
-        vis[tid] = visible(qq, a);
-      } else {
-        lse2s[tid] = 0.f;
-        Dss[tid] = 0.f;
-        vis[tid] = 0;
-      }
+      const bool qv = qq < qend;
+      lse2s[tid] = (qv && pl != kNegInf) ? pl * kLog2e : 0.f;
+      Dss[tid] = qv ? pd : 0.f;
+      vis[tid] = qv ? visible(qq, a) : 0;
     }
+    if (kAhead && q0 + 64 < qend) load_tile(q0 + 64);
     lds_barrier();
     const int s0 = q0 + 16 * wave;  // each wave takes one 16-query sub-tile
     if (s0 < qend) {

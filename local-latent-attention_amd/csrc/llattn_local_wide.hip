@@ -653,14 +653,14 @@ __global__ __launch_bounds__(256, DHP <= 64 ? 3 : 2) void local_fwd32_kernel(con
   }
 
   // ---- epilogue: normalise, gate, mix.  Lane (c32, h) holds dims 32 db + 8 j + 4 h .. +3 of its query ----
-  lds_barrier();  // every wave is done with the key / value buffers
-  {
-    RowTile<T, DHP> rr;
+  {  // the remote rows of both query halves in flight together, issued before the wait for the other waves
+    RowTile<T, DHP> rr0, rr1;
     const T* rbase = static_cast<const T*>(a.rem) + b * a.r_sb + hd * a.r_sh;
-    rr.load_div(rbase, a.r_sn, q0, T_, a.q_block, Dh);
-    rr.template store<KP>(SQ);
-    rr.load_div(rbase, a.r_sn, q0 + 64, T_, a.q_block, Dh);
-    rr.template store<KP>(SQ + TILE);
+    rr0.load_div(rbase, a.r_sn, q0, T_, a.q_block, Dh);
+    rr1.load_div(rbase, a.r_sn, q0 + 64, T_, a.q_block, Dh);
+    lds_barrier();  // every wave is done with the key / value buffers
+    rr0.template store<KP>(SQ);
+    rr1.template store<KP>(SQ + TILE);
   }
   lds_barrier();
   const float l = l_run + __shfl_xor(l_run, 32);
