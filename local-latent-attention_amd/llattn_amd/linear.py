@@ -102,9 +102,19 @@ class _Project(torch.autograd.Function):
             y = linear_fwd(x2, wcat, bcat, heads)
             pooled = []
             if pools:
+                from . import _lib as L
                 from .ops import _contig, pool_fwd_into
                 xc = x2.view(x.shape) if x.dtype == BF16 else _contig(x)
+                means = (L.DIV_COUNT, L.DIV_SEG)
                 for seg, n_seg, divisor in pools:
+                    # with every segment full, the token-count mean and the segment mean are the same values
+                    # (one formula, sum * (1 / seg)): such a pooling is computed once and returned again as a
+                    # view, which keeps its gradient apart from the first one's
+                    twin = next((p for p, (s2, n2, d2) in zip(pooled, pools) if (s2, n2) == (seg, n_seg)
+                                 and n_seg * seg <= x.shape[1] and d2 in means and divisor in means), None)
+                    if twin is not None:
+                        pooled.append(twin.view(twin.shape))
+                        continue
                     p = torch.empty((x.shape[0], n_seg, K), dtype=x.dtype, device=x.device)
                     pool_fwd_into(xc, p, seg, n_seg, divisor)
                     pooled.append(p)

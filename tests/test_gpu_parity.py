@@ -381,6 +381,40 @@ def test_c4_macro_block_rows_match_fp32_reference():
     _config_row_check("c4", rows=(0, 3))
 
 
+def test_macro_block_equal_poolings_share_one_launch():
+    """Macro-block mode with the latent chunk equal to the query block and T a multiple of it (config 4's
+    64 / 64 at T = 8192): the query-block mean and the latent mean are the same values, so the forward pools
+    x once.  Output and every gradient still match the fp32 reference, with the two poolings' gradients
+    reaching x separately (reference models.py:159-230)."""
+    from llattn_amd import ops
+    from oracle import torch_ref
+    dev = require_cuda()
+    _print_case("shared pooling", "T 512, chunk 16, query block 16")
+    shape = orc.BlockShape(d_model=256, n_heads=4, window=96, local_block_size=64, latent_tokens=32,
+                           latent_d_model=128, latent_heads=2, latent_query_block_size=16)
+    torch.manual_seed(5)
+    m = build_module(shape, None, dev)
+    with torch.no_grad():
+        for p in m.parameters():
+            p.normal_(0.0, 0.05)
+    x = torch.randn(2, 512, 256, device=dev).to(torch.bfloat16)
+    dout = torch.randn(2, 512, 256, device=dev)
+    ops.EVENT_LOG = []
+    try:
+        out, dx, grads = run_module(m, x, dout, autocast_bf16=True)
+        calls = [e[0] for e in ops.EVENT_LOG]
+    finally:
+        ops.EVENT_LOG = None
+    # one in the forward (both poolings of x), one in the backward (dremote summed over each query block)
+    assert calls.count("llattn_pool_fwd") == 2, calls
+    params = {n: p.detach().float().cpu() for n, p in m.named_parameters()}
+    o_ref, dx_ref, g_ref = torch_ref.block_forward_backward(params, x.float().cpu(), dout.float().cpu(), shape)
+    assert_bf16_close(out, o_ref.numpy(), "out")
+    assert_bf16_close(dx, dx_ref.numpy(), "dx")
+    for n in g_ref:
+        assert_bf16_close(grads[n], g_ref[n].numpy(), n)
+
+
 # ---------------------------------------------------------------- profiling API (reference models.py:131-157)
 
 PROFILE_KEYS = ("profile_local_latent_total_ms", "profile_qkv_ms", "profile_pool_ms", "profile_local_attention_ms",
