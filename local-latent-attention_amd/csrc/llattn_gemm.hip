@@ -954,11 +954,16 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const GemmArgs a) {
   __shared__ __align__(16) unsigned char As[2][SBT * 128], Bs[2][SBT * 128];
   const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
   const int wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
-  const int tn_count = (a.N + SBT - 1) / SBT;
-  const int tm = blockIdx.x / tn_count, tn = blockIdx.x % tn_count;
+  const int tn_count = (a.N + SBT - 1) / SBT, tiles = ((a.M + SBT - 1) / SBT) * tn_count;
+  // EPI_PART: split blockIdx / tiles takes chunks [s C / S, (s+1) C / S) of the C 64-wide chunks
+  const int split = EPI == EPI_PART ? blockIdx.x / tiles : 0, t = EPI == EPI_PART ? blockIdx.x % tiles : blockIdx.x;
+  const int tm = t / tn_count, tn = t % tn_count;
   const int m0 = tm * SBT, n0 = tn * SBT;
   const bool want_rowsum = a.rowsum && tn == 0;
-  const int nchunks = (a.K + SBK - 1) / SBK;
+  const int call = (a.K + SBK - 1) / SBK;
+  const int cbeg = EPI == EPI_PART ? split * call / a.n_split : 0;
+  const int nchunks = (EPI == EPI_PART ? (split + 1) * call / a.n_split : call) - cbeg;
+  const int kbase = cbeg * SBK;
   f32x4 acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -969,8 +974,10 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const GemmArgs a) {
   uint4 va[4][2], vb[4][2];
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
-    small_load<AK>(va[d], a.A, a.lda, m0, a.M, d * SBK, a.K, tid);
-    small_load<BKM>(vb[d], a.B, a.ldb, n0, a.N, d * SBK, a.K, tid);
+    if (d < nchunks) {
+      small_load<AK>(va[d], a.A, a.lda, m0, a.M, kbase + d * SBK, a.K, tid);
+      small_load<BKM>(vb[d], a.B, a.ldb, n0, a.N, kbase + d * SBK, a.K, tid);
+    }
   }
   auto chunk = [&](int c, uint4 (&ra)[2], uint4 (&rb)[2]) {
     unsigned char* pa = As[c & 1];
@@ -979,8 +986,8 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const GemmArgs a) {
     small_store<BKM>(rb, pb, tid);
     __syncthreads();  // the panels of chunk c are complete; the other buffer (chunk c-1) is no longer read
     if (c + 4 < nchunks) {  // this register set is free again: chunk c + 4
-      small_load<AK>(ra, a.A, a.lda, m0, a.M, (c + 4) * SBK, a.K, tid);
-      small_load<BKM>(rb, a.B, a.ldb, n0, a.N, (c + 4) * SBK, a.K, tid);
+      small_load<AK>(ra, a.A, a.lda, m0, a.M, kbase + (c + 4) * SBK, a.K, tid);
+      small_load<BKM>(rb, a.B, a.ldb, n0, a.N, kbase + (c + 4) * SBK, a.K, tid);
     }
     if (want_rowsum && tid < SBT) {
 #pragma unroll
@@ -1017,20 +1024,25 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const GemmArgs a) {
     if (c + 2 < nchunks) chunk(c + 2, va[2], vb[2]);
     if (c + 3 < nchunks) chunk(c + 3, va[3], vb[3]);
   }
-  if (want_rowsum && tid < SBT && m0 + tid < a.M) a.rowsum[m0 + tid] = rs;
+  if (want_rowsum && tid < SBT && m0 + tid < a.M) {
+    if constexpr (EPI == EPI_PART) a.part[(int64_t)a.n_split * a.M * a.N + (int64_t)split * a.M + m0 + tid] = rs;
+    else a.rowsum[m0 + tid] = rs;
+  }
   // lane (r, g) holds C[m0 + wm*32 + 16i + r][n0 + wn*32 + 16j + 4g + e]
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int col = n0 + wn * 32 + 16 * j + 4 * g;
     if (col >= a.N) continue;
-    const float4 b4 = (EPI == EPI_BF16 && a.bias) ? *reinterpret_cast<const float4*>(a.bias + col)
+    const float4 b4 = (EPI != EPI_PART && a.bias) ? *reinterpret_cast<const float4*>(a.bias + col)
                                                    : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int row = m0 + wm * 32 + 16 * i + r;
       if (row >= a.M) continue;
       float v[4] = {acc[i][j][0] + b4.x, acc[i][j][1] + b4.y, acc[i][j][2] + b4.z, acc[i][j][3] + b4.w};
-      if constexpr (EPI == EPI_BF16) {
+      if constexpr (EPI == EPI_PART) {  // this split's fp32 partial [split][M][N]
+        *reinterpret_cast<float4*>(a.part + ((int64_t)split * a.M + row) * a.N + col) = make_float4(v[0], v[1], v[2], v[3]);
+      } else if constexpr (EPI == EPI_BF16) {
         uint16_t* p = static_cast<uint16_t*>(a.C) + (int64_t)row * a.ldc + col;
         if (a.accumulate) {
           float o[4];
@@ -1053,9 +1065,18 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const GemmArgs a) {
 
 template <bool AK, bool BKM>
 void launch_small(const GemmArgs& a, int c_dtype, hipStream_t st) {
-  const dim3 grid(((a.M + SBT - 1) / SBT) * ((a.N + SBT - 1) / SBT)), block(256);
-  if (c_dtype == LLATTN_F32) hipLaunchKernelGGL((gemm_small_kernel<AK, BKM, EPI_F32>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((gemm_small_kernel<AK, BKM, EPI_BF16>), grid, block, 0, st, a);
+  const int tiles = ((a.M + SBT - 1) / SBT) * ((a.N + SBT - 1) / SBT);
+  const dim3 block(256);
+  if (a.n_split > 1) {  // K splits: fp32 partials, then the ordered reduction of the large products
+    hipLaunchKernelGGL((gemm_small_kernel<AK, BKM, EPI_PART>), dim3(tiles * a.n_split), block, 0, st, a);
+    const int64_t quads = (int64_t)a.M * (a.N / 4) + (a.rowsum ? a.M : 0);
+    const dim3 rg((unsigned)((quads + 255) / 256));
+    if (c_dtype == LLATTN_F32) hipLaunchKernelGGL((splitk_reduce_kernel<EPI_F32>), rg, block, 0, st, a, a.n_split);
+    else hipLaunchKernelGGL((splitk_reduce_kernel<EPI_BF16>), rg, block, 0, st, a, a.n_split);
+    return;
+  }
+  if (c_dtype == LLATTN_F32) hipLaunchKernelGGL((gemm_small_kernel<AK, BKM, EPI_F32>), dim3(tiles), block, 0, st, a);
+  else hipLaunchKernelGGL((gemm_small_kernel<AK, BKM, EPI_BF16>), dim3(tiles), block, 0, st, a);
 }
 
 // The small-tile path: no K split requested, no activation or row addends, an output of at most 32 tiles of
@@ -1065,6 +1086,26 @@ bool use_small(const llattn_gemm_desc* d) {
   return d->split_k == 0 && d->act == LLATTN_ACT_NONE && !d->rowadd[0].ptr && !d->rowadd[1].ptr &&
          d->c_heads.T == 0 && tiles <= 32 &&
          std::min(d->M, d->N) <= 1024 && d->K <= 4096;
+}
+
+// K splits of a small product: its 64 x 64 tiles run their chunks one after another, ~0.7 us per 64-wide
+// chunk when a few workgroups cover the output, so a long contraction over few tiles is split while the
+// splits fit one round on the chip; the ordered reduction then costs ~3.5 us plus its fp32 traffic (E.g.
+// the 512 x 64 x 1024 query-block projection of config 4: 8 tiles of 16 chunks, 8 splits of 2.)
+int small_split(const llattn_gemm_desc* d) {
+  const int64_t tiles = (int64_t)((d->M + SBT - 1) / SBT) * ((d->N + SBT - 1) / SBT);
+  const int64_t chunks = (d->K + SBK - 1) / SBK;
+  int best = 1;
+  double best_t = (double)chunks * 0.7e-6;
+  for (int64_t S = 2; S <= std::min<int64_t>(chunks / 2, 16) && tiles * S <= 256; ++S) {
+    const double t = (double)((chunks + S - 1) / S) * 0.7e-6 + 3.5e-6 +
+                     2.0 * S * d->M * (double)(d->N + (d->a_rowsum ? 1 : 0)) * 4.0 / 5e12;
+    if (t < best_t * 0.9) {
+      best_t = t;
+      best = (int)S;
+    }
+  }
+  return best;
 }
 
 // Number of K splits: 1 when the output tiles alone fill most of the chip; otherwise the split count S
@@ -1106,8 +1147,7 @@ using namespace llattn::gemm;
 
 extern "C" size_t llattn_gemm_workspace_size(const llattn_gemm_desc* d) {
   if (!d) return 0;
-  if (use_small(d)) return 0;
-  const int S = resolve_split(d);
+  const int S = use_small(d) ? small_split(d) : resolve_split(d);
   return S > 1 ? (size_t)S * d->M * (d->N + (d->a_rowsum ? 1 : 0)) * sizeof(float) : 0;
 }
 
@@ -1179,8 +1219,8 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
                 "accumulation, activation, row addends or K split, and K > %d", 2 * BK);
   const size_t need = llattn_gemm_workspace_size(d);
   if (need && (!workspace || workspace_bytes < need || !aligned16(workspace)))
-    return fail(LLATTN_ERR_WORKSPACE, "llattn_gemm: %d K splits need %zu workspace bytes (got %zu)", S, need,
-                workspace_bytes);
+    return fail(LLATTN_ERR_WORKSPACE, "llattn_gemm: %d K splits need %zu workspace bytes (got %zu)",
+                use_small(d) ? small_split(d) : S, need, workspace_bytes);
   GemmArgs a{};
   a.M = d->M; a.N = d->N; a.K = d->K; a.k_pairs = k_pairs; a.n_split = S;
   a.tiles_m = (d->M + BM - 1) / BM; a.tiles_n = (d->N + BN - 1) / BN;
@@ -1205,6 +1245,7 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
   a.ld_aux = d->ld_aux;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (use_small(d)) {
+    a.n_split = small_split(d);
     if (!d->a_trans && !d->b_trans) launch_small<true, true>(a, d->c_dtype, st);
     else if (!d->a_trans && d->b_trans) launch_small<true, false>(a, d->c_dtype, st);
     else if (d->a_trans && d->b_trans) launch_small<false, false>(a, d->c_dtype, st);

@@ -37,6 +37,25 @@ def test_linear_with_bias(M, N, K):
     assert _err(gemm.linear(x, w, b), ref) < BF16_TOL
 
 
+@pytest.mark.parametrize("M,N,K,dt,acc", [(512, 64, 1024, torch.float32, False), (97, 40, 192, torch.float32, False),
+                                          (512, 128, 1000, torch.float32, True), (512, 64, 1024, torch.bfloat16, True),
+                                          (256, 1024, 1408, torch.bfloat16, False)])
+def test_small_product_bias_and_accumulate(M, N, K, dt, acc):
+    """Products of few 64 x 64 tiles over a long contraction (the pooled-latent and query-block projections)
+    run as K splits plus the ordered reduction; bias and accumulation apply once, for an fp32 output too."""
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: small product", M, N, K, dt, acc, flush=True)
+    g = torch.Generator(device=dev).manual_seed(M + 3 * N + K)
+    x, w = _rand(M, K, gen=g, dev=dev), _rand(N, K, gen=g, dev=dev)
+    b = torch.randn(N, device=dev, generator=g)
+    c0 = torch.randn(M, N, device=dev, generator=g).to(dt)
+    out = c0.clone() if acc else torch.empty((M, N), dtype=dt, device=dev)
+    gemm.linear(x, w, b, out=out, accumulate=acc)
+    ref = x.float() @ w.float().T + b + (c0.float() if acc else 0.0)
+    assert _err(out, ref) < BF16_TOL
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 8, 8), (1, 40, 72), (97, 40, 200), (33, 264, 1000), (4096, 512, 200),
                                    (2000, 136, 8), (194, 208, 88)])
 def test_linear_k_tail(M, N, K):
