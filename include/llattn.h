@@ -61,8 +61,9 @@ typedef struct llattn_tensor {
 
 typedef struct llattn_shape {
   int32_t B, T;          /* batch, sequence length */
-  int32_t H, Dh;         /* local heads, head dim (reference models.py:66-68) */
-  int32_t Lh, Ldh;       /* latent heads, latent head dim (reference models.py:72-74) */
+  int32_t H, Dh;         /* local heads, head dim (reference models.py:66-68); multiples of 8 up to 256 in bf16,
+                            of 4 up to 128 in fp32 */
+  int32_t Lh, Ldh;       /* latent heads, latent head dim (reference models.py:72-74); the same limits */
   int32_t window;        /* local window W (reference models.py:69) */
   int32_t block;         /* resolved local block size min(T, max(W, local_block_size)) (reference models.py:249) */
   int32_t chunk;         /* latent chunk ceil(T / min(latent_tokens, T)) (reference models.py:175-180) */

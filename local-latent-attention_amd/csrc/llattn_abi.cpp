@@ -52,12 +52,13 @@ int32_t check_shape(const llattn_shape* s) {
   if (s->q_block <= 0 || s->n_q <= 0 || (int64_t)(s->n_q - 1) * s->q_block >= s->T ||
       (int64_t)s->n_q * s->q_block < s->T)
     return fail(LLATTN_ERR_SHAPE, "latent query block %d x %d queries does not tile T=%d", s->q_block, s->n_q, s->T);
-  const int vec = s->dtype == LLATTN_F32 ? 4 : 8;
-  if (s->Dh % vec || padded_head_dim(s->Dh) == 0)
-    return fail(LLATTN_ERR_UNSUPPORTED, "head_dim %d unsupported (needs a multiple of %d, at most 128)", s->Dh, vec);
-  if (s->Ldh % vec || padded_head_dim(s->Ldh) == 0)
-    return fail(LLATTN_ERR_UNSUPPORTED, "latent head_dim %d unsupported (needs a multiple of %d, at most 128)", s->Ldh,
-                vec);
+  const int vec = s->dtype == LLATTN_F32 ? 4 : 8, dmax = s->dtype == LLATTN_F32 ? 128 : 256;
+  if (s->Dh % vec || padded_head_dim(s->Dh) == 0 || s->Dh > dmax)
+    return fail(LLATTN_ERR_UNSUPPORTED, "head_dim %d unsupported (needs a multiple of %d, at most %d)", s->Dh, vec,
+                dmax);
+  if (s->Ldh % vec || padded_head_dim(s->Ldh) == 0 || s->Ldh > dmax)
+    return fail(LLATTN_ERR_UNSUPPORTED, "latent head_dim %d unsupported (needs a multiple of %d, at most %d)", s->Ldh,
+                vec, dmax);
   return LLATTN_OK;
 }
 

@@ -19,13 +19,14 @@ int32_t check_launch(const char* what);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline int64_t elem_size(int32_t dtype) { return dtype == LLATTN_F32 ? 4 : 2; }
-// smallest padded head dim (multiple of 32) supported by the compiled kernels, or 0
+// smallest padded head dim supported by the compiled kernels (32, 64, 96, 128 or 256), or 0
 inline int padded_head_dim(int d) {
   if (d <= 0) return 0;
   if (d <= 32) return 32;
   if (d <= 64) return 64;
   if (d <= 96) return 96;
   if (d <= 128) return 128;
+  if (d <= 256) return 256;
   return 0;
 }
 // Validates a view whose innermost (head-dim) rows are read with 16-byte accesses.

@@ -375,6 +375,12 @@ bool dispatch(int dhp, bool fwd, const LatentArgs& a, hipStream_t st) {
     case 64: launch<T, 64>(fwd, a, st); return true;
     case 96: launch<T, 96>(fwd, a, st); return true;
     case 128: launch<T, 128>(fwd, a, st); return true;
+    case 256:  // bf16 only: the fp32 tiles of 256 dims exceed the LDS
+      if constexpr (std::is_same_v<T, uint16_t>) {
+        launch<T, 256>(fwd, a, st);
+        return true;
+      }
+      return false;
     default: return false;
   }
 }

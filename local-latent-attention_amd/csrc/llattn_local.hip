@@ -984,6 +984,12 @@ bool dispatch(int dhp, bool fwd, const LocalArgs& a, hipStream_t s) {
     case 64: fwd ? launch_fwd<T, 64>(a, s) : launch_bwd<T, 64>(a, s); return true;
     case 96: fwd ? launch_fwd<T, 96>(a, s) : launch_bwd<T, 96>(a, s); return true;
     case 128: fwd ? launch_fwd<T, 128>(a, s) : launch_bwd<T, 128>(a, s); return true;
+    case 256:  // bf16 only: the fp32 tiles of 256 dims exceed the LDS
+      if constexpr (std::is_same_v<T, uint16_t>) {
+        fwd ? launch_fwd<T, 256>(a, s) : launch_bwd<T, 256>(a, s);
+        return true;
+      }
+      return false;
     default: return false;
   }
 }

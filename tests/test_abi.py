@@ -114,8 +114,8 @@ def test_workspace_sizes():
     ("T", 0, 1, b"sizes must be positive"),
     ("dtype", 5, 2, b"unknown dtype"),
     ("Dh", 20, 4, b"head_dim 20 unsupported"),
-    ("Dh", 160, 4, b"head_dim 160 unsupported"),
-    ("Ldh", 136, 4, b"latent head_dim 136 unsupported"),
+    ("Dh", 264, 4, b"head_dim 264 unsupported (needs a multiple of 8, at most 256)"),
+    ("Ldh", 272, 4, b"latent head_dim 272 unsupported"),
     ("chunk", 5, 1, b"does not tile"),
     ("n_q", 50, 1, b"does not tile"),
     ("block", 98, 1, b"local block size"),
@@ -130,6 +130,18 @@ def test_shape_validation_codes(field, value, code, msg):
     assert msg in lib.llattn_last_error()
     with pytest.raises(ValueError):
         L.check(rc, "llattn_local_gate_fwd")
+
+
+@pytest.mark.parametrize("field,value", [("Dh", 160), ("Ldh", 136), ("Dh", 256)])
+def test_fp32_head_dims_above_128_unsupported(field, value):
+    """bf16 takes head dims up to 256; fp32 stops at 128 (its 256-dim tiles would not fit the LDS)."""
+    L, lib = _lib()
+    s = _shape(L, dtype=L.F32, **{field: value})
+    t = L.LlattnTensor(None, 0, 0, 0)
+    rc = lib.llattn_local_gate_fwd(ctypes.byref(s), *(ctypes.byref(t),) * 4, None, None, ctypes.byref(t),
+                                   ctypes.byref(t), None, None, None)
+    assert rc == L.ERR_UNSUPPORTED
+    assert b"at most 128" in lib.llattn_last_error()
 
 
 def test_null_and_misaligned_views_are_layout_errors():

@@ -205,6 +205,49 @@ OP_CASES = [
 ]
 
 
+# bf16 head dims above 128 (padded to 256) on the generic tile kernels: local forward and two-pass backward,
+# latent forward and backward; a window below and above 64, macro-block queries, a ragged head dim
+WIDE_HEAD_CASES = [
+    (2, 150, 2, 256, 2, 256, 40, 64, 10, 0),
+    (1, 200, 2, 160, 1, 192, 100, 64, 13, 16),
+    (1, 97, 1, 136, 2, 24, 300, 300, 7, 0),
+]
+
+
+@pytest.mark.parametrize("case", WIDE_HEAD_CASES)
+def test_op_bf16_wide_head_dims_match_oracle(case):
+    _print_case("op bf16 wide head", case)
+    got, ref = _op_case(*case, seed=hash(case) % 1000 + 2, dtype=torch.bfloat16)
+    floor = ref.pop("_floor")
+    for k in ref:
+        assert_bf16_close(got[k], ref[k], k, floor=floor.get(k))
+
+
+def test_module_bf16_head_dim_256_matches_fp32_reference():
+    """A block with 256-dim heads (d_model 512, 2 heads; 2 latent heads of 128) under bf16 autocast against the
+    fp32 reference: the projections, head layouts and the 256-dim tile kernels together
+    (reference models.py:64-74 accepts any divisible head split)."""
+    from oracle import torch_ref
+    dev = require_cuda()
+    _print_case("module bf16 head dim 256")
+    shape = orc.BlockShape(d_model=512, n_heads=2, window=96, local_block_size=128, latent_tokens=16,
+                           latent_d_model=256, latent_heads=2)
+    torch.manual_seed(11)
+    m = build_module(shape, None, dev)
+    with torch.no_grad():
+        for p in m.parameters():
+            p.normal_(0.0, 0.03)
+    x = torch.randn(2, 256, 512, device=dev).to(torch.bfloat16)
+    dout = torch.randn(2, 256, 512, device=dev)
+    out, dx, grads = run_module(m, x, dout, autocast_bf16=True)
+    params = {n: p.detach().float().cpu() for n, p in m.named_parameters()}
+    o_ref, dx_ref, g_ref = torch_ref.block_forward_backward(params, x.float().cpu(), dout.float().cpu(), shape)
+    assert_bf16_close(out, o_ref.numpy(), "out")
+    assert_bf16_close(dx, dx_ref.numpy(), "dx")
+    for n in g_ref:
+        assert_bf16_close(grads[n], g_ref[n].numpy(), n)
+
+
 @pytest.mark.parametrize("case", OP_CASES)
 def test_op_fp32_matches_oracle(case):
     _print_case("op fp32", case)
