@@ -164,10 +164,15 @@ constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, gfx9 family
 // flight: it would otherwise make every later LDS read wait for all of it
 // (vmcnt(0)), although the reads target another stage.  The main loop waits
 // for these loads itself (vmcnt) before the barrier that publishes them.
+// The descriptor and the LDS address are wave-uniform at every call; readfirstlane states it for the
+// cases where the compiler cannot prove it (it then keeps them in SGPRs, as the instruction requires).
 __device__ __forceinline__ void dma_block(const i32x4& rs, uint32_t off, const unsigned char* dst) {
+  const i32x4 srs = {__builtin_amdgcn_readfirstlane(rs[0]), __builtin_amdgcn_readfirstlane(rs[1]),
+                     __builtin_amdgcn_readfirstlane(rs[2]), __builtin_amdgcn_readfirstlane(rs[3])};
+  const uint32_t sdst = __builtin_amdgcn_readfirstlane(lds_addr(dst));
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                :
-               : "v"(off), "s"(rs), "s"(lds_addr(dst))
+               : "v"(off), "s"(srs), "s"(sdst)
                : "memory", "m0");
 }
 
@@ -572,36 +577,43 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
   }
 }
 
-// Persistent variant for bf16 C = A Bᵀ (+ bias) with k-contiguous A and B and no K split: one
-// workgroup per CU walks tiles v = blockIdx.x, + gridDim.x, ...  The 4-stage DMA ring runs on
-// across tiles (the last four k steps of a tile fetch the first four of the next), and the
-// epilogue stores straight from the accumulators (permuted B fragments give each lane 8
-// consecutive columns), so a tile's output drains to memory while the next tile's MFMAs run
-// instead of in a burst that every CU pays at the same moment.
+// Persistent kernel for bf16 C = A Bᵀ (+ bias) (+ row addends) with k-contiguous A and B and no K split:
+// one workgroup per CU walks tiles v = blockIdx.x, + gridDim.x, ...
 //
-// Memory operations per tile boundary are fixed (one DMA of the next tile's bias slice into LDS,
-// 32 stores, 32 more for the GELU output; masked lanes use out-of-range buffer offsets, and the first
-// tile issues the same ones with nothing to store), so the vmcnt immediates below are exact: the
-// first three k steps after a boundary wait with 16 + EPI_OPS younger operations in flight (at most
-// 63, the counter's range: with the GELU output the oldest stores are waited for too), the others
-// with 16.
-template <int ACT>
-constexpr int epi_ops() { return 1 + 32 * (ACT == LLATTN_ACT_GELU ? 2 : 1); }  // bias DMA + stores per boundary
+// K advances in 64-wide steps through two LDS stages of 64 KB (A then B, 256 rows of 128 bytes each).
+// A DMA instruction moves 8 rows x 128 bytes, so every row of a step arrives as one whole cache line.
+// Step g's stage is g % 2; the DMA of step g + 2 goes into it once every wave has read it, which the
+// barrier in the middle of step g establishes, so the loads of a step have one step of MFMAs to land:
+//   sub-step 0: 64 MFMAs on k 0..31 of the stage, with the fragment reads of k 32..63;
+//   wait for this wave's DMA of step g + 1 and its fragment reads; barrier;
+//   sub-step 1: 64 MFMAs on k 32..63, with the fragment reads of step g + 1's k 0..31 (other stage)
+//               and the 16 DMA instructions of step g + 2 (this stage).
+// The DMA runs on across tiles (the last two steps of a tile fetch the first two of the next), and the
+// epilogue stores straight from the accumulators (permuted B fragments give each lane 8 consecutive
+// columns), so a tile's output drains to memory while the next tile's first MFMAs run.  The per-lane DMA
+// offsets do not depend on the tile or the step (both lie in the scalar buffer descriptor), so the main
+// loop does no per-lane address arithmetic.
+//
+// Waits never count stores: stores may retire before older loads, so a vmcnt that allowed an epilogue's
+// stores in flight could pass with DMA data still missing.  The last step of a tile therefore waits for
+// all its DMA (the next tile's steps 0 and 1) before the epilogue issues its stores; the next tile's first
+// barrier then waits for nothing in vmcnt, and every later barrier waits for vmcnt(0), the youngest
+// load being the DMA it publishes (the stores have had a step to drain by then).
+constexpr int PBK = 64;                  // k per LDS stage
+constexpr int PTILE = BM * PBK * 2;      // 32 KB per operand per stage
+constexpr int PSTAGE = 2 * PTILE;        // A then B
+constexpr int PDMA = PTILE / 1024 / 4;   // 1 KB DMA blocks per wave per operand and step (8)
 
-// Byte offsets relative to the tile origin (row/column 0 of the tile, k = 0) of this lane's
-// 16-byte chunk in each of the wave's blocks of a k-contiguous operand tile.
+// 128-byte LDS rows: 16-byte chunk c of row r sits at slot c ^ pswz(r).  A fragments read rows o16 + r,
+// eight consecutive rows per LDS cycle -> r & 7.  B fragments read the permuted rows o16 + 8 (r / 4) + r % 4
+// -> (r & 3) | (bit 3 of the row at bit 2).  Both conflict-free.
 template <bool PERM>
-__device__ __forceinline__ void tile_rel_offsets(uint32_t (&off)[DMA_PER_TILE], int64_t ld, int wave, int lane) {
-#pragma unroll
-  for (int i = 0; i < DMA_PER_TILE; ++i) {
-    const int row = 16 * (wave * DMA_PER_TILE + i) + (lane >> 2);
-    const int c = (lane & 3) ^ kswz<PERM>(row);
-    off[i] = (uint32_t)(((int64_t)row * ld + 8 * c) * 2);
-  }
+__device__ __forceinline__ int pswz(int row) {
+  return PERM ? ((row & 3) | (((row >> 3) & 1) << 2)) : (row & 7);
 }
 
-// Buffer descriptor of a k-contiguous operand from row o0 and step k0 on.  Rows past the operand
-// read zero (their offsets are past `bytes`); they only feed outputs that are never stored.
+// Buffer descriptor of a k-contiguous operand from row o0 and k0 on.  Rows past the operand read zero
+// (their offsets are past `bytes`); they only feed outputs that are never stored.
 __device__ __forceinline__ i32x4 tile_rsrc(const uint16_t* base, int64_t ld, int64_t bytes, int o0, int k0) {
   const int64_t skip = ((int64_t)o0 * ld + k0) * 2;
   const uint64_t addr = reinterpret_cast<uint64_t>(base) + (uint64_t)skip;
@@ -615,43 +627,62 @@ __device__ __forceinline__ void tile_origin(const GemmArgs& a, int v, int total,
   constexpr int GM = 8;
   const int group = t / (GM * a.tiles_n), first_m = group * GM;
   const int gm = min(a.tiles_m - first_m, GM);
-  m0 = (first_m + (t % (GM * a.tiles_n)) % gm) * BM;
-  n0 = ((t % (GM * a.tiles_n)) / gm) * BN;
+  // wave-uniform by construction; readfirstlane keeps them in SGPRs (the DMA descriptors need scalars)
+  m0 = __builtin_amdgcn_readfirstlane((first_m + (t % (GM * a.tiles_n)) % gm) * BM);
+  n0 = __builtin_amdgcn_readfirstlane(((t % (GM * a.tiles_n)) / gm) * BN);
 }
 
-template <int ACT, bool CH = false>
+// RA: the row addends of GemmArgs (ra_ptr) are added before the rounding, after the bias, in the same order
+// as gemm_kernel's bf16 epilogue.
+template <int ACT, bool CH = false, bool RA = false>
 __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) {
-  constexpr int EPI_OPS = epi_ops<ACT>();
-  __shared__ __align__(1024) unsigned char smem[NST * STAGE_BYTES];
+  __shared__ __align__(1024) unsigned char smem[2 * PSTAGE];
   __shared__ __align__(16) float sbias[2][BN];  // bias of the tile being finished / fetched, by tile parity
   const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const int total = a.tiles_m * a.tiles_n, nk = 2 * a.k_pairs;  // nk >= 4 (launcher)
+  const int total = a.tiles_m * a.tiles_n, nk = a.k_pairs;  // 64-wide k steps per tile (>= 2: launcher)
 
-  auto bcol = [&](int j) { return wn * 128 + 32 * (j >> 1) + 4 * (j & 1); };
-  auto opaque_lane = [&]() {
-    int zero;
-    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
-    return lane + zero;
+  // DMA block i of this wave: rows 8 (8 wave + i) .. + 7 of the operand tile; lane -> row + lane / 8, and
+  // its LDS slot lane % 8 receives the row's chunk (lane % 8) ^ pswz(row).  kc*: first k of that chunk.
+  uint32_t offa[PDMA], offb[PDMA];
+  int kca[PDMA], kcb[PDMA];
+#pragma unroll
+  for (int i = 0; i < PDMA; ++i) {
+    const int row = 8 * (wave * PDMA + i) + (lane >> 3);
+    const int ca = (lane & 7) ^ pswz<false>(row), cb = (lane & 7) ^ pswz<true>(row);
+    offa[i] = (uint32_t)(((int64_t)row * a.lda + 8 * ca) * 2);
+    offb[i] = (uint32_t)(((int64_t)row * a.ldb + 8 * cb) * 2);
+    kca[i] = 8 * ca;
+    kcb[i] = 8 * cb;
+  }
+  // LDS byte offsets within a stage of this lane's fragment of sub-step h (k 32h .. 32h + 31)
+  const int arow = r, brow = 8 * (r >> 2) + (r & 3);
+  uint32_t abase[2], bbase[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    abase[h] = arow * 128 + (((4 * h + g) ^ pswz<false>(arow)) << 4);
+    bbase[h] = PTILE + brow * 128 + (((4 * h + g) ^ pswz<true>(brow)) << 4);
+  }
+  // fragment block i of A (rows wm*128 + 16i ..), j of B (permuted: block pairs interleave by fours)
+  auto frag_a = [&](int stage, int h, int i) {
+    return *reinterpret_cast<const bf16x8*>(smem + stage * PSTAGE + abase[h] + (wm * 128 + 16 * i) * 128);
   };
-  // Per-lane offsets are recomputed in every step from an opaque copy of the lane index rather
-  // than kept live across the tile loop: with 256 accumulators and two fragment buffers the
-  // register file is full, and a spilled offset would be reloaded with a vmcnt wait that drains
-  // the previous tile's stores.
-  // klim: K - k0 of the step (K tail: lanes from klim on read zero, see kmask)
-  auto dma = [&](const i32x4& rsa, const i32x4& rsb, int stage, int q, int ln, int klim) {
-    unsigned char* st = smem + stage * STAGE_BYTES;
-    uint32_t off[DMA_PER_TILE];
-    if (q < DMA_PER_TILE) {
-      tile_rel_offsets<false>(off, a.lda, wave, ln);
-      const uint32_t o = klim < BK ? kmask(off[q], lane_k0<false>(ln), klim) : off[q];
-      dma_block(rsa, o, st + (wave * DMA_PER_TILE + q) * 1024);
+  auto frag_b = [&](int stage, int h, int j) {
+    return *reinterpret_cast<const bf16x8*>(smem + stage * PSTAGE + bbase[h] +
+                                            (wn * 128 + 32 * (j >> 1) + 4 * (j & 1)) * 128);
+  };
+  // DMA block q (0..7: A, 8..15: B) of a step into `stage`; klim = K - k0 of the step (K tail: a lane whose
+  // chunk starts at or past K reads zero)
+  auto dma = [&](const i32x4& rsa, const i32x4& rsb, int stage, int q, int klim) {
+    unsigned char* st = smem + stage * PSTAGE;
+    if (q < PDMA) {
+      const uint32_t o = klim < PBK ? kmask(offa[q], kca[q], klim) : offa[q];
+      dma_block(rsa, o, st + (wave * PDMA + q) * 1024);
     } else {
-      tile_rel_offsets<true>(off, a.ldb, wave, ln);
-      const int qb = q - DMA_PER_TILE;
-      const uint32_t o = klim < BK ? kmask(off[qb], lane_k0<true>(ln), klim) : off[qb];
-      dma_block(rsb, o, st + TILE_BYTES + (wave * DMA_PER_TILE + qb) * 1024);
+      const int qb = q - PDMA;
+      const uint32_t o = klim < PBK ? kmask(offb[qb], kcb[qb], klim) : offb[qb];
+      dma_block(rsb, o, st + PTILE + (wave * PDMA + qb) * 1024);
     }
   };
 
@@ -665,13 +696,12 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
     const uint64_t addr = reinterpret_cast<uint64_t>(a.bias) + (uint64_t)n0t * 4;
     const int64_t bytes = a.bias ? (int64_t)(a.N - n0t) * 4 : 0;
     const i32x4 rs{(int)(uint32_t)addr, (int)((addr >> 32) & 0xffff), (int)(uint32_t)bytes, kRsrcWord3};
-    const int ln = opaque_lane();
-    if (ln < 16) dma_block(rs, (uint32_t)(wave * 256 + ln * 16), reinterpret_cast<const unsigned char*>(&sbias[slot][wave * 64]));
+    if (lane < 16) dma_block(rs, (uint32_t)(wave * 256 + lane * 16), reinterpret_cast<const unsigned char*>(&sbias[slot][wave * 64]));
   };
 
   int v = blockIdx.x, m0, n0;
   tile_origin(a, v, total, m0, n0);
-  // the tile whose steps the DMA ring fetches after this one, if any
+  // the tile whose steps the DMA fetches after this one, if any
   int vn = v + gridDim.x, m0n = 0, n0n = 0;
   if (vn < total) tile_origin(a, vn, total, m0n, n0n);
 
@@ -681,111 +711,144 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // prologue: steps 0..3 of the first tile, then the boundary's 40 operations with nothing to move
+  // prologue: steps 0 and 1 of the first tile and its bias, all landed before the first barrier (as at a
+  // tile boundary)
 #pragma unroll
-  for (int s = 0; s < NST; ++s) {
-    const i32x4 rsa = tile_rsrc(a.A, a.lda, a.a_bytes, m0, s * BK), rsb = tile_rsrc(a.B, a.ldb, a.b_bytes, n0, s * BK);
+  for (int s = 0; s < 2; ++s) {
+    const i32x4 rsa = tile_rsrc(a.A, a.lda, a.a_bytes, m0, s * PBK), rsb = tile_rsrc(a.B, a.ldb, a.b_bytes, n0, s * PBK);
 #pragma unroll
-    for (int q = 0; q < DMA_PER_STEP; ++q) dma(rsa, rsb, s, q, lane, a.K - s * BK);
+    for (int q = 0; q < 2 * PDMA; ++q) dma(rsa, rsb, s, q, a.K - s * PBK);
   }
   bias_dma(n0, 0);
-#pragma unroll
-  for (int u = 0; u < EPI_OPS - 1; ++u) __builtin_amdgcn_raw_buffer_store_b128(i32x4{0, 0, 0, 0}, rc, kOffOOB, 0, 0);
-  __builtin_amdgcn_s_waitcnt(wait_vm(std::min(63, (NST - 1) * DMA_PER_STEP + EPI_OPS)));
+  __builtin_amdgcn_s_waitcnt(wait_vm(0));
   __builtin_amdgcn_s_barrier();
-  bf16x8 fa0[8], fb0[8], fa1[8], fb1[8];
+  bf16x8 fa0[8], fb0[8], fa1[8], fb1[8];  // k 0..31 and 32..63 of a step
 #pragma unroll
-  for (int i = 0; i < 8; ++i) fa0[i] = frag<true>(smem, wm * 128 + 16 * i, r, g);
+  for (int i = 0; i < 8; ++i) fa0[i] = frag_a(0, 0, i);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) fb0[j] = frag<true, true>(smem + TILE_BYTES, bcol(j), r, g);
+  for (int j = 0; j < 8; ++j) fb0[j] = frag_b(0, 0, j);
 
-  int gs = 0;    // global step index of the tile's step 0 (stage of step kt: (gs + kt) % 4)
+  int gs = 0;    // global step index of the tile's step 0 (stage of step kt: (gs + kt) % 2)
   int slot = 0;  // sbias slot of the current tile
-  // One k step (see gemm_kernel); WAIT: the vmcnt immediate (younger operations allowed in flight).
-  // The DMA of global step gs+kt+4 fetches the tile's step kt+4, else the next tile's step
-  // kt+4-nk, else (last tile) reloads the last step into the free stage.
-  int tln = lane;  // the lane index as seen by this tile's steps (re-derived per tile, see dma)
-  auto step = [&](auto wait_tag, int kt, const bf16x8 (&ca)[8], const bf16x8 (&cb)[8], bf16x8 (&na)[8],
-                  bf16x8 (&nb)[8]) {
-    constexpr int WAIT = decltype(wait_tag)::value;
+  // One 64-k step; VMW: the vmcnt wait at its barrier (63: none, step 0 of a tile; 0 otherwise).  The DMA of
+  // global step gs+kt+2 fetches the tile's step kt+2, else the next tile's step kt+2-nk, else (last tile)
+  // reloads the last step into the free stage, which is never read again.
+  auto step = [&](auto vmw_tag, int kt) {
+    constexpr int VMW = decltype(vmw_tag)::value;
+    const int s = (gs + kt) & 1;
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(WAIT));
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      if (q < 8) fa1[q] = frag_a(s, 1, q);
+      else fb1[q - 8] = frag_b(s, 1, q - 8);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {  // B first: lane (r, g) accumulates C[m = r][n = 4g + e]
+        const int n = 4 * q + u, i = n >> 3, j = n & 7;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb0[j], fa0[i], acc[i][j], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(VMW));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    const unsigned char* Ns = smem + ((gs + kt + 1) % NST) * STAGE_BYTES;
-    const int ka = kt + NST;
+    const int ka = kt + 2;
     i32x4 rsa, rsb;
     int klim;
     if (ka < nk) {
-      rsa = tile_rsrc(a.A, a.lda, a.a_bytes, m0, ka * BK);
-      rsb = tile_rsrc(a.B, a.ldb, a.b_bytes, n0, ka * BK);
-      klim = a.K - ka * BK;
+      rsa = tile_rsrc(a.A, a.lda, a.a_bytes, m0, ka * PBK);
+      rsb = tile_rsrc(a.B, a.ldb, a.b_bytes, n0, ka * PBK);
+      klim = a.K - ka * PBK;
     } else if (vn < total) {
-      rsa = tile_rsrc(a.A, a.lda, a.a_bytes, m0n, (ka - nk) * BK);
-      rsb = tile_rsrc(a.B, a.ldb, a.b_bytes, n0n, (ka - nk) * BK);
-      klim = a.K - (ka - nk) * BK;
+      rsa = tile_rsrc(a.A, a.lda, a.a_bytes, m0n, (ka - nk) * PBK);
+      rsb = tile_rsrc(a.B, a.ldb, a.b_bytes, n0n, (ka - nk) * PBK);
+      klim = a.K - (ka - nk) * PBK;
     } else {
-      rsa = tile_rsrc(a.A, a.lda, a.a_bytes, m0, (nk - 1) * BK);
-      rsb = tile_rsrc(a.B, a.ldb, a.b_bytes, n0, (nk - 1) * BK);
-      klim = a.K - (nk - 1) * BK;
+      rsa = tile_rsrc(a.A, a.lda, a.a_bytes, m0, (nk - 1) * PBK);
+      rsb = tile_rsrc(a.B, a.ldb, a.b_bytes, n0, (nk - 1) * PBK);
+      klim = a.K - (nk - 1) * PBK;
     }
-    const int dstage = (gs + kt) % NST;
-    const int ln = tln, rr = ln & 15, gg = ln >> 4;
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
-      if (q < 8) na[q] = frag<true>(Ns, wm * 128 + 16 * q, rr, gg);
-      else nb[q - 8] = frag<true, true>(Ns + TILE_BYTES, bcol(q - 8), rr, gg);
-      if (q & 1) dma(rsa, rsb, dstage, q >> 1, ln, klim);
+      if (q < 8) fa0[q] = frag_a(s ^ 1, 0, q);
+      else fb0[q - 8] = frag_b(s ^ 1, 0, q - 8);
+      dma(rsa, rsb, s, q, klim);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int n = 4 * q + u, i = n >> 3, j = n & 7;
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cb[j], ca[i], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb1[j], fa1[i], acc[i][j], 0, 0, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  using W56 = std::integral_constant<int, std::min(63, 2 * DMA_PER_STEP + EPI_OPS)>;
-  using W16 = std::integral_constant<int, 2 * DMA_PER_STEP>;
-
   while (true) {
-    tln = opaque_lane();
-    step(W56{}, 0, fa0, fb0, fa1, fb1);
-    step(W56{}, 1, fa1, fb1, fa0, fb0);
-    step(W56{}, 2, fa0, fb0, fa1, fb1);
-    step(W16{}, 3, fa1, fb1, fa0, fb0);
-    for (int kt = 4; kt < nk; kt += 2) {
-      step(W16{}, kt, fa0, fb0, fa1, fb1);
-      step(W16{}, kt + 1, fa1, fb1, fa0, fb0);
-    }
+    step(std::integral_constant<int, 63>{}, 0);
+    for (int kt = 1; kt < nk; ++kt) step(std::integral_constant<int, 0>{}, kt);
     __builtin_amdgcn_sched_barrier(0);
-    bias_dma(vn < total ? n0n : n0, slot ^ 1);  // the next tile's bias, after the DMA of its 4th step
+    __builtin_amdgcn_s_waitcnt(wait_vm(0));  // the next tile's first two steps have landed: no store in flight yet
+    bias_dma(vn < total ? n0n : n0, slot ^ 1);  // the next tile's bias, after the DMA of its 2nd step
     // ---- epilogue: lane (r, g) holds C[m0 + wm*128 + 16i + r][n0 + wn*128 + 32p + 8g + e'],
     //      e' = 0..7 in acc[i][2p] (e' < 4) and acc[i][2p+1] (e' >= 4) ----
-    const int eln = opaque_lane(), er = eln & 15, eg = eln >> 4;
-    const int rowb = m0 + wm * 128 + er, colb = n0 + wn * 128 + 8 * eg;
+    const int rowb = m0 + wm * 128 + r, colb = n0 + wn * 128 + 8 * g;
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int col = colb + 32 * p;
-      const float* bl = &sbias[slot][wn * 128 + 32 * p + 8 * eg];
-      const float4 b0 = *reinterpret_cast<const float4*>(bl), b1 = *reinterpret_cast<const float4*>(bl + 4);
+    for (int i = 0; i < 8; ++i) {
+      const int row = rowb + 16 * i;
+      const uint16_t* rap[2] = {nullptr, nullptr};
+      float rsc[2] = {0.f, 0.f};
+      if constexpr (RA) {  // addend rows of this output row (rows past M are never stored)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int row = rowb + 16 * i;
-        const f32x4 u = acc[i][2 * p], w = acc[i][2 * p + 1];
-        const uint4 x = make_uint4(pack_bf16x2(u[0] + b0.x, u[1] + b0.y), pack_bf16x2(u[2] + b0.z, u[3] + b0.w),
-                                   pack_bf16x2(w[0] + b1.x, w[1] + b1.y), pack_bf16x2(w[2] + b1.z, w[3] + b1.w));
+        for (int q = 0; q < 2; ++q) {
+          if (!a.ra_ptr[q]) continue;
+          const int m = min(row, a.M - 1), T = a.ra_T[q], seg = a.ra_seg[q], t = m % T, sg = t / seg;
+          rsc[q] = a.ra_div[q] == LLATTN_DIV_COUNT ? 1.f / (float)(min((sg + 1) * seg, T) - sg * seg)
+                 : a.ra_div[q] == LLATTN_DIV_SEG ? 1.f / (float)seg : 1.f;
+          rap[q] = a.ra_ptr[q] + ((int64_t)(m / T) * a.ra_nseg[q] + sg) * a.ra_ld[q];
+        }
+      }
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const int col = colb + 32 * p;
+        const float* bl = &sbias[slot][wn * 128 + 32 * p + 8 * g];
+        const float4 b0 = *reinterpret_cast<const float4*>(bl), b1 = *reinterpret_cast<const float4*>(bl + 4);
+        // the accumulators leave the AGPRs here, eight at a time: left to the compiler, all 256 were copied
+        // out at the end of the main loop and the register peak pushed the loop's offsets into scratch
+        float u[4], w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(u[e]) : "a"(acc[i][2 * p][e]));
+          asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(w[e]) : "a"(acc[i][2 * p + 1][e]));
+        }
+        float v8[8] = {u[0] + b0.x, u[1] + b0.y, u[2] + b0.z, u[3] + b0.w,
+                       w[0] + b1.x, w[1] + b1.y, w[2] + b1.z, w[3] + b1.w};
+        if constexpr (RA) {  // addend rows are 8-byte aligned (two 8-byte loads per 8 columns)
+          const int cc = min(col, a.N - 8);  // columns past N are never stored
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            if (!a.ra_ptr[q]) continue;
+            float lo[4] = {v8[0], v8[1], v8[2], v8[3]}, hi[4] = {v8[4], v8[5], v8[6], v8[7]};
+            add_bf16x4(*reinterpret_cast<const uint2*>(rap[q] + cc), rsc[q], lo);
+            add_bf16x4(*reinterpret_cast<const uint2*>(rap[q] + cc + 4), rsc[q], hi);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v8[e] = lo[e];
+              v8[4 + e] = hi[e];
+            }
+          }
+        }
+        const uint4 x = make_uint4(pack_bf16x2(v8[0], v8[1]), pack_bf16x2(v8[2], v8[3]),
+                                   pack_bf16x2(v8[4], v8[5]), pack_bf16x2(v8[6], v8[7]));
         const uint32_t oc = (row < a.M && col < a.N)
                                 ? (CH ? heads_off(a.ch, (uint32_t)row, (uint32_t)col) : (uint32_t)((int64_t)row * a.ldc + col)) * 2u
                                 : kOffOOB;
         if constexpr (ACT == LLATTN_ACT_GELU) {
-          uint4 g, gp;
-          gelu_bf16x8(x, g, gp);
+          uint4 gl, gp;
+          gelu_bf16x8(x, gl, gp);
           const uint32_t oa = (row < a.M && col < a.N) ? (uint32_t)((int64_t)row * a.ld_aux + col) * 2u : kOffOOB;
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, g), rc, oc, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, gl), rc, oc, 0, 0);
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, gp), raux, oa, 0, 0);
         } else {
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, x), rc, oc, 0, 0);
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     if (vn >= total) break;
@@ -1117,6 +1180,8 @@ int small_split(const llattn_gemm_desc* d) {
 int resolve_split(const llattn_gemm_desc* d) {
   if (d->split_k > 0) return d->split_k;
   if (d->c_heads.T != 0) return 1;  // a split-head C comes from the persistent kernel
+  // so do row addends with a k-contiguous B (an input gradient through the transposed weight)
+  if (!d->a_trans && !d->b_trans && (d->rowadd[0].ptr || d->rowadd[1].ptr)) return 1;
   const int64_t tiles = (int64_t)((d->M + BM - 1) / BM) * ((d->N + BN - 1) / BN);
   if (tiles >= 224) return 1;
   const int64_t pairs = (d->K + 2 * BK - 1) / (2 * BK);
@@ -1188,9 +1253,8 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
   for (int q = 0; q < 2; ++q) {
     const llattn_gemm_rowadd& ra = d->rowadd[q];
     if (!ra.ptr) continue;
-    if (d->c_dtype != LLATTN_BF16 || !d->b_trans || d->a_trans)
-      return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: row addends need bf16 C and the input-gradient layout "
-                  "(a_trans = 0, b_trans = 1)");
+    if (d->c_dtype != LLATTN_BF16 || d->a_trans)
+      return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: row addends need bf16 C and a k-contiguous A (a_trans = 0)");
     if (ra.rows_per_seq <= 0 || d->M % ra.rows_per_seq || ra.seg <= 0 || ra.n_seg != (ra.rows_per_seq + ra.seg - 1) / ra.seg ||
         (ra.divisor != LLATTN_DIV_COUNT && ra.divisor != LLATTN_DIV_SEG && ra.divisor != LLATTN_DIV_ONE))
       return fail(LLATTN_ERR_SHAPE, "llattn_gemm: row addend %d: M=%d must be whole sequences of %d rows, n_seg=%d "
@@ -1252,8 +1316,10 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
     else launch_small<false, true>(a, d->c_dtype, st);
     return check_launch("llattn_gemm");
   }
-  // bf16 x Wᵀ (+ bias) without K split or accumulation: the persistent kernel, one workgroup per CU
+  // bf16 x Wᵀ (+ bias) (+ row addends) without K split or accumulation: the persistent kernel, one workgroup
+  // per CU
   const int64_t c_bytes = ((int64_t)(d->M - 1) * d->ldc + d->N) * 2;
+  const bool rowadd = d->rowadd[0].ptr || d->rowadd[1].ptr;
   if (!d->a_trans && !d->b_trans && S == 1 && d->c_dtype == LLATTN_BF16 && !d->accumulate && k_pairs >= 2 &&
       c_bytes < (int64_t(1) << 31)) {
     int dev = 0, cus = 256;
@@ -1264,11 +1330,16 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
       hipLaunchKernelGGL(gemm_persistent_kernel<LLATTN_ACT_GELU>, dim3(std::min(tiles, cus)), dim3(256), 0, st, a);
     else if (ch.T)
       hipLaunchKernelGGL((gemm_persistent_kernel<LLATTN_ACT_NONE, true>), dim3(std::min(tiles, cus)), dim3(256), 0, st, a);
+    else if (rowadd)
+      hipLaunchKernelGGL((gemm_persistent_kernel<LLATTN_ACT_NONE, false, true>), dim3(std::min(tiles, cus)), dim3(256), 0, st, a);
     else
       hipLaunchKernelGGL(gemm_persistent_kernel<LLATTN_ACT_NONE>, dim3(std::min(tiles, cus)), dim3(256), 0, st, a);
   } else if (ch.T) {
     return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: a split-head C of %lld bytes: the persistent kernel takes outputs "
                 "below 2 GiB", (long long)c_bytes);
+  } else if (rowadd && !d->b_trans) {
+    return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: row addends with a k-contiguous B need the persistent kernel "
+                "(no K split or accumulation, K > %d, C below 2 GiB)", 2 * BK);
   } else if (!d->a_trans && !d->b_trans) launch<true, true>(a, S, d->c_dtype, st);
   else if (!d->a_trans && d->b_trans) launch<true, false>(a, S, d->c_dtype, st);
   else if (d->a_trans && d->b_trans) launch<false, false>(a, S, d->c_dtype, st);

@@ -72,8 +72,9 @@ def _run(M: int, N: int, K: int, A: torch.Tensor, a_trans: bool, B: torch.Tensor
 
 
 def linear(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None, out: torch.Tensor | None = None,
-           accumulate: bool = False, heads=None) -> torch.Tensor:
-    """``x [M, K] @ w [N, K]^T (+ bias fp32 [N])`` -> bf16 ``[M, N]`` (``heads``: stored split-head)."""
+           accumulate: bool = False, heads=None, rowadd=()) -> torch.Tensor:
+    """``x [M, K] @ w [N, K]^T (+ bias fp32 [N])`` -> bf16 ``[M, N]`` (``heads``: stored split-head; ``rowadd``:
+    the broadcast row addends of :func:`matmul_nn`, on the persistent kernel only)."""
     _check2d("x", x)
     _check2d("w", w)
     M, K = x.shape
@@ -82,7 +83,7 @@ def linear(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None, o
         raise ValueError(f"x is [{M}, {K}] but w is {tuple(w.shape)}")
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
-    _run(M, N, K, x, False, w, False, out, bias, accumulate, c_heads=heads)
+    _run(M, N, K, x, False, w, False, out, bias, accumulate, c_heads=heads, rowadd=rowadd)
     return out
 
 
@@ -144,15 +145,19 @@ def transpose(w: torch.Tensor) -> torch.Tensor:
     return out
 
 
+# input gradients with row addends through the transposed weight and the persistent kernel (else matmul_nn)
+ROWADD_PERSISTENT = True
+
+
 def input_grad(dy: torch.Tensor, w: torch.Tensor, rowadd=()) -> torch.Tensor:
     """``dy [M, N] @ w [N, K]`` (+ the ``rowadd`` addends of :func:`matmul_nn`) -> bf16 ``[M, K]``, the input
-    gradient of ``y = x w^T``.  Without addends and for large M as ``dy (w^T)^T`` on the persistent kernel
-    with a transposed copy of ``w`` (both operands k-contiguous: plain LDS fragment reads, the epilogue
-    overlapped with the next tile); otherwise :func:`matmul_nn` (transposing fragment reads of ``w``)."""
+    gradient of ``y = x w^T``.  For large M as ``dy (w^T)^T`` on the persistent kernel with a transposed copy of
+    ``w`` (both operands k-contiguous: plain LDS fragment reads, the epilogue overlapped with the next tile);
+    otherwise :func:`matmul_nn` (transposing fragment reads of ``w``).  Both give the same bits."""
     M, N = dy.shape
     K = w.shape[1]
-    if not rowadd and M >= 4096 and K % 8 == 0 and N % 8 == 0 and N > 64:
-        return linear(dy, transpose(w))
+    if (not rowadd or ROWADD_PERSISTENT) and M >= 4096 and K % 8 == 0 and N % 8 == 0 and N > 64:
+        return linear(dy, transpose(w), rowadd=rowadd)
     return matmul_nn(dy, w, rowadd=rowadd)
 
 

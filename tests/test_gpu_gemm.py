@@ -389,6 +389,37 @@ def test_input_grad_through_transposed_weight(M, N, K):
     assert _err(gemm.input_grad(dy, w), dy.float() @ w.float()) < BF16_TOL
 
 
+@pytest.mark.parametrize("B,T,N,K,pools,bitwise", [
+    (16, 2048, 1408, 4736, [(128, 0)], True),          # config 2: the qkv input gradient with the latent pooling
+    (4, 2000, 520, 264, [(64, 0), (100, 1)], True),    # ragged segments, two addends, K with a 64-wide tail
+    (2, 4096, 136, 1024, [(512, 2)], False),           # 32 tiles: the tiled kernel splits K here
+])
+def test_input_grad_rowadd_persistent_equals_tiled(B, T, N, K, pools, bitwise):
+    """The input gradient with pooled-gradient row addends through the transposed weight and the persistent
+    kernel matches fp32 torch, and gives the same bits as the tiled kernel with transposing fragment reads
+    wherever that one does not split K (same k order, same epilogue arithmetic)."""
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: input grad rowadd persistent", B, T, N, K, pools, flush=True)
+    g = torch.Generator(device=dev).manual_seed(B * T + N + K)
+    dy, w = _rand(B * T, K, gen=g, dev=dev), _rand(K, N, gen=g, dev=dev)
+    ref = dy.float() @ w.float()
+    rowadd = []
+    t = torch.arange(T, device=dev)
+    for seg, div in pools:
+        n_seg = -(-T // seg)
+        rows = _rand(B * n_seg, N, gen=g, dev=dev) * 4
+        s_id = t // seg
+        count = torch.minimum((s_id + 1) * seg, torch.full_like(s_id, T)) - s_id * seg
+        scale = {0: 1.0 / count.float(), 1: torch.full((T,), 1.0 / seg, device=dev), 2: torch.ones(T, device=dev)}[div]
+        ref = ref + (rows.float().view(B, n_seg, N)[:, s_id] * scale[None, :, None]).reshape(B * T, N)
+        rowadd.append((rows, T, seg, n_seg, div))
+    got = gemm.input_grad(dy, w, rowadd=rowadd)
+    if bitwise:
+        assert torch.equal(got, gemm.matmul_nn(dy, w, rowadd=rowadd))
+    assert _err(got, ref) < BF16_TOL
+
+
 # ---- split-head operands (llattn_heads_layout): the q|k|v projection output stored as head slabs ----
 
 def _to_heads(x: torch.Tensor, T: int, dh: int, n: int) -> torch.Tensor:
