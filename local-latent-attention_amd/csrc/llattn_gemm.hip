@@ -11,16 +11,17 @@
 //
 // Tiling: a 256-thread workgroup (4 waves, 2 x 2) owns a 256 x 256 tile of C;
 // each wave owns 128 x 128 (64 accumulators of 16 x 16, v_mfma_f32_16x16x32_bf16,
-// held in AGPRs).  K advances in steps of 32 through four LDS stages of 32 KB.
+// held in AGPRs).  K advances in steps of 64 through two LDS stages of 64 KB.
 // Tiles move from HBM to LDS with buffer_load_dwordx4 ... lds (no register
-// staging); the loads of three steps are in flight while a step's 64 MFMAs per
-// wave run, and the next step's fragments are read from LDS meanwhile.
+// staging); a step's loads land while the previous step's 128 MFMAs per wave
+// run, and the next sub-step's fragments are read from LDS meanwhile.
 //
 // LDS layouts (XOR-swizzled at 16-byte granularity, bank-conflict free):
-//   k-contiguous tile  [256 rows][32 k]:  chunk c (8 k) of row r at c ^ ((r >> 1) & 3)
-//   mn-contiguous tile [32 k][256 cols]:  chunk c (8 cols) of k-row k at c ^ 2(k & 3)
+//   k-contiguous tile  [256 rows][64 k]:  chunk c (8 k) of row r at c ^ (r & 7) (A), or at
+//                                         c ^ ((r & 3) | (bit 3 of r at bit 2)) (permuted B reads)
+//   mn-contiguous tile [64 k][256 cols]:  chunk c (8 cols) of k-row k at c ^ 2(k & 3)
 // Operands of one MFMA: lane (r, g) (r = lane % 16, g = lane / 16) supplies
-// row r's eight k values 8g .. 8g+7 of the step -- one ds_read_b128 from a
+// row r's eight k values 8g .. 8g+7 of a 32-k sub-step -- one ds_read_b128 from a
 // k-contiguous tile, two ds_read_b64_tr_b16 from an mn-contiguous one.  Both
 // operands use the same k assignment, so the contraction is exact whichever
 // layout each comes from.
@@ -45,11 +46,7 @@
 namespace llattn {
 namespace gemm {
 
-constexpr int BM = 256, BN = 256, BK = 32, NST = 4;
-constexpr int TILE_BYTES = BM * BK * 2;        // 16 KB per operand per stage
-constexpr int STAGE_BYTES = 2 * TILE_BYTES;    // A + B
-constexpr int DMA_PER_TILE = TILE_BYTES / 1024 / 4;  // 1 KB blocks per wave per operand tile
-constexpr int DMA_PER_STEP = 2 * DMA_PER_TILE;       // per wave
+constexpr int BM = 256, BN = 256;  // output tile
 
 enum Epi { EPI_BF16 = 0, EPI_F32 = 1, EPI_PART = 2 };
 
@@ -181,45 +178,10 @@ __device__ __forceinline__ void dma_block(const i32x4& rs, uint32_t off, const u
 constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0070 | 0x0F00; }       // vmcnt(n)
 constexpr int wait_vm_lgkm0(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0070; }        // vmcnt(n) lgkmcnt(0)
 
-// Byte offsets (relative to the operand base at k = 0) of this lane's 16-byte
-// chunk in each of the wave's blocks of an operand tile (rows/cols
-// [o0, o0+256)).  Rows (k-contiguous) or columns (mn-contiguous) past `omax`
-// are clamped to a valid address; the outputs they feed are never stored.
-// k-contiguous tiles: chunk c of row `row` sits at c ^ swz(row).  PERM selects the swizzle of the
-// B operand whose fragments read rows in the permuted order of frag<KMAJ, true> (conflict-free for it).
-template <bool PERM>
-__device__ __forceinline__ int kswz(int row) {
-  return PERM ? (((row >> 1) & 1) | (((row >> 3) & 1) << 1)) : ((row >> 1) & 3);
-}
-
 // An offset past every operand extent (operands are below 4 GiB - 16 bytes): the lane reads zero.
 constexpr uint32_t kOffPastK = 0xFFFFFFF0u;
-// First k (0, 8, 16 or 24) of the 16-byte chunk that lane `lane` moves in every DMA block of a
-// k-contiguous tile: the swizzle depends on the row only through bits that equal those of lane / 4.
-template <bool PERM>
-__device__ __forceinline__ int lane_k0(int lane) { return 8 * ((lane & 3) ^ kswz<PERM>(lane >> 2)); }
-// A k-contiguous lane's offset for a step whose K tail starts `klim` elements in (klim >= BK: no tail).
+// A k-contiguous lane's offset for a step whose K tail starts `klim` elements in, its chunk starting at kc.
 __device__ __forceinline__ uint32_t kmask(uint32_t off, int kc, int klim) { return kc < klim ? off : kOffPastK; }
-
-template <bool KMAJ, bool PERM = false>
-__device__ __forceinline__ void tile_offsets(uint32_t (&off)[DMA_PER_TILE], int64_t ld, int o0, int omax, int wave,
-                                             int lane) {
-#pragma unroll
-  for (int i = 0; i < DMA_PER_TILE; ++i) {
-    const int bi = wave * DMA_PER_TILE + i;
-    if constexpr (KMAJ) {  // block bi = rows 16bi .. 16bi+15, 4 chunks each
-      const int row = 16 * bi + (lane >> 2);
-      const int c = (lane & 3) ^ kswz<PERM>(row);
-      const int gr = min(o0 + row, omax - 1);
-      off[i] = (uint32_t)(((int64_t)gr * ld + 8 * c) * 2);
-    } else {  // block bi = k-rows 2bi, 2bi+1, 32 chunks each
-      const int k = 2 * bi + (lane >> 5);
-      const int c = (lane & 31) ^ (2 * (k & 3));
-      const int col = min(o0 + 8 * c, omax - 8);
-      off[i] = (uint32_t)(((int64_t)k * ld + col) * 2);
-    }
-  }
-}
 
 // Buffer descriptor of an operand from step k0 on (`bytes`: storage extent of the operand).
 template <bool KMAJ>
@@ -231,38 +193,86 @@ __device__ __forceinline__ i32x4 step_rsrc(const uint16_t* base, int64_t ld, int
   return i32x4{(int)(uint32_t)addr, (int)((addr >> 32) & 0xffff), (int)(uint32_t)ext, kRsrcWord3};
 }
 
-// 8 k values (8g .. 8g+7 of the step) of tile row/column o16 + r for lane (r, g).  PERM (k-contiguous
-// B only): lane r reads row o16 + 8(r/4) + r%4 instead, so that with o16 = 32p + 4u the output
-// columns a lane accumulates for the block pair (u = 0, 1) are 8 consecutive ones, 32p + 8g + 0..7.
+// 64-k LDS stages (two of 64 KB), shared by gemm_kernel and the persistent kernel.  k-contiguous tiles:
+// 256 rows of 128 bytes, 16-byte chunk c of row r at slot c ^ pswz(r) (A fragments read rows o16 + r, eight
+// consecutive rows per LDS cycle -> r & 7; permuted B fragments read rows o16 + 8 (r / 4) + r % 4 ->
+// (r & 3) | (bit 3 of the row at bit 2); both conflict-free).  mn-contiguous tiles: 64 k-rows of 512 bytes,
+// chunk c of k-row k at c ^ 2 (k & 3) (transposing reads, conflict-free).
+constexpr int PBK = 64;                  // k per LDS stage
+constexpr int PTILE = BM * PBK * 2;      // 32 KB per operand per stage
+constexpr int PSTAGE = 2 * PTILE;        // A then B
+constexpr int PDMA = PTILE / 1024 / 4;   // 1 KB DMA blocks per wave per operand and step (8)
+
+template <bool PERM>
+__device__ __forceinline__ int pswz(int row) {
+  return PERM ? ((row & 3) | (((row >> 3) & 1) << 2)) : (row & 7);
+}
+
+// Byte offsets (relative to the operand base at the step's first k) of this lane's 16-byte chunk in each
+// of the wave's 8 DMA blocks of a 64-k operand tile (rows / columns [o0, o0 + 256)).  k-contiguous: block i
+// = rows 8 (8 wave + i) .. + 7, lane -> row + lane / 8, LDS slot lane % 8 receives the row's chunk
+// (lane % 8) ^ pswz(row); rows past omax are clamped to a valid row (their outputs are never stored).
+// mn-contiguous: block i = k-rows 2 (8 wave + i) + lane / 32, 32 chunks each; columns clamped likewise.
+// kc: first k of the lane's chunk (k-contiguous K tail; mn-contiguous rows past K lie beyond the extent).
 template <bool KMAJ, bool PERM = false>
-__device__ __forceinline__ bf16x8 frag(const unsigned char* tile, int o16, int r, int g) {
+__device__ __forceinline__ void tile_offsets64(uint32_t (&off)[PDMA], int (&kc)[PDMA], int64_t ld, int o0, int omax,
+                                               int wave, int lane) {
+#pragma unroll
+  for (int i = 0; i < PDMA; ++i) {
+    const int bi = wave * PDMA + i;
+    if constexpr (KMAJ) {
+      const int row = 8 * bi + (lane >> 3);
+      const int c = (lane & 7) ^ pswz<PERM>(row);
+      off[i] = (uint32_t)(((int64_t)min(o0 + row, omax - 1) * ld + 8 * c) * 2);
+      kc[i] = 8 * c;
+    } else {
+      const int k = 2 * bi + (lane >> 5);
+      const int c = (lane & 31) ^ (2 * (k & 3));
+      off[i] = (uint32_t)(((int64_t)k * ld + min(o0 + 8 * c, omax - 8)) * 2);
+      kc[i] = 0;
+    }
+  }
+}
+
+// 8 k values (32h + 8g .. + 7 of a 64-k stage) of tile row / column o16 + r for lane (r, g).  PERM
+// (k-contiguous B only): lane r reads row o16 + 8 (r / 4) + r % 4 instead, so that with o16 = 32p + 4u the
+// output columns a lane accumulates for the block pair (u = 0, 1) are 8 consecutive ones.
+template <bool KMAJ, bool PERM = false>
+__device__ __forceinline__ bf16x8 frag64(const unsigned char* tile, int o16, int r, int g, int h) {
   if constexpr (KMAJ) {
     const int row = PERM ? o16 + 8 * (r >> 2) + (r & 3) : o16 + r;
-    return *reinterpret_cast<const bf16x8*>(tile + row * 64 + ((g ^ kswz<PERM>(row)) << 4));
+    return *reinterpret_cast<const bf16x8*>(tile + row * 128 + (((4 * h + g) ^ pswz<PERM>(row)) << 4));
   } else {
-    // transposing reads: the 16 lanes of group g supply rows kb + j/4, 8 bytes at
-    // column o16 + 4(j%4); lane r receives column o16 + r of those four rows
-    const int kb = 8 * g;
+    // transposing reads: the 16 lanes of group g supply k-rows kb + j/4, 8 bytes at column o16 + 4(j%4);
+    // lane r receives column o16 + r of those four rows
+    const int kb = 32 * h + 8 * g;
     const int col = o16 + 4 * (r & 3), chunk = col >> 3, inner = (col & 7) << 1;
-    bf16x4 h[2];
+    bf16x4 hv[2];
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       const int k = kb + 4 * half + (r >> 2);
       const unsigned char* p = tile + k * 512 + ((chunk ^ (2 * (k & 3))) << 4) + inner;
-      h[half] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)(p));
+      hv[half] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)(p));
     }
-    return bf16x8{h[0][0], h[0][1], h[0][2], h[0][3], h[1][0], h[1][1], h[1][2], h[1][3]};
+    return bf16x8{hv[0][0], hv[0][1], hv[0][2], hv[0][3], hv[1][0], hv[1][1], hv[1][2], hv[1][3]};
   }
 }
 
 // RS: row sums of A for an N with no spare column (a multiple of 256): every lane adds the 8 k values of each of
-// its A fragments into one fp32 sum per fragment block (v_dot2 against a pair of ones, 32 per step, beside the
-// 64 products), and the waves that own the left half of the first tile column store them.
+// its A fragments into one fp32 sum per fragment block (v_dot2 against a pair of ones, 32 per 32-k sub-step,
+// beside the 64 products), and the waves that own the left half of the first tile column store them.
+//
+// Pipeline (as the persistent kernel's, one tile per workgroup): step kt (64 k) lives in stage kt % 2;
+//   sub-step 0: 64 MFMAs on k 0..31, with the fragment reads of k 32..63;
+//   wait for this wave's DMA of step kt + 1 (the youngest load: vmcnt(0)) and its reads; barrier;
+//   sub-step 1: 64 MFMAs on k 32..63, with the fragment reads of step kt + 1's k 0..31 and the DMA of step
+//               kt + 2 into this step's stage (past the last step: the last step again, never read).
+// No stores are in flight before the epilogue, so the waits are exact.
 template <bool AK, bool BKM, int EPI, bool RS = false>
 __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
   // bf16 output from a k-contiguous B: permuted B fragments, so each lane writes 16-byte rows directly
   constexpr bool PB = BKM && EPI == EPI_BF16;
-  __shared__ __align__(1024) unsigned char smem[NST * STAGE_BYTES];
+  __shared__ __align__(1024) unsigned char smem[2 * PSTAGE];
   const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
@@ -279,7 +289,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
   const int m0 = tm * BM, n0 = tn * BN;
   // split s takes 64-wide steps [s P / S, (s+1) P / S): uneven by at most one step
   const int p0 = split * a.k_pairs / a.n_split, p1 = (split + 1) * a.k_pairs / a.n_split;
-  const int kbeg = p0 * 2 * BK, nk = 2 * (p1 - p0);
+  const int kbeg = p0 * PBK, nk = p1 - p0;
 
   f32x4 acc[8][8];
 #pragma unroll
@@ -289,9 +299,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
 
   // first B row / column of fragment block j (PB: block pairs interleave in groups of four)
   auto bcol = [&](int j) { return PB ? wn * 128 + 32 * (j >> 1) + 4 * (j & 1) : wn * 128 + 16 * j; };
-  uint32_t offa[DMA_PER_TILE], offb[DMA_PER_TILE];
-  tile_offsets<AK>(offa, a.lda, m0, a.M, wave, lane);
-  tile_offsets<BKM, PB>(offb, a.ldb, n0, a.N, wave, lane);
+  uint32_t offa[PDMA], offb[PDMA];
+  int kca[PDMA], kcb[PDMA];
+  tile_offsets64<AK>(offa, kca, a.lda, m0, a.M, wave, lane);
+  tile_offsets64<BKM, PB>(offb, kcb, a.ldb, n0, a.N, wave, lane);
   // Row sums of A: column N of the product (never stored as C) contracts against ones.  It lies in
   // B fragment block `jones` (wave-uniform; -1: not in this wave's columns) at lane r == rones.
   const int nrel = a.N - n0 - wn * 128;
@@ -304,59 +315,38 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
     }
   };
   const bool rs_wave = RS && tn == 0 && wn == 0;  // wave-uniform
-  float rsum[8];  // RS: lane (r, g)'s part (k = 8g .. 8g+7 of each step) of sum_k A(m0 + wm*128 + 16i + r, k)
+  float rsum[8];  // RS: lane (r, g)'s part (k = 8g .. 8g+7 of each sub-step) of sum_k A(m0 + wm*128 + 16i + r, k)
 #pragma unroll
   for (int i = 0; i < 8; ++i) rsum[i] = 0.f;
-  // DMA of this wave's block q (0..3: operand A, 4..7: operand B) of a step into `stage`; klim = K - k0 of
-  // the step (wave-uniform): below BK, k-contiguous lanes from klim on read zero
-  const int kca = lane_k0<false>(lane), kcb = lane_k0<PB>(lane);
+  // DMA of this wave's block q (0..7: operand A, 8..15: operand B) of a step into `stage`; klim = K - k0 of
+  // the step (wave-uniform): below PBK, k-contiguous lanes whose chunk starts at or past K read zero
   auto dma = [&](const i32x4& rsa, const i32x4& rsb, int stage, int q, int klim) {
-    unsigned char* st = smem + stage * STAGE_BYTES;
-    if (q < DMA_PER_TILE) {
-      const uint32_t o = (AK && klim < BK) ? kmask(offa[q], kca, klim) : offa[q];
-      dma_block(rsa, o, st + (wave * DMA_PER_TILE + q) * 1024);
+    unsigned char* st = smem + stage * PSTAGE;
+    if (q < PDMA) {
+      const uint32_t o = (AK && klim < PBK) ? kmask(offa[q], kca[q], klim) : offa[q];
+      dma_block(rsa, o, st + (wave * PDMA + q) * 1024);
     } else {
-      const uint32_t o = (BKM && klim < BK) ? kmask(offb[q - DMA_PER_TILE], kcb, klim) : offb[q - DMA_PER_TILE];
-      dma_block(rsb, o, st + TILE_BYTES + (wave * DMA_PER_TILE + q - DMA_PER_TILE) * 1024);
+      const int qb = q - PDMA;
+      const uint32_t o = (BKM && klim < PBK) ? kmask(offb[qb], kcb[qb], klim) : offb[qb];
+      dma_block(rsb, o, st + PTILE + (wave * PDMA + qb) * 1024);
     }
   };
   auto step_rsrcs = [&](int kt, i32x4& rsa, i32x4& rsb) {
-    const int k0 = kbeg + kt * BK;
+    const int k0 = kbeg + kt * PBK;
     rsa = step_rsrc<AK>(a.A, a.lda, a.a_bytes, k0);
     rsb = step_rsrc<BKM>(a.B, a.ldb, a.b_bytes, k0);
   };
-
-  // Pipeline over NST = 4 stages, one barrier per 32-k step.  Iteration kt:
-  //   wait until this wave's fragment reads of step kt and its DMA of step kt+1
-  //   are done; barrier (now every wave's DMA of step kt+1 has landed and no
-  //   wave reads stage kt%4 any more); then step kt's 64 MFMAs per wave, with
-  //   the 16 fragment reads of step kt+1 and the 8 DMA blocks of step kt+4 (into
-  //   stage kt%4) interleaved between them so that the LDS and address queues
-  //   drain while the MFMA pipe stays busy.
-  // Every iteration issues exactly one step of DMA (past the last step it
-  // reloads the last step into the free stage, which is never read again), so
-  // "step kt+1 landed" is always vmcnt <= 2 steps: vmcnt counts this wave's
-  // loads in issue order.  s_barrier is used without a fence: a fence would
-  // also wait for the DMA that is meant to stay in flight.
-  bf16x8 fa0[8], fb0[8], fa1[8], fb1[8];
-  auto step = [&](int kt, const bf16x8 (&ca)[8], const bf16x8 (&cb)[8], bf16x8 (&na)[8], bf16x8 (&nb)[8]) {
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(2 * DMA_PER_STEP));
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    const unsigned char* Ns = smem + ((kt + 1) % NST) * STAGE_BYTES;  // past the last step: unused data
-    i32x4 rsa, rsb;
-    const int kd = min(kt + NST, nk - 1), klim = a.K - (kbeg + kd * BK);
-    step_rsrcs(kd, rsa, rsb);
+  auto frag_a = [&](int stage, int h, int i) { return frag64<AK>(smem + stage * PSTAGE, wm * 128 + 16 * i, r, g, h); };
+  auto frag_b = [&](int stage, int h, int j) {
+    bf16x8 f = frag64<BKM, PB>(smem + stage * PSTAGE + PTILE, bcol(j), r, g, h);
+    if (!PB) ones_fix(f, j);
+    return f;
+  };
+  // 64 MFMAs of a sub-step on (ca, cb), the row sums of ca (RS), and per q the reads / DMA `io(q)`
+  auto sub = [&](const bf16x8 (&ca)[8], const bf16x8 (&cb)[8], auto io) {
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
-      if (q < 8) {
-        na[q] = frag<AK>(Ns, wm * 128 + 16 * q, r, g);
-      } else {
-        nb[q - 8] = frag<BKM, PB>(Ns + TILE_BYTES, bcol(q - 8), r, g);
-        if (!PB) ones_fix(nb[q - 8], q - 8);
-      }
-      if (q & 1) dma(rsa, rsb, kt % NST, q >> 1, klim);
+      io(q);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {  // B first: lane (r, g) accumulates C[m = r][n = 4g + e]
         const int n = 4 * q + u, i = n >> 3, j = n & 7;
@@ -377,25 +367,38 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
   };
 
 #pragma unroll
-  for (int s = 0; s < NST; ++s) {
+  for (int s = 0; s < 2; ++s) {
     i32x4 rsa, rsb;
-    const int kd = min(s, nk - 1), klim = a.K - (kbeg + kd * BK);
+    const int kd = min(s, nk - 1);
     step_rsrcs(kd, rsa, rsb);
 #pragma unroll
-    for (int q = 0; q < DMA_PER_STEP; ++q) dma(rsa, rsb, s, q, klim);
+    for (int q = 0; q < 2 * PDMA; ++q) dma(rsa, rsb, s, q, a.K - (kbeg + kd * PBK));
   }
-  __builtin_amdgcn_s_waitcnt(wait_vm((NST - 1) * DMA_PER_STEP));
+  __builtin_amdgcn_s_waitcnt(wait_vm(2 * PDMA));  // loads complete in issue order: step 0 has landed
   __builtin_amdgcn_s_barrier();
+  bf16x8 fa0[8], fb0[8], fa1[8], fb1[8];  // k 0..31 and 32..63 of a step
 #pragma unroll
-  for (int i = 0; i < 8; ++i) fa0[i] = frag<AK>(smem, wm * 128 + 16 * i, r, g);
+  for (int i = 0; i < 8; ++i) fa0[i] = frag_a(0, 0, i);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    fb0[j] = frag<BKM, PB>(smem + TILE_BYTES, bcol(j), r, g);
-    if (!PB) ones_fix(fb0[j], j);
-  }
-  for (int kt = 0; kt < nk; kt += 2) {  // nk is even; fragment buffers alternate between steps
-    step(kt, fa0, fb0, fa1, fb1);
-    step(kt + 1, fa1, fb1, fa0, fb0);
+  for (int j = 0; j < 8; ++j) fb0[j] = frag_b(0, 0, j);
+  for (int kt = 0; kt < nk; ++kt) {
+    const int s = kt & 1;
+    __builtin_amdgcn_sched_barrier(0);
+    sub(fa0, fb0, [&](int q) {
+      if (q < 8) fa1[q] = frag_a(s, 1, q);
+      else fb1[q - 8] = frag_b(s, 1, q - 8);
+    });
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    i32x4 rsa, rsb;
+    const int kd = min(kt + 2, nk - 1), klim = a.K - (kbeg + kd * PBK);
+    step_rsrcs(kd, rsa, rsb);
+    sub(fa1, fb1, [&](int q) {
+      if (q < 8) fa0[q] = frag_a(s ^ 1, 0, q);
+      else fb0[q - 8] = frag_b(s ^ 1, 0, q - 8);
+      dma(rsa, rsb, s, q, klim);
+    });
   }
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));  // no DMA may land after the workgroup exits
@@ -599,19 +602,6 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
 // all its DMA (the next tile's steps 0 and 1) before the epilogue issues its stores; the next tile's first
 // barrier then waits for nothing in vmcnt, and every later barrier waits for vmcnt(0), the youngest
 // load being the DMA it publishes (the stores have had a step to drain by then).
-constexpr int PBK = 64;                  // k per LDS stage
-constexpr int PTILE = BM * PBK * 2;      // 32 KB per operand per stage
-constexpr int PSTAGE = 2 * PTILE;        // A then B
-constexpr int PDMA = PTILE / 1024 / 4;   // 1 KB DMA blocks per wave per operand and step (8)
-
-// 128-byte LDS rows: 16-byte chunk c of row r sits at slot c ^ pswz(r).  A fragments read rows o16 + r,
-// eight consecutive rows per LDS cycle -> r & 7.  B fragments read the permuted rows o16 + 8 (r / 4) + r % 4
-// -> (r & 3) | (bit 3 of the row at bit 2).  Both conflict-free.
-template <bool PERM>
-__device__ __forceinline__ int pswz(int row) {
-  return PERM ? ((row & 3) | (((row >> 3) & 1) << 2)) : (row & 7);
-}
-
 // Buffer descriptor of a k-contiguous operand from row o0 and k0 on.  Rows past the operand read zero
 // (their offsets are past `bytes`); they only feed outputs that are never stored.
 __device__ __forceinline__ i32x4 tile_rsrc(const uint16_t* base, int64_t ld, int64_t bytes, int o0, int k0) {
@@ -1184,9 +1174,9 @@ int resolve_split(const llattn_gemm_desc* d) {
   if (!d->a_trans && !d->b_trans && (d->rowadd[0].ptr || d->rowadd[1].ptr)) return 1;
   const int64_t tiles = (int64_t)((d->M + BM - 1) / BM) * ((d->N + BN - 1) / BN);
   if (tiles >= 224) return 1;
-  const int64_t pairs = (d->K + 2 * BK - 1) / (2 * BK);
+  const int64_t pairs = (d->K + PBK - 1) / PBK;
   const int64_t smax = std::max<int64_t>(1, pairs / 4);
-  const double t_tile = 2.0 * BM * BN * (double)pairs * (2 * BK) / 4.4e12;  // seconds per whole tile
+  const double t_tile = 2.0 * BM * BN * (double)pairs * PBK / 4.4e12;  // seconds per whole tile
   int best = 1;
   double best_t = 1e30;
   for (int64_t S = 1; S <= std::min<int64_t>(smax, 64); ++S) {
@@ -1223,13 +1213,13 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
   if (d->c_dtype != LLATTN_BF16 && d->c_dtype != LLATTN_F32)
     return fail(LLATTN_ERR_DTYPE, "llattn_gemm: unknown output dtype %d", d->c_dtype);
   const int S = resolve_split(d);
-  const int k_pairs = (d->K + 2 * BK - 1) / (2 * BK);
+  const int k_pairs = (d->K + PBK - 1) / PBK;
   if ((!d->a_trans || !d->b_trans) && d->K % 8 != 0)
     return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: K=%d must be a multiple of 8 when an operand is k-contiguous",
                 d->K);
   if (S < 1 || S > k_pairs)
     return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: %d K splits for K=%d: at most one per %d-wide k step", S, d->K,
-                2 * BK);
+                PBK);
   if (d->N % 8 != 0 || (d->a_trans && d->M % 8 != 0))
     return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: N (and M of a transposed A) must be multiples of 8 (M=%d N=%d)",
                 d->M, d->N);
@@ -1280,7 +1270,7 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
   if (ch.T && (d->a_trans || d->b_trans || d->c_dtype != LLATTN_BF16 || d->accumulate || d->act != LLATTN_ACT_NONE ||
                d->rowadd[0].ptr || d->rowadd[1].ptr || S != 1 || k_pairs < 2))
     return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: a split-head C needs a_trans = b_trans = 0, bf16 C, no "
-                "accumulation, activation, row addends or K split, and K > %d", 2 * BK);
+                "accumulation, activation, row addends or K split, and K > %d", PBK);
   const size_t need = llattn_gemm_workspace_size(d);
   if (need && (!workspace || workspace_bytes < need || !aligned16(workspace)))
     return fail(LLATTN_ERR_WORKSPACE, "llattn_gemm: %d K splits need %zu workspace bytes (got %zu)",
@@ -1339,7 +1329,7 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
                 "below 2 GiB", (long long)c_bytes);
   } else if (rowadd && !d->b_trans) {
     return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: row addends with a k-contiguous B need the persistent kernel "
-                "(no K split or accumulation, K > %d, C below 2 GiB)", 2 * BK);
+                "(no K split or accumulation, K > %d, C below 2 GiB)", PBK);
   } else if (!d->a_trans && !d->b_trans) launch<true, true>(a, S, d->c_dtype, st);
   else if (!d->a_trans && d->b_trans) launch<true, false>(a, S, d->c_dtype, st);
   else if (d->a_trans && d->b_trans) launch<false, false>(a, S, d->c_dtype, st);
