@@ -305,8 +305,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
   tile_offsets64<BKM, PB>(offb, kcb, a.ldb, n0, a.N, wave, lane);
   // Row sums of A: column N of the product (never stored as C) contracts against ones.  It lies in
   // B fragment block `jones` (wave-uniform; -1: not in this wave's columns) at lane r == rones.
+  // Only the waves whose columns hold N run the main loop with the substitution (a wave-uniform branch
+  // around the whole loop): in the others no select waits for a fragment read in the sub-step that
+  // issues it.
   const int nrel = a.N - n0 - wn * 128;
-  const int jones = (!PB && a.rowsum && nrel >= 0 && nrel < 128) ? (nrel >> 4) : -1;
+  const int jones = __builtin_amdgcn_readfirstlane((!PB && a.rowsum && nrel >= 0 && nrel < 128) ? (nrel >> 4) : -1);
   const bool lane_ones = (r == (nrel & 15));
   auto ones_fix = [&](bf16x8& f, int j) {
     if (j == jones && lane_ones) {
@@ -337,9 +340,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
     rsb = step_rsrc<BKM>(a.B, a.ldb, a.b_bytes, k0);
   };
   auto frag_a = [&](int stage, int h, int i) { return frag64<AK>(smem + stage * PSTAGE, wm * 128 + 16 * i, r, g, h); };
-  auto frag_b = [&](int stage, int h, int j) {
+  auto frag_b = [&](auto ones, int stage, int h, int j) {
     bf16x8 f = frag64<BKM, PB>(smem + stage * PSTAGE + PTILE, bcol(j), r, g, h);
-    if (!PB) ones_fix(f, j);
+    if constexpr (decltype(ones)::value) ones_fix(f, j);
     return f;
   };
   // 64 MFMAs of a sub-step on (ca, cb), the row sums of ca (RS), and per q the reads / DMA `io(q)`
@@ -377,29 +380,33 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
   __builtin_amdgcn_s_waitcnt(wait_vm(2 * PDMA));  // loads complete in issue order: step 0 has landed
   __builtin_amdgcn_s_barrier();
   bf16x8 fa0[8], fb0[8], fa1[8], fb1[8];  // k 0..31 and 32..63 of a step
+  auto main_loop = [&](auto ones) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) fa0[i] = frag_a(0, 0, i);
+    for (int i = 0; i < 8; ++i) fa0[i] = frag_a(0, 0, i);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) fb0[j] = frag_b(0, 0, j);
-  for (int kt = 0; kt < nk; ++kt) {
-    const int s = kt & 1;
-    __builtin_amdgcn_sched_barrier(0);
-    sub(fa0, fb0, [&](int q) {
-      if (q < 8) fa1[q] = frag_a(s, 1, q);
-      else fb1[q - 8] = frag_b(s, 1, q - 8);
-    });
-    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    i32x4 rsa, rsb;
-    const int kd = min(kt + 2, nk - 1), klim = a.K - (kbeg + kd * PBK);
-    step_rsrcs(kd, rsa, rsb);
-    sub(fa1, fb1, [&](int q) {
-      if (q < 8) fa0[q] = frag_a(s ^ 1, 0, q);
-      else fb0[q - 8] = frag_b(s ^ 1, 0, q - 8);
-      dma(rsa, rsb, s, q, klim);
-    });
-  }
+    for (int j = 0; j < 8; ++j) fb0[j] = frag_b(ones, 0, 0, j);
+    for (int kt = 0; kt < nk; ++kt) {
+      const int s = kt & 1;
+      __builtin_amdgcn_sched_barrier(0);
+      sub(fa0, fb0, [&](int q) {
+        if (q < 8) fa1[q] = frag_a(s, 1, q);
+        else fb1[q - 8] = frag_b(ones, s, 1, q - 8);
+      });
+      __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      i32x4 rsa, rsb;
+      const int kd = min(kt + 2, nk - 1), klim = a.K - (kbeg + kd * PBK);
+      step_rsrcs(kd, rsa, rsb);
+      sub(fa1, fb1, [&](int q) {
+        if (q < 8) fa0[q] = frag_a(s ^ 1, 0, q);
+        else fb0[q - 8] = frag_b(ones, s ^ 1, 0, q - 8);
+        dma(rsa, rsb, s, q, klim);
+      });
+    }
+  };
+  if (jones >= 0) main_loop(std::true_type{});
+  else main_loop(std::false_type{});
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));  // no DMA may land after the workgroup exits
 
