@@ -161,10 +161,12 @@ int32_t llattn_local_gate_bwd(const llattn_shape* s, const llattn_tensor* q, con
  * forbid hipMalloc): llattn_local_gate_bwd with the same arguments and
  * results, minus the workspace.  Its scratch is a library-owned device array
  * of LLATTN_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends): the
- * gate partial sums, H*3*Dh*rows fp32 (rows = B * query segments for the
- * fused bf16 backward, W <= 64; B * ceil(T/64) otherwise), plus dO_local and
- * D (B*T*H*Dh elements, B*H*T fp32) for the two-kernel backward.  A shape
- * that needs more returns LLATTN_ERR_WORKSPACE.  Calls share their GPU's
+ * gate partial sums, H*3*Dh*rows fp32, where rows = B * query segments for the
+ * fused bf16 backward (W <= 64), B * ceil(T/128) for the bf16 wide-window
+ * backward (W > 64, head dims up to 128) and B * ceil(T/64) otherwise; every
+ * two-kernel path (all but the fused one) also holds dO_local and D there
+ * (B*T*H*Dh elements, B*H*T fp32).  A shape that needs more returns
+ * LLATTN_ERR_WORKSPACE.  Calls share their GPU's
  * array, so two calls that overlap on one GPU (different streams, threads or
  * processes) race; calls on one stream are ordered.  Allocates nothing. */
 #define LLATTN_NOALLOC_SCRATCH_BYTES (8u << 20)

@@ -42,13 +42,15 @@ class _FeedForward(torch.autograd.Function):
             g, gp = gemm.linear_gelu(x2, w1b, _bias(b1))
             y = gemm.linear(g, w2b, _bias(b2))
         ctx.save_for_backward(x2, gp, g, w1b, w2b)
-        ctx.meta = (lead, x.dtype, w1.dtype, w2.dtype, b1 is not None, b2 is not None)
+        ctx.meta = (lead, x.dtype, w1.dtype, w2.dtype, None if b1 is None else b1.dtype,
+                    None if b2 is None else b2.dtype)
         return y.view(*lead, w2.shape[0])
 
     @staticmethod
     def backward(ctx, dy):
         x2, gp, g, w1b, w2b = ctx.saved_tensors
-        lead, xdt, w1dt, w2dt, has_b1, has_b2 = ctx.meta
+        lead, xdt, w1dt, w2dt, b1dt, b2dt = ctx.meta
+        has_b1, has_b2 = b1dt is not None, b2dt is not None
         with torch.autocast(device_type="cuda", enabled=False):
             dy2 = dy.reshape(-1, dy.shape[-1]).to(BF16)
             if not dy2.is_contiguous():
@@ -58,7 +60,7 @@ class _FeedForward(torch.autograd.Function):
             dx = gemm.input_grad(dh, w1b) if ctx.needs_input_grad[0] else None
             dw1, db1 = weight_grad(dh, x2, has_b1)
         return (None if dx is None else dx.view(*lead, x2.shape[1]).to(xdt), dw1.to(w1dt),
-                None if db1 is None else db1.to(w1dt), dw2.to(w2dt), None if db2 is None else db2.to(w2dt))
+                None if db1 is None else db1.to(b1dt), dw2.to(w2dt), None if db2 is None else db2.to(b2dt))
 
 
 def feed_forward(x: torch.Tensor, w1: torch.nn.Linear, w2: torch.nn.Linear) -> torch.Tensor:

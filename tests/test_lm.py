@@ -216,6 +216,69 @@ def test_c5_full_size_step_against_reference_path_loss():
     assert abs(loss0 - loss_ref) < 2e-2
 
 
+@pytest.mark.gpu
+def test_checkpointed_blocks_give_the_same_bits():
+    """Activation checkpointing (reference models.py:571-572, the trainer's --checkpoint-blocks, train.py:136): a
+    small LocalLatentLM with checkpoint_blocks=True re-runs each HIP block's forward in the backward.  The block's
+    forward is pure and deterministic, so one bf16 training step gives the loss and every parameter gradient of
+    the same model and tokens without checkpointing, bit for bit (the unfused residual norms that checkpointing
+    selects give the same bits as the fused ones)."""
+    from gpu_helpers import require_cuda
+    from llattn_amd.lm import build_model
+    dev = require_cuda()
+    kw = dict(vocab_size=384, max_seq_len=512, d_model=256, n_heads=4, n_layers=3, d_ff=512, local_window=64,
+              local_block_size=128, latent_tokens=8, latent_d_model=128, latent_heads=2)
+    g = torch.Generator(device=dev).manual_seed(11)
+    tokens = torch.randint(0, kw["vocab_size"], (2, 385), device=dev, generator=g)
+    inputs, targets = tokens[:, :-1], tokens[:, 1:]
+    results = []
+    for ckpt in (False, True):
+        torch.manual_seed(0)
+        model = build_model(checkpoint_blocks=ckpt, **kw).to(dev)
+        model.train()
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+            loss, _ = model.loss(inputs, targets)
+            loss.backward()
+        results.append((loss.detach().clone(), {n: p.grad.detach().clone() for n, p in model.named_parameters()}))
+    (l0, g0), (l1, g1) = results
+    assert torch.equal(l0, l1), (float(l0), float(l1))
+    assert g0.keys() == g1.keys()
+    for n in g0:
+        assert torch.equal(g0[n], g1[n]), n
+
+
+@pytest.mark.gpu
+def test_block_under_torch_checkpoint_gives_the_same_bits():
+    """One HIP block called through torch.utils.checkpoint(use_reentrant=False) (the call the reference LM makes
+    for each block, models.py:571-572) against a plain call: output, input gradient and every parameter gradient
+    bit for bit, under bf16 autocast at a macro-block shape and a token-wise one."""
+    from torch.utils.checkpoint import checkpoint
+
+    import bench
+    from gpu_helpers import require_cuda
+    dev = require_cuda()
+    for cfg in (dict(B=2, T=1024, d_model=512, n_heads=8, window=64, local_block_size=256, latent_tokens=16,
+                     latent_d_model=128, latent_heads=2, qbs=0),
+                dict(B=2, T=1024, d_model=512, n_heads=8, window=128, local_block_size=256, latent_tokens=16,
+                     latent_d_model=128, latent_heads=2, qbs=64)):
+        m = bench.make_module(cfg, dev)
+        g = torch.Generator(device=dev).manual_seed(3)
+        x0 = torch.randn(cfg["B"], cfg["T"], cfg["d_model"], device=dev, generator=g)
+        dy = torch.randn(cfg["B"], cfg["T"], cfg["d_model"], device=dev, generator=g)
+        outs = []
+        for ckpt in (False, True):
+            m.zero_grad(set_to_none=True)
+            x = x0.clone().requires_grad_(True)
+            with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+                y = checkpoint(m, x, use_reentrant=False) if ckpt else m(x)
+            y.backward(dy.to(y.dtype))
+            outs.append((y.detach().clone(), x.grad.clone(), {n: p.grad.clone() for n, p in m.named_parameters()}))
+        (y0, dx0, g0), (y1, dx1, g1) = outs
+        assert torch.equal(y0, y1) and torch.equal(dx0, dx1), cfg
+        for n in g0:
+            assert torch.equal(g0[n], g1[n]), (n, cfg)
+
+
 def test_odd_vocabulary_takes_the_full_logits_loss(monkeypatch):
     """A vocabulary the chunked head kernels do not take (50257, GPT-2's: not a multiple of 8) makes
     LocalLatentLM.loss fall back to full logits + lm_loss, as the reference computes it, instead of raising."""

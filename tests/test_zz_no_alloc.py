@@ -73,6 +73,41 @@ def _backward(L, shape, views, keep, noalloc, device):
     return [*outs, dgl, dgr, dbr]
 
 
+def test_noalloc_backward_under_graph_capture():
+    """The entry point's first call of the process made inside HIP graph capture (torch.cuda.graph): the
+    per-device scratch address is looked up there.  The captured graph is replayed three times, with eager
+    kernels and synchronizations between the replays, and every replay matches the workspace backward bit
+    for bit.  Defined first in this file so that no earlier test has called the entry point."""
+    from llattn_amd import _lib as L
+    dev = require_cuda()
+    B, T, H, Dh, W, block, dt = 2, 1024, 16, 88, 64, 256, torch.bfloat16
+    print(f"noalloc graph capture: B={B} T={T} H={H} Dh={Dh} W={W} {dt}", flush=True)
+    shape, views, keep = _inputs(L, B, T, H, Dh, W, block, dt, False, seed=23, device=dev)
+    ref = _backward(L, shape, views, keep, noalloc=False, device=dev)
+    q, k, v, rem = views
+    qkv, remote, gl, gr, dy, ol, lse, w = keep
+    outs = [torch.full((B, T, H, Dh), float("nan"), dtype=dt, device=dev) for _ in range(4)]
+    dgl, dgr = torch.full((Dh,), float("nan"), device=dev), torch.full((Dh,), float("nan"), device=dev)
+    dbr = torch.full((H * Dh,), float("nan"), device=dev)
+    args = [_byref(shape), _byref(q), _byref(k), _byref(v), _byref(rem), gl.data_ptr(), gr.data_ptr(),
+            _byref(L.view_bnhd(ol)), lse.data_ptr(), w.data_ptr(), _byref(L.view(dy, dy.stride(0), dy.stride(1), Dh)),
+            *[_byref(L.view_bnhd(o)) for o in outs], dgl.data_ptr(), dgr.data_ptr(), dbr.data_ptr()]
+    lib = L.load()
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = lib.llattn_local_gate_bwd_noalloc(*args, L.stream_ptr(dev))
+    L.check(rc, "llattn_local_gate_bwd_noalloc (captured)")
+    for rep in range(3):
+        for o in (*outs, dgl, dgr, dbr):
+            o.fill_(float("nan"))
+        _backward(L, shape, views, keep, noalloc=False, device=dev)  # eager work between the replays
+        graph.replay()
+        torch.cuda.synchronize(dev)
+        for j, (a, b) in enumerate(zip([*outs, dgl, dgr, dbr], ref)):
+            assert torch.equal(a, b), f"replay {rep} output {j}: max diff {(a.float() - b.float()).abs().max().item()}"
+
+
 # (B, T, H, Dh, W, block, dtype, per_head): a large call, then a smaller one on the same path
 CASES = [
     ("bf16 fused (config-2 heads)", [(4, 2048, 16, 88, 64, 256, torch.bfloat16, False),
