@@ -21,15 +21,22 @@ CONFIGS = (("config 1 fp32", "C1 (fp32, golden from the reference)"),
 
 def main(path: str) -> None:
     rows = [json.loads(line) for line in open(path)]
-    print("| config | tensor | raw max-abs | max abs ref | scaled max-abs | mean-rel | bar (max-abs / mean-rel) |")
-    print("|---|---|---:|---:|---:|---:|---|")
+    bars = [r for r in rows if "scaled_max_abs" in r]
+    # raw max-abs of the reference's own math under CPU bf16 autocast, by (config, tensor)
+    floors = {(r["case"].split()[0], r["tensor"]): r["floor_raw_max_abs"] for r in rows if "floor_raw_max_abs" in r}
+    print("| config | tensor | raw max-abs | max abs ref | scaled max-abs | mean-rel | bar (max-abs / mean-rel) | "
+          "reference bf16 floor (raw) | raw / floor |")
+    print("|---|---|---:|---:|---:|---:|---|---:|---:|")
     for prefix, label in CONFIGS:
-        for r in rows:
+        for r in bars:
             if not r["case"].startswith(prefix):
                 continue
             bar = f"{r['max_abs_bar']:.0e}" + ("" if r["mean_rel_bar"] is None else f" / {r['mean_rel_bar']:.0e}")
+            fl = floors.get((r["case"].split()[0], r["tensor"]))
+            fl_s = "" if fl is None else f"{fl:.3e}"
+            ratio = "" if not fl else f"{r['raw_max_abs'] / fl:.2f}"
             print(f"| {label} | {r['tensor']} | {r['raw_max_abs']:.3e} | {r['max_ref']:.3e} | "
-                  f"{r['scaled_max_abs']:.3e} | {r['mean_rel']:.3e} | {bar} |")
+                  f"{r['scaled_max_abs']:.3e} | {r['mean_rel']:.3e} | {bar} | {fl_s} | {ratio} |")
 
 
 if __name__ == "__main__":

@@ -14,7 +14,8 @@ import pytest
 import torch
 
 from conftest import E2E_CASES, load_case, shape_from_meta
-from gpu_helpers import (assert_bf16_close, assert_fp32_close, bf16_floor, build_module, err_stats, require_cuda,
+from gpu_helpers import (assert_bf16_close, assert_fp32_close, assert_within_floor, bf16_floor, build_module, err_stats,
+                         reference_bf16_errors, require_cuda,
                          run_module)
 from oracle import llattn_oracle as orc
 
@@ -350,15 +351,21 @@ def test_c2_bf16_batch_slices_match_fp32_reference():
     torch.set_num_threads(max(1, torch.get_num_threads()))
     for b in (0, 15):
         _print_case("c2 reference row", b)
-        o_ref, dx_ref, _ = torch_ref.block_forward_backward(params, x[b:b + 1].float().cpu(),
-                                                            dout[b:b + 1].float().cpu(), shape)
+        xb, db = x[b:b + 1].float().cpu(), dout[b:b + 1].float().cpu()
+        o_ref, dx_ref, _ = torch_ref.block_forward_backward(params, xb, db, shape)
         assert_bf16_close(out[b:b + 1], o_ref.numpy(), f"out[{b}]")
         assert_bf16_close(dx[b:b + 1], dx_ref.numpy(), f"dx[{b}]")
+        floor = reference_bf16_errors(params, xb, db, shape, {"out": o_ref.numpy(), "dx": dx_ref.numpy()})
+        assert_within_floor(out[b:b + 1], o_ref.numpy(), floor["out"], f"out[{b}]")
+        assert_within_floor(dx[b:b + 1], dx_ref.numpy(), floor["dx"], f"dx[{b}]")
     _print_case("c2 weight grads B=2")
     out2, dx2, g2 = run_module(m, x[:2], dout[:2], autocast_bf16=True)
-    _, _, g_ref = torch_ref.block_forward_backward(params, x[:2].float().cpu(), dout[:2].float().cpu(), shape)
+    x2, d2 = x[:2].float().cpu(), dout[:2].float().cpu()
+    _, _, g_ref = torch_ref.block_forward_backward(params, x2, d2, shape)
+    floor = reference_bf16_errors(params, x2, d2, shape, {n: g_ref[n].numpy() for n in g_ref})
     for n in g_ref:
         assert_bf16_close(g2[n], g_ref[n].numpy(), n)
+        assert_within_floor(g2[n], g_ref[n].numpy(), floor[n], n)
 
 
 def test_c2_deterministic_and_finite():
@@ -401,10 +408,15 @@ def _config_row_check(cfg_name, rows):
     del grads
     for b in rows:
         _print_case(cfg_name, "reference row", b)
-        o_ref, dx_ref, g_ref = torch_ref.block_forward_backward(params, x[b:b + 1].float().cpu(),
-                                                                dout[b:b + 1].float().cpu(), shape)
+        xb, db = x[b:b + 1].float().cpu(), dout[b:b + 1].float().cpu()
+        o_ref, dx_ref, g_ref = torch_ref.block_forward_backward(params, xb, db, shape)
         assert_bf16_close(out[b:b + 1], o_ref.numpy(), f"out[{b}]")
         assert_bf16_close(dx[b:b + 1], dx_ref.numpy(), f"dx[{b}]")
+        _print_case(cfg_name, "reference bf16 floor of row", b)
+        floor = reference_bf16_errors(params, xb, db, shape, {"out": o_ref.numpy(), "dx": dx_ref.numpy(),
+                                                               **{n: g_ref[n].numpy() for n in g_ref}})
+        assert_within_floor(out[b:b + 1], o_ref.numpy(), floor["out"], f"out[{b}]")
+        assert_within_floor(dx[b:b + 1], dx_ref.numpy(), floor["dx"], f"dx[{b}]")
         # every parameter gradient of that sequence alone (full T: the window > 64 two-pass local backward,
         # its gate partial rows, r_out's bias from dremote, the column-sum bias gradients of the D = 1024
         # projections, the macro-block scatter in config 4)
@@ -413,6 +425,7 @@ def _config_row_check(cfg_name, rows):
         assert set(g_row) == set(g_ref)
         for n in g_ref:
             assert_bf16_close(g_row[n], g_ref[n].numpy(), f"{n}[{b}]")
+            assert_within_floor(g_row[n], g_ref[n].numpy(), floor[n], f"{n}[{b}]")
     return m, x, dout, params, shape
 
 
