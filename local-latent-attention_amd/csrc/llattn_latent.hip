@@ -17,6 +17,8 @@
 //           the segment's queries (the four waves split the query sub-tiles and
 //           are summed in LDS in wave order); a last kernel adds the segment
 //           partials in segment order.
+//   With one latent tile (bf16, at most 16 latents) both passes run as one kernel
+//   per query segment (latent_bwd_fused_kernel), with the products of the two.
 #include "llattn_abi.h"
 #include "llattn_device.h"
 
@@ -38,12 +40,18 @@ struct LatentArgs {
   float* part;  // workspace [B][Lh][n_seg][n_lt*16][2][Ldh]
 };
 
+// The one-pass backward (bf16, one latent tile of at most 16 latents, padded head dims up to 128)
+bool latent_one_pass(int n_lt, bool bf16, int dhp) { return bf16 && n_lt == 1 && dhp <= 128; }
+
 // Queries per segment of the latent-stationary pass (a multiple of 64): about 1024 workgroups (B Lh n_lt
 // segments) fill the chip; segments stay at least 256 queries long, since each one adds fp32 partials
-// (16 n_lt x 2 Ldh per (b, lh)) that are written and then read back by the ordered reduction.
-int latent_seg(int B, int Lh, int n_chunks, int n_q) {
+// (16 n_lt x 2 Ldh per (b, lh)) that are written and then read back by the ordered reduction.  The
+// one-pass kernel (two workgroups per CU by its LDS) targets 512: one round of longer, pipelined segments
+// (config 2: 49 us against 51 at 1024 and 256 workgroups).
+int latent_seg(int B, int Lh, int n_chunks, int n_q, bool fused) {
   const int64_t units = (int64_t)B * Lh * ((n_chunks + 15) / 16);
-  const int64_t want = std::max<int64_t>(1, (1024 + units - 1) / units);  // segments per (b, lh, latent tile)
+  const int64_t wgs = fused ? 512 : 1024;
+  const int64_t want = std::max<int64_t>(1, (wgs + units - 1) / units);  // segments per (b, lh, latent tile)
   const int64_t seg = ((n_q + want - 1) / want + 63) / 64 * 64;
   return (int)std::max<int64_t>(256, seg);
 }
@@ -332,6 +340,161 @@ __global__ __launch_bounds__(256) void latent_bwd_kv_kernel(const LatentArgs a) 
   }
 }
 
+// ----------------------------------------------------------------------------
+// backward in one pass, bf16, one latent tile (n_chunks <= 16: config 2's 16 latents).  One workgroup per
+// (batch, latent head, segment of a.seg queries): gk / gv are staged once, and each 64-query tile of the
+// segment is read once.  Per 16-query sub-tile a wave computes, with the queries in lanes (as pass Q), D and
+// drq, and, with the latents in lanes (as pass KV), the segment's dgk / dgv sums -- the products of the two
+// passes, without re-reading rq and dL or writing D to the workspace (where the first query that sees a
+// latent starts a 64-query tile and the segments are the same, as at config 2 with 16 latents, the
+// summation order is theirs too).  The next query tile loads while the current one is worked on.
+// ----------------------------------------------------------------------------
+template <int DHP>
+__global__ __launch_bounds__(256) void latent_bwd_fused_kernel(const LatentArgs a) {
+  using T = uint16_t;
+  constexpr int DQ = DHP / 4, NT = DHP / 16, KP = DHP + kRowPad<T>;
+  __shared__ __align__(16) T Ks[64 * KP];   // gk rows (rows >= n_chunks zero)
+  __shared__ __align__(16) T Kt[DHP * kTP]; // gk transposed
+  __shared__ __align__(16) T Vs[64 * KP];   // gv rows
+  __shared__ __align__(16) T Qs[64 * KP];   // rq rows of the query tile
+  __shared__ __align__(16) T Qt[DHP * kTP]; // rq transposed
+  __shared__ __align__(16) T Os[64 * KP];   // dL rows
+  __shared__ __align__(16) T Ot[DHP * kTP]; // dL transposed
+  __shared__ float lse2s[64], Dss[64];
+  __shared__ int vis[64];
+  static_assert(sizeof(T) * 64 * KP >= 2 * DHP * 16 * sizeof(float), "reduction buffer does not fit in Qs");
+  float* red = reinterpret_cast<float*>(Qs);  // [2][DHP][16] after the query loop
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane & 15, g = lane >> 4;
+  const int seg = blockIdx.x % a.n_seg, bh = blockIdx.x / a.n_seg, lh = bh % a.Lh, b = bh / a.Lh;
+  const bool kv = r < a.n_chunks;  // this lane's latent (latents in lanes)
+  const T* rqb = static_cast<const T*>(a.rq) + b * a.rq_sb + lh * a.rq_sh;
+  const T* dlb = static_cast<const T*>(a.dout) + b * a.do_sb + lh * a.do_sh;
+  const int64_t hrow = ((int64_t)b * a.Lh + lh) * a.n_q;
+  const int qbeg = seg * a.seg, qend = (int)min((int64_t)(seg + 1) * a.seg, (int64_t)a.n_q);
+
+  TransTile<T, DHP> tq, to;
+  float pl = 0.f;
+  auto load_tile = [&](int q0) {
+    tq.load(rqb, a.rq_sn, q0, qend, a.Ldh);
+    to.load(dlb, a.do_sn, q0, qend, a.Ldh);
+    if (tid < 64) pl = a.lse[hrow + min(q0 + tid, qend - 1)];
+  };
+  {  // the latents and the first query tile in flight together
+    TransTile<T, DHP> tk;
+    RowTile<T, DHP> tv;
+    tk.load(static_cast<const T*>(a.gk) + b * a.gk_sb + lh * a.gk_sh, a.gk_sn, 0, a.n_chunks, a.Ldh);
+    tv.load(static_cast<const T*>(a.gv) + b * a.gv_sb + lh * a.gv_sh, a.gv_sn, 0, a.n_chunks, a.Ldh);
+    load_tile(qbeg);
+    tk.template store_rows<KP>(Ks);
+    tk.store_t(Kt);
+    tv.template store<KP>(Vs);
+  }
+  lds_barrier();
+  RowFrag<T, DQ> kf, vf;  // latent r's rows, for both orientations
+  kf.load_lds(Ks + r * KP, g);
+  vf.load_lds(Vs + r * KP, g);
+  f32x4 dk[NT], dv[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) dk[t] = dv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int q0 = qbeg; q0 < qend; q0 += 64) {
+    lds_barrier();  // every wave is done with the previous tile
+    tq.template store_rows<KP>(Qs);
+    tq.store_t(Qt);
+    to.template store_rows<KP>(Os);
+    to.store_t(Ot);
+    if (tid < 64) {
+      const int qq = q0 + tid;
+      const bool qv = qq < qend;
+      lse2s[tid] = (qv && pl != kNegInf) ? pl * kLog2e : 0.f;
+      vis[tid] = qv ? visible(qq, a) : 0;
+    }
+    if (q0 + 64 < qend) load_tile(q0 + 64);
+    lds_barrier();
+    const int sq = 16 * wave;  // this wave's 16-query sub-tile of the tile
+    if (q0 + sq >= qend) continue;  // uniform
+    RowFrag<T, DQ> qf, of;
+    qf.load_lds(Qs + (sq + r) * KP, g);
+    of.load_lds(Os + (sq + r) * KP, g);
+    // ---- queries in lanes (pass Q): S^T[latent 4g+i][query r], D, dS, drq ----
+    {
+      const int ql = sq + r, qi = q0 + ql;
+      const int ncq = vis[ql];
+      const float lse2 = lse2s[ql];
+      const f32x4 s = row_mma(kf, qf, f32x4{0.f, 0.f, 0.f, 0.f});
+      const f32x4 dp = row_mma(vf, of, f32x4{0.f, 0.f, 0.f, 0.f});
+      float D = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (4 * g + i < ncq) D += fast_exp2(s[i] * a.scale_log2 - lse2) * dp[i];
+      D = sum_groups(D);
+      float ds[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = (4 * g + i < ncq) ? fast_exp2(s[i] * a.scale_log2 - lse2) : 0.f;
+        ds[i] = p * (dp[i] - D);
+      }
+      if (g == 0) Dss[ql] = D;  // read below by the lanes that hold this query's latents
+      f32x4 acc[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[t] = col_mma(Kt + (16 * t + r) * kTP + 4 * g, ds, f32x4{0.f, 0.f, 0.f, 0.f});
+      if (qi < qend) {
+        T* p = static_cast<T*>(a.drq) + b * a.drq_sb + lh * a.drq_sh + (int64_t)qi * a.drq_sn;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const int d = 16 * t + 4 * g;
+          if (d < a.Ldh) {
+            float v4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v4[i] = acc[t][i] * a.scale;
+            store4<T>(p + d, v4);
+          }
+        }
+      }
+    }
+    // ---- latents in lanes (pass KV): S[query 4g+i][latent r], dgk / dgv over the sub-tile's queries ----
+    {
+      const f32x4 s = row_mma(qf, kf, f32x4{0.f, 0.f, 0.f, 0.f});
+      const f32x4 dp = row_mma(of, vf, f32x4{0.f, 0.f, 0.f, 0.f});
+      float p[4], ds[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ql = sq + 4 * g + i;
+        p[i] = (kv && r < vis[ql]) ? fast_exp2(s[i] * a.scale_log2 - lse2s[ql]) : 0.f;
+        ds[i] = p[i] * (dp[i] - Dss[ql]);
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        dv[t] = col_mma(Ot + (16 * t + r) * kTP + sq + 4 * g, p, dv[t]);
+        dk[t] = col_mma(Qt + (16 * t + r) * kTP + sq + 4 * g, ds, dk[t]);
+      }
+    }
+  }
+  // sum the four waves in order: red[which][dim][latent]
+  for (int w = 0; w < 4; ++w) {
+    lds_barrier();
+    if (wave == w) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d = 16 * t + 4 * g + i;
+          float* rk = red + (0 * DHP + d) * 16 + r;
+          float* rv = red + (1 * DHP + d) * 16 + r;
+          *rk = (w == 0 ? 0.f : *rk) + dk[t][i] * a.scale;
+          *rv = (w == 0 ? 0.f : *rv) + dv[t][i];
+        }
+    }
+  }
+  lds_barrier();
+  float* part = a.part + (((int64_t)b * a.Lh + lh) * a.n_seg + seg) * 16 * 2 * a.Ldh;
+  for (int idx = tid; idx < 16 * 2 * a.Ldh; idx += 256) {
+    const int n = idx / (2 * a.Ldh), which = (idx / a.Ldh) % 2, d = idx % a.Ldh;
+    part[(int64_t)n * 2 * a.Ldh + which * a.Ldh + d] = red[(which * DHP + d) * 16 + n];
+  }
+}
+
 // dgk / dgv [b][n][lh][d] = sum over segments (in order) of the partials.
 template <typename T>
 __global__ __launch_bounds__(256) void latent_reduce_kernel(const LatentArgs a) {
@@ -361,8 +524,13 @@ void launch(bool fwd, const LatentArgs& a, hipStream_t st) {
   if (fwd) {
     hipLaunchKernelGGL((latent_fwd_kernel<T, DHP>), dim3(a.B * a.Lh * a.n_qt), dim3(256), 0, st, a);
   } else {
-    hipLaunchKernelGGL((latent_bwd_q_kernel<T, DHP>), dim3(a.B * a.Lh * a.n_qt), dim3(256), 0, st, a);
-    hipLaunchKernelGGL((latent_bwd_kv_kernel<T, DHP>), dim3(a.B * a.Lh * a.n_lt * a.n_seg), dim3(256), 0, st, a);
+    if (latent_one_pass(a.n_lt, std::is_same_v<T, uint16_t>, DHP)) {  // one latent tile: both passes in one
+      hipLaunchKernelGGL((latent_bwd_fused_kernel<DHP <= 128 ? DHP : 128>), dim3(a.B * a.Lh * a.n_seg), dim3(256), 0,
+                         st, a);
+    } else {
+      hipLaunchKernelGGL((latent_bwd_q_kernel<T, DHP>), dim3(a.B * a.Lh * a.n_qt), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((latent_bwd_kv_kernel<T, DHP>), dim3(a.B * a.Lh * a.n_lt * a.n_seg), dim3(256), 0, st, a);
+    }
     const int64_t total = (int64_t)a.B * a.Lh * a.n_chunks * 2 * a.Ldh;
     const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
     hipLaunchKernelGGL((latent_reduce_kernel<T>), dim3(blocks), dim3(256), 0, st, a);
@@ -397,7 +565,8 @@ int32_t common(const llattn_shape* s, const llattn_tensor* rq, const llattn_tens
   a->chunk = s->chunk; a->n_chunks = s->n_chunks;
   a->n_qt = (s->n_q + 63) / 64;
   a->n_lt = (s->n_chunks + 15) / 16;
-  a->seg = latent_seg(s->B, s->Lh, s->n_chunks, s->n_q);
+  a->seg = latent_seg(s->B, s->Lh, s->n_chunks, s->n_q, latent_one_pass(a->n_lt, s->dtype == LLATTN_BF16,
+                                                                   padded_head_dim(s->Ldh)));
   a->n_seg = (s->n_q + a->seg - 1) / a->seg;
   a->scale = 1.0f / sqrtf((float)s->Ldh);
   a->scale_log2 = a->scale * kLog2e;
@@ -411,8 +580,10 @@ int32_t common(const llattn_shape* s, const llattn_tensor* rq, const llattn_tens
 
 size_t latent_workspace_bytes(const llattn_shape* s) {
   auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
-  const int seg = latent_seg(s->B, s->Lh, s->n_chunks, s->n_q);
-  const size_t n_lt = (s->n_chunks + 15) / 16, n_seg = (s->n_q + seg - 1) / seg;
+  const size_t n_lt = (s->n_chunks + 15) / 16;
+  const int seg = latent_seg(s->B, s->Lh, s->n_chunks, s->n_q,
+                             latent_one_pass((int)n_lt, s->dtype == LLATTN_BF16, padded_head_dim(s->Ldh)));
+  const size_t n_seg = (s->n_q + seg - 1) / seg;
   return up((size_t)s->B * s->Lh * s->n_q * 4) + up((size_t)s->B * s->Lh * n_seg * n_lt * 16 * 2 * s->Ldh * 4);
 }
 
