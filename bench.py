@@ -425,7 +425,8 @@ def bench_gemm_products(args):
     """The config-2 step's nine large GEMM products, each timed alone (HIP events, 20 calls after 3 warm-up
     calls) on this library's kernel and on torch's library GEMM (hipBLASLt) with the same bf16 operands;
     then board power and GFX clock sampled by ``amd-smi`` during 4-second loops of the largest product on
-    each.  Output: one JSON line."""
+    each, and the same for a square 8192 x 8192 x 8192 bf16 product (the board's sustained ceiling on a shape
+    with a long k loop, next to the step's K = 1408 products).  Output: one JSON line."""
     import threading
 
     from llattn_amd import gemm
@@ -509,6 +510,20 @@ def bench_gemm_products(args):
     power = {"idle": None if idle is None else {"power_w": idle[0], "gfx_mhz": idle[1]},
              "ours qkv|rq forward loop": sustained(ours, 2.0 * m * n * k),
              "library qkv|rq forward loop": sustained(lib, 2.0 * m * n * k)}
+    del prods
+    S = 8192
+    a, b, c = rnd(S, S), rnd(S, S), torch.empty(S, S, device=dev, dtype=bf)
+    sq_ours = lambda: gemm.linear(a, b, out=c)  # noqa: E731
+    sq_lib = lambda: torch.matmul(a, b.t(), out=c)  # noqa: E731
+    ref = torch.matmul(a, b.t()).float()
+    sq_err = float((gemm.linear(a, b).float() - ref).abs().max() / ref.abs().max())
+    del ref
+    flop = 2.0 * S ** 3
+    for name, fn in (("ours", sq_ours), ("library", sq_lib)):
+        t = timed(fn)
+        power[f"{name} 8192^3 loop"] = {"burst_us": round(t, 1), "burst_tflops": round(flop / t / 1e6, 1),
+                                       **sustained(fn, flop)}
+    power["8192^3 ours vs library max rel"] = sq_err
     log(json.dumps(power))
     tot_o = sum(r["us"] for r in rows)
     tot_l = sum(r["library_us"] for r in rows)

@@ -276,6 +276,17 @@ int32_t llattn_colsum(const void* x, int64_t ld, int32_t M, int32_t N, float* ou
 int32_t llattn_cast(int32_t nseg, const float* const* src, void* const* dst, const int64_t* n,
                     const int32_t* dst_dtype, void* stream);
 
+/* llattn_cast, and for each segment i with dst_t[i] non-null also the transposed bf16 copy of the cast:
+ * segment i is then a row-major fp32 [rows[i], n[i] / rows[i]] matrix (rows and columns multiples of 8,
+ * src, dst and dst_t 16-byte aligned, bf16 output) and dst_t[i][c * ld_t[i] + r] = bf16(src[i][r * cols + c])
+ * (ld_t[i] >= rows[i], a multiple of 8).  dst_t, ld_t and rows are nseg-entry arrays, or dst_t is NULL for
+ * none.  The bf16 W^T copies that input gradients run on (dy W as dy (W^T)^T on the persistent GEMM, the
+ * nn.Linear backward of reference models.py:80-84 under autocast), written while the cast reads W anyway:
+ * one extra 2-byte write per element instead of an llattn_transpose pass in the backward. */
+int32_t llattn_cast_transposed(int32_t nseg, const float* const* src, void* const* dst, const int64_t* n,
+                               const int32_t* dst_dtype, void* const* dst_t, const int64_t* ld_t,
+                               const int32_t* rows, void* stream);
+
 /* dst[c][r] = src[r][c] for a bf16 matrix of rows x cols (both multiples of 8; 16-byte aligned, leading
  * dimensions in elements, multiples of 8).  The input gradient dy W of a projection runs as
  * dy (W^T)^T on the persistent GEMM (both operands k-contiguous) with this transposed copy of the bf16

@@ -2,9 +2,13 @@
 // autocast performs once per forward for every nn.Linear of the block, and the concatenated biases
 // of projections that share one GEMM.  HBM-bound; one pass over each array.
 //
-// The launch covers the concatenation of all segments in chunks of 8 elements (32 bytes read); each
+// Plain segments: the launch covers their concatenation in chunks of 8 elements (32 bytes read); each
 // thread finds its segment by a scan over the (at most LLATTN_CAST_MAX_SEGS) segment starts.  Segments whose
 // source and destination are 16-byte aligned move with 16-byte loads and stores, others element by element.
+// Segments that also want a transposed bf16 copy (the weights whose input gradients run as dy (W^T)^T) are
+// cut into 64 x 64 tiles, one workgroup each, placed before the chunk workgroups: each tile is read once
+// (fp32 rows), written as bf16 rows, and written again transposed through LDS, so W^T costs 2 bytes per
+// element on top of the cast instead of a separate read and write of W.
 // Conversion rounds to nearest even, as a torch .to(torch.bfloat16) does.
 #include "llattn_abi.h"
 #include "llattn_device.h"
@@ -19,12 +23,58 @@ struct CastArgs {
   int64_t n[LLATTN_CAST_MAX_SEGS];
   int32_t bf16[LLATTN_CAST_MAX_SEGS];
   int32_t vec[LLATTN_CAST_MAX_SEGS];  // source and destination 16-byte aligned: vector loads and stores
+  uint16_t* tdst[LLATTN_CAST_MAX_SEGS];  // non-null: segment written in tiles, transposed copy here
+  int64_t tld[LLATTN_CAST_MAX_SEGS];     // leading dimension of tdst (elements)
+  int32_t rows[LLATTN_CAST_MAX_SEGS];    // the tiled segment as a row-major [rows][n / rows] matrix
+  int32_t tile_start[LLATTN_CAST_MAX_SEGS + 1];  // first tile workgroup of segment i (tiled segments only)
   int32_t nseg;
 };
 
+// One 64 x 64 tile of a tiled segment: fp32 rows in (16-byte loads), bf16 rows out (8-byte stores), and the
+// transposed bf16 tile out through LDS (16-byte stores of 8 consecutive rows).  rows and cols are multiples
+// of 8, so a 4-column load group and an 8-row store group are either wholly inside the matrix or wholly out.
+__device__ __forceinline__ void cast_tile(const float* __restrict__ src, uint16_t* __restrict__ dst,
+                                          uint16_t* __restrict__ tdst, int64_t tld, int rows, int cols, int tile,
+                                          uint16_t (*t)[72]) {
+  const int tiles_c = (cols + 63) >> 6;
+  const int r0 = (tile / tiles_c) * 64, c0 = (tile % tiles_c) * 64, tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = tid + 256 * i, rl = q >> 4, cl = 4 * (q & 15);
+    float4 u = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (r0 + rl < rows && c0 + cl < cols) {
+      const int64_t e = (int64_t)(r0 + rl) * cols + c0 + cl;
+      u = *reinterpret_cast<const float4*>(src + e);
+      *reinterpret_cast<uint2*>(dst + e) = make_uint2(pack_bf16x2(u.x, u.y), pack_bf16x2(u.z, u.w));
+    }
+    t[cl][rl] = f2bf(u.x);
+    t[cl + 1][rl] = f2bf(u.y);
+    t[cl + 2][rl] = f2bf(u.z);
+    t[cl + 3][rl] = f2bf(u.w);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int q = tid + 256 * i, cl = q >> 3, rl = 8 * (q & 7);
+    if (c0 + cl < cols && r0 + rl < rows)
+      *reinterpret_cast<uint4*>(tdst + (int64_t)(c0 + cl) * tld + r0 + rl) = *reinterpret_cast<const uint4*>(&t[cl][rl]);
+  }
+}
+
 __global__ __launch_bounds__(256) void cast_kernel(const CastArgs a) {
+  __shared__ uint16_t t[64][72];
+  const int tiles = a.tile_start[a.nseg];
+  if ((int)blockIdx.x < tiles) {  // a tile of a transposed segment (workgroup-uniform branch)
+    int s = 0;
+    while (s + 1 < a.nseg && (int)blockIdx.x >= a.tile_start[s + 1]) ++s;
+    const int rows = a.rows[s];
+    cast_tile(a.src[s], static_cast<uint16_t*>(a.dst[s]), a.tdst[s], a.tld[s], rows, (int)(a.n[s] / rows),
+              (int)blockIdx.x - a.tile_start[s], t);
+    return;
+  }
   const int64_t total = a.start[a.nseg];
-  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < total; c += (int64_t)gridDim.x * 256) {
+  const int64_t nblk = (int64_t)gridDim.x - tiles;
+  for (int64_t c = ((int64_t)blockIdx.x - tiles) * 256 + threadIdx.x; c < total; c += nblk * 256) {
     int s = 0;
     while (s + 1 < a.nseg && c >= a.start[s + 1]) ++s;
     const int64_t e0 = (c - a.start[s]) * 8;  // first element of the chunk within segment s
@@ -96,14 +146,17 @@ extern "C" int32_t llattn_transpose(const void* src, int64_t ld_src, int32_t row
   return check_launch("llattn_transpose");
 }
 
-extern "C" int32_t llattn_cast(int32_t nseg, const float* const* src, void* const* dst, const int64_t* n,
-                               const int32_t* dst_dtype, void* stream) {
+extern "C" int32_t llattn_cast_transposed(int32_t nseg, const float* const* src, void* const* dst,
+                                          const int64_t* n, const int32_t* dst_dtype, void* const* dst_t,
+                                          const int64_t* ld_t, const int32_t* rows, void* stream) {
   if (nseg < 1 || nseg > LLATTN_CAST_MAX_SEGS)
     return fail(LLATTN_ERR_SHAPE, "llattn_cast: %d segments (1 to %d supported)", nseg, LLATTN_CAST_MAX_SEGS);
   if (!src || !dst || !n || !dst_dtype) return fail(LLATTN_ERR_LAYOUT, "llattn_cast: null argument array");
+  if (dst_t && (!ld_t || !rows))
+    return fail(LLATTN_ERR_LAYOUT, "llattn_cast_transposed: dst_t given without ld_t and rows");
   CastArgs a{};
   a.nseg = nseg;
-  int64_t chunks = 0;
+  int64_t chunks = 0, tiles = 0;
   for (int i = 0; i < nseg; ++i) {
     if (n[i] < 0) return fail(LLATTN_ERR_SHAPE, "llattn_cast: segment %d has negative length %lld", i, (long long)n[i]);
     if (dst_dtype[i] != LLATTN_BF16 && dst_dtype[i] != LLATTN_F32)
@@ -116,11 +169,33 @@ extern "C" int32_t llattn_cast(int32_t nseg, const float* const* src, void* cons
     a.bf16[i] = dst_dtype[i] == LLATTN_BF16;
     a.vec[i] = aligned16(src[i]) && aligned16(dst[i]);
     a.start[i] = chunks;
-    chunks += (n[i] + 7) / 8;
+    a.tile_start[i] = (int32_t)tiles;
+    if (dst_t && dst_t[i] && n[i] > 0) {
+      const int64_t r = rows[i], c = r > 0 ? n[i] / r : 0;
+      if (r <= 0 || r * c != n[i] || r % 8 || c % 8 || r > (1 << 20) || c > (1 << 20))
+        return fail(LLATTN_ERR_SHAPE, "llattn_cast_transposed: segment %d: %lld elements are not a [rows, cols] "
+                    "matrix with rows = %d and both multiples of 8 (at most 2^20)", i, (long long)n[i], rows[i]);
+      if (!a.bf16[i] || !a.vec[i] || !aligned16(dst_t[i]) || ld_t[i] % 8 || ld_t[i] < r)
+        return fail(LLATTN_ERR_LAYOUT, "llattn_cast_transposed: segment %d: bf16 output, 16-byte aligned arrays "
+                    "and a transposed leading dimension >= rows, a multiple of 8, needed", i);
+      a.tdst[i] = static_cast<uint16_t*>(dst_t[i]);
+      a.tld[i] = ld_t[i];
+      a.rows[i] = (int32_t)r;
+      tiles += ((r + 63) / 64) * ((c + 63) / 64);
+      if (tiles > (1 << 30)) return fail(LLATTN_ERR_SHAPE, "llattn_cast_transposed: too many tiles");
+    } else {
+      chunks += (n[i] + 7) / 8;
+    }
   }
   a.start[nseg] = chunks;
-  if (chunks == 0) return LLATTN_OK;
-  const int64_t blocks = std::min<int64_t>((chunks + 255) / 256, 4096);
+  a.tile_start[nseg] = (int32_t)tiles;
+  if (chunks == 0 && tiles == 0) return LLATTN_OK;
+  const int64_t blocks = tiles + std::min<int64_t>((chunks + 255) / 256, 4096);
   hipLaunchKernelGGL(cast_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), a);
   return check_launch("llattn_cast");
+}
+
+extern "C" int32_t llattn_cast(int32_t nseg, const float* const* src, void* const* dst, const int64_t* n,
+                               const int32_t* dst_dtype, void* stream) {
+  return llattn_cast_transposed(nseg, src, dst, n, dst_dtype, nullptr, nullptr, nullptr, stream);
 }

@@ -82,6 +82,7 @@ SIGNATURES = {
     "llattn_colsum_workspace_size": (_SZ, [_I32, _I32]),
     "llattn_colsum": (_I32, [_P, _I64, _I32, _I32, _P, _P, _SZ, _P]),
     "llattn_cast": (_I32, [_I32, _P, _P, _P, _P, _P]),
+    "llattn_cast_transposed": (_I32, [_I32, _P, _P, _P, _P, _P, _P, _P, _P]),
     "llattn_transpose": (_I32, [_P, _I64, _I32, _I32, _P, _I64, _P]),
     "llattn_rmsnorm_fwd": (_I32, [_P, _I32, _I64, _P, _I32, _I32, ctypes.c_float, _P, _I32, _I64, _P, _P, _I32, _I64,
                                   _P, _I64, _P]),

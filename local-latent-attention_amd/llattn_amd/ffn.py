@@ -38,17 +38,18 @@ class _FeedForward(torch.autograd.Function):
             x2 = x.reshape(-1, D).to(BF16)
             if not x2.is_contiguous():
                 x2 = x2.contiguous()
-            w1b, w2b = pack_params([([w1], BF16), ([w2], BF16)])  # the autocast casts, one launch
+            # the autocast casts, one launch; w1 also transposed for the input gradient
+            (w1b, w1t), w2b = pack_params([([w1], BF16, True), ([w2], BF16)])
             g, gp = gemm.linear_gelu(x2, w1b, _bias(b1))
             y = gemm.linear(g, w2b, _bias(b2))
-        ctx.save_for_backward(x2, gp, g, w1b, w2b)
+        ctx.save_for_backward(x2, gp, g, w1b, w1t, w2b)
         ctx.meta = (lead, x.dtype, w1.dtype, w2.dtype, None if b1 is None else b1.dtype,
                     None if b2 is None else b2.dtype)
         return y.view(*lead, w2.shape[0])
 
     @staticmethod
     def backward(ctx, dy):
-        x2, gp, g, w1b, w2b = ctx.saved_tensors
+        x2, gp, g, w1b, w1t, w2b = ctx.saved_tensors
         lead, xdt, w1dt, w2dt, b1dt, b2dt = ctx.meta
         has_b1, has_b2 = b1dt is not None, b2dt is not None
         with torch.autocast(device_type="cuda", enabled=False):
@@ -57,7 +58,7 @@ class _FeedForward(torch.autograd.Function):
                 dy2 = dy2.contiguous()
             dh = gemm.matmul_nn_scaled(dy2, w2b, gp)         # (dy W2) * gelu'(h), bf16
             dw2, db2 = weight_grad(dy2, g, has_b2)           # fp32
-            dx = gemm.input_grad(dh, w1b) if ctx.needs_input_grad[0] else None
+            dx = gemm.input_grad(dh, w1b, w_t=w1t) if ctx.needs_input_grad[0] else None
             dw1, db1 = weight_grad(dh, x2, has_b1)
         return (None if dx is None else dx.view(*lead, x2.shape[1]).to(xdt), dw1.to(w1dt),
                 None if db1 is None else db1.to(b1dt), dw2.to(w2dt), None if db2 is None else db2.to(b2dt))

@@ -149,15 +149,20 @@ def transpose(w: torch.Tensor) -> torch.Tensor:
 ROWADD_PERSISTENT = True
 
 
-def input_grad(dy: torch.Tensor, w: torch.Tensor, rowadd=()) -> torch.Tensor:
+def input_grad(dy: torch.Tensor, w: torch.Tensor, rowadd=(), w_t: torch.Tensor | None = None) -> torch.Tensor:
     """``dy [M, N] @ w [N, K]`` (+ the ``rowadd`` addends of :func:`matmul_nn`) -> bf16 ``[M, K]``, the input
     gradient of ``y = x w^T``.  For large M as ``dy (w^T)^T`` on the persistent kernel with a transposed copy of
-    ``w`` (both operands k-contiguous: plain LDS fragment reads, the epilogue overlapped with the next tile);
-    otherwise :func:`matmul_nn` (transposing fragment reads of ``w``).  Both give the same bits."""
+    ``w`` (both operands k-contiguous: plain LDS fragment reads, the epilogue overlapped with the next tile):
+    ``w_t`` when the caller has it (``llattn_cast_transposed`` writes it with the weight cast), else made here;
+    otherwise :func:`matmul_nn` (transposing fragment reads of ``w``).  All routes give the same bits."""
     M, N = dy.shape
     K = w.shape[1]
     if (not rowadd or ROWADD_PERSISTENT) and M >= 4096 and K % 8 == 0 and N % 8 == 0 and N > 64:
-        return linear(dy, transpose(w), rowadd=rowadd)
+        if w_t is None:
+            w_t = transpose(w)
+        elif tuple(w_t.shape) != (K, N):
+            raise ValueError(f"w_t is {tuple(w_t.shape)}, expected the transpose of w {tuple(w.shape)}")
+        return linear(dy, w_t, rowadd=rowadd)
     return matmul_nn(dy, w, rowadd=rowadd)
 
 

@@ -21,26 +21,45 @@ MAX_SEGS = 8  # LLATTN_CAST_MAX_SEGS
 
 
 def pack_params(groups):
-    """``groups``: ``[(tensors, dtype), ...]`` of fp32 parameters.  Returns one new contiguous tensor per group,
-    ``torch.cat(tensors)`` converted to ``dtype`` (bf16: round to nearest even, as ``.to(torch.bfloat16)``), all
-    written by one ``llattn_cast`` launch (per 8 arrays): the weight casts bf16 autocast makes once per forward."""
+    """``groups``: ``[(tensors, dtype), ...]`` of fp32 parameters, or ``(tensors, torch.bfloat16, True)`` for a
+    group of 2-D weights that also wants its transposed copy.  Returns one new contiguous tensor per group,
+    ``torch.cat(tensors)`` converted to ``dtype`` (bf16: round to nearest even, as ``.to(torch.bfloat16)``), or
+    for a transposed group the pair ``(cat, cat.t().contiguous())`` -- ``(cat, None)`` when a weight's rows or
+    columns are not multiples of 8, which the tiled copy needs; all written by one ``llattn_cast_transposed``
+    launch (per 8 arrays): the weight casts bf16 autocast makes once per forward, and the ``W^T`` copies that the
+    input gradients run on (:func:`llattn_amd.gemm.input_grad`)."""
     import ctypes
 
     from . import _lib as L
     from .ops import _call
     outs, segs = [], []
-    for tensors, dtype in groups:
+    for group in groups:
+        tensors, dtype = group[0], group[1]
         ts = [t.detach() for t in tensors]
+        if any(t.shape[1:] != ts[0].shape[1:] for t in ts):
+            raise ValueError("the tensors of one group must share their trailing dimensions")
+        want_t = len(group) > 2 and group[2]
+        pair = want_t
+        if want_t and (dtype != BF16 or any(t.dim() != 2 for t in ts)):
+            raise ValueError("transposed copies are made of 2-D weights cast to bf16")
+        want_t = want_t and all(t.shape[0] % 8 == 0 and t.shape[1] % 8 == 0 for t in ts)
         lead = sum(t.shape[0] for t in ts)
         out = torch.empty((lead, *ts[0].shape[1:]), dtype=dtype, device=ts[0].device)
+        out_t = None
+        if want_t:
+            out_t = torch.empty((ts[0].shape[1], lead), dtype=dtype, device=ts[0].device)
         o = 0
         for t in ts:
             if t.dtype != torch.float32 or not t.is_contiguous():
                 t = t.float().contiguous()
+            if want_t and t.data_ptr() % 16:
+                t = t.clone()  # the tiled copy reads 16-byte rows
             n = t.shape[0]
-            segs.append((t, out[o:o + n], t.numel(), L.dtype_code(dtype)))
+            # segment i of W^T: columns o .. o + n of [cols, lead]
+            tr = (out_t[:, o:].data_ptr(), lead, n) if want_t else (None, 0, 0)
+            segs.append((t, out[o:o + n], t.numel(), L.dtype_code(dtype), *tr))
             o += n
-        outs.append(out)
+        outs.append((out, out_t) if pair else out)
     L.require_gpu(*[sg[0] for sg in segs])
     for i in range(0, len(segs), MAX_SEGS):
         chunk = segs[i:i + MAX_SEGS]
@@ -49,7 +68,13 @@ def pack_params(groups):
         dst = (ctypes.c_void_p * k)(*[sg[1].data_ptr() for sg in chunk])
         n = (ctypes.c_int64 * k)(*[sg[2] for sg in chunk])
         dt = (ctypes.c_int32 * k)(*[sg[3] for sg in chunk])
-        _call("llattn_cast", k, src, dst, n, dt, L.stream_ptr(chunk[0][0].device))
+        if any(sg[4] is not None for sg in chunk):
+            tdst = (ctypes.c_void_p * k)(*[sg[4] for sg in chunk])
+            tld = (ctypes.c_int64 * k)(*[sg[5] for sg in chunk])
+            rows = (ctypes.c_int32 * k)(*[sg[6] for sg in chunk])
+            _call("llattn_cast_transposed", k, src, dst, n, dt, tdst, tld, rows, L.stream_ptr(chunk[0][0].device))
+        else:
+            _call("llattn_cast", k, src, dst, n, dt, L.stream_ptr(chunk[0][0].device))
     return outs
 
 
@@ -59,10 +84,11 @@ def linear_fwd(x2: torch.Tensor, w: torch.Tensor, b32: torch.Tensor | None, head
     return gemm.linear(x2, w, b32, heads=heads)
 
 
-def input_grad(dy2: torch.Tensor, w: torch.Tensor, rowadd=()) -> torch.Tensor:
+def input_grad(dy2: torch.Tensor, w: torch.Tensor, rowadd=(), w_t: torch.Tensor | None = None) -> torch.Tensor:
     """bf16 ``dy2 @ w`` (w [N, K] read row-major), plus the broadcast ``rowadd`` pooling gradients
-    added in the GEMM's epilogue (:func:`llattn_amd.gemm.input_grad`)."""
-    return gemm.input_grad(dy2, w, rowadd=rowadd)
+    added in the GEMM's epilogue (:func:`llattn_amd.gemm.input_grad`; ``w_t``: ``w``'s transposed copy from
+    :func:`pack_params`, if made)."""
+    return gemm.input_grad(dy2, w, rowadd=rowadd, w_t=w_t)
 
 
 def weight_grad(dy2: torch.Tensor, x2: torch.Tensor, bias_grad: bool = False):
@@ -79,7 +105,8 @@ def weight_grad(dy2: torch.Tensor, x2: torch.Tensor, bias_grad: bool = False):
 class _Project(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, pools, packed, heads, *params):
-        # packed: (bf16 weights, fp32 biases) already concatenated by pack_params, or None
+        # packed: (bf16 weights, fp32 biases[, bf16 transposed weights]) already concatenated by pack_params,
+        # or None
         ctx.set_materialize_grads(False)
         ws, bs = params[0::2], params[1::2]
         has_bias = bs[0] is not None
@@ -89,8 +116,10 @@ class _Project(torch.autograd.Function):
             x2 = x.reshape(-1, K).to(BF16)
             if not x2.is_contiguous():
                 x2 = x2.contiguous()
+            wcat_t = None
             if packed is not None:
-                wcat, bcat = packed
+                wcat, bcat = packed[0], packed[1]
+                wcat_t = packed[2] if len(packed) > 2 else None
             elif len(ws) == 1:
                 wcat = ws[0].detach().to(BF16)
                 b = bs[0]
@@ -118,14 +147,14 @@ class _Project(torch.autograd.Function):
                     p = torch.empty((x.shape[0], n_seg, K), dtype=x.dtype, device=x.device)
                     pool_fwd_into(xc, p, seg, n_seg, divisor)
                     pooled.append(p)
-        ctx.save_for_backward(x2, wcat)
+        ctx.save_for_backward(x2, wcat, wcat_t)
         ctx.meta = (tuple(x.shape[:-1]), rows, has_bias, [w.dtype for w in ws], [None if b is None else b.dtype
                                                                                  for b in bs], x.dtype, tuple(pools))
         return (y.view(*x.shape[:-1], sum(rows)), *pooled)
 
     @staticmethod
     def backward(ctx, dy, *dpooled):
-        x2, wcat = ctx.saved_tensors
+        x2, wcat, wcat_t = ctx.saved_tensors
         lead, rows, has_bias, wdt, bdt, xdt, pools = ctx.meta
         N = sum(rows)
         K = x2.shape[1]
@@ -145,7 +174,7 @@ class _Project(torch.autograd.Function):
                             if g is not None:
                                 rowadd.append((_contig(g).view(-1, K), lead[1], seg, n_seg, divisor))
                         dpooled = ()
-                    dx = input_grad(dy2, wcat, rowadd).view(*lead, K).to(xdt)
+                    dx = input_grad(dy2, wcat, rowadd, wcat_t).view(*lead, K).to(xdt)
                 dw, db = weight_grad(dy2, x2, has_bias)
             if ctx.needs_input_grad[0] and any(g is not None for g in dpooled):
                 # pooling backward accumulates straight into the projection's input gradient
@@ -175,7 +204,8 @@ def project(x: torch.Tensor, *linears: torch.nn.Linear, pools=(), packed=None, h
     :func:`llattn_amd.ops.pool`) returned after the projection, ``(y, pooled_1, ...)``; their backward adds
     into the projection's input gradient in place, so the block's input gradient is formed once.  Without
     ``pools`` the projection alone is returned.  ``packed``: ``(bf16 [sum N_i, K] weights, fp32 biases or None)``
-    already cast and concatenated (:func:`pack_params`), so a caller casts all its weights in one launch.
+    already cast and concatenated (:func:`pack_params`), so a caller casts all its weights in one launch; a
+    third entry, the bf16 ``[K, sum N_i]`` transposed weights (or None), feeds the input gradient.
     ``heads``: ``(T, dh, n)`` -- the output ``[B, T, N]`` is stored split-head (its first ``n * dh`` columns as
     ``[B][n][T][dh]`` slabs, the rest packed after them; :mod:`llattn_amd.gemm`), for a consumer that reads it
     by strides (:class:`llattn_amd.ops.LLAttnCore`); its gradient comes back as a plain row-major tensor."""

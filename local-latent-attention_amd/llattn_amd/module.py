@@ -159,21 +159,29 @@ class LocalLatentAttentionTriton(nn.Module):
 
     def _packed_weights(self, macro: bool) -> dict:
         """The bf16 copies of every projection weight that this forward multiplies with (what bf16 autocast casts
-        per forward), and the concatenated fp32 biases of qkv_proj + rq_proj, written by one llattn_cast launch.
-        Single projections take their fp32 bias as it is."""
+        per forward), the concatenated fp32 biases of qkv_proj + rq_proj, and bf16 W^T copies of the qkv|rq,
+        out and r_out weights for their input gradients, written by one llattn_cast_transposed launch.  Single
+        projections take their fp32 bias as it is."""
         qkv = [self.qkv_proj] if macro else [self.qkv_proj, self.rq_proj]
         has_b = self.qkv_proj.bias is not None
-        groups = [([m.weight for m in qkv], torch.bfloat16)]
+        # the weights whose input gradients have token-count rows also get their W^T copy from the same launch
+        groups = [([m.weight for m in qkv], torch.bfloat16, True)]
         if has_b:
             groups.append(([m.bias for m in qkv], torch.float32))
         singles = (["rq"] if macro else []) + ["rkv", "out", "r_out"]
         mods = {"rq": self.rq_proj, "rkv": self.rkv_proj, "out": self.out, "r_out": self.r_out}
-        groups += [([mods[k].weight], torch.bfloat16) for k in singles]
+        groups += [([mods[k].weight], torch.bfloat16, k in ("out", "r_out")) for k in singles]
         outs = pack_params(groups)
-        packed = {"qkv": (outs[0], outs[1] if has_b else None)}
+        w, w_t = outs[0]
+        packed = {"qkv": (w, outs[1] if has_b else None, w_t)}
         for i, k in enumerate(singles):
-            b = mods[k].bias
-            packed[k] = outs[(2 if has_b else 1) + i] if k == "r_out" else (outs[(2 if has_b else 1) + i], b)
+            o = outs[(2 if has_b else 1) + i]
+            if k == "r_out":
+                packed[k] = o  # (W, W^T)
+            elif k == "out":
+                packed[k] = (o[0], mods[k].bias, o[1])
+            else:
+                packed[k] = (o, mods[k].bias)
         return packed
 
     def _record_profile(self, prof, lay: L.Layout) -> None:

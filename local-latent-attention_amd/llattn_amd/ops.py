@@ -199,7 +199,7 @@ def _core_forward(lay: L.Layout, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, r_b, 
 
 
 def _core_backward(lay: L.Layout, dy, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, has_rb, lat, lse_lat, R, ol, lse,
-                   w, dq, dk, dv, drq, dgk, dgv, dt, device):
+                   w, dq, dk, dv, drq, dgk, dgv, dt, device, r_wt=None):
     """Writes dq/dk/dv/drq/dgk/dgv (LlattnTensor views) and returns (dgate_l, dgate_r, dr_w, dr_b): the gate
     gradients per head ([H, Dh]) or, for a shared gate, already summed over heads ([Dh]); r_out's bias
     gradient comes from the local backward (the column sums of dremote).  ``dy``: [B, T, H, Dh] with any
@@ -227,7 +227,7 @@ def _core_backward(lay: L.Layout, dy, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, 
         dR = drem
     with torch.autocast(device_type="cuda", enabled=False):
         dR2 = dR.view(B * lay.n_q, D)
-        dlat = (input_grad(dR2, r_w.to(dt)) if dt == torch.bfloat16 else torch.mm(dR2, r_w.to(dt))).view(
+        dlat = (input_grad(dR2, r_w.to(dt), w_t=r_wt) if dt == torch.bfloat16 else torch.mm(dR2, r_w.to(dt))).view(
             B, lay.n_q, Lh, Ldh)
         if dt == torch.bfloat16:
             dr_w, _ = weight_grad(dR2, lat.view(B * lay.n_q, Ld), False)
@@ -307,12 +307,17 @@ class LLAttnCore(torch.autograd.Function):
             rqv = L.view(rq, rq.stride(0), rq.stride(1), Ldh)
         gk = L.view(gkgv, gkgv.stride(0), gkgv.stride(1), Ldh)
         gv = L.view(gkgv, gkgv.stride(0), gkgv.stride(1), Ldh, Ld)
-        # cast once (or given cast): the backward's input gradient reuses it
-        r_wd = r_w_cast if r_w_cast is not None and r_w_cast.dtype == dt else r_w.detach().to(dt)
+        # cast once (or given cast, with or without its transposed copy): the backward's input gradient reuses it
+        r_wt = None
+        if isinstance(r_w_cast, (tuple, list)):
+            r_w_cast, r_wt = r_w_cast
+        if r_w_cast is None or r_w_cast.dtype != dt:
+            r_w_cast, r_wt = None, None
+        r_wd = r_w_cast if r_w_cast is not None else r_w.detach().to(dt)
         y, ol, lse, w, lat, lse_lat, R = _core_forward(lay, q, k, v, rqv, gk, gv, gl, gr, r_wd, r_b, dt, device, prof,
                                                        saved=saved)
         if saved:
-            ctx.save_for_backward(qkv, rq, gkgv, gl, gr, r_wd, lat, lse_lat, R, ol, lse, w)
+            ctx.save_for_backward(qkv, rq, gkgv, gl, gr, r_wd, r_wt, lat, lse_lat, R, ol, lse, w)
         ctx.lay, ctx.has_rb, ctx.packed, ctx.heads = lay, r_b is not None, rq is None, heads
         ctx.r_w_dtype = r_w.dtype
         ctx.gate_like = (gate_l, gate_r)
@@ -323,7 +328,7 @@ class LLAttnCore(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dy):
-        qkv, rq, gkgv, gl, gr, r_w, lat, lse_lat, R, ol, lse, w = ctx.saved_tensors
+        qkv, rq, gkgv, gl, gr, r_w, r_wt, lat, lse_lat, R, ol, lse, w = ctx.saved_tensors
         lay = ctx.lay
         dt, device = qkv.dtype, qkv.device
         H, Dh, Lh, Ldh = lay.H, lay.Dh, lay.Lh, lay.Ldh
@@ -347,7 +352,7 @@ class LLAttnCore(torch.autograd.Function):
         dgk = L.view(dgkgv, dgkgv.stride(0), dgkgv.stride(1), Ldh)
         dgv = L.view(dgkgv, dgkgv.stride(0), dgkgv.stride(1), Ldh, Ld)
         dgl, dgr, dr_w, dr_b = _core_backward(lay, dy, q, k, v, rqv, gk, gv, gl, gr, r_w, ctx.has_rb, lat, lse_lat,
-                                              R, ol, lse, w, dq, dk, dv, drq, dgk, dgv, dt, device)
+                                              R, ol, lse, w, dq, dk, dv, drq, dgk, dgv, dt, device, r_wt)
         gate_l, gate_r = ctx.gate_like
         return (dqkv, drq_t, dgkgv, _gate_grad(dgl, gate_l), _gate_grad(dgr, gate_r), dr_w.to(ctx.r_w_dtype),
                 None if dr_b is None else dr_b.to(ctx.r_b_dtype), None, None, None, None, None)

@@ -24,7 +24,7 @@ def _declared_functions():
 def test_library_exports_every_declared_symbol():
     L, lib = _lib()
     names = _declared_functions()
-    assert len(names) == 20, names
+    assert len(names) == 21, names
     for n in names:
         assert hasattr(lib, n), n
         assert n in L.SIGNATURES, f"{n} has no ctypes signature"
@@ -329,6 +329,28 @@ def test_cast_validation():
     assert rc == L.ERR_SHAPE and b"negative" in lib.llattn_last_error()
     rc = lib.llattn_cast(1, src, dst, (I64 * 1)(0), dt, None)  # nothing to copy: no launch, success
     assert rc == L.OK
+
+
+def test_cast_transposed_validation():
+    """llattn_cast_transposed takes a transposed copy only of a bf16 [rows, cols] segment with both sizes
+    multiples of 8, 16-byte aligned arrays and ld_t >= rows, and checks it before launching anything."""
+    L, lib = _lib()
+    P, I64, I32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
+    src, dst = (P * 2)(0x1000, 0x2000), (P * 2)(0x3000, 0x4000)
+    n, dt = (I64 * 2)(64 * 16, 8), (I32 * 2)(L.BF16, L.F32)
+    tdst, tld, rows = (P * 2)(0x5000, 0), (I64 * 2)(64, 0), (I32 * 2)(64, 0)
+    rc = lib.llattn_cast_transposed(2, src, dst, n, dt, tdst, None, rows, None)
+    assert rc == L.ERR_LAYOUT and b"without ld_t" in lib.llattn_last_error()
+    rc = lib.llattn_cast_transposed(2, src, dst, n, dt, tdst, tld, (I32 * 2)(60, 0), None)  # 60 does not divide
+    assert rc == L.ERR_SHAPE and b"rows = 60" in lib.llattn_last_error()
+    rc = lib.llattn_cast_transposed(2, src, dst, (I64 * 2)(4 * 16, 8), dt, tdst, tld, (I32 * 2)(4, 0), None)
+    assert rc == L.ERR_SHAPE and b"multiples of 8" in lib.llattn_last_error()
+    rc = lib.llattn_cast_transposed(2, src, dst, n, dt, tdst, (I64 * 2)(32, 0), rows, None)  # ld_t < rows
+    assert rc == L.ERR_LAYOUT and b"leading dimension" in lib.llattn_last_error()
+    rc = lib.llattn_cast_transposed(2, src, dst, n, (I32 * 2)(L.F32, L.F32), tdst, tld, rows, None)  # fp32 out
+    assert rc == L.ERR_LAYOUT and b"bf16 output" in lib.llattn_last_error()
+    rc = lib.llattn_cast_transposed(2, src, dst, n, dt, (P * 2)(0x5008, 0), tld, rows, None)  # misaligned W^T
+    assert rc == L.ERR_LAYOUT
 
 
 def test_xent_validation():

@@ -300,6 +300,37 @@ def test_pack_params_matches_torch_casts(sizes):
         assert torch.equal(outs[1], torch.cat(ts[half:]))
 
 
+@pytest.mark.parametrize("sizes", [
+    [(4224, 1408), (512, 1408)],   # config 2's qkv | rq weights: two segments of one W^T
+    [(1408, 512)],                 # r_out
+    [(8, 72), (200, 72), (64, 72)],  # ragged 64-tiles, an 8-row segment
+    [(12, 16)],                    # rows not a multiple of 8: no transposed copy
+    [(64, 64)] * 9,                # more than 8 segments: two launches
+])
+def test_pack_params_transposed_copy(sizes):
+    """llattn_cast_transposed through pack_params: the cast and its transposed copy equal torch's
+    .to(bfloat16) and .t().contiguous() bit for bit, next to a plain bf16 group and an fp32 group in the same
+    launch; with rows that are not multiples of 8 the pair carries None."""
+    from llattn_amd.linear import pack_params
+    dev = require_cuda()
+    print("case: pack transposed", sizes, flush=True)
+    g = torch.Generator(device=dev).manual_seed(7 + len(sizes))
+    ts = [torch.randn(*s, device=dev, generator=g) * 3.0 for s in sizes]
+    ts[0].view(-1)[:4] = torch.tensor([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -2.5e-39, float("inf")], device=dev)
+    plain = [torch.randn(37, device=dev, generator=g)]
+    bias = [torch.randn(24, device=dev, generator=g)]
+    (w, w_t), wp, b = pack_params([(ts, torch.bfloat16, True), (plain, torch.bfloat16), (bias, torch.float32)])
+    ref = torch.cat(ts).to(torch.bfloat16)
+    assert torch.equal(w.view(torch.int16), ref.view(torch.int16))
+    if all(s[0] % 8 == 0 and s[1] % 8 == 0 for s in sizes):
+        assert w_t is not None and w_t.is_contiguous()
+        assert torch.equal(w_t.view(torch.int16), ref.t().contiguous().view(torch.int16))
+    else:
+        assert w_t is None
+    assert torch.equal(wp.view(torch.int16), plain[0].to(torch.bfloat16).view(torch.int16))
+    assert torch.equal(b, bias[0])
+
+
 def _gelu_and_grad(u):
     uu = u.float().requires_grad_(True)
     g = torch.nn.functional.gelu(uu)
