@@ -533,6 +533,79 @@ def bench_gemm_products(args):
                     "has bf16 output and a separate column sum, ours fp32 output with the bias gradient in the pass"}
 
 
+def bench_stream_overlap(args):
+    """Whether an HBM-bound kernel and a power-bound GEMM gain from running on two streams at once: this
+    library's cast (llattn_cast: 128 Mi fp32 -> bf16, 768 MB of traffic) and the config-2 ``out`` weight
+    gradient (fp32 dy^T x over 32768 tokens with the bias gradient, split-K), timed back to back on one stream,
+    on two streams of the default priority joined by events, and on two streams restricted to disjoint halves
+    of the CUs (hipExtStreamCreateWithCUMask).  Wall time per pair over 20 pairs after 3 warm-up pairs."""
+    import ctypes
+
+    from llattn_amd.linear import pack_params, weight_grad
+
+    dev = torch.device("cuda:0")
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(11)
+    M, D = 32768, 1408
+    dy = (torch.randn(M, D, device=dev, generator=g) * 0.5).to(bf)
+    x = (torch.randn(M, D, device=dev, generator=g) * 0.5).to(bf)
+    big = torch.randn(128 << 20, device=dev, generator=g)
+
+    def gemm_op():
+        weight_grad(dy, x, True)
+
+    def hbm_op():
+        pack_params([([big], bf)])
+
+    def timed(fn, n=20):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return round((time.perf_counter() - t0) / n * 1e6, 1)
+
+    main = torch.cuda.current_stream()
+
+    def pair(s_hbm, s_gemm):
+        def f():
+            ev = torch.cuda.Event()
+            ev.record(main)
+            s_hbm.wait_event(ev)
+            s_gemm.wait_event(ev)
+            with torch.cuda.stream(s_hbm):
+                hbm_op()
+            with torch.cuda.stream(s_gemm):
+                gemm_op()
+            main.wait_stream(s_hbm)
+            main.wait_stream(s_gemm)
+        return f
+
+    res = {"gemm alone": timed(gemm_op), "hbm alone": timed(hbm_op),
+           "one stream (serial)": timed(lambda: (hbm_op(), gemm_op()))}
+    s1, s2 = torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)
+    res["two streams"] = timed(pair(s1, s2))
+    hip = ctypes.CDLL("libamdhip64.so")
+
+    def masked(words):
+        s = ctypes.c_void_p()
+        arr = (ctypes.c_uint32 * len(words))(*words)
+        rc = hip.hipExtStreamCreateWithCUMask(ctypes.byref(s), len(words), arr)
+        return torch.cuda.ExternalStream(s.value, device=dev) if rc == 0 else None
+
+    sg, sh = masked([0xFFFFFFFF] * 4 + [0] * 4), masked([0] * 4 + [0xFFFFFFFF] * 4)
+    if sg is not None and sh is not None:
+        with torch.cuda.stream(sg):
+            res["gemm alone, half the CUs"] = timed(gemm_op)
+        with torch.cuda.stream(sh):
+            res["hbm alone, half the CUs"] = timed(hbm_op)
+        res["two streams, disjoint CU halves"] = timed(pair(sh, sg))
+    log(json.dumps(res))
+    return {"stream_overlap_us": res}
+
+
 def read_traffic(config: str, kernel: str):
     """HBM bytes per call of the entry point `kernel` at `config`, as measured by the rocprofv3 --pmc
     FETCH_SIZE / WRITE_SIZE runs summarised in profiles/ (scaled by a plain copy), or None."""
@@ -562,6 +635,9 @@ def main():
     ap.add_argument("--gemm-products", action="store_true",
                     help="only time the config-2 step's GEMM products alone, ours against torch's library GEMM, "
                          "with board power and clock under sustained loops, and exit")
+    ap.add_argument("--stream-overlap", action="store_true",
+                    help="only time an HBM-bound kernel and a weight-gradient GEMM serial against two streams, "
+                         "and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -583,6 +659,9 @@ def main():
 
     if args.gemm_products:
         print(json.dumps(bench_gemm_products(args)), flush=True)
+        return
+    if args.stream_overlap:
+        print(json.dumps(bench_stream_overlap(args)), flush=True)
         return
     if args.config == "c5":
         print(json.dumps(bench_lm(args)), flush=True)
