@@ -256,6 +256,14 @@ typedef struct llattn_gemm_desc {
 size_t llattn_gemm_workspace_size(const llattn_gemm_desc* d);
 int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_t workspace_bytes, void* stream);
 
+/* The same products in fp32: C = A Bᵀ (+ bias) (+ C with accumulate) with fp32 A, B and C (c_dtype
+ * LLATTN_F32), the operand layouts of llattn_gemm (a_trans / b_trans, leading dimensions in elements,
+ * 4-byte alignment) and optionally a_rowsum (any layout here); no K split, row addends, activation or
+ * split-head C.  fp32 accumulation on v_mfma_f32_16x16x4_f32 in a fixed order, no workspace.  The
+ * reference's nn.Linear products in fp32 (models.py:80-84, 315, 333-353, 395, 462) and their autograd,
+ * for the fp32 module. */
+int32_t llattn_gemm_f32(const llattn_gemm_desc* d, void* stream);
+
 /* Column sums out[n] = sum_m x[m][n] in fp32 of a bf16 matrix x (M rows of
  * leading dimension ld): the bias gradient of a projection (sum over tokens of
  * its output gradient).  Two passes through a workspace of

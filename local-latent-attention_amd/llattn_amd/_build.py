@@ -17,7 +17,7 @@ SRC_DIR = PKG_DIR.parent / "csrc"
 INCLUDE_DIR = PKG_DIR.parents[1] / "include"
 LIB_NAME = "libllattn_gfx950.so"
 SOURCES = ("llattn_abi.cpp", "llattn_pool.hip", "llattn_latent.hip", "llattn_local.hip", "llattn_local_wide.hip",
-           "llattn_gemm.hip",
+           "llattn_gemm.hip", "llattn_gemm_f32.hip",
            "llattn_colsum.hip", "llattn_cast.hip", "llattn_norm.hip",
            "llattn_xent.hip")
 ARCH = "gfx950"

@@ -79,6 +79,7 @@ SIGNATURES = {
                                              _P]),
     "llattn_gemm_workspace_size": (_SZ, [_G]),
     "llattn_gemm": (_I32, [_G, _P, _SZ, _P]),
+    "llattn_gemm_f32": (_I32, [_G, _P]),
     "llattn_colsum_workspace_size": (_SZ, [_I32, _I32]),
     "llattn_colsum": (_I32, [_P, _I64, _I32, _I32, _P, _P, _SZ, _P]),
     "llattn_cast": (_I32, [_I32, _P, _P, _P, _P, _P]),

@@ -198,3 +198,74 @@ def colsum(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     _call("llattn_colsum", x.data_ptr(), x.stride(0), M, N, out.data_ptr(), ws.data_ptr(), nws, L.stream_ptr(x.device),
           work=M * N * 2 + N * 4)
     return out
+
+
+# ---------------------------------------------------------------------------
+# fp32 products (``llattn_gemm_f32``): the fp32 module's projections
+# ---------------------------------------------------------------------------
+
+def _check2d_f32(name: str, t: torch.Tensor) -> None:
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be a 2-D view with a contiguous inner dimension, got shape "
+                         f"{tuple(t.shape)} strides {t.stride()}")
+    if t.dtype != torch.float32:
+        raise ValueError(f"{name} must be float32 (got {t.dtype})")
+
+
+def _run_f32(M: int, N: int, K: int, A: torch.Tensor, a_trans: bool, B: torch.Tensor, b_trans: bool,
+             C: torch.Tensor, bias: torch.Tensor | None = None, accumulate: bool = False,
+             rowsum: torch.Tensor | None = None) -> None:
+    L.require_gpu(A, B, C)
+    if C.dim() != 2 or C.stride(1) != 1 or C.dtype != torch.float32:
+        raise ValueError("output must be a 2-D fp32 view with a contiguous inner dimension")
+    if bias is not None and (bias.dtype != torch.float32 or not bias.is_contiguous() or bias.numel() != N):
+        raise ValueError(f"bias must be a contiguous fp32 vector of {N} elements")
+    if rowsum is not None and (rowsum.dtype != torch.float32 or not rowsum.is_contiguous() or rowsum.numel() != M):
+        raise ValueError(f"rowsum must be a contiguous fp32 vector of {M} elements")
+    desc = L.LlattnGemmDesc(M, N, K, int(a_trans), int(b_trans), A.data_ptr(), A.stride(0), B.data_ptr(),
+                            B.stride(0), C.data_ptr(), C.stride(0), L.F32, int(accumulate),
+                            None if bias is None else bias.data_ptr(), 0,
+                            None if rowsum is None else rowsum.data_ptr())
+    from .ops import _call
+    _call("llattn_gemm_f32", ctypes.byref(desc), L.stream_ptr(C.device), work=2 * M * N * K)
+
+
+def linear_f32(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 ``x [M, K] @ w [N, K]^T (+ bias [N])`` -> ``[M, N]`` (``nn.Linear`` in fp32)."""
+    _check2d_f32("x", x)
+    _check2d_f32("w", w)
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError(f"x is [{M}, {K}] but w is {tuple(w.shape)}")
+    out = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    _run_f32(M, N, K, x, False, w, False, out, bias)
+    return out
+
+
+def matmul_nn_f32(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """fp32 ``a [M, K] @ b [K, N]`` (an input gradient ``dy W``)."""
+    _check2d_f32("a", a)
+    _check2d_f32("b", b)
+    M, K = a.shape
+    N = b.shape[1]
+    if b.shape[0] != K:
+        raise ValueError(f"a is [{M}, {K}] but b is {tuple(b.shape)}")
+    out = torch.empty((M, N), dtype=torch.float32, device=a.device)
+    _run_f32(M, N, K, a, False, b, True, out)
+    return out
+
+
+def matmul_tn_f32(a: torch.Tensor, b: torch.Tensor, rowsum: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 ``a [K, M]^T @ b [K, N]`` (a weight gradient ``dy^T x``); with ``rowsum`` (fp32 ``[M]``,
+    overwritten) also ``a.sum(0)``, the bias gradient, from the same pass."""
+    _check2d_f32("a", a)
+    _check2d_f32("b", b)
+    K, M = a.shape
+    N = b.shape[1]
+    if b.shape[0] != K:
+        raise ValueError(f"a is [{K}, {M}] but b is {tuple(b.shape)}")
+    out = torch.empty((M, N), dtype=torch.float32, device=a.device)
+    _run_f32(M, N, K, a, True, b, True, out, rowsum=rowsum)
+    return out
+

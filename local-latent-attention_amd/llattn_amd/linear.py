@@ -214,3 +214,62 @@ def project(x: torch.Tensor, *linears: torch.nn.Linear, pools=(), packed=None, h
         params += [lin.weight, lin.bias]
     out = _Project.apply(x, tuple(pools), packed, heads, *params)
     return out if pools else out[0]
+
+
+class _ProjectF32(torch.autograd.Function):
+    """fp32 ``x @ cat(W_i)^T + cat(b_i)`` with its gradients on ``llattn_gemm_f32``: the fp32 module's
+    projections (reference models.py:80-84, 315, 333-353, 395, 462 without autocast)."""
+
+    @staticmethod
+    def forward(ctx, x, *params):
+        ctx.set_materialize_grads(False)
+        ws, bs = params[0::2], params[1::2]
+        has_bias = bs[0] is not None
+        K = x.shape[-1]
+        rows = [w.shape[0] for w in ws]
+        x2 = x.reshape(-1, K)
+        if x2.dtype != torch.float32 or not x2.is_contiguous():
+            x2 = x2.float().contiguous()
+        # one copy kernel concatenates the projections that share the input (llattn_cast, fp32 -> fp32)
+        groups = [(ws, torch.float32)] + ([(bs, torch.float32)] if has_bias else [])
+        if len(ws) == 1 and all(t.is_contiguous() and t.dtype == torch.float32 for t in (ws[0], bs[0]) if t is not None):
+            wcat, bcat = ws[0].detach(), (bs[0].detach() if has_bias else None)
+        else:
+            packs = pack_params(groups)
+            wcat, bcat = packs[0], (packs[1] if has_bias else None)
+        y = gemm.linear_f32(x2, wcat, bcat)
+        ctx.save_for_backward(x2, wcat)
+        ctx.meta = (tuple(x.shape[:-1]), rows, has_bias, [w.dtype for w in ws],
+                    [None if b is None else b.dtype for b in bs], x.dtype)
+        return y.view(*x.shape[:-1], sum(rows))
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, wcat = ctx.saved_tensors
+        lead, rows, has_bias, wdt, bdt, xdt = ctx.meta
+        N, K = sum(rows), x2.shape[1]
+        if dy is None:
+            return (None, *([None] * (2 * len(rows))))
+        dy2 = dy.reshape(-1, N)
+        if dy2.dtype != torch.float32 or not dy2.is_contiguous():
+            dy2 = dy2.float().contiguous()
+        dx = gemm.matmul_nn_f32(dy2, wcat).view(*lead, K).to(xdt) if ctx.needs_input_grad[0] else None
+        db = torch.empty((N,), dtype=torch.float32, device=dy2.device) if has_bias else None
+        dw = gemm.matmul_tn_f32(dy2, x2, rowsum=db)
+        grads = []
+        o = 0
+        for n, wd, bd in zip(rows, wdt, bdt):
+            grads.append(dw[o:o + n].to(wd))
+            grads.append(None if db is None else db[o:o + n].to(bd))
+            o += n
+        return (dx, *grads)
+
+
+def project_f32(x: torch.Tensor, *linears: torch.nn.Linear) -> torch.Tensor:
+    """fp32 ``x @ [W_1; W_2; ...]^T + [b_1; b_2; ...]`` for ``nn.Linear`` layers that read the same input; every
+    product of the forward and the backward runs on ``llattn_gemm_f32`` (GPU only)."""
+    params = []
+    for lin in linears:
+        params += [lin.weight, lin.bias]
+    return _ProjectF32.apply(x, *params)
+

@@ -25,10 +25,9 @@ from typing import Optional
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from . import _lib as L
-from .linear import pack_params, project
+from .linear import pack_params, project, project_f32
 from .ops import LLAttnCore, _Prof, heads_layout_ok, pool
 
 
@@ -127,15 +126,13 @@ class LocalLatentAttentionTriton(nn.Module):
                                        packed=packed["qkv"], heads=hl)
             rq = project(pq, self.rq_proj, packed=packed["rq"])
         elif macro:
-            qkvr = self.qkv_proj(x)
-            rq = self.rq_proj(pool(x, lay.q_block, lay.n_q, L.DIV_SEG))
+            qkvr = project_f32(x, self.qkv_proj)
+            rq = project_f32(pool(x, lay.q_block, lay.n_q, L.DIV_SEG), self.rq_proj)
         elif bf16:
             qkvr, pooled = project(x, self.qkv_proj, self.rq_proj, pools=[latents], packed=packed["qkv"], heads=hl)
             rq = None
         else:
-            w = torch.cat([self.qkv_proj.weight, self.rq_proj.weight], dim=0)
-            b = None if self.qkv_proj.bias is None else torch.cat([self.qkv_proj.bias, self.rq_proj.bias], dim=0)
-            qkvr = F.linear(x, w, b)
+            qkvr = project_f32(x, self.qkv_proj, self.rq_proj)
             rq = None
         if prof is not None:
             prof.lap("qkv_ms")
@@ -143,7 +140,7 @@ class LocalLatentAttentionTriton(nn.Module):
             pooled = pool(x, *latents)
         # the pooled latents' projection (256 rows at config 2) on the MFMA GEMM as well: split-K forward,
         # bias gradient from the weight-gradient pass
-        gkgv = project(pooled, self.rkv_proj, packed=packed["rkv"]) if bf16 else self.rkv_proj(pooled)
+        gkgv = project(pooled, self.rkv_proj, packed=packed["rkv"]) if bf16 else project_f32(pooled, self.rkv_proj)
         if prof is not None:
             prof.lap("pool_ms")
         rqc = None if rq is None else rq.to(qkvr.dtype)
@@ -155,7 +152,7 @@ class LocalLatentAttentionTriton(nn.Module):
             # the gate mix runs in the local kernel's epilogue: its time is in local_attention_ms
             prof.t["gate_mix_ms"] = 0.0
             self._record_profile(prof, lay)
-        return project(y, self.out, packed=packed["out"]) if bf16 else self.out(y)
+        return project(y, self.out, packed=packed["out"]) if bf16 else project_f32(y, self.out)
 
     def _packed_weights(self, macro: bool) -> dict:
         """The bf16 copies of every projection weight that this forward multiplies with (what bf16 autocast casts

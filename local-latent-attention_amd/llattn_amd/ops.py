@@ -22,9 +22,9 @@ import ctypes
 import time
 
 import torch
-import torch.nn.functional as F
 
 from . import _lib as L
+from .gemm import linear_f32, matmul_nn_f32, matmul_tn_f32
 from .linear import input_grad, linear_fwd, weight_grad
 
 _byref = ctypes.byref
@@ -179,8 +179,9 @@ def _core_forward(lay: L.Layout, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, r_b, 
             rh = (lay.n_q, Dh, H) if _remote_heads(lay, dt) else None
             R = linear_fwd(lat.view(B * lay.n_q, Ld), r_w.to(dt), None if r_b is None else r_b.float(),
                            rh).view(B, lay.n_q, D)
-        else:
-            R = F.linear(lat.view(B, lay.n_q, Ld), r_w.to(dt), None if r_b is None else r_b.to(dt))
+        else:  # fp32: the fp32 GEMM
+            R = linear_f32(lat.view(B * lay.n_q, Ld), _contig(r_w.detach().float()),
+                           None if r_b is None else _contig(r_b.detach().float())).view(B, lay.n_q, D)
     if prof is not None:
         prof.lap("latent_attention_ms")
     y = _empty((B, T, H, Dh), dt, device)
@@ -227,12 +228,12 @@ def _core_backward(lay: L.Layout, dy, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, 
         dR = drem
     with torch.autocast(device_type="cuda", enabled=False):
         dR2 = dR.view(B * lay.n_q, D)
-        dlat = (input_grad(dR2, r_w.to(dt), w_t=r_wt) if dt == torch.bfloat16 else torch.mm(dR2, r_w.to(dt))).view(
-            B, lay.n_q, Lh, Ldh)
+        dlat = (input_grad(dR2, r_w.to(dt), w_t=r_wt) if dt == torch.bfloat16
+                else matmul_nn_f32(dR2, _contig(r_w.float()))).view(B, lay.n_q, Lh, Ldh)
         if dt == torch.bfloat16:
             dr_w, _ = weight_grad(dR2, lat.view(B * lay.n_q, Ld), False)
         else:
-            dr_w = torch.mm(dR2.t(), lat.view(B * lay.n_q, Ld))
+            dr_w = matmul_tn_f32(dR2, lat.view(B * lay.n_q, Ld))
     ws2 = _empty((L.workspace_bytes(shape, L.WS_LATENT_BWD),), torch.uint8, device)
     _call("llattn_latent_bwd", _byref(shape), _byref(rq), _byref(gk), _byref(gv), lse_lat.data_ptr(),
           _byref(L.view_bnhd(dlat)), _byref(drq), _byref(dgk), _byref(dgv), ws2.data_ptr(), ws2.numel(), stream)

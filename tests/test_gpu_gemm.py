@@ -498,3 +498,33 @@ def test_linear_split_head_output(case):
     assert _err(_from_heads(got, T, dh, n), x.float() @ w.float().T + b) < BF16_TOL
     if M * N >= 1 << 24:  # both on the persistent kernel: only the store order differs
         assert torch.equal(got, _to_heads(gemm.linear(x, w, b), T, dh, n))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 8, 1), (97, 40, 64), (64, 64, 16), (300, 264, 1000), (33, 130, 37),
+                                   (2048, 1408, 256), (256, 1024, 1408)])
+def test_gemm_f32_products(M, N, K):
+    """The fp32 products of llattn_gemm_f32 against float64 CPU references: x W^T + b, dy W (through a strided
+    view of W), dy^T x with the row sums of dy^T (the bias gradient), and accumulation into C; ragged tiles
+    and contraction lengths that are not multiples of 4 or 16 included."""
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: gemm f32", M, N, K, flush=True)
+    g = torch.Generator(device=dev).manual_seed(M * 7 + N + K)
+    x = torch.randn(M, K, device=dev, generator=g)
+    w_full = torch.randn(N, K + 8, device=dev, generator=g)
+    w = w_full[:, :K]  # leading dimension K + 8
+    b = torch.randn(N, device=dev, generator=g)
+    ref = (x.double() @ w.double().T + b.double()).float()
+    assert _err(gemm.linear_f32(x, w, b), ref) < 1e-5
+    dy = torch.randn(M, N, device=dev, generator=g)
+    assert _err(gemm.matmul_nn_f32(dy, w), (dy.double() @ w.double()).float()) < 1e-5
+    rs = torch.full((N,), float("nan"), device=dev)
+    dw = gemm.matmul_tn_f32(dy, x, rowsum=rs)
+    assert _err(dw, (dy.double().T @ x.double()).float()) < 1e-5
+    assert _err(rs, dy.double().sum(0).float()) < 1e-5
+    assert torch.equal(dw, gemm.matmul_tn_f32(dy, x))  # the same products with and without the row sums
+    out = torch.randn(M, N, device=dev, generator=g)
+    ref_acc = out.double() + x.double() @ w.double().T
+    gemm._run_f32(M, N, K, x, False, w, False, out, accumulate=True)
+    assert _err(out, ref_acc.float()) < 1e-5
+
