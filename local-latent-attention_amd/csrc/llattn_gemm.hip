@@ -411,6 +411,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
   __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));  // no DMA may land after the workgroup exits
 
   // ---- epilogue ----
+  // The lane's coordinates again, from the exec mask (mbcnt) rather than held in registers across the main
+  // loop: held, the pair was spilled to scratch before the loop and reloaded here.
+  {
+  const int lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)), r = lane & 15, g = lane >> 4;
   if constexpr (PB) {
     // Lane (r, g) holds C[m0 + wm*128 + 16i + r][n0 + wn*128 + 32p + 8g + e'] for e' = 0..7 in
     // acc[i][2p] (e' < 4) and acc[i][2p+1] (e' >= 4): one 16-byte store per (i, p), 16 rows x 64
@@ -583,6 +587,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
         else a.rowsum[row] = v;
       }
     }
+  }
   }
   }
 }

@@ -105,18 +105,21 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const DYT* __restrict_
   const int nw = gridDim.x * 4, gw = blockIdx.x * 4 + wave;
   const int per = (M + nw - 1) / nw;
   const int r0 = min(M, gw * per), r1 = min(M, r0 + per);
+  // Chunks past the row read a valid chunk (0) and are then zeroed by a select: every array element is
+  // written unconditionally, so the arrays stay in registers (element writes under a branch made the
+  // compiler keep them in scratch memory).
   float wv[NCH][4], dw[NCH][4];
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
     const int c = lane + 64 * i;
+    const bool ok = c < nq;
+    const float4 w4 = *reinterpret_cast<const float4*>(w + 4 * (ok ? c : 0));
+    wv[i][0] = ok ? w4.x : 0.f;
+    wv[i][1] = ok ? w4.y : 0.f;
+    wv[i][2] = ok ? w4.z : 0.f;
+    wv[i][3] = ok ? w4.w : 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) dw[i][e] = 0.f;
-    if (c < nq) {
-      const float4 w4 = *reinterpret_cast<const float4*>(w + 4 * c);
-      wv[i][0] = w4.x; wv[i][1] = w4.y; wv[i][2] = w4.z; wv[i][3] = w4.w;
-    } else {
-      wv[i][0] = wv[i][1] = wv[i][2] = wv[i][3] = 0.f;
-    }
   }
   const float inv_d = 1.0f / (float)D;
   // row data of the next row -- x, dy and rstd -- is loaded before the current row is computed (two
@@ -128,12 +131,14 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const DYT* __restrict_
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
       const int c = lane + 64 * i;
-      if (c < nq) {
-        ld4(xr + 4 * c, xv[i]);
-        ld4(dr + 4 * c, dv[i]);
-      } else {
+      const bool ok = c < nq;
+      float xt[4], dt[4];
+      ld4(xr + 4 * (ok ? c : 0), xt);
+      ld4(dr + 4 * (ok ? c : 0), dt);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) xv[i][e] = dv[i][e] = 0.f;
+      for (int e = 0; e < 4; ++e) {
+        xv[i][e] = ok ? xt[e] : 0.f;
+        dv[i][e] = ok ? dt[e] : 0.f;
       }
     }
   };
