@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define LLATTN_ABI_VERSION 7
+#define LLATTN_ABI_VERSION 8
 
 /* status codes */
 #define LLATTN_OK 0
@@ -212,18 +212,23 @@ typedef struct llattn_gemm_rowadd {
 #define LLATTN_ACT_MUL_AUX 2
 
 /* Split-head storage of a bf16 matrix of token rows: a [rows][ld] matrix (rows = batch x T) keeps its first
- * n * dh columns as n head slabs per sequence, [batch][n][T][dh], followed by its other ld - n * dh
- * columns as one packed [rows][ld - n * dh] block.  Element (r, c), r = b T + t, sits at
- *   ((b n + c / dh) T + t) dh + c % dh            for c < n dh,
- *   rows n dh + r (ld - n dh) + c - n dh          otherwise.
- * The forward of the block's q|k|v (| token-wise latent query) projection writes it this way (n = 3 H
- * heads of dh = Dh), so that each head of a sequence is one contiguous run for the local-attention
- * kernels, which read q, k and v by strides, in place of the packed [tokens][3 D (+ Ld)] matrix
- * (reference models.py:315-316, view(B, T, 3, H, Dh)).  T = 0: plain row-major storage. */
+ * n * dh columns as n head slabs per sequence, [batch][n][T][dh], followed by its other w = ld - n * dh
+ * columns in a block of rows * w elements: packed rows [rows][w] (tail_dh = 0), or w / tail_dh slabs of
+ * tail_dh columns, [batch][w / tail_dh][T][tail_dh] (tail_dh > 0).  Element (r, c), r = b T + t, sits at
+ *   ((b n + c / dh) T + t) dh + c % dh                                  for c < n dh,
+ *   rows n dh + r w + c'                                                 (tail_dh = 0),
+ *   rows n dh + ((b w / tail_dh + c' / tail_dh) T + t) tail_dh + c' % tail_dh   (tail_dh > 0),
+ * with c' = c - n dh.  The forward of the block's q|k|v (| token-wise latent query) projection writes it
+ * this way (n = 3 H heads of dh = Dh, the latent queries as Lh slabs of tail_dh = Ldh), so that each head
+ * of a sequence is one contiguous run for the attention kernels, which read q, k, v and the latent queries
+ * by strides, in place of the packed [tokens][3 D (+ Ld)] matrix (reference models.py:315-316,
+ * view(B, T, 3, H, Dh), and models.py:348-353, view(B, T, Lh, Ldh).transpose(1, 2)).  T = 0: plain row-major
+ * storage. */
 typedef struct llattn_heads_layout {
-  int32_t T;   /* rows per sequence; 0: none */
-  int32_t dh;  /* columns per head, a multiple of 8 */
-  int32_t n;   /* head slabs per sequence */
+  int32_t T;        /* rows per sequence; 0: none */
+  int32_t dh;       /* columns per head, a multiple of 8 */
+  int32_t n;        /* head slabs per sequence */
+  int32_t tail_dh;  /* 0: the other columns as packed rows; else their slab width, a multiple of 8 */
 } llattn_heads_layout;
 
 typedef struct llattn_gemm_desc {

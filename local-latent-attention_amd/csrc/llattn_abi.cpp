@@ -91,6 +91,14 @@ int32_t heads_map(const char* who, const llattn_heads_layout* l, int64_t rows, i
   magic_div((uint32_t)l->dh, &out->md, &out->sd);
   out->tail = (uint32_t)(rows * cols);
   out->tail_ld = (int)(ld - cols);
+  if (l->tail_dh != 0) {
+    if (l->tail_dh < 0 || l->tail_dh % 8 || (ld - cols) % l->tail_dh)
+      return fail(LLATTN_ERR_LAYOUT, "%s: split-head tail slabs of %d columns: needs a positive multiple of 8 that "
+                  "divides the %lld columns past the heads (ld %lld)", who, l->tail_dh, (long long)(ld - cols),
+                  (long long)ld);
+    out->tdh = l->tail_dh;
+    magic_div((uint32_t)l->tail_dh, &out->mtd, &out->std);
+  }
   return LLATTN_OK;
 }
 

@@ -41,8 +41,10 @@ size_t latent_workspace_bytes(const llattn_shape* s);
 struct HeadsMap {
   int T, dh, n, cols;       // cols = n dh; T = 0: plain row-major storage
   uint32_t mt, st, md, sd;  // reciprocals of T and dh
-  uint32_t tail;            // element offset of the packed block: rows * cols
-  int tail_ld;              // its row length: ld - cols
+  uint32_t tail;            // element offset of the block of the other columns: rows * cols
+  int tail_ld;              // their number per row: ld - cols
+  int tdh;                  // 0: that block as packed rows; else as slabs of tdh columns
+  uint32_t mtd, std;        // reciprocal of tdh
 };
 // The reciprocal (m, s) of a divisor 1 <= d < 2^31.
 void magic_div(uint32_t d, uint32_t* m, uint32_t* s);

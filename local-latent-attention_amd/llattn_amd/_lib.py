@@ -16,7 +16,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libllattn_gfx950.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 OK, ERR_SHAPE, ERR_DTYPE, ERR_LAYOUT, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_LAUNCH = range(7)
 F32, BF16 = 0, 1
@@ -45,7 +45,7 @@ class LlattnGemmRowadd(ctypes.Structure):
 
 class LlattnHeadsLayout(ctypes.Structure):
     """Split-head storage of a token-row matrix (include/llattn.h llattn_heads_layout); T = 0: row-major."""
-    _fields_ = [("T", ctypes.c_int32), ("dh", ctypes.c_int32), ("n", ctypes.c_int32)]
+    _fields_ = [("T", ctypes.c_int32), ("dh", ctypes.c_int32), ("n", ctypes.c_int32), ("tail_dh", ctypes.c_int32)]
 
 
 class LlattnGemmDesc(ctypes.Structure):

@@ -10,9 +10,9 @@ transpose copy (all operands bf16, fp32 accumulation):
 Each takes 2-D views whose innermost dimension is contiguous; outputs may be
 passed in (``out=``) and accumulated into (``accumulate=True``).
 
-Split-head output: ``linear(..., heads=(T, dh, n))`` stores the ``[tokens, width]`` product with its first
-``n * dh`` columns as per-sequence head slabs ``[batch][n][T][dh]`` followed by the other columns packed
-(``llattn_heads_layout`` of the C ABI).  The tensor returned is the ``[tokens, width]`` view of that storage;
+Split-head output: ``linear(..., heads=(T, dh, n[, tail_dh]))`` stores the ``[tokens, width]`` product with its
+first ``n * dh`` columns as per-sequence head slabs ``[batch][n][T][dh]`` followed by the other columns, packed
+or (``tail_dh``) as slabs ``[batch][(width - n dh) / tail_dh][T][tail_dh]`` (``llattn_heads_layout`` of the C ABI).  The tensor returned is the ``[tokens, width]`` view of that storage;
 it is read by strides (the local-attention kernels), not as a row-major matrix.
 """
 from __future__ import annotations
@@ -33,7 +33,7 @@ def _check2d(name: str, t: torch.Tensor) -> None:
 
 
 def _heads(h) -> L.LlattnHeadsLayout:
-    return L.LlattnHeadsLayout(0, 0, 0) if h is None else L.LlattnHeadsLayout(*h)
+    return L.LlattnHeadsLayout(0, 0, 0, 0) if h is None else L.LlattnHeadsLayout(*h)
 
 
 def _run(M: int, N: int, K: int, A: torch.Tensor, a_trans: bool, B: torch.Tensor, b_trans: bool, C: torch.Tensor,
@@ -149,20 +149,29 @@ def transpose(w: torch.Tensor) -> torch.Tensor:
 ROWADD_PERSISTENT = True
 
 
-def input_grad(dy: torch.Tensor, w: torch.Tensor, rowadd=(), w_t: torch.Tensor | None = None) -> torch.Tensor:
+def input_grad_persistent(M: int, N: int, K: int, rowadd=()) -> bool:
+    """Whether :func:`input_grad` of ``dy [M, N]`` and ``w [N, K]`` runs on the persistent kernel."""
+    return (not rowadd or ROWADD_PERSISTENT) and M >= 4096 and K % 8 == 0 and N % 8 == 0 and N > 64
+
+
+def input_grad(dy: torch.Tensor, w: torch.Tensor, rowadd=(), w_t: torch.Tensor | None = None,
+               heads=None) -> torch.Tensor:
     """``dy [M, N] @ w [N, K]`` (+ the ``rowadd`` addends of :func:`matmul_nn`) -> bf16 ``[M, K]``, the input
-    gradient of ``y = x w^T``.  For large M as ``dy (w^T)^T`` on the persistent kernel with a transposed copy of
-    ``w`` (both operands k-contiguous: plain LDS fragment reads, the epilogue overlapped with the next tile):
-    ``w_t`` when the caller has it (``llattn_cast_transposed`` writes it with the weight cast), else made here;
-    otherwise :func:`matmul_nn` (transposing fragment reads of ``w``).  All routes give the same bits."""
+    gradient of ``y = x w^T``.  For large M (:func:`input_grad_persistent`) as ``dy (w^T)^T`` on the persistent
+    kernel with a transposed copy of ``w`` (both operands k-contiguous: plain LDS fragment reads, the epilogue
+    overlapped with the next tile): ``w_t`` when the caller has it (``llattn_cast_transposed`` writes it with the
+    weight cast), else made here; otherwise :func:`matmul_nn` (transposing fragment reads of ``w``).  All routes
+    give the same bits.  ``heads``: the output stored split-head as :func:`linear` does (persistent route only)."""
     M, N = dy.shape
     K = w.shape[1]
-    if (not rowadd or ROWADD_PERSISTENT) and M >= 4096 and K % 8 == 0 and N % 8 == 0 and N > 64:
+    if input_grad_persistent(M, N, K, rowadd):
         if w_t is None:
             w_t = transpose(w)
         elif tuple(w_t.shape) != (K, N):
             raise ValueError(f"w_t is {tuple(w_t.shape)}, expected the transpose of w {tuple(w.shape)}")
-        return linear(dy, w_t, rowadd=rowadd)
+        return linear(dy, w_t, rowadd=rowadd, heads=heads)
+    if heads is not None:
+        raise ValueError(f"a split-head input gradient needs the persistent kernel (M={M}, N={N}, K={K})")
     return matmul_nn(dy, w, rowadd=rowadd)
 
 

@@ -84,11 +84,12 @@ def linear_fwd(x2: torch.Tensor, w: torch.Tensor, b32: torch.Tensor | None, head
     return gemm.linear(x2, w, b32, heads=heads)
 
 
-def input_grad(dy2: torch.Tensor, w: torch.Tensor, rowadd=(), w_t: torch.Tensor | None = None) -> torch.Tensor:
+def input_grad(dy2: torch.Tensor, w: torch.Tensor, rowadd=(), w_t: torch.Tensor | None = None,
+               heads=None) -> torch.Tensor:
     """bf16 ``dy2 @ w`` (w [N, K] read row-major), plus the broadcast ``rowadd`` pooling gradients
     added in the GEMM's epilogue (:func:`llattn_amd.gemm.input_grad`; ``w_t``: ``w``'s transposed copy from
-    :func:`pack_params`, if made)."""
-    return gemm.input_grad(dy2, w, rowadd=rowadd, w_t=w_t)
+    :func:`pack_params`, if made; ``heads``: the output stored split-head)."""
+    return gemm.input_grad(dy2, w, rowadd=rowadd, w_t=w_t, heads=heads)
 
 
 def weight_grad(dy2: torch.Tensor, x2: torch.Tensor, bias_grad: bool = False):
@@ -206,9 +207,10 @@ def project(x: torch.Tensor, *linears: torch.nn.Linear, pools=(), packed=None, h
     ``pools`` the projection alone is returned.  ``packed``: ``(bf16 [sum N_i, K] weights, fp32 biases or None)``
     already cast and concatenated (:func:`pack_params`), so a caller casts all its weights in one launch; a
     third entry, the bf16 ``[K, sum N_i]`` transposed weights (or None), feeds the input gradient.
-    ``heads``: ``(T, dh, n)`` -- the output ``[B, T, N]`` is stored split-head (its first ``n * dh`` columns as
-    ``[B][n][T][dh]`` slabs, the rest packed after them; :mod:`llattn_amd.gemm`), for a consumer that reads it
-    by strides (:class:`llattn_amd.ops.LLAttnCore`); its gradient comes back as a plain row-major tensor."""
+    ``heads``: ``(T, dh, n[, tail_dh])`` -- the output ``[B, T, N]`` is stored split-head (its first ``n * dh``
+    columns as ``[B][n][T][dh]`` slabs, the rest after them, packed or as slabs of ``tail_dh`` columns;
+    :mod:`llattn_amd.gemm`), for a consumer that reads it by strides (:class:`llattn_amd.ops.LLAttnCore`); its
+    gradient comes back as a plain row-major tensor."""
     params = []
     for lin in linears:
         params += [lin.weight, lin.bias]

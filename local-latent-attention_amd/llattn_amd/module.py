@@ -116,10 +116,10 @@ class LocalLatentAttentionTriton(nn.Module):
         latents = (lay.chunk, lay.n_chunks, L.DIV_COUNT)
         pooled = None
         packed = self._packed_weights(macro) if bf16 else {}
-        # bf16: q|k|v stored split-head -- each head of a sequence one contiguous run for the local-attention
-        # kernels, written and read in that order by the projection's GEMMs
+        # bf16: q|k|v (and token-wise latent queries) stored split-head -- each head of a sequence one contiguous
+        # run for the attention kernels, written and read in that order by the projection's GEMMs
         heads = bf16 and heads_layout_ok(lay, D, not macro)
-        hl = (T, lay.Dh, 3 * self.n_heads) if heads else None
+        hl = (T, lay.Dh, 3 * self.n_heads, 0 if macro else lay.Ldh) if heads else None
         if macro and bf16:
             # both poolings of x ride on the projection, whose backward adds their gradients in place
             qkvr, pq, pooled = project(x, self.qkv_proj, pools=[(lay.q_block, lay.n_q, L.DIV_SEG), latents],

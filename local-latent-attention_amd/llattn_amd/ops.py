@@ -24,7 +24,7 @@ import time
 import torch
 
 from . import _lib as L
-from .gemm import linear_f32, matmul_nn_f32, matmul_tn_f32
+from .gemm import input_grad_persistent, linear_f32, matmul_nn_f32, matmul_tn_f32
 from .linear import input_grad, linear_fwd, weight_grad
 
 _byref = ctypes.byref
@@ -151,6 +151,16 @@ def _remote_heads(lay: L.Layout, dt) -> bool:
         lay.B * lay.n_q * lay.H * lay.Dh * 2 < (1 << 31)
 
 
+def _latent_grad_heads(lay: L.Layout) -> bool:
+    """Whether the bf16 gradient of the latent output [B, n_q, Ld] is stored split-head ([B][Lh][n_q][Ldh]
+    slabs): where ``r_out``'s input gradient runs on the persistent kernel with at least 224 output tiles of
+    256 x 256 (row-major it then runs there unsplit too, so both layouts hold the same bits; with fewer tiles a
+    row-major product is split over k), below 2 GiB."""
+    D, Ld, M = lay.H * lay.Dh, lay.Lh * lay.Ldh, lay.B * lay.n_q
+    return input_grad_persistent(M, D, Ld) and lay.Ldh % 8 == 0 and D > 64 and M * Ld * 2 < (1 << 31) and \
+        ((M + 255) // 256) * ((Ld + 255) // 256) >= 224
+
+
 def _remote_view(lay: L.Layout, R: torch.Tensor, heads: bool) -> L.LlattnTensor:
     if heads:
         return L.view(R, lay.H * lay.n_q * lay.Dh, lay.Dh, lay.n_q * lay.Dh)
@@ -228,15 +238,21 @@ def _core_backward(lay: L.Layout, dy, q, k, v, rq, gk, gv, gate_l, gate_r, r_w, 
         dR = drem
     with torch.autocast(device_type="cuda", enabled=False):
         dR2 = dR.view(B * lay.n_q, D)
-        dlat = (input_grad(dR2, r_w.to(dt), w_t=r_wt) if dt == torch.bfloat16
-                else matmul_nn_f32(dR2, _contig(r_w.float()))).view(B, lay.n_q, Lh, Ldh)
+        # bf16: the latent output's gradient stored as [B][Lh][n_q][Ldh] slabs, so that the latent backward reads
+        # each latent head of a sequence as one contiguous run
+        lh = dt == torch.bfloat16 and _latent_grad_heads(lay)
+        if dt == torch.bfloat16:
+            dlat = input_grad(dR2, r_w.to(dt), w_t=r_wt, heads=(lay.n_q, Ldh, Lh) if lh else None)
+        else:
+            dlat = matmul_nn_f32(dR2, _contig(r_w.float()))
+        dlat_v = L.view(dlat, Lh * lay.n_q * Ldh, Ldh, lay.n_q * Ldh) if lh else L.view_bnhd(dlat.view(B, lay.n_q, Lh, Ldh))
         if dt == torch.bfloat16:
             dr_w, _ = weight_grad(dR2, lat.view(B * lay.n_q, Ld), False)
         else:
             dr_w = matmul_tn_f32(dR2, lat.view(B * lay.n_q, Ld))
     ws2 = _empty((L.workspace_bytes(shape, L.WS_LATENT_BWD),), torch.uint8, device)
     _call("llattn_latent_bwd", _byref(shape), _byref(rq), _byref(gk), _byref(gv), lse_lat.data_ptr(),
-          _byref(L.view_bnhd(dlat)), _byref(drq), _byref(dgk), _byref(dgv), ws2.data_ptr(), ws2.numel(), stream)
+          _byref(dlat_v), _byref(drq), _byref(dgk), _byref(dgv), ws2.data_ptr(), ws2.numel(), stream)
     return dgl, dgr, dr_w, dr_b
 
 
@@ -250,8 +266,8 @@ def _gate_grad(dg: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
 
 def _qkv_views(lay: L.Layout, qkv: torch.Tensor, token_rq: bool, heads: bool):
     """q, k, v (and, for token-wise latent queries, rq) views of the projection output ``qkv`` [B, T, 3D (+Ld)]:
-    packed rows (``view(B, T, 3, H, Dh)``, reference models.py:315-316) or, with ``heads``, split-head storage
-    -- the 3H heads as ``[B][3H][T][Dh]`` slabs, then the latent queries packed as ``[B T][Ld]``."""
+    packed rows (``view(B, T, 3, H, Dh)``, reference models.py:315-316, 348-353) or, with ``heads``, split-head
+    storage -- the 3H heads as ``[B][3H][T][Dh]`` slabs, then the latent queries as ``[B][Lh][T][Ldh]`` slabs."""
     B, T, H, Dh, Ldh = lay.B, lay.T, lay.H, lay.Dh, lay.Ldh
     D, Ld = H * Dh, lay.Lh * Ldh
     if not heads:
@@ -259,7 +275,7 @@ def _qkv_views(lay: L.Layout, qkv: torch.Tensor, token_rq: bool, heads: bool):
         q, k, v = (L.view(qkv, sb, sn, Dh, i * D) for i in range(3))
         return q, k, v, (L.view(qkv, sb, sn, Ldh, 3 * D) if token_rq else None)
     q, k, v = (L.view(qkv, 3 * H * T * Dh, Dh, T * Dh, i * H * T * Dh) for i in range(3))
-    return q, k, v, (L.view(qkv, T * Ld, Ld, Ldh, B * T * 3 * D) if token_rq else None)
+    return q, k, v, (L.view(qkv, T * Ld, Ldh, T * Ldh, B * T * 3 * D) if token_rq else None)
 
 
 def heads_layout_ok(lay: L.Layout, d_model: int, token_rq: bool) -> bool:
@@ -267,7 +283,8 @@ def heads_layout_ok(lay: L.Layout, d_model: int, token_rq: bool) -> bool:
     GEMM writes it from its persistent kernel (d_model > 64), all of it below 2 GiB."""
     D = lay.H * lay.Dh
     width = 3 * D + (lay.Lh * lay.Ldh if token_rq else 0)
-    return d_model > 64 and lay.Dh % 8 == 0 and width % 8 == 0 and lay.B * lay.T * width * 2 < (1 << 31)
+    return d_model > 64 and lay.Dh % 8 == 0 and lay.Ldh % 8 == 0 and width % 8 == 0 and \
+        lay.B * lay.T * width * 2 < (1 << 31)
 
 
 class LLAttnCore(torch.autograd.Function):
@@ -280,7 +297,7 @@ class LLAttnCore(torch.autograd.Function):
     (reference models.py:333-342); the shared gate weights [1, Dh] (or per-head
     [H, Dh]); ``r_out`` weight [D, Ld] and bias [D].  Returns the gate-mixed
     heads [B, T, D] ready for the output projection (reference models.py:438).
-    ``heads``: ``qkv`` is stored split-head (``project(..., heads=(T, Dh, 3H))``); the gradient returned for
+    ``heads``: ``qkv`` is stored split-head (``project(..., heads=(T, Dh, 3H, Ldh))``); the gradient returned for
     it is a plain row-major [B, T, 3D (+Ld)] tensor either way.
     """
 

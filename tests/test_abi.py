@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_empty_error():
     L, lib = _lib()
-    assert lib.llattn_abi_version() == L.ABI_VERSION == 7
+    assert lib.llattn_abi_version() == L.ABI_VERSION == 8
 
 
 def test_struct_layouts_match_header(tmp_path):
@@ -268,10 +268,14 @@ def test_gemm_rowsum_validation(kw, msg):
     ((2048, 84, 48), {}, 3, b"multiple of 8"),
     ((3000, 88, 48), {}, 3, b"whole sequences"),
     ((2048, 88, 60), {}, 3, b"head columns"),
+    ((2048, 88, 48, 12), {}, 3, b"tail slabs"),
+    ((2048, 88, 48, 24), {}, 3, b"tail slabs"),
+    ((2048, 88, 48, -64), {}, 3, b"tail slabs"),
 ])
 def test_gemm_split_head_c_validation(hl, kw, code, msg):
     """A split-head C (the q|k|v projection output stored as head slabs) only comes from the persistent
-    kernel's path, with whole sequences and 8-aligned heads that fit the output width."""
+    kernel's path, with whole sequences, 8-aligned heads that fit the output width and tail slabs that divide
+    the columns past the heads."""
     L, lib = _lib()
     base = dict(M=32768, N=4736, K=1408, a_trans=0, b_trans=0, lda=1408, ldb=1408, ldc=4736, c_dtype=L.BF16)
     base.update(kw)

@@ -456,30 +456,41 @@ def test_input_grad_rowadd_persistent_equals_tiled(B, T, N, K, pools, bitwise):
 
 # ---- split-head operands (llattn_heads_layout): the q|k|v projection output stored as head slabs ----
 
-def _to_heads(x: torch.Tensor, T: int, dh: int, n: int) -> torch.Tensor:
+def _to_heads(x: torch.Tensor, T: int, dh: int, n: int, tdh: int = 0) -> torch.Tensor:
     """Row-major [B T, W] -> the same matrix in split-head storage, as a [B T, W] tensor: the first n dh
-    columns as [B][n][T][dh] slabs, then the other columns packed [B T][W - n dh] (torch permute, independent
-    of the kernels' offset arithmetic)."""
+    columns as [B][n][T][dh] slabs, then the other columns packed [B T][W - n dh] (tdh = 0) or as
+    [B][(W - n dh) / tdh][T][tdh] slabs (torch permute, independent of the kernels' offset arithmetic)."""
     R, W = x.shape
     B, c = R // T, n * dh
     head = x[:, :c].reshape(B, T, n, dh).permute(0, 2, 1, 3).reshape(-1)
-    return torch.cat([head, x[:, c:].reshape(-1)]).view(R, W)
+    rest = x[:, c:]
+    if tdh:
+        rest = rest.reshape(B, T, (W - c) // tdh, tdh).permute(0, 2, 1, 3)
+    return torch.cat([head, rest.reshape(-1)]).view(R, W)
 
 
-def _from_heads(s: torch.Tensor, T: int, dh: int, n: int) -> torch.Tensor:
+def _from_heads(s: torch.Tensor, T: int, dh: int, n: int, tdh: int = 0) -> torch.Tensor:
     R, W = s.shape
     B, c = R // T, n * dh
     flat = s.reshape(-1)
     head = flat[:R * c].view(B, n, T, dh).permute(0, 2, 1, 3).reshape(R, c)
-    return torch.cat([head, flat[R * c:].view(R, W - c)], dim=1)
+    rest = flat[R * c:]
+    rest = rest.view(B, (W - c) // tdh, T, tdh).permute(0, 2, 1, 3).reshape(R, W - c) if tdh else rest.view(R, W - c)
+    return torch.cat([head, rest], dim=1)
 
 
-HEADS_CASES = [  # (B, T, dh, n, tail, K): head columns n dh, plus `tail` packed columns; K the contraction
-    (2, 160, 32, 6, 64, 192),
-    (3, 97, 88, 12, 0, 136),      # T not a multiple of 32 or 256: slabs start inside tiles and k steps
-    (2, 300, 16, 6, 512, 256),
-    (1, 64, 64, 3, 8, 72),
-    (16, 2048, 88, 48, 512, 1408),  # config 2: q|k|v|rq of the 0.55b layer
+HEADS_CASES = [  # (B, T, dh, n, tail, K, tdh): head columns n dh, plus `tail` columns (packed, or as slabs of tdh
+    # columns); K the contraction
+    (2, 160, 32, 6, 64, 192, 0),
+    (3, 97, 88, 12, 0, 136, 0),      # T not a multiple of 32 or 256: slabs start inside tiles and k steps
+    (2, 300, 16, 6, 512, 256, 0),
+    (1, 64, 64, 3, 8, 72, 0),
+    (16, 2048, 88, 48, 512, 1408, 0),  # config 2's q|k|v|rq with the latent queries packed
+    (2, 160, 32, 6, 64, 192, 16),
+    (3, 97, 88, 12, 96, 136, 24),    # tail slabs that start inside tiles, heads not a multiple of 16 wide
+    (2, 300, 16, 6, 512, 256, 64),
+    (16, 2048, 88, 48, 512, 1408, 64),  # config 2: q|k|v|rq of the 0.55b layer
+    (16, 2048, 64, 8, 0, 1408, 0),   # config 2: the latent output's gradient as Lh slabs
 ]
 
 
@@ -487,17 +498,35 @@ HEADS_CASES = [  # (B, T, dh, n, tail, K): head columns n dh, plus `tail` packed
 def test_linear_split_head_output(case):
     """The persistent kernel's stores in split-head order: the same product as the row-major output."""
     from llattn_amd import gemm
-    B, T, dh, n, tail, K = case
+    B, T, dh, n, tail, K, tdh = case
     dev = require_cuda()
     print("case: linear split-head C", case, flush=True)
-    g = torch.Generator(device=dev).manual_seed(B * T + dh + n + tail)
+    g = torch.Generator(device=dev).manual_seed(B * T + dh + n + tail + tdh)
     M, N = B * T, n * dh + tail
     x, w = _rand(M, K, gen=g, dev=dev), _rand(N, K, gen=g, dev=dev)
     b = torch.randn(N, device=dev, generator=g)
-    got = gemm.linear(x, w, b, heads=(T, dh, n))
-    assert _err(_from_heads(got, T, dh, n), x.float() @ w.float().T + b) < BF16_TOL
+    got = gemm.linear(x, w, b, heads=(T, dh, n, tdh))
+    assert _err(_from_heads(got, T, dh, n, tdh), x.float() @ w.float().T + b) < BF16_TOL
     if M * N >= 1 << 24:  # both on the persistent kernel: only the store order differs
-        assert torch.equal(got, _to_heads(gemm.linear(x, w, b), T, dh, n))
+        assert torch.equal(got, _to_heads(gemm.linear(x, w, b), T, dh, n, tdh))
+
+
+def test_input_grad_split_head_output():
+    """The input gradient on the persistent kernel stored as head slabs (the latent output's gradient of
+    config 2, [B][Lh][n_q][Ldh]): the same bits as the row-major input gradient (256 output tiles: unsplit on
+    the persistent kernel too), permuted; the small-M route refuses a split-head output."""
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: input_grad split-head", flush=True)
+    g = torch.Generator(device=dev).manual_seed(5)
+    B, T, Lh, Ldh, D = 16, 2048, 8, 64, 1408
+    dy, w = _rand(B * T, D, gen=g, dev=dev), _rand(D, Lh * Ldh, gen=g, dev=dev)
+    plain = gemm.input_grad(dy, w)
+    got = gemm.input_grad(dy, w, heads=(T, Ldh, Lh))
+    assert torch.equal(got, _to_heads(plain, T, Ldh, Lh))
+    assert _err(plain, dy.float() @ w.float()) < BF16_TOL
+    with pytest.raises(ValueError, match="persistent"):
+        gemm.input_grad(dy[:1024], w, heads=(1024, Ldh, Lh))
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 8, 1), (97, 40, 64), (64, 64, 16), (300, 264, 1000), (33, 130, 37),

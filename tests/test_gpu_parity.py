@@ -528,15 +528,16 @@ def test_profile_stats_on_config1(c1_golden, bf16):
     assert m.get_profile_stats() == {}
 
 
-@pytest.mark.parametrize("cfg", ["c2_b2", "macro"])
+@pytest.mark.parametrize("cfg", ["c2_b2", "c2_b16", "macro"])
 def test_split_head_qkv_matches_packed_layout(cfg, monkeypatch):
-    """bf16 module forward + backward with the q|k|v projection and r_out's output stored split-head (the
-    default) against packed rows: only addresses differ, so the output and every gradient agree bit for bit."""
+    """bf16 module forward + backward with the q|k|v|rq projection, r_out's output and the latent output's
+    gradient stored split-head (the default) against packed rows: only addresses differ, so the output and every
+    gradient agree bit for bit."""
     import llattn_amd.module as mod
     import llattn_amd.ops as ops
     dev = require_cuda()
-    if cfg == "c2_b2":
-        shape, B, T = _c2_shape(), 2, 2048
+    if cfg.startswith("c2"):
+        shape, B, T = _c2_shape(), int(cfg[4:]), 2048
     else:
         shape = orc.BlockShape(d_model=256, n_heads=4, window=96, local_block_size=64, latent_tokens=24,
                                latent_d_model=128, latent_heads=2, latent_query_block_size=16)
@@ -550,8 +551,10 @@ def test_split_head_qkv_matches_packed_layout(cfg, monkeypatch):
     dout = torch.randn(B, T, shape.d_model, device=dev)
     a = run_module(m, x, dout, autocast_bf16=True)
     assert ops._remote_heads(lay, torch.bfloat16)
+    assert ops._latent_grad_heads(lay) == (cfg == "c2_b16")
     monkeypatch.setattr(mod, "heads_layout_ok", lambda *args: False)
     monkeypatch.setattr(ops, "_remote_heads", lambda *args: False)
+    monkeypatch.setattr(ops, "_latent_grad_heads", lambda *args: False)
     b = run_module(m, x, dout, autocast_bf16=True)
     np.testing.assert_array_equal(a[0], b[0])
     np.testing.assert_array_equal(a[1], b[1])
