@@ -105,7 +105,7 @@ def weight_grad(dy2: torch.Tensor, x2: torch.Tensor, bias_grad: bool = False):
 
 class _Project(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, pools, packed, heads, *params):
+    def forward(ctx, x, pools, packed, heads, grad_heads, *params):
         # packed: (bf16 weights, fp32 biases[, bf16 transposed weights]) already concatenated by pack_params,
         # or None
         ctx.set_materialize_grads(False)
@@ -151,6 +151,7 @@ class _Project(torch.autograd.Function):
         ctx.save_for_backward(x2, wcat, wcat_t)
         ctx.meta = (tuple(x.shape[:-1]), rows, has_bias, [w.dtype for w in ws], [None if b is None else b.dtype
                                                                                  for b in bs], x.dtype, tuple(pools))
+        ctx.grad_heads = grad_heads
         return (y.view(*x.shape[:-1], sum(rows)), *pooled)
 
     @staticmethod
@@ -175,7 +176,7 @@ class _Project(torch.autograd.Function):
                             if g is not None:
                                 rowadd.append((_contig(g).view(-1, K), lead[1], seg, n_seg, divisor))
                         dpooled = ()
-                    dx = input_grad(dy2, wcat, rowadd, wcat_t).view(*lead, K).to(xdt)
+                    dx = input_grad(dy2, wcat, rowadd, wcat_t, heads=ctx.grad_heads).view(*lead, K).to(xdt)
                 dw, db = weight_grad(dy2, x2, has_bias)
             if ctx.needs_input_grad[0] and any(g is not None for g in dpooled):
                 # pooling backward accumulates straight into the projection's input gradient
@@ -193,10 +194,10 @@ class _Project(torch.autograd.Function):
             grads.append(None if dw is None else dw[o:o + n].to(wd))
             grads.append(None if db is None else db[o:o + n].to(bd))
             o += n
-        return (dx, None, None, None, *grads)
+        return (dx, None, None, None, None, *grads)
 
 
-def project(x: torch.Tensor, *linears: torch.nn.Linear, pools=(), packed=None, heads=None):
+def project(x: torch.Tensor, *linears: torch.nn.Linear, pools=(), packed=None, heads=None, grad_heads=None):
     """bf16 ``x @ [W_1; W_2; ...]^T + [b_1; b_2; ...]`` (all layers share the input width); backward gives
     fp32 weight and bias gradients in the parameters' dtypes.  Every product (forward, input and weight
     gradient) runs on the gfx950 MFMA GEMM; shapes it does not take raise.
@@ -210,11 +211,16 @@ def project(x: torch.Tensor, *linears: torch.nn.Linear, pools=(), packed=None, h
     ``heads``: ``(T, dh, n[, tail_dh])`` -- the output ``[B, T, N]`` is stored split-head (its first ``n * dh``
     columns as ``[B][n][T][dh]`` slabs, the rest after them, packed or as slabs of ``tail_dh`` columns;
     :mod:`llattn_amd.gemm`), for a consumer that reads it by strides (:class:`llattn_amd.ops.LLAttnCore`); its
-    gradient comes back as a plain row-major tensor."""
+    gradient comes back as a plain row-major tensor.  ``grad_heads``: the input gradient (bf16, on the
+    persistent kernel's route of :func:`llattn_amd.gemm.input_grad`, no poolings) is stored split-head that way
+    instead, for a producer of ``x`` whose backward reads its output gradient by strides (``dy_heads`` of
+    :class:`llattn_amd.ops.LLAttnCore`)."""
     params = []
     for lin in linears:
         params += [lin.weight, lin.bias]
-    out = _Project.apply(x, tuple(pools), packed, heads, *params)
+    if grad_heads is not None and pools:
+        raise ValueError("grad_heads: a split-head input gradient takes no pooling gradients")
+    out = _Project.apply(x, tuple(pools), packed, heads, grad_heads, *params)
     return out if pools else out[0]
 
 

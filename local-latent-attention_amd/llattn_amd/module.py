@@ -28,7 +28,7 @@ import torch.nn as nn
 
 from . import _lib as L
 from .linear import pack_params, project, project_f32
-from .ops import LLAttnCore, _Prof, heads_layout_ok, pool
+from .ops import LLAttnCore, _Prof, grad_heads_ok, heads_layout_ok, pool
 
 
 class LocalLatentAttentionTriton(nn.Module):
@@ -146,13 +146,18 @@ class LocalLatentAttentionTriton(nn.Module):
         rqc = None if rq is None else rq.to(qkvr.dtype)
         # forward only (no_grad, e.g. generation): the kernels skip what only the backward reads
         saved = torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))
+        # bf16: the output projection's input gradient comes back as [B][H][T][Dh] slabs for the local backward
+        dy_heads = bf16 and grad_heads_ok(B * T, self.d_model, D, lay.Dh)
         y = LLAttnCore.apply(qkvr, rqc, gkgv.to(qkvr.dtype), self.gate_local.weight, self.gate_remote.weight,
-                             self.r_out.weight, self.r_out.bias, lay, prof, packed.get("r_out"), saved, heads)
+                             self.r_out.weight, self.r_out.bias, lay, prof, packed.get("r_out"), saved, heads,
+                             dy_heads)
         if prof is not None:
             # the gate mix runs in the local kernel's epilogue: its time is in local_attention_ms
             prof.t["gate_mix_ms"] = 0.0
             self._record_profile(prof, lay)
-        return project(y, self.out, packed=packed["out"]) if bf16 else project_f32(y, self.out)
+        if not bf16:
+            return project_f32(y, self.out)
+        return project(y, self.out, packed=packed["out"], grad_heads=(T, lay.Dh, self.n_heads) if dy_heads else None)
 
     def _packed_weights(self, macro: bool) -> dict:
         """The bf16 copies of every projection weight that this forward multiplies with (what bf16 autocast casts

@@ -151,14 +151,19 @@ def _remote_heads(lay: L.Layout, dt) -> bool:
         lay.B * lay.n_q * lay.H * lay.Dh * 2 < (1 << 31)
 
 
+def grad_heads_ok(M: int, N: int, K: int, dh: int) -> bool:
+    """Whether a bf16 input gradient ``dy [M, N] @ w [N, K]`` can be stored split-head with heads of ``dh``
+    columns: on the persistent kernel with at least 224 output tiles of 256 x 256 (row-major it then runs there
+    unsplit too, so both layouts hold the same bits; with fewer tiles a row-major product is split over k),
+    below 2 GiB."""
+    return input_grad_persistent(M, N, K) and dh % 8 == 0 and N > 64 and M * K * 2 < (1 << 31) and \
+        ((M + 255) // 256) * ((K + 255) // 256) >= 224
+
+
 def _latent_grad_heads(lay: L.Layout) -> bool:
-    """Whether the bf16 gradient of the latent output [B, n_q, Ld] is stored split-head ([B][Lh][n_q][Ldh]
-    slabs): where ``r_out``'s input gradient runs on the persistent kernel with at least 224 output tiles of
-    256 x 256 (row-major it then runs there unsplit too, so both layouts hold the same bits; with fewer tiles a
-    row-major product is split over k), below 2 GiB."""
-    D, Ld, M = lay.H * lay.Dh, lay.Lh * lay.Ldh, lay.B * lay.n_q
-    return input_grad_persistent(M, D, Ld) and lay.Ldh % 8 == 0 and D > 64 and M * Ld * 2 < (1 << 31) and \
-        ((M + 255) // 256) * ((Ld + 255) // 256) >= 224
+    """Whether the bf16 gradient of the latent output [B, n_q, Ld] (``r_out``'s input gradient) is stored
+    split-head, as [B][Lh][n_q][Ldh] slabs."""
+    return grad_heads_ok(lay.B * lay.n_q, lay.H * lay.Dh, lay.Lh * lay.Ldh, lay.Ldh)
 
 
 def _remote_view(lay: L.Layout, R: torch.Tensor, heads: bool) -> L.LlattnTensor:
@@ -298,12 +303,14 @@ class LLAttnCore(torch.autograd.Function):
     [H, Dh]); ``r_out`` weight [D, Ld] and bias [D].  Returns the gate-mixed
     heads [B, T, D] ready for the output projection (reference models.py:438).
     ``heads``: ``qkv`` is stored split-head (``project(..., heads=(T, Dh, 3H, Ldh))``); the gradient returned for
-    it is a plain row-major [B, T, 3D (+Ld)] tensor either way.
+    it is a plain row-major [B, T, 3D (+Ld)] tensor either way.  ``dy_heads``: the gradient that the backward
+    receives for the output is stored as [B][H][T][Dh] slabs in its [B, T, D] tensor (``project(y, out,
+    grad_heads=(T, Dh, H))`` writes it so), so that the local backward reads each head as one contiguous run.
     """
 
     @staticmethod
     def forward(ctx, qkv, rq, gkgv, gate_l, gate_r, r_w, r_b, lay: L.Layout, prof=None, r_w_cast=None,
-                saved: bool = True, heads: bool = False):
+                saved: bool = True, heads: bool = False, dy_heads: bool = False):
         L.require_gpu(qkv, rq, gkgv)
         dt, device = qkv.dtype, qkv.device
         H, Dh, Lh, Ldh = lay.H, lay.Dh, lay.Lh, lay.Ldh
@@ -336,7 +343,7 @@ class LLAttnCore(torch.autograd.Function):
                                                        saved=saved)
         if saved:
             ctx.save_for_backward(qkv, rq, gkgv, gl, gr, r_wd, r_wt, lat, lse_lat, R, ol, lse, w)
-        ctx.lay, ctx.has_rb, ctx.packed, ctx.heads = lay, r_b is not None, rq is None, heads
+        ctx.lay, ctx.has_rb, ctx.packed, ctx.heads, ctx.dy_heads = lay, r_b is not None, rq is None, heads, dy_heads
         ctx.r_w_dtype = r_w.dtype
         ctx.gate_like = (gate_l, gate_r)
         ctx.r_b_dtype = None if r_b is None else r_b.dtype
@@ -351,7 +358,13 @@ class LLAttnCore(torch.autograd.Function):
         dt, device = qkv.dtype, qkv.device
         H, Dh, Lh, Ldh = lay.H, lay.Dh, lay.Lh, lay.Ldh
         D, Ld = H * Dh, Lh * Ldh
-        dy = _contig(dy.to(dt)).view(lay.B, lay.T, H, Dh)
+        if ctx.dy_heads:  # [B][H][T][Dh] slabs in the storage of a contiguous [B, T, D] tensor
+            if dy.dtype != dt or not dy.is_contiguous() or tuple(dy.shape) != (lay.B, lay.T, D):
+                raise ValueError("dy_heads: the output gradient must be the contiguous split-head tensor that its "
+                                 f"consumer's backward wrote (got {dy.dtype}, {tuple(dy.shape)}, {dy.stride()})")
+            dy = dy.view(lay.B, H, lay.T, Dh).permute(0, 2, 1, 3)
+        else:
+            dy = _contig(dy.to(dt)).view(lay.B, lay.T, H, Dh)
         q, k, v, rqv = _qkv_views(lay, qkv, rq is None, ctx.heads)
         if rq is not None:
             rqv = L.view(rq, rq.stride(0), rq.stride(1), Ldh)
@@ -373,7 +386,7 @@ class LLAttnCore(torch.autograd.Function):
                                               R, ol, lse, w, dq, dk, dv, drq, dgk, dgv, dt, device, r_wt)
         gate_l, gate_r = ctx.gate_like
         return (dqkv, drq_t, dgkgv, _gate_grad(dgl, gate_l), _gate_grad(dgr, gate_r), dr_w.to(ctx.r_w_dtype),
-                None if dr_b is None else dr_b.to(ctx.r_b_dtype), None, None, None, None, None)
+                None if dr_b is None else dr_b.to(ctx.r_b_dtype), None, None, None, None, None, None)
 
 
 # ---------------------------------------------------------------------------

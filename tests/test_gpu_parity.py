@@ -530,9 +530,9 @@ def test_profile_stats_on_config1(c1_golden, bf16):
 
 @pytest.mark.parametrize("cfg", ["c2_b2", "c2_b16", "macro"])
 def test_split_head_qkv_matches_packed_layout(cfg, monkeypatch):
-    """bf16 module forward + backward with the q|k|v|rq projection, r_out's output and the latent output's
-    gradient stored split-head (the default) against packed rows: only addresses differ, so the output and every
-    gradient agree bit for bit."""
+    """bf16 module forward + backward with the q|k|v|rq projection, r_out's output and the gradients of the
+    latent output and of the core's output stored split-head (the default) against packed rows: only addresses
+    differ, so the output and every gradient agree bit for bit."""
     import llattn_amd.module as mod
     import llattn_amd.ops as ops
     dev = require_cuda()
@@ -552,7 +552,9 @@ def test_split_head_qkv_matches_packed_layout(cfg, monkeypatch):
     a = run_module(m, x, dout, autocast_bf16=True)
     assert ops._remote_heads(lay, torch.bfloat16)
     assert ops._latent_grad_heads(lay) == (cfg == "c2_b16")
+    assert mod.grad_heads_ok(B * T, shape.d_model, shape.d_model, lay.Dh) == (cfg == "c2_b16")
     monkeypatch.setattr(mod, "heads_layout_ok", lambda *args: False)
+    monkeypatch.setattr(mod, "grad_heads_ok", lambda *args: False)
     monkeypatch.setattr(ops, "_remote_heads", lambda *args: False)
     monkeypatch.setattr(ops, "_latent_grad_heads", lambda *args: False)
     b = run_module(m, x, dout, autocast_bf16=True)
