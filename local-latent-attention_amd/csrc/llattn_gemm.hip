@@ -604,8 +604,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
 //   sub-step 1: 64 MFMAs on k 32..63, with the fragment reads of step g + 1's k 0..31 (other stage)
 //               and the 16 DMA instructions of step g + 2 (this stage).
 // The DMA runs on across tiles (the last two steps of a tile fetch the first two of the next), and the
-// epilogue stores straight from the accumulators (permuted B fragments give each lane 8 consecutive
-// columns), so a tile's output drains to memory while the next tile's first MFMAs run.  The per-lane DMA
+// epilogue stores straight from the accumulators, so a tile's output drains to memory while the next tile's
+// first MFMAs run.  B fragment block j of a wave reads the tile rows wn 128 + 8 r + j (lane r), so lane
+// (r, g) accumulates C[16 i + 4 g + e][8 r + j] in acc[i][j][e]: for each (i, e) the eight blocks j hold 8
+// consecutive columns, and one 16-byte store per lane writes 4 rows x 256 bytes (two whole cache lines per
+// row; 16 rows x 64 bytes per store took 3-8% longer).  The per-lane DMA
 // offsets do not depend on the tile or the step (both lie in the scalar buffer descriptor), so the main
 // loop does no per-lane address arithmetic.
 //
@@ -652,27 +655,29 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
 #pragma unroll
   for (int i = 0; i < PDMA; ++i) {
     const int row = 8 * (wave * PDMA + i) + (lane >> 3);
-    const int ca = (lane & 7) ^ pswz<false>(row), cb = (lane & 7) ^ pswz<true>(row);
+    // B: chunk c of row n at slot c ^ ((n >> 3) & 7), so that the eight rows 8 r + j (r = 0..7) that one
+    // LDS cycle of a fragment read serves sit in eight distinct slots
+    const int ca = (lane & 7) ^ pswz<false>(row), cb = (lane & 7) ^ ((row >> 3) & 7);
     offa[i] = (uint32_t)(((int64_t)row * a.lda + 8 * ca) * 2);
     offb[i] = (uint32_t)(((int64_t)row * a.ldb + 8 * cb) * 2);
     kca[i] = 8 * ca;
     kcb[i] = 8 * cb;
   }
-  // LDS byte offsets within a stage of this lane's fragment of sub-step h (k 32h .. 32h + 31)
-  const int arow = r, brow = 8 * (r >> 2) + (r & 3);
+  // LDS byte offsets within a stage of this lane's fragment of sub-step h (k 32h .. 32h + 31); the B row
+  // wn 128 + 8 r + j has swizzle (r & 7) for every j
+  const int arow = r, brow = 8 * r;
   uint32_t abase[2], bbase[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     abase[h] = arow * 128 + (((4 * h + g) ^ pswz<false>(arow)) << 4);
-    bbase[h] = PTILE + brow * 128 + (((4 * h + g) ^ pswz<true>(brow)) << 4);
+    bbase[h] = PTILE + brow * 128 + (((4 * h + g) ^ (r & 7)) << 4);
   }
-  // fragment block i of A (rows wm*128 + 16i ..), j of B (permuted: block pairs interleave by fours)
+  // fragment block i of A (rows wm*128 + 16i + r), j of B (rows wn*128 + 8r + j)
   auto frag_a = [&](int stage, int h, int i) {
     return *reinterpret_cast<const bf16x8*>(smem + stage * PSTAGE + abase[h] + (wm * 128 + 16 * i) * 128);
   };
   auto frag_b = [&](int stage, int h, int j) {
-    return *reinterpret_cast<const bf16x8*>(smem + stage * PSTAGE + bbase[h] +
-                                            (wn * 128 + 32 * (j >> 1) + 4 * (j & 1)) * 128);
+    return *reinterpret_cast<const bf16x8*>(smem + stage * PSTAGE + bbase[h] + (wn * 128 + j) * 128);
   };
   // DMA block q (0..7: A, 8..15: B) of a step into `stage`; klim = K - k0 of the step (K tail: a lane whose
   // chunk starts at or past K reads zero)
@@ -744,9 +749,9 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
       if (q < 8) fa1[q] = frag_a(s, 1, q);
       else fb1[q - 8] = frag_b(s, 1, q - 8);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {  // B first: lane (r, g) accumulates C[m = r][n = 4g + e]
+      for (int u = 0; u < 4; ++u) {  // lane (r, g) accumulates C[m = 4g + e][n = r] of block (i, j)
         const int n = 4 * q + u, i = n >> 3, j = n & 7;
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb0[j], fa0[i], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa0[i], fb0[j], acc[i][j], 0, 0, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -777,7 +782,7 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int n = 4 * q + u, i = n >> 3, j = n & 7;
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb1[j], fa1[i], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa1[i], fb1[j], acc[i][j], 0, 0, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -788,51 +793,44 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(wait_vm(0));  // the next tile's first two steps have landed: no store in flight yet
     bias_dma(vn < total ? n0n : n0, slot ^ 1);  // the next tile's bias, after the DMA of its 2nd step
-    // ---- epilogue: lane (r, g) holds C[m0 + wm*128 + 16i + r][n0 + wn*128 + 32p + 8g + e'],
-    //      e' = 0..7 in acc[i][2p] (e' < 4) and acc[i][2p+1] (e' >= 4) ----
-    const int rowb = m0 + wm * 128 + r, colb = n0 + wn * 128 + 8 * g;
+    // ---- epilogue: lane (r, g) holds C[m0 + wm*128 + 16i + 4g + e][n0 + wn*128 + 8r + j] in acc[i][j][e] ----
+    const int rowb = m0 + wm * 128 + 4 * g, col = n0 + wn * 128 + 8 * r;
+    float bv[8];  // this lane's 8 bias columns, the same for every row
+    {
+      const float* bl = &sbias[slot][wn * 128 + 8 * r];
+      const float4 b0 = *reinterpret_cast<const float4*>(bl), b1 = *reinterpret_cast<const float4*>(bl + 4);
+      bv[0] = b0.x; bv[1] = b0.y; bv[2] = b0.z; bv[3] = b0.w;
+      bv[4] = b1.x; bv[5] = b1.y; bv[6] = b1.z; bv[7] = b1.w;
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int row = rowb + 16 * i;
-      const uint16_t* rap[2] = {nullptr, nullptr};
-      float rsc[2] = {0.f, 0.f};
-      if constexpr (RA) {  // addend rows of this output row (rows past M are never stored)
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          if (!a.ra_ptr[q]) continue;
-          const int m = min(row, a.M - 1), T = a.ra_T[q], seg = a.ra_seg[q], t = m % T, sg = t / seg;
-          rsc[q] = a.ra_div[q] == LLATTN_DIV_COUNT ? 1.f / (float)(min((sg + 1) * seg, T) - sg * seg)
-                 : a.ra_div[q] == LLATTN_DIV_SEG ? 1.f / (float)seg : 1.f;
-          rap[q] = a.ra_ptr[q] + ((int64_t)(m / T) * a.ra_nseg[q] + sg) * a.ra_ld[q];
-        }
-      }
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const int col = colb + 32 * p;
-        const float* bl = &sbias[slot][wn * 128 + 32 * p + 8 * g];
-        const float4 b0 = *reinterpret_cast<const float4*>(bl), b1 = *reinterpret_cast<const float4*>(bl + 4);
+      for (int e = 0; e < 4; ++e) {
+        const int row = rowb + 16 * i + e;
         // the accumulators leave the AGPRs here, eight at a time: left to the compiler, all 256 were copied
         // out at the end of the main loop and the register peak pushed the loop's offsets into scratch
-        float u[4], w[4];
+        float v8[8];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(u[e]) : "a"(acc[i][2 * p][e]));
-          asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(w[e]) : "a"(acc[i][2 * p + 1][e]));
+        for (int j = 0; j < 8; ++j) {
+          asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v8[j]) : "a"(acc[i][j][e]));
+          v8[j] += bv[j];
         }
-        float v8[8] = {u[0] + b0.x, u[1] + b0.y, u[2] + b0.z, u[3] + b0.w,
-                       w[0] + b1.x, w[1] + b1.y, w[2] + b1.z, w[3] + b1.w};
-        if constexpr (RA) {  // addend rows are 8-byte aligned (two 8-byte loads per 8 columns)
-          const int cc = min(col, a.N - 8);  // columns past N are never stored
+        if constexpr (RA) {  // addend rows of this output row (rows past M are never stored; rows 8-byte aligned)
+          const int m = min(row, a.M - 1), cc = min(col, a.N - 8);  // columns past N are never stored
 #pragma unroll
           for (int q = 0; q < 2; ++q) {
             if (!a.ra_ptr[q]) continue;
+            const int T = a.ra_T[q], seg = a.ra_seg[q], t = m % T, sg = t / seg;
+            const float rsc = a.ra_div[q] == LLATTN_DIV_COUNT ? 1.f / (float)(min((sg + 1) * seg, T) - sg * seg)
+                            : a.ra_div[q] == LLATTN_DIV_SEG ? 1.f / (float)seg : 1.f;
+            const uint16_t* rap = a.ra_ptr[q] + ((int64_t)(m / T) * a.ra_nseg[q] + sg) * a.ra_ld[q];
             float lo[4] = {v8[0], v8[1], v8[2], v8[3]}, hi[4] = {v8[4], v8[5], v8[6], v8[7]};
-            add_bf16x4(*reinterpret_cast<const uint2*>(rap[q] + cc), rsc[q], lo);
-            add_bf16x4(*reinterpret_cast<const uint2*>(rap[q] + cc + 4), rsc[q], hi);
+            add_bf16x4(*reinterpret_cast<const uint2*>(rap + cc), rsc, lo);
+            add_bf16x4(*reinterpret_cast<const uint2*>(rap + cc + 4), rsc, hi);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              v8[e] = lo[e];
-              v8[4 + e] = hi[e];
+            for (int u = 0; u < 4; ++u) {
+              v8[u] = lo[u];
+              v8[4 + u] = hi[u];
             }
           }
         }
