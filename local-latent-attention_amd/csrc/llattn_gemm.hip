@@ -655,29 +655,33 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
 #pragma unroll
   for (int i = 0; i < PDMA; ++i) {
     const int row = 8 * (wave * PDMA + i) + (lane >> 3);
-    // B: chunk c of row n at slot c ^ ((n >> 3) & 7), so that the eight rows 8 r + j (r = 0..7) that one
-    // LDS cycle of a fragment read serves sit in eight distinct slots
-    const int ca = (lane & 7) ^ pswz<false>(row), cb = (lane & 7) ^ ((row >> 3) & 7);
+    // B: row n of the tile sits at LDS row position n with bits 0 and 3 swapped, its chunk c at slot
+    // c ^ ((position >> 4) & 7): the 16 rows 8 r + j (r = 0..15) of fragment block j then alternate
+    // between the two halves of the banks and take eight distinct slots in each (conflict-free; with the
+    // rows in place all 16 fell in one half)
+    const int brow = (row & ~9) | ((row & 1) << 3) | ((row >> 3) & 1);
+    const int ca = (lane & 7) ^ pswz<false>(row), cb = (lane & 7) ^ ((row >> 4) & 7);
     offa[i] = (uint32_t)(((int64_t)row * a.lda + 8 * ca) * 2);
-    offb[i] = (uint32_t)(((int64_t)row * a.ldb + 8 * cb) * 2);
+    offb[i] = (uint32_t)(((int64_t)brow * a.ldb + 8 * cb) * 2);
     kca[i] = 8 * ca;
     kcb[i] = 8 * cb;
   }
   // LDS byte offsets within a stage of this lane's fragment of sub-step h (k 32h .. 32h + 31); the B row
-  // wn 128 + 8 r + j has swizzle (r & 7) for every j
-  const int arow = r, brow = 8 * r;
+  // wn 128 + 8 r + j sits at position wn 128 + 16 (r >> 1) + (r & 1) + 8 (j & 1) + (j & 6), swizzle r >> 1
+  const int arow = r;
   uint32_t abase[2], bbase[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     abase[h] = arow * 128 + (((4 * h + g) ^ pswz<false>(arow)) << 4);
-    bbase[h] = PTILE + brow * 128 + (((4 * h + g) ^ (r & 7)) << 4);
+    bbase[h] = PTILE + (16 * (r >> 1) + (r & 1)) * 128 + (((4 * h + g) ^ (r >> 1)) << 4);
   }
   // fragment block i of A (rows wm*128 + 16i + r), j of B (rows wn*128 + 8r + j)
   auto frag_a = [&](int stage, int h, int i) {
     return *reinterpret_cast<const bf16x8*>(smem + stage * PSTAGE + abase[h] + (wm * 128 + 16 * i) * 128);
   };
   auto frag_b = [&](int stage, int h, int j) {
-    return *reinterpret_cast<const bf16x8*>(smem + stage * PSTAGE + bbase[h] + (wn * 128 + j) * 128);
+    return *reinterpret_cast<const bf16x8*>(smem + stage * PSTAGE + bbase[h] +
+                                            (wn * 128 + 8 * (j & 1) + (j & 6)) * 128);
   };
   // DMA block q (0..7: A, 8..15: B) of a step into `stage`; klim = K - k0 of the step (K tail: a lane whose
   // chunk starts at or past K reads zero)
