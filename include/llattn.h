@@ -254,7 +254,7 @@ typedef struct llattn_gemm_desc {
   void* aux;                    /* bf16 [M][ld_aux]: gelu' written (LLATTN_ACT_GELU) or read (_MUL_AUX) */
   int64_t ld_aux;
   /* bf16 C [M][ldc] stored split-head (the forward of a projection: a_trans = b_trans = 0, no K split,
-     accumulation or activation, K > 64). */
+     accumulation or activation). */
   llattn_heads_layout c_heads;
 } llattn_gemm_desc;
 

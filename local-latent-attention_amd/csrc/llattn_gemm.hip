@@ -646,7 +646,7 @@ __global__ __launch_bounds__(256) void gemm_persistent_kernel(const GemmArgs a) 
   const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const int total = a.tiles_m * a.tiles_n, nk = a.k_pairs;  // 64-wide k steps per tile (>= 2: launcher)
+  const int total = a.tiles_m * a.tiles_n, nk = a.k_pairs;  // 64-wide k steps per tile (>= 2: launcher pads K)
 
   // DMA block i of this wave: rows 8 (8 wave + i) .. + 7 of the operand tile; lane -> row + lane / 8, and
   // its LDS slot lane % 8 receives the row's chunk (lane % 8) ^ pswz(row).  kc*: first k of that chunk.
@@ -1282,9 +1282,9 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
   HeadsMap ch;
   if (const int32_t rc = heads_map("llattn_gemm (C)", &d->c_heads, d->M, d->ldc, d->N, &ch)) return rc;
   if (ch.T && (d->a_trans || d->b_trans || d->c_dtype != LLATTN_BF16 || d->accumulate || d->act != LLATTN_ACT_NONE ||
-               d->rowadd[0].ptr || d->rowadd[1].ptr || S != 1 || k_pairs < 2))
+               d->rowadd[0].ptr || d->rowadd[1].ptr || S != 1))
     return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: a split-head C needs a_trans = b_trans = 0, bf16 C, no "
-                "accumulation, activation, row addends or K split, and K > %d", PBK);
+                "accumulation, activation, row addends or K split");
   const size_t need = llattn_gemm_workspace_size(d);
   if (need && (!workspace || workspace_bytes < need || !aligned16(workspace)))
     return fail(LLATTN_ERR_WORKSPACE, "llattn_gemm: %d K splits need %zu workspace bytes (got %zu)",
@@ -1324,8 +1324,11 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
   // per CU
   const int64_t c_bytes = ((int64_t)(d->M - 1) * d->ldc + d->N) * 2;
   const bool rowadd = d->rowadd[0].ptr || d->rowadd[1].ptr;
-  if (!d->a_trans && !d->b_trans && S == 1 && d->c_dtype == LLATTN_BF16 && !d->accumulate && k_pairs >= 2 &&
+  if (!d->a_trans && !d->b_trans && S == 1 && d->c_dtype == LLATTN_BF16 && !d->accumulate &&
       c_bytes < (int64_t(1) << 31)) {
+    // the pipeline fetches two 64-wide steps ahead: a contraction of one step runs as two, the second reading
+    // zeros past K (every lane's chunk lies past it), which leaves the sums unchanged
+    a.k_pairs = std::max(2, k_pairs);
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
       cus = 256;
@@ -1343,7 +1346,7 @@ extern "C" int32_t llattn_gemm(const llattn_gemm_desc* d, void* workspace, size_
                 "below 2 GiB", (long long)c_bytes);
   } else if (rowadd && !d->b_trans) {
     return fail(LLATTN_ERR_UNSUPPORTED, "llattn_gemm: row addends with a k-contiguous B need the persistent kernel "
-                "(no K split or accumulation, K > %d, C below 2 GiB)", PBK);
+                "(no K split or accumulation, C below 2 GiB)");
   } else if (!d->a_trans && !d->b_trans) launch<true, true>(a, S, d->c_dtype, st);
   else if (!d->a_trans && d->b_trans) launch<true, false>(a, S, d->c_dtype, st);
   else if (d->a_trans && d->b_trans) launch<false, false>(a, S, d->c_dtype, st);

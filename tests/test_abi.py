@@ -262,7 +262,6 @@ def test_gemm_rowsum_validation(kw, msg):
 
 @pytest.mark.parametrize("hl,kw,code,msg", [
     ((2048, 88, 48), dict(accumulate=1), 4, b"split-head C needs"),
-    ((2048, 88, 48), dict(K=64, lda=64, ldb=64), 4, b"split-head C needs"),
     ((2048, 88, 48), dict(c_dtype=0), 4, b"split-head C needs"),
     ((2048, 88, 48), dict(split_k=2), 4, b"split-head C needs"),
     ((2048, 84, 48), {}, 3, b"multiple of 8"),

@@ -72,6 +72,26 @@ def test_linear_k_tail(M, N, K):
     assert _err(gemm.linear(x, w, b), x.float() @ w.float().T + b) < BF16_TOL
 
 
+@pytest.mark.parametrize("M,N,K", [(32768, 1024, 64), (8192, 1408, 40), (32768, 256, 8)])
+def test_linear_single_k_step(M, N, K):
+    """A contraction of at most one 64-wide step on the persistent kernel (config 3's r_out forward, K = Ld =
+    64): the pipeline runs it as two steps, the second reading zeros; the split-head store gives the same
+    bits."""
+    from llattn_amd import gemm
+    dev = require_cuda()
+    print("case: linear single k step", M, N, K, flush=True)
+    g = torch.Generator(device=dev).manual_seed(M + 5 * N + K)
+    xb, wb = _rand(M, K + 24, gen=g, dev=dev), _rand(N, K + 24, gen=g, dev=dev)
+    x, w = xb[:, :K], wb[:, :K]
+    b = torch.randn(N, device=dev, generator=g)
+    got = gemm.linear(x, w, b)
+    assert _err(got, x.float() @ w.float().T + b) < BF16_TOL
+    if N % 64 == 0:
+        T = 2048
+        heads = gemm.linear(x, w, b, heads=(T, 64, N // 64))
+        assert torch.equal(heads, _to_heads(got, T, 64, N // 64))
+
+
 @pytest.mark.parametrize("M,N,K", [(97, 40, 208), (300, 264, 1000), (3, 512, 72)])
 def test_matmul_nn_k_tail(M, N, K):
     from llattn_amd import gemm
