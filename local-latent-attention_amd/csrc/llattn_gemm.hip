@@ -1191,6 +1191,11 @@ int resolve_split(const llattn_gemm_desc* d) {
   const int64_t pairs = (d->K + PBK - 1) / PBK;
   const int64_t smax = std::max<int64_t>(1, pairs / 4);
   const double t_tile = 2.0 * BM * BN * (double)pairs * PBK / 4.4e12;  // seconds per whole tile
+  // unsplit, a bf16 product of k-contiguous operands runs on the persistent kernel, whose tiles pay no
+  // fill or partial epilogue of their own (config 3's r_out input gradient, 128 tiles of 16 steps with 64
+  // valid columns: 25.5 us unsplit against 32.4 us in 2 splits plus their reduction)
+  const bool persistent = !d->a_trans && !d->b_trans && d->c_dtype == LLATTN_BF16 && !d->accumulate &&
+                          d->act == LLATTN_ACT_NONE;
   int best = 1;
   double best_t = 1e30;
   for (int64_t S = 1; S <= std::min<int64_t>(smax, 64); ++S) {
@@ -1198,7 +1203,7 @@ int resolve_split(const llattn_gemm_desc* d) {
     // needs a second round must save more than that (52 tiles, K = 32768: 4 splits in one round 260 us,
     // 9 splits in two rounds ~300 us)
     const double rounds = (double)((tiles * S + 255) / 256);
-    const double t = rounds * (t_tile / (double)S + 15e-6) +
+    const double t = rounds * (t_tile / (double)S + (S == 1 && persistent ? 0.0 : 15e-6)) +
                      (S > 1 ? 2.0 * S * d->M * (double)d->N * 4.0 / 5e12 : 0.0);
     if (t < best_t * 0.999) {
       best_t = t;
