@@ -469,6 +469,8 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
   __shared__ __align__(16) float gls[DHP], grs[DHP];
   __shared__ __align__(16) float lse2s[2][64], Dss[2][64];
   __shared__ __align__(16) int los[2][64];
+  constexpr int SPP = DHP + 8;              // row pitch of the output staging rows
+  __shared__ __align__(16) T SST[8 * 16 * SPP];  // per wave: 16 output rows on their way to HBM
 
   const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -493,26 +495,33 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
     __builtin_amdgcn_raw_buffer_store_b64(x, rs, off, 0, 0);
   };
 
-  // An accumulator tile row (lane (r, g) holds columns 16t + 4g .. 16t + 4g + 3 of block t, t < NT) times
-  // `scale`, as bf16 16-byte pieces: for each block pair (2p, 2p+1) lanes g and g ^ 1 (16 lanes apart)
-  // swap halves with v_permlane16_swap, so an even g holds columns 32p + 4g .. +7 and an odd g columns
-  // 32p + 16 + 4(g-1) .. +7, and one store writes 64 contiguous bytes of each of 16 rows.  Every lane
-  // takes part in the swaps; rows or columns out of range store past the buffer extent (dropped).
-  auto store_acc16 = [&](__amdgpu_buffer_rsrc_t rs, bool ok, int grow, int st, const f32x4 (&v)[NT], float sc) {
+  // The wave's 16 accumulator rows (lane (r, g) holds columns 16t + 4g .. 16t + 4g + 3 of row r for block
+  // t < NT) times `sc`, as bf16, to rows grow0 .. grow0 + 15 of the output: staged through this wave's LDS
+  // rows, then stored as 16-byte chunks in row order, so one store instruction writes whole rows (about
+  // five rows of Dh 2 bytes each) instead of 16 rows x 64 bytes.  Rows past T_ (or all of them when !ok)
+  // and columns past Dh store past the buffer extent (dropped).  The LDS operations of a wave run in order,
+  // so the wave's own staging rows need no barrier.
+  auto store_acc16 = [&](__amdgpu_buffer_rsrc_t rs, bool ok, int grow0, int st, const f32x4 (&v)[NT], float sc) {
     typedef int i32x4_t __attribute__((ext_vector_type(4)));
+    // the lane's coordinates from the exec mask (mbcnt), recomputed here rather than kept live across the
+    // callers' loops
+    const int ln = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)), lr = ln & 15, lg = ln >> 4;
+    T* sw = SST + wave * 16 * SPP;
 #pragma unroll
-    for (int p = 0; p < NT / 2; ++p) {
-      const f32x4 u = v[2 * p], w = v[2 * p + 1];
-      const auto s0 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(u[0] * sc, u[1] * sc),
-                                                        pack_bf16x2(w[0] * sc, w[1] * sc), false, false);
-      const auto s1 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(u[2] * sc, u[3] * sc),
-                                                        pack_bf16x2(w[2] * sc, w[3] * sc), false, false);
-      const int d = 32 * p + ((g & 1) ? 16 + 4 * (g - 1) : 4 * g);
-      const i32x4_t x = {(int)s0[0], (int)s1[0], (int)s0[1], (int)s1[1]};
-      __builtin_amdgcn_raw_buffer_store_b128(x, rs, (ok && d < Dh) ? (uint32_t)(grow * st + d) * 2u : kOffOOB, 0, 0);
+    for (int t = 0; t < NT; ++t)
+      *reinterpret_cast<uint2*>(sw + lr * SPP + 16 * t + 4 * lg) =
+          make_uint2(pack_bf16x2(v[t][0] * sc, v[t][1] * sc), pack_bf16x2(v[t][2] * sc, v[t][3] * sc));
+    constexpr int CPR = DHP / 8;  // 16-byte chunks per staged row; 16 CPR is a multiple of 64
+    static_assert((16 * CPR) % 64 == 0, "whole store instructions");
+#pragma unroll
+    for (int it = 0; it < 16 * CPR / 64; ++it) {
+      const int idx = 64 * it + ln, rr = idx / CPR, c = idx % CPR, grr = grow0 + rr;
+      const uint4 x = *reinterpret_cast<const uint4*>(sw + rr * SPP + 8 * c);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, x), rs,
+                                             (ok && grr < T_ && 8 * c < Dh) ? (uint32_t)(grr * st + 8 * c) * 2u : kOffOOB,
+                                             0, 0);
     }
   };
-  static_assert(NT % 2 == 0, "block pairs");
 
   for (int d = tid; d < DHP; d += 512) {
     gls[d] = d < Dh ? a.gl[h * a.gate_hs + d] : 0.f;
@@ -749,7 +758,7 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
         }
       }
       // lane holds dQ[query qi][16t + 4g + i]
-      store_acc16(rdq, full && qv, qi, dq_st, dq, a.scale);
+      store_acc16(rdq, full, qw, dq_st, dq, a.scale);
       lds_barrier();  // tile qt+1 is staged and gated; every wave is done with tile qt-1's buffers
     }
   } else {
@@ -818,9 +827,8 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
           }
         }
         if (half == 0) {  // key tile qt-1 is complete: lane holds dK / dV[key kj][16t + 4g + i]
-          const bool st_ok = own_prev && kv;
-          store_acc16(rdk, st_ok, kj, dk_st, dk, a.scale);
-          store_acc16(rdv, st_ok, kj, dv_st, dv, 1.f);
+          store_acc16(rdk, own_prev, kw, dk_st, dk, a.scale);
+          store_acc16(rdv, own_prev, kw, dv_st, dv, 1.f);
         } else {
 #pragma unroll
           for (int t = 0; t < NT; ++t) {
@@ -833,9 +841,9 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
     }
     // a segment that ends the sequence: its last key tile gets no more queries
     if (t1 == a.n_qt) {
-      const int kj = (t1 - 1) * 64 + row;
-      store_acc16(rdk, kj < T_, kj, dk_st, pk, a.scale);
-      store_acc16(rdv, kj < T_, kj, dv_st, pv, 1.f);
+      const int kw = (t1 - 1) * 64 + w4 * 16;
+      store_acc16(rdk, true, kw, dk_st, pk, a.scale);
+      store_acc16(rdv, true, kw, dv_st, pv, 1.f);
     }
   }
   // gate and dremote partials of the segment: the 32 row threads of each dim (two rows each) added in
