@@ -238,6 +238,7 @@ __global__ __launch_bounds__(256) void latent_bwd_kv_kernel(const LatentArgs a) 
   __shared__ __align__(16) T Qt[DHP * kTP];
   __shared__ __align__(16) T Os[64 * KP];
   __shared__ __align__(16) T Ot[DHP * kTP];
+  __shared__ __align__(16) T Rs[64 * KP];  // drq rows of the tile (wave w: rows 16 w .. 16 w + 15)
   __shared__ float lse2s[64], Dss[64];
   __shared__ int vis[64];
   static_assert(sizeof(T) * 64 * KP >= 2 * DHP * 16 * sizeof(float), "reduction buffer does not fit in Qs");
@@ -360,6 +361,7 @@ __global__ __launch_bounds__(256) void latent_bwd_fused_kernel(const LatentArgs 
   __shared__ __align__(16) T Qt[DHP * kTP]; // rq transposed
   __shared__ __align__(16) T Os[64 * KP];   // dL rows
   __shared__ __align__(16) T Ot[DHP * kTP]; // dL transposed
+  __shared__ __align__(16) T Rs[64 * KP];  // drq rows of the tile (wave w: rows 16 w .. 16 w + 15)
   __shared__ float lse2s[64], Dss[64];
   __shared__ int vis[64];
   static_assert(sizeof(T) * 64 * KP >= 2 * DHP * 16 * sizeof(float), "reduction buffer does not fit in Qs");
@@ -439,18 +441,23 @@ __global__ __launch_bounds__(256) void latent_bwd_fused_kernel(const LatentArgs 
       f32x4 acc[NT];
 #pragma unroll
       for (int t = 0; t < NT; ++t) acc[t] = col_mma(Kt + (16 * t + r) * kTP + 4 * g, ds, f32x4{0.f, 0.f, 0.f, 0.f});
-      if (qi < qend) {
-        T* p = static_cast<T*>(a.drq) + b * a.drq_sb + lh * a.drq_sh + (int64_t)qi * a.drq_sn;
+      // drq: the sub-tile's 16 rows staged in this wave's LDS rows (a wave's LDS operations run in order: no
+      // barrier), then stored as 16-byte chunks in row order, so a store writes whole rows (8 rows of 64
+      // dims) instead of 16 rows x 8 bytes
+      T* sr = Rs + sq * KP;
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          const int d = 16 * t + 4 * g;
-          if (d < a.Ldh) {
-            float v4[4];
+      for (int t = 0; t < NT; ++t)
+        *reinterpret_cast<uint2*>(sr + r * KP + 16 * t + 4 * g) =
+            make_uint2(pack_bf16x2(acc[t][0] * a.scale, acc[t][1] * a.scale),
+                       pack_bf16x2(acc[t][2] * a.scale, acc[t][3] * a.scale));
+      constexpr int CPR = DHP / 8;  // 16-byte chunks per row; 16 CPR is a multiple of 64
+      static_assert((16 * CPR) % 64 == 0, "whole store instructions");
+      T* dbase = static_cast<T*>(a.drq) + b * a.drq_sb + lh * a.drq_sh;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v4[i] = acc[t][i] * a.scale;
-            store4<T>(p + d, v4);
-          }
-        }
+      for (int it = 0; it < 16 * CPR / 64; ++it) {
+        const int idx = 64 * it + lane, rr = idx / CPR, c = idx % CPR, q = q0 + sq + rr;
+        const uint4 x = *reinterpret_cast<const uint4*>(sr + rr * KP + 8 * c);
+        if (q < qend && 8 * c < a.Ldh) *reinterpret_cast<uint4*>(dbase + (int64_t)q * a.drq_sn + 8 * c) = x;
       }
     }
     // ---- latents in lanes (pass KV): S[query 4g+i][latent r], dgk / dgv over the sub-tile's queries ----
