@@ -377,6 +377,20 @@ struct BufTile {
       x[it] = buf_ld16<POLICY>(rs, (task < TASKS && col < Dh) ? (uint32_t)(row * st + col) * 2u : kOffOOB);
     }
   }
+  // rows (r0 + i) / div of the view for r0 + i < r_end (one row per latent query of div tokens); tile rows
+  // past r_end read zero
+  template <int POLICY = kCached>
+  __device__ __forceinline__ void load_div(const uint16_t* base, int st, int r0, int r_end, int div, int Dh,
+                                           int tid) {
+    const int b0 = r0 / div, b_end = r_end > r0 ? (r_end - 1) / div + 1 : b0;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(base + (int64_t)b0 * st, ((int64_t)(b_end - b0 - 1) * st + Dh) * 2);
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int task = tid + NTHR * it, row = task / CPR, col = (task % CPR) * 8, rr = r0 + row;
+      x[it] = buf_ld16<POLICY>(rs, (task < TASKS && rr < r_end && col < Dh) ? (uint32_t)((rr / div - b0) * st + col) * 2u
+                                                                           : kOffOOB);
+    }
+  }
   // tid: the thread's index among the NTHR threads that share the tile
   template <int P>
   __device__ __forceinline__ void store(uint16_t* lds, int tid) const {

@@ -556,6 +556,8 @@ __global__ __launch_bounds__(256, DHP <= 64 ? 3 : 2) void local_fwd32_kernel(con
   const int k_st = (int)a.k_st, v_st = (int)a.v_st;
   const T* kbase = static_cast<const T*>(a.k) + b * a.k_sb + hd * a.k_sh;
   const T* vbase = static_cast<const T*>(a.v) + b * a.v_sb + hd * a.v_sh;
+  const T* rbase = static_cast<const T*>(a.rem) + b * a.r_sb + hd * a.r_sh;
+  const int r_sn = (int)a.r_sn;
 
   const int kbeg = max(0, q0 - W), kend = min(T_, q0 + kWideRows) - 1;  // keys [kbeg, kend)
   const int nch = kend > kbeg ? (kend - kbeg + 63) / 64 : 0;
@@ -600,6 +602,9 @@ __global__ __launch_bounds__(256, DHP <= 64 ? 3 : 2) void local_fwd32_kernel(con
     if (ci + 1 < nch) {
       tk.template load<kStream>(kbase, k_st, c0 + 64, kend, Dh, tid);
       tv.template load<kStream>(vbase, v_st, c0 + 64, kend, Dh, tid);
+    } else {  // the last chunk: the epilogue's remote rows of both query halves, in the key / value registers
+      tk.load_div(rbase, r_sn, q0, min(T_, q0 + 64), a.q_block, Dh, tid);
+      tv.load_div(rbase, r_sn, q0 + 64, min(T_, q0 + kWideRows), a.q_block, Dh, tid);
     }
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
@@ -653,15 +658,13 @@ __global__ __launch_bounds__(256, DHP <= 64 ? 3 : 2) void local_fwd32_kernel(con
   }
 
   // ---- epilogue: normalise, gate, mix.  Lane (c32, h) holds dims 32 db + 8 j + 4 h .. +3 of its query ----
-  {  // the remote rows of both query halves in flight together, issued before the wait for the other waves
-    RowTile<T, DHP> rr0, rr1;
-    const T* rbase = static_cast<const T*>(a.rem) + b * a.r_sb + hd * a.r_sh;
-    rr0.load_div(rbase, a.r_sn, q0, T_, a.q_block, Dh);
-    rr1.load_div(rbase, a.r_sn, q0 + 64, T_, a.q_block, Dh);
-    lds_barrier();  // every wave is done with the key / value buffers
-    rr0.template store<KP>(SQ);
-    rr1.template store<KP>(SQ + TILE);
+  if (nch == 0) {  // no key chunk: the remote rows load here
+    tk.load_div(rbase, r_sn, q0, min(T_, q0 + 64), a.q_block, Dh, tid);
+    tv.load_div(rbase, r_sn, q0 + 64, min(T_, q0 + kWideRows), a.q_block, Dh, tid);
   }
+  lds_barrier();  // every wave is done with the key / value buffers
+  tk.template store<KP>(SQ, tid);
+  tv.template store<KP>(SQ + TILE, tid);
   lds_barrier();
   const float l = l_run + __shfl_xor(l_run, 32);
   const float inv = l > 0.f ? 1.f / l : 0.f;
