@@ -730,30 +730,42 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
         const float lse2 = lse2s[par][row], Dq = Dss[par][row];
         const int lo = los[par][row], hi = qi - 1;
         const int wlo = max(0, qw - a.W), whi = min(qw + 15, T_ - 1) - 1;
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const int kt = qt - 1 + half;
+        // one 16-key sub-step st of key tile kt
+        auto substep = [&](int kt, int st) {
           const T* Ks = SK + ((kt + 3) % 3) * TILE;
           const T* Vs = SV + ((kt + 3) % 3) * TILE;
+          const int s0 = kt * 64 + 16 * st;
+          RowFrag<T, DQ> kf, vf;
+          kf.load_lds(Ks + (16 * st + r) * KP, g);
+          vf.load_lds(Vs + (16 * st + r) * KP, g);
+          const f32x4 sv = row_mma(kf, qf, f32x4{0.f, 0.f, 0.f, 0.f});    // S^T[key][query]
+          const f32x4 dp = row_mma(vf, dof, f32x4{0.f, 0.f, 0.f, 0.f});  // dP^T[key][query]
+          float ds[4];
 #pragma unroll
-          for (int st = 0; st < 4; ++st) {
-            const int s0 = kt * 64 + 16 * st;
-            if (s0 + 15 < wlo || s0 > whi) continue;  // uniform over the wave (also skips tile -1)
-            RowFrag<T, DQ> kf, vf;
-            kf.load_lds(Ks + (16 * st + r) * KP, g);
-            vf.load_lds(Vs + (16 * st + r) * KP, g);
-            const f32x4 sv = row_mma(kf, qf, f32x4{0.f, 0.f, 0.f, 0.f});    // S^T[key][query]
-            const f32x4 dp = row_mma(vf, dof, f32x4{0.f, 0.f, 0.f, 0.f});  // dP^T[key][query]
-            float ds[4];
+          for (int i = 0; i < 4; ++i) {
+            const int j = s0 + 4 * g + i;
+            const float p = fast_exp2(sv[i] * a.scale_log2 - lse2);
+            ds[i] = ((j >= lo) & (j <= hi)) ? p * (dp[i] - Dq) : 0.f;
+          }
+          const i16x4 dsb = pack_bf16x4(ds);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int j = s0 + 4 * g + i;
-              const float p = fast_exp2(sv[i] * a.scale_log2 - lse2);
-              ds[i] = ((j >= lo) & (j <= hi)) ? p * (dp[i] - Dq) : 0.f;
-            }
-            const i16x4 dsb = pack_bf16x4(ds);
+          for (int t = 0; t < NT; ++t) dq[t] = col_mma_rm<KP>(Ks + (16 * st) * KP + 16 * t, dsb, dq[t]);
+        };
+        if (qt > 0) {
+          // The keys [qw - W, qw + 15) of this wave's queries (W <= 64) lie in the five sub-steps w4 .. w4 + 4
+          // of key tiles qt-1 and qt, both staged: run exactly those, without branches, so the products of one
+          // sub-step can overlap the softmax of the next (keys outside the window are masked to zero)
 #pragma unroll
-            for (int t = 0; t < NT; ++t) dq[t] = col_mma_rm<KP>(Ks + (16 * st) * KP + 16 * t, dsb, dq[t]);
+          for (int i = 0; i < 5; ++i) {
+            const int sidx = w4 + i;
+            substep(qt - 1 + (sidx >> 2), sidx & 3);
+          }
+        } else {
+#pragma unroll
+          for (int st = 0; st < 4; ++st) {  // key tile 0 only (there is no tile -1)
+            const int s0 = 16 * st;
+            if (s0 + 15 < wlo || s0 > whi) continue;  // uniform over the wave
+            substep(0, st);
           }
         }
       }
