@@ -640,22 +640,14 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
           }
         }
       }
-      // dremote in the pieces the row was read in
-      {
-        const bool ok = full && qv;
-        if constexpr (GS != 4) {
-          typedef int i32x4_t __attribute__((ext_vector_type(4)));
-          const uint2 lo = (GS == 12 && !ev) ? drp[1] : drp[0], hi = (GS == 12 && !ev) ? drp[GV - 1] : drp[1];
-          const i32x4_t x = {(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
-          __builtin_amdgcn_raw_buffer_store_b128(x, rdr, (ok && dA < Dh) ? (uint32_t)(qi * dr_st + dA) * 2u : kOffOOB,
-                                                 0, 0);
-        }
-        if constexpr (GS != 8) {
-          const uint2 x = (GS == 12 && ev) ? drp[GV - 1] : drp[0];
-          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned int, x), rdr,
-                                                (ok && dB < Dh) ? (uint32_t)(qi * dr_st + dB) * 2u : kOffOOB, 0, 0);
-        }
-      }
+      // dremote: row gr0 + 32 u into row 8 u + lane / 8 of this wave's LDS staging rows (the wave's 16 rows
+      // are 8 w .. 8 w + 7 and 32 + 8 w .. 32 + 8 w + 7 of the tile), stored by flush_dr after the dQ
+      // products: a store issued between the loads of the next tile and their first use makes the
+      // compiler's wait for that use count the store too (one counter for loads and stores, which may
+      // retire out of order), and that wait then also covers loads issued after it
+#pragma unroll
+      for (int j = 0; j < GV; ++j)
+        *reinterpret_cast<uint2*>(SST + (wave * 16 + 8 * u + (lane >> 3)) * SPP + gd0 + 4 * j) = drp[j];
       Dp = sum_lanes8(Dp);
       if ((rtid & 7) == 0) {
         Dss[par][grow] = qv ? Dp : 0.f;
@@ -665,6 +657,25 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
         const int blk = (qb0 + (qr0 + grow >= a.bs)) * a.bs;
         los[par][grow] = qv ? max(max(0, qi - a.W), blk - a.W + 1) : INT_MAX;
       }
+    }
+  };
+
+  // the dremote rows of tile qt that its gate staged in this wave's LDS rows, as 16-byte chunks in row order
+  auto flush_dr = [&](int qt, const __amdgpu_buffer_rsrc_t& rdr) {
+    typedef int i32x4_t __attribute__((ext_vector_type(4)));
+    constexpr int CPR = DHP / 8;
+    static_assert((16 * CPR) % 64 == 0, "whole store instructions");
+    const bool okr = qt < t1;
+    const int q0r = qt * 64;
+    const T* sw = SST + wave * 16 * SPP;
+#pragma unroll
+    for (int it = 0; it < 16 * CPR / 64; ++it) {
+      const int idx = 64 * it + lane, rr = idx / CPR, c = idx % CPR;
+      const int qr = q0r + 8 * wave + (rr & 7) + 32 * (rr >> 3);
+      const uint4 x = *reinterpret_cast<const uint4*>(sw + rr * SPP + 8 * c);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, x), rdr,
+                                             (okr && qr < T_ && 8 * c < Dh) ? (uint32_t)(qr * dr_st + 8 * c) * 2u : kOffOOB,
+                                             0, 0);
     }
   };
 
@@ -691,6 +702,7 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
     for (int e = 0; e < GS; ++e) accl[e] = accr[e] = accb[e] = 0.f;
     load_gate(t0);
     gate(t0, slab(static_cast<T*>(a.dr) + b * a.dr_sb + h * a.dr_sh, dr_st));
+    flush_dr(t0, slab(static_cast<T*>(a.dr) + b * a.dr_sb + h * a.dr_sh, dr_st));
     load_gate(t0 + 1);
   } else {
     if (t0 > 0) {
@@ -769,6 +781,7 @@ __global__ __launch_bounds__(512) void local_bwd_fused_kernel(const LocalArgs a,
           }
         }
       }
+      if (qt + 1 <= tlast) flush_dr(qt + 1, rdr);
       // lane holds dQ[query qi][16t + 4g + i]
       store_acc16(rdq, full, qw, dq_st, dq, a.scale);
       lds_barrier();  // tile qt+1 is staged and gated; every wave is done with tile qt-1's buffers
