@@ -400,6 +400,22 @@ __global__ __launch_bounds__(256) void latent_bwd_fused_kernel(const LatentArgs 
 #pragma unroll
   for (int t = 0; t < NT; ++t) dk[t] = dv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // the drq rows of the previous tile's sub-tile, staged in this wave's LDS rows, as 16-byte chunks in row
+  // order: a store writes whole rows (8 rows of 64 dims) instead of 16 rows x 8 bytes.  They are stored
+  // before the next tile's loads are issued: a store between those loads and their first use would make the
+  // compiler's wait there count it as well (one counter for loads and stores, which may retire out of order).
+  T* dbase = static_cast<T*>(a.drq) + b * a.drq_sb + lh * a.drq_sh;
+  auto flush_drq = [&](int q0p) {
+    constexpr int CPR = DHP / 8;  // 16-byte chunks per row; 16 CPR is a multiple of 64
+    static_assert((16 * CPR) % 64 == 0, "whole store instructions");
+    const T* sr = Rs + 16 * wave * KP;
+#pragma unroll
+    for (int it = 0; it < 16 * CPR / 64; ++it) {
+      const int idx = 64 * it + lane, rr = idx / CPR, c = idx % CPR, q = q0p + 16 * wave + rr;
+      const uint4 x = *reinterpret_cast<const uint4*>(sr + rr * KP + 8 * c);
+      if (q < qend && 8 * c < a.Ldh) *reinterpret_cast<uint4*>(dbase + (int64_t)q * a.drq_sn + 8 * c) = x;
+    }
+  };
   for (int q0 = qbeg; q0 < qend; q0 += 64) {
     lds_barrier();  // every wave is done with the previous tile
     tq.template store_rows<KP>(Qs);
@@ -412,6 +428,7 @@ __global__ __launch_bounds__(256) void latent_bwd_fused_kernel(const LatentArgs 
       lse2s[tid] = (qv && pl != kNegInf) ? pl * kLog2e : 0.f;
       vis[tid] = qv ? visible(qq, a) : 0;
     }
+    if (q0 > qbeg) flush_drq(q0 - 64);
     if (q0 + 64 < qend) load_tile(q0 + 64);
     lds_barrier();
     const int sq = 16 * wave;  // this wave's 16-query sub-tile of the tile
@@ -442,23 +459,13 @@ __global__ __launch_bounds__(256) void latent_bwd_fused_kernel(const LatentArgs 
 #pragma unroll
       for (int t = 0; t < NT; ++t) acc[t] = col_mma(Kt + (16 * t + r) * kTP + 4 * g, ds, f32x4{0.f, 0.f, 0.f, 0.f});
       // drq: the sub-tile's 16 rows staged in this wave's LDS rows (a wave's LDS operations run in order: no
-      // barrier), then stored as 16-byte chunks in row order, so a store writes whole rows (8 rows of 64
-      // dims) instead of 16 rows x 8 bytes
+      // barrier), stored by flush_drq at the next step
       T* sr = Rs + sq * KP;
 #pragma unroll
       for (int t = 0; t < NT; ++t)
         *reinterpret_cast<uint2*>(sr + r * KP + 16 * t + 4 * g) =
             make_uint2(pack_bf16x2(acc[t][0] * a.scale, acc[t][1] * a.scale),
                        pack_bf16x2(acc[t][2] * a.scale, acc[t][3] * a.scale));
-      constexpr int CPR = DHP / 8;  // 16-byte chunks per row; 16 CPR is a multiple of 64
-      static_assert((16 * CPR) % 64 == 0, "whole store instructions");
-      T* dbase = static_cast<T*>(a.drq) + b * a.drq_sb + lh * a.drq_sh;
-#pragma unroll
-      for (int it = 0; it < 16 * CPR / 64; ++it) {
-        const int idx = 64 * it + lane, rr = idx / CPR, c = idx % CPR, q = q0 + sq + rr;
-        const uint4 x = *reinterpret_cast<const uint4*>(sr + rr * KP + 8 * c);
-        if (q < qend && 8 * c < a.Ldh) *reinterpret_cast<uint4*>(dbase + (int64_t)q * a.drq_sn + 8 * c) = x;
-      }
     }
     // ---- latents in lanes (pass KV): S[query 4g+i][latent r], dgk / dgv over the sub-tile's queries ----
     {
@@ -478,6 +485,7 @@ __global__ __launch_bounds__(256) void latent_bwd_fused_kernel(const LatentArgs 
       }
     }
   }
+  if (qend > qbeg) flush_drq(qbeg + (qend - qbeg - 1) / 64 * 64);  // the last tile's drq rows
   // sum the four waves in order: red[which][dim][latent]
   for (int w = 0; w < 4; ++w) {
     lds_barrier();
