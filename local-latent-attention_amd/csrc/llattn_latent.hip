@@ -510,25 +510,33 @@ __global__ __launch_bounds__(256) void latent_bwd_fused_kernel(const LatentArgs 
   }
 }
 
-// dgk / dgv [b][n][lh][d] = sum over segments (in order) of the partials.
+// dgk / dgv [b][n][lh][d] = sum over segments (in order) of the partials; four dims per thread (the latent
+// head dim is a multiple of 4, the partials' rows 16-byte aligned)
 template <typename T>
 __global__ __launch_bounds__(256) void latent_reduce_kernel(const LatentArgs a) {
-  const int64_t total = (int64_t)a.B * a.Lh * a.n_chunks * 2 * a.Ldh;
+  const int dq = a.Ldh / 4;
+  const int64_t total = (int64_t)a.B * a.Lh * a.n_chunks * 2 * dq;
   const int64_t seg_stride = (int64_t)a.n_lt * 16 * 2 * a.Ldh;
   for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
     int64_t rest = idx;
-    const int d = rest % a.Ldh; rest /= a.Ldh;
+    const int d = (int)(rest % dq) * 4; rest /= dq;
     const int which = rest % 2; rest /= 2;
     const int n = rest % a.n_chunks; rest /= a.n_chunks;
     const int lh = rest % a.Lh;
     const int b = rest / a.Lh;
     const float* p = a.part + ((int64_t)b * a.Lh + lh) * a.n_seg * seg_stride + (int64_t)n * 2 * a.Ldh +
                      which * a.Ldh + d;
-    float s = 0.f;
-    for (int k = 0; k < a.n_seg; ++k) s += p[k * seg_stride];
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < a.n_seg; ++k) {
+      const float4 v = *reinterpret_cast<const float4*>(p + k * seg_stride);
+      s[0] += v.x;
+      s[1] += v.y;
+      s[2] += v.z;
+      s[3] += v.w;
+    }
     T* out = which == 0 ? static_cast<T*>(a.dgk) + b * a.dgk_sb + lh * a.dgk_sh + (int64_t)n * a.dgk_sn + d
                         : static_cast<T*>(a.dgv) + b * a.dgv_sb + lh * a.dgv_sh + (int64_t)n * a.dgv_sn + d;
-    *out = from_f<T>(s);
+    store4<T>(out, s);
   }
 }
 
@@ -546,8 +554,8 @@ void launch(bool fwd, const LatentArgs& a, hipStream_t st) {
       hipLaunchKernelGGL((latent_bwd_q_kernel<T, DHP>), dim3(a.B * a.Lh * a.n_qt), dim3(256), 0, st, a);
       hipLaunchKernelGGL((latent_bwd_kv_kernel<T, DHP>), dim3(a.B * a.Lh * a.n_lt * a.n_seg), dim3(256), 0, st, a);
     }
-    const int64_t total = (int64_t)a.B * a.Lh * a.n_chunks * 2 * a.Ldh;
-    const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
+    const int64_t total = (int64_t)a.B * a.Lh * a.n_chunks * 2 * (a.Ldh / 4);
+    const int blocks = (int)std::min<int64_t>((total + 255) / 256, 1024);
     hipLaunchKernelGGL((latent_reduce_kernel<T>), dim3(blocks), dim3(256), 0, st, a);
   }
 }
