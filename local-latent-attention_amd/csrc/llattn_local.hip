@@ -438,13 +438,14 @@ __global__ __launch_bounds__(256) void local_bwd_kv_kernel(const LocalArgs a) {
 // query tiles qt and qt+1, so after step qt key tile qt-1 is complete.  Every
 // row of q, k, v, dy, o_local and remote is read from HBM once per segment
 // (plus one tile of halo at each end), dO never leaves LDS, and each output
-// row is written once, straight from registers.
+// row is written once, through the wave's LDS staging rows (whole-row stores).
 //
 // The two roles work one tile apart, with ONE LDS barrier per step:
 //   query waves 0-3: gate backward of tile qt+1 (8 threads per row, 2 rows per
-//     thread: dO into LDS, D / lse / key bounds, dremote to HBM, gate partial
-//     sums kept per thread in LDS for the segment), then dQ of tile qt over key
-//     tiles qt-1 and qt (16 queries per wave);
+//     thread: dO into LDS, D / lse / key bounds, dremote staged for a store
+//     after the dQ, gate partial sums kept per thread in registers for the
+//     segment), then dQ of tile qt over key tiles qt-1 and qt (16 queries per
+//     wave);
 //   key waves 4-7: stage q / k / v of tile qt+1 into LDS (prefetched one step
 //     ahead), then the dK / dV contributions of tile qt's queries to key tiles
 //     qt-1 (then complete and stored) and qt (kept in registers).
