@@ -108,8 +108,28 @@ __global__ __launch_bounds__(256) void latent_fwd_kernel(const LatentArgs a) {
     }
   }
   const float l = sum_groups(l_run);
-  if (qv) {
-    const float inv = l > 0.f ? 1.f / l : 0.f;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  if (qv && g == 0 && a.lse)
+    a.lse[((int64_t)b * a.Lh + lh) * a.n_q + qi] = l > 0.f ? (m_run + __log2f(l)) * kLn2 : kNegInf;
+  if constexpr (std::is_same_v<T, uint16_t>) {
+    // bf16: the wave's 16 output rows through its own LDS rows of Ks (after a barrier: every wave has read
+    // its last key fragments), then 16-byte chunks in row order, so a store writes whole rows
+    lds_barrier();
+    T* sw = Ks + 16 * wave * KP;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      *reinterpret_cast<uint2*>(sw + r * KP + 16 * t + 4 * g) =
+          make_uint2(pack_bf16x2(acc[t][0] * inv, acc[t][1] * inv), pack_bf16x2(acc[t][2] * inv, acc[t][3] * inv));
+    constexpr int CPR = DHP / 8;  // 16-byte chunks per row; 16 CPR is a multiple of 64
+    static_assert((16 * CPR) % 64 == 0, "whole store instructions");
+    T* obase = static_cast<T*>(a.out) + b * a.o_sb + lh * a.o_sh;
+#pragma unroll
+    for (int it = 0; it < 16 * CPR / 64; ++it) {
+      const int idx = 64 * it + lane, rr = idx / CPR, c = idx % CPR, q = qw + rr;
+      const uint4 x = *reinterpret_cast<const uint4*>(sw + rr * KP + 8 * c);
+      if (q < a.n_q && 8 * c < a.Ldh) *reinterpret_cast<uint4*>(obase + (int64_t)q * a.o_sn + 8 * c) = x;
+    }
+  } else if (qv) {
     T* op = static_cast<T*>(a.out) + b * a.o_sb + lh * a.o_sh + (int64_t)qi * a.o_sn;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -121,7 +141,6 @@ __global__ __launch_bounds__(256) void latent_fwd_kernel(const LatentArgs a) {
         store4<T>(op + d, v4);
       }
     }
-    if (g == 0 && a.lse) a.lse[((int64_t)b * a.Lh + lh) * a.n_q + qi] = l > 0.f ? (m_run + __log2f(l)) * kLn2 : kNegInf;
   }
 }
 
