@@ -503,25 +503,42 @@ __global__ __launch_bounds__(256, DHP <= 64 ? 2 : 1) void local_bwd_wkv_kernel(c
     }
   }
 
-  // ---- rows out: lane (c32, h) holds dims 32 db + 8 j + 4 h .. +3 of key kj ----
-  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-  const auto rdk = make_rsrc(static_cast<T*>(a.dk) + b * a.dk_sb + hd * a.dk_sh,
-                             ((int64_t)(T_ - 1) * a.dk_st + Dh) * 2);
-  const auto rdv = make_rsrc(static_cast<T*>(a.dv) + b * a.dv_sb + hd * a.dv_sh,
-                             ((int64_t)(T_ - 1) * a.dv_st + Dh) * 2);
-  const int dk_st = (int)a.dk_st, dv_st = (int)a.dv_st;
+  // ---- rows out: lane (c32, h) holds dims 32 db + 8 j + 4 h .. +3 of key kj.  The wave's 32 dK and 32 dV
+  // rows go through its own LDS rows (after a barrier: every wave is done with the query chunks), then out
+  // as 16-byte chunks in row order, so a store writes whole rows instead of 32 rows x 8 bytes ----
+  lds_barrier();
+  T* sk = SQO + kw * KP;                // dK rows of the wave: rows kw .. kw + 31
+  T* sv = SQO + (kWideRows + kw) * KP;  // dV rows
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int d = 32 * db + 8 * j + 4 * h;
-      const bool ok = kj < T_ && d < Dh;
-      const u32x2 kv = {pack_bf16x2(dk[db][4 * j] * a.scale, dk[db][4 * j + 1] * a.scale),
-                        pack_bf16x2(dk[db][4 * j + 2] * a.scale, dk[db][4 * j + 3] * a.scale)};
-      const u32x2 vv = {pack_bf16x2(dv[db][4 * j], dv[db][4 * j + 1]), pack_bf16x2(dv[db][4 * j + 2], dv[db][4 * j + 3])};
-      __builtin_amdgcn_raw_buffer_store_b64(kv, rdk, ok ? (uint32_t)(kj * dk_st + d) * 2u : kOffOOB, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b64(vv, rdv, ok ? (uint32_t)(kj * dv_st + d) * 2u : kOffOOB, 0, 0);
+      *reinterpret_cast<uint2*>(sk + c32 * KP + d) =
+          make_uint2(pack_bf16x2(dk[db][4 * j] * a.scale, dk[db][4 * j + 1] * a.scale),
+                     pack_bf16x2(dk[db][4 * j + 2] * a.scale, dk[db][4 * j + 3] * a.scale));
+      *reinterpret_cast<uint2*>(sv + c32 * KP + d) =
+          make_uint2(pack_bf16x2(dv[db][4 * j], dv[db][4 * j + 1]), pack_bf16x2(dv[db][4 * j + 2], dv[db][4 * j + 3]));
     }
+  typedef int i32x4_t __attribute__((ext_vector_type(4)));
+  const auto rdk = make_rsrc(static_cast<T*>(a.dk) + b * a.dk_sb + hd * a.dk_sh,
+                             ((int64_t)(T_ - 1) * a.dk_st + Dh) * 2);
+  const auto rdv = make_rsrc(static_cast<T*>(a.dv) + b * a.dv_sb + hd * a.dv_sh,
+                             ((int64_t)(T_ - 1) * a.dv_st + Dh) * 2);
+  const int dk_st = (int)a.dk_st, dv_st = (int)a.dv_st;
+  constexpr int CPR = DHP / 8;  // 16-byte chunks per row; 32 CPR is a multiple of 64
+  static_assert((32 * CPR) % 64 == 0, "whole store instructions");
+#pragma unroll
+  for (int it = 0; it < 32 * CPR / 64; ++it) {
+    const int idx = 64 * it + lane, rr = idx / CPR, c = idx % CPR, key = j0 + kw + rr;
+    const bool ok = key < T_ && 8 * c < Dh;
+    const uint4 xk = *reinterpret_cast<const uint4*>(sk + rr * KP + 8 * c);
+    const uint4 xv = *reinterpret_cast<const uint4*>(sv + rr * KP + 8 * c);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, xk), rdk,
+                                           ok ? (uint32_t)(key * dk_st + 8 * c) * 2u : kOffOOB, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, xv), rdv,
+                                           ok ? (uint32_t)(key * dv_st + 8 * c) * 2u : kOffOOB, 0, 0);
+  }
 }
 
 // ----------------------------------------------------------------------------
