@@ -93,7 +93,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const XT* x, int64_t l
 }
 
 template <typename XT, typename DYT, int NCH>
-__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const DYT* __restrict__ dy, int64_t lddy,
+__global__ __launch_bounds__(256, NCH <= 6 ? 2 : 1) void rmsnorm_bwd_kernel(const DYT* __restrict__ dy, int64_t lddy,
                                                           const XT* __restrict__ x, int64_t ldx,
                                                           const float* __restrict__ rstd,
                                                           const float* __restrict__ w, int M, int D,
