@@ -65,7 +65,7 @@ __device__ __forceinline__ int visible(int s, const LatentArgs& a) {
 // forward
 // ----------------------------------------------------------------------------
 template <typename T, int DHP>
-__global__ __launch_bounds__(256) void latent_fwd_kernel(const LatentArgs a) {
+__global__ __launch_bounds__(256, DHP <= 64 ? 5 : 1) void latent_fwd_kernel(const LatentArgs a) {
   constexpr int DQ = DHP / 4, NT = DHP / 16, KP = DHP + kRowPad<T>;
   __shared__ __align__(16) T Ks[64 * KP];
   __shared__ __align__(16) T Vt[DHP * kTP];
