@@ -251,7 +251,7 @@ __global__ __launch_bounds__(256) void latent_bwd_q_kernel(const LatentArgs a) {
 // backward pass KV: dgk / dgv partial sums of one 16-latent tile over one segment of queries
 // ----------------------------------------------------------------------------
 template <typename T, int DHP>
-__global__ __launch_bounds__(256) void latent_bwd_kv_kernel(const LatentArgs a) {
+__global__ __launch_bounds__(256, DHP <= 32 ? 5 : 1) void latent_bwd_kv_kernel(const LatentArgs a) {
   constexpr int DQ = DHP / 4, NT = DHP / 16, KP = DHP + kRowPad<T>;
   __shared__ __align__(16) T Qs[64 * KP];
   __shared__ __align__(16) T Qt[DHP * kTP];
